@@ -1,0 +1,428 @@
+"""KTIR text generators for the benchmark configurations.
+
+Each generator returns a KTIR module in the surface syntax of the reference's
+examples (``examples/triton-ktir/*.mlir``) and notebook generators
+(``notebooks/demo_gen_mlir.py:109-567``): memory views over pointer
+arguments, access tiles indexed by core id / loop variables, ``ktdp.load`` /
+``ktdp.store``, and arith/math/linalg/tensor compute on the loaded tiles.
+The same text runs on the NumPy oracle and on the GPU backend.
+
+Configurations (all shapes parameterised so tests can shrink them):
+
+1. ``vector_add``       out = x + y, f16, BLOCK elements per block.
+2. ``gather_scatter_add`` out[idx[i], :] += f32(table[idx[i], :]) through
+   indirect access tiles, in chunks of CH rows per step.
+3. ``softmax`` / ``rmsnorm`` row kernels, f32 row reductions.
+4. ``gemm``              C = A @ B, f16 in, f32 accumulate, f16 out.
+5. ``flash_attention``   causal attention, bf16 in/out, online softmax over
+   KV tiles with f32 state.
+"""
+
+from __future__ import annotations
+
+
+def _view(name, ptr, sizes, strides, dtype, indent="    "):
+    dims = ", ".join(f"d{i}" for i in range(len(sizes)))
+    cons = ", ".join(f"d{i} >= 0, -d{i} + {s - 1} >= 0" for i, s in enumerate(sizes))
+    mt = "x".join(str(s) for s in sizes) + "x" + dtype
+    return (f"{indent}%{name} = ktdp.construct_memory_view %{ptr}, sizes: {list(sizes)}, "
+            f"strides: {list(strides)} {{\n"
+            f"{indent}  coordinate_set = affine_set<({dims}) : ({cons})>, "
+            f"memory_space = #ktdp.memory_space<global>\n"
+            f"{indent}}} : memref<{mt}>")
+
+
+def _tile(name, view, idx, shape, view_shape, dtype, indent="    "):
+    dims = ", ".join(f"d{i}" for i in range(len(shape)))
+    cons = ", ".join(f"d{i} >= 0, -d{i} + {s - 1} >= 0" for i, s in enumerate(shape))
+    vt = "x".join(str(s) for s in view_shape) + "x" + dtype
+    at = "x".join(str(s) for s in shape)
+    return (f"{indent}%{name} = ktdp.construct_access_tile %{view}[{', '.join(idx)}] {{\n"
+            f"{indent}  access_tile_set = affine_set<({dims}) : ({cons})>,\n"
+            f"{indent}  access_tile_order = affine_map<({dims}) -> ({dims})>\n"
+            f"{indent}}} : memref<{vt}> -> !ktdp.access_tile<{at}xindex>")
+
+
+def _t(shape, dtype):
+    return "tensor<" + "x".join(str(s) for s in shape) + ("x" if shape else "") + dtype + ">"
+
+
+# ---------------------------------------------------------------------------
+# 1. vector_add
+# ---------------------------------------------------------------------------
+
+def vector_add(n: int = 4096, block: int = 128, cores: int = 32) -> str:
+    """out[i] = x[i] + y[i]; core c owns blocks [c*bpc, (c+1)*bpc)."""
+    assert n % (cores * block) == 0
+    bpc = n // (cores * block)
+    views = "\n".join(_view(v, p, [n], [1], "f16") for v, p in
+                      (("x_view", "x_ptr"), ("y_view", "y_ptr"), ("out_view", "output_ptr")))
+    ind = "      " if bpc > 1 else "    "
+    body = "\n".join([
+        _tile("x_tile", "x_view", ["%offset"], [block], [n], "f16", ind),
+        _tile("y_tile", "y_view", ["%offset"], [block], [n], "f16", ind),
+        f"{ind}%x = ktdp.load %x_tile : !ktdp.access_tile<{block}xindex> -> {_t([block], 'f16')}",
+        f"{ind}%y = ktdp.load %y_tile : !ktdp.access_tile<{block}xindex> -> {_t([block], 'f16')}",
+        f"{ind}%output = arith.addf %x, %y : {_t([block], 'f16')}",
+        _tile("out_tile", "out_view", ["%offset"], [block], [n], "f16", ind),
+        f"{ind}ktdp.store %output, %out_tile : {_t([block], 'f16')}, !ktdp.access_tile<{block}xindex>",
+    ])
+    if bpc == 1:
+        loop = f"    %offset = arith.muli %core_id, %BLOCK_SIZE : index\n{body}\n"
+    else:
+        loop = (f"    %c0 = arith.constant 0 : index\n    %c1 = arith.constant 1 : index\n"
+                f"    %bpc = arith.constant {bpc} : index\n"
+                f"    %first = arith.muli %core_id, %bpc : index\n"
+                f"    scf.for %b = %c0 to %bpc step %c1 : index {{\n"
+                f"      %blk = arith.addi %first, %b : index\n"
+                f"      %offset = arith.muli %blk, %BLOCK_SIZE : index\n{body}\n"
+                f"      scf.yield\n    }}\n")
+    return f"""module {{
+  func.func @add_kernel(%x_ptr: index, %y_ptr: index, %output_ptr: index, %BLOCK_SIZE: index)
+      attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+{views}
+{loop}    return
+  }}
+}}
+"""
+
+
+# ---------------------------------------------------------------------------
+# 2. indirect gather + scatter-add
+# ---------------------------------------------------------------------------
+
+def gather_scatter_add(rows: int = 1 << 20, dim: int = 128, n_idx: int = 262144,
+                       cores: int = 64, chunk: int = 128) -> str:
+    """For each index i (core-major, chunk by chunk):
+    ``g = table[idx[i], :]`` (f16), ``o = out[idx[i], :]`` (f32),
+    ``out[idx[i], :] = o + extf(g)`` — a load/add/store through the same
+    indirect access tile, so duplicates inside one chunk keep the last
+    writer and duplicates across chunks/cores accumulate in order.
+    """
+    per_core = n_idx // cores
+    assert per_core * cores == n_idx and per_core % chunk == 0
+    nch = per_core // chunk
+    vss = (f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {chunk - 1} >= 0, "
+           f"d1 >= 0, -d1 + {dim - 1} >= 0)>")
+    vso = "affine_map<(d0, d1) -> (d0, d1)>"
+
+    def iat(name, view, dtype):
+        return (f"      %{name} = ktdp.construct_indirect_access_tile intermediate_variables(%r, %c)\n"
+                f"          %{view}[ind(%idx_view[%row0 + %r]), (%c)] {{\n"
+                f"        variables_space_set = {vss},\n"
+                f"        variables_space_order = {vso}\n"
+                f"      }} : memref<{rows}x{dim}x{dtype}>, memref<{n_idx}xi32> "
+                f"-> !ktdp.access_tile<{chunk}x{dim}xindex>")
+
+    return f"""module {{
+  func.func @gather_scatter_add(%table_ptr: index, %idx_ptr: index, %out_ptr: index)
+      attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %nch = arith.constant {nch} : index
+    %per_core = arith.constant {per_core} : index
+    %chunk = arith.constant {chunk} : index
+{_view("table_view", "table_ptr", [rows, dim], [dim, 1], "f16")}
+{_view("idx_view", "idx_ptr", [n_idx], [1], "i32")}
+{_view("out_view", "out_ptr", [rows, dim], [dim, 1], "f32")}
+    %core_base = arith.muli %core_id, %per_core : index
+    scf.for %ch = %c0 to %nch step %c1 : index {{
+      %ch_off = arith.muli %ch, %chunk : index
+      %row0 = arith.addi %core_base, %ch_off : index
+{iat("g_tile", "table_view", "f16")}
+{iat("o_tile", "out_view", "f32")}
+      %g = ktdp.load %g_tile : !ktdp.access_tile<{chunk}x{dim}xindex> -> {_t([chunk, dim], 'f16')}
+      %o = ktdp.load %o_tile : !ktdp.access_tile<{chunk}x{dim}xindex> -> {_t([chunk, dim], 'f32')}
+      %g32 = arith.extf %g : {_t([chunk, dim], 'f16')} to {_t([chunk, dim], 'f32')}
+      %sum = arith.addf %o, %g32 : {_t([chunk, dim], 'f32')}
+      ktdp.store %sum, %o_tile : {_t([chunk, dim], 'f32')}, !ktdp.access_tile<{chunk}x{dim}xindex>
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+
+
+# ---------------------------------------------------------------------------
+# 3. row softmax and RMSNorm
+# ---------------------------------------------------------------------------
+
+def _row_header(fn, args, rows, cols, cores, rows_per_core):
+    return (f"  func.func @{fn}({args})\n      attributes {{grid = [{cores}, 1]}} {{\n"
+            f"    %core_id = ktdp.get_compute_tile_id : index\n"
+            f"    %c0 = arith.constant 0 : index\n"
+            f"    %rpc = arith.constant {rows_per_core} : index\n"
+            f"    %row_base = arith.muli %core_id, %rpc : index\n")
+
+
+def softmax(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8) -> str:
+    """y = softmax(x) per row: f32 max, exp, f32 sum, divide, round to f16."""
+    rpc = rows // cores
+    assert rpc * cores == rows and rpc % rblk == 0
+    T16, T32, V32 = _t([rblk, cols], "f16"), _t([rblk, cols], "f32"), _t([rblk], "f32")
+    return f"""module {{
+{_row_header("softmax_kernel", "%x_ptr: index, %y_ptr: index", rows, cols, cores, rpc)}
+    %step = arith.constant {rblk} : index
+{_view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16")}
+{_view("y_view", "y_ptr", [rows, cols], [cols, 1], "f16")}
+    %neg_inf = arith.constant 0xFF800000 : f32
+    %zero = arith.constant 0.0 : f32
+    scf.for %r = %c0 to %rpc step %step : index {{
+      %row = arith.addi %row_base, %r : index
+{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+      %x = ktdp.load %x_acc : !ktdp.access_tile<{rblk}x{cols}xindex> -> {T16}
+      %xf = arith.extf %x : {T16} to {T32}
+      %max_init = tensor.splat %neg_inf : {V32}
+      %mx = linalg.reduce {{ arith.maximumf }} ins(%xf : {T32}) outs(%max_init : {V32}) dimensions = [1]
+      %mxb_init = tensor.empty() : {T32}
+      %mxb = linalg.broadcast ins(%mx : {V32}) outs(%mxb_init : {T32}) dimensions = [1]
+      %d = arith.subf %xf, %mxb : {T32}
+      %e = math.exp %d : {T32}
+      %sum_init = tensor.splat %zero : {V32}
+      %s = linalg.reduce {{ arith.addf }} ins(%e : {T32}) outs(%sum_init : {V32}) dimensions = [1]
+      %sb_init = tensor.empty() : {T32}
+      %sb = linalg.broadcast ins(%s : {V32}) outs(%sb_init : {T32}) dimensions = [1]
+      %p = arith.divf %e, %sb : {T32}
+      %y = arith.truncf %p : {T32} to {T16}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+      ktdp.store %y, %y_acc : {T16}, !ktdp.access_tile<{rblk}x{cols}xindex>
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+
+
+def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8) -> str:
+    """y = x * rsqrt(mean(x^2) + eps) * w, with f32 math and a f16 result."""
+    rpc = rows // cores
+    assert rpc * cores == rows and rpc % rblk == 0
+    T16, T32, V32 = _t([rblk, cols], "f16"), _t([rblk, cols], "f32"), _t([rblk], "f32")
+    W16, W32 = _t([cols], "f16"), _t([cols], "f32")
+    return f"""module {{
+{_row_header("rmsnorm_kernel", "%x_ptr: index, %w_ptr: index, %y_ptr: index, %eps: f32", rows, cols, cores, rpc)}
+    %step = arith.constant {rblk} : index
+{_view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16")}
+{_view("w_view", "w_ptr", [cols], [1], "f16")}
+{_view("y_view", "y_ptr", [rows, cols], [cols, 1], "f16")}
+    %zero = arith.constant 0.0 : f32
+    %ncols = arith.constant {float(cols)} : f32
+{_tile("w_acc", "w_view", ["%c0"], [cols], [cols], "f16")}
+    %w = ktdp.load %w_acc : !ktdp.access_tile<{cols}xindex> -> {W16}
+    %wf = arith.extf %w : {W16} to {W32}
+    scf.for %r = %c0 to %rpc step %step : index {{
+      %row = arith.addi %row_base, %r : index
+{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+      %x = ktdp.load %x_acc : !ktdp.access_tile<{rblk}x{cols}xindex> -> {T16}
+      %xf = arith.extf %x : {T16} to {T32}
+      %sq = arith.mulf %xf, %xf : {T32}
+      %ss_init = tensor.splat %zero : {V32}
+      %ss = linalg.reduce {{ arith.addf }} ins(%sq : {T32}) outs(%ss_init : {V32}) dimensions = [1]
+      %n_t = tensor.splat %ncols : {V32}
+      %ms = arith.divf %ss, %n_t : {V32}
+      %eps_t = tensor.splat %eps : {V32}
+      %mse = arith.addf %ms, %eps_t : {V32}
+      %rstd = math.rsqrt %mse : {V32}
+      %rb_init = tensor.empty() : {T32}
+      %rb = linalg.broadcast ins(%rstd : {V32}) outs(%rb_init : {T32}) dimensions = [1]
+      %xn = arith.mulf %xf, %rb : {T32}
+      %wb_init = tensor.empty() : {T32}
+      %wb = linalg.broadcast ins(%wf : {W32}) outs(%wb_init : {T32}) dimensions = [0]
+      %yf = arith.mulf %xn, %wb : {T32}
+      %y = arith.truncf %yf : {T32} to {T16}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+      ktdp.store %y, %y_acc : {T16}, !ktdp.access_tile<{rblk}x{cols}xindex>
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+
+
+# ---------------------------------------------------------------------------
+# 4. GEMM
+# ---------------------------------------------------------------------------
+
+def gemm(M: int = 8192, N: int = 8192, K: int = 8192, bm: int = 128, bn: int = 128, bk: int = 64,
+         gm: int = 8, gn: int = 8) -> str:
+    """C = A @ B on a gm x gn grid; each core loops over its (M/gm)x(N/gn)
+    block in bm x bn tiles, accumulating f32 over K in bk steps."""
+    tm, tn = M // gm // bm, N // gn // bn
+    assert tm * gm * bm == M and tn * gn * bn == N and K % bk == 0
+    A16, B16 = _t([bm, bk], "f16"), _t([bk, bn], "f16")
+    A32, B32, C32, C16 = _t([bm, bk], "f32"), _t([bk, bn], "f32"), _t([bm, bn], "f32"), _t([bm, bn], "f16")
+    return f"""module {{
+  func.func @gemm_kernel(%a_ptr: index, %b_ptr: index, %c_ptr: index)
+      attributes {{grid = [{gm}, {gn}]}} {{
+    %pid_m, %pid_n = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %K = arith.constant {K} : index
+    %BK = arith.constant {bk} : index
+    %BM = arith.constant {bm} : index
+    %BN = arith.constant {bn} : index
+    %TM = arith.constant {tm} : index
+    %TN = arith.constant {tn} : index
+    %zero = arith.constant 0.0 : f32
+{_view("a_view", "a_ptr", [M, K], [K, 1], "f16")}
+{_view("b_view", "b_ptr", [K, N], [N, 1], "f16")}
+{_view("c_view", "c_ptr", [M, N], [N, 1], "f16")}
+    %m_blk = arith.muli %pid_m, %TM : index
+    %n_blk = arith.muli %pid_n, %TN : index
+    scf.for %i = %c0 to %TM step %c1 : index {{
+      scf.for %j = %c0 to %TN step %c1 : index {{
+        %mt = arith.addi %m_blk, %i : index
+        %nt = arith.addi %n_blk, %j : index
+        %m0 = arith.muli %mt, %BM : index
+        %n0 = arith.muli %nt, %BN : index
+        %acc0 = tensor.splat %zero : {C32}
+        %acc = scf.for %k0 = %c0 to %K step %BK iter_args(%acc_i = %acc0) -> ({C32}) {{
+{_tile("a_acc", "a_view", ["%m0", "%k0"], [bm, bk], [M, K], "f16", "          ")}
+{_tile("b_acc", "b_view", ["%k0", "%n0"], [bk, bn], [K, N], "f16", "          ")}
+          %a = ktdp.load %a_acc : !ktdp.access_tile<{bm}x{bk}xindex> -> {A16}
+          %b = ktdp.load %b_acc : !ktdp.access_tile<{bk}x{bn}xindex> -> {B16}
+          %a32 = arith.extf %a : {A16} to {A32}
+          %b32 = arith.extf %b : {B16} to {B32}
+          %acc_n = linalg.matmul ins(%a32, %b32 : {A32}, {B32}) outs(%acc_i : {C32}) -> {C32}
+          scf.yield %acc_n : {C32}
+        }}
+        %c16 = arith.truncf %acc : {C32} to {C16}
+{_tile("c_acc", "c_view", ["%m0", "%n0"], [bm, bn], [M, N], "f16", "        ")}
+        ktdp.store %c16, %c_acc : {C16}, !ktdp.access_tile<{bm}x{bn}xindex>
+        scf.yield
+      }}
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+
+
+# ---------------------------------------------------------------------------
+# 5. Flash attention (causal)
+# ---------------------------------------------------------------------------
+
+def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: int = 128) -> str:
+    """O = softmax(Q K^T * scale, causal) V with online softmax over KV tiles.
+
+    Grid [S/blk, H, B]; core (qb, h, b) owns query rows [qb*blk, (qb+1)*blk)
+    of head (b, h) and visits KV tiles 0..qb (the causal prefix).
+    """
+    nq = S // blk
+    shp = [B, H, S, D]
+    strides = [H * S * D, S * D, D, 1]
+    T4 = _t([1, 1, blk, D], "bf16")
+    Tb, Tf = _t([blk, D], "bf16"), _t([blk, D], "f32")
+    Sf = _t([blk, blk], "f32")
+    Vf = _t([blk], "f32")
+    at = f"!ktdp.access_tile<1x1x{blk}x{D}xindex>"
+
+    def tile(name, view, row):
+        return _tile(name, view, ["%b", "%h", row, "%c0"], [1, 1, blk, D], shp, "bf16", "      ")
+
+    return f"""module {{
+  func.func @flash_attention(%q_ptr: index, %k_ptr: index, %v_ptr: index, %o_ptr: index, %scale: f32)
+      attributes {{grid = [{nq}, {H}, {B}]}} {{
+    %qb, %h, %b = ktdp.get_compute_tile_id : index, index, index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %BLK = arith.constant {blk} : index
+    %zero = arith.constant 0.0 : f32
+    %neg_inf = arith.constant 0xFF800000 : f32
+{_view("q_view", "q_ptr", shp, strides, "bf16")}
+{_view("k_view", "k_ptr", shp, strides, "bf16")}
+{_view("v_view", "v_ptr", shp, strides, "bf16")}
+{_view("o_view", "o_ptr", shp, strides, "bf16")}
+    %q0 = arith.muli %qb, %BLK : index
+{_tile("q_acc", "q_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, "bf16")}
+    %q4 = ktdp.load %q_acc : {at} -> {T4}
+    %q2 = tensor.collapse_shape %q4 [[0, 1, 2], [3]] : {T4} into {Tb}
+    %q = arith.extf %q2 : {Tb} to {Tf}
+    %scale_t = tensor.splat %scale : {Sf}
+    %m_init = tensor.splat %neg_inf : {Vf}
+    %l_init = tensor.splat %zero : {Vf}
+    %acc_init = tensor.splat %zero : {Tf}
+    %n_kv = arith.addi %qb, %c1 : index
+    %m_f, %l_f, %acc_f = scf.for %j = %c0 to %n_kv step %c1
+        iter_args(%m = %m_init, %l = %l_init, %acc = %acc_init) -> ({Vf}, {Vf}, {Tf}) {{
+      %k0 = arith.muli %j, %BLK : index
+{tile("k_acc", "k_view", "%k0")}
+{tile("v_acc", "v_view", "%k0")}
+      %k4 = ktdp.load %k_acc : {at} -> {T4}
+      %v4 = ktdp.load %v_acc : {at} -> {T4}
+      %k2 = tensor.collapse_shape %k4 [[0, 1, 2], [3]] : {T4} into {Tb}
+      %v2 = tensor.collapse_shape %v4 [[0, 1, 2], [3]] : {T4} into {Tb}
+      %kf = arith.extf %k2 : {Tb} to {Tf}
+      %vf = arith.extf %v2 : {Tb} to {Tf}
+      %kt_init = tensor.empty() : {_t([D, blk], "f32")}
+      %kt = linalg.transpose ins(%kf : {Tf}) outs(%kt_init : {_t([D, blk], "f32")}) permutation = [1, 0]
+      %s_init = tensor.splat %zero : {Sf}
+      %qk = linalg.matmul ins(%q, %kt : {Tf}, {_t([D, blk], "f32")}) outs(%s_init : {Sf}) -> {Sf}
+      %s = arith.mulf %scale_t, %qk : {Sf}
+      %sm_init = tensor.empty() : {Sf}
+      %sm = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>],
+                            iterator_types = ["parallel", "parallel"]}}
+          ins(%s : {Sf}) outs(%sm_init : {Sf}) {{
+        ^bb0(%sv: f32, %out: f32):
+          %row = linalg.index 0 : index
+          %col = linalg.index 1 : index
+          %qpos = arith.addi %q0, %row : index
+          %kpos = arith.addi %k0, %col : index
+          %keep = arith.cmpi ule, %kpos, %qpos : index
+          %r = arith.select %keep, %sv, %neg_inf : f32
+          linalg.yield %r : f32
+      }} -> {Sf}
+      %rm_init = tensor.splat %neg_inf : {Vf}
+      %rm = linalg.reduce {{ arith.maximumf }} ins(%sm : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
+      %m_new = arith.maximumf %m, %rm : {Vf}
+      %p_init = tensor.empty() : {Sf}
+      %p = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0)>,
+                                            affine_map<(d0, d1) -> (d0, d1)>],
+                           iterator_types = ["parallel", "parallel"]}}
+          ins(%sm, %m_new : {Sf}, {Vf}) outs(%p_init : {Sf}) {{
+        ^bb0(%sv: f32, %mv: f32, %out: f32):
+          %dd = arith.subf %sv, %mv : f32
+          %ee = math.exp %dd : f32
+          linalg.yield %ee : f32
+      }} -> {Sf}
+      %ls_init = tensor.splat %zero : {Vf}
+      %ls = linalg.reduce {{ arith.addf }} ins(%p : {Sf}) outs(%ls_init : {Vf}) dimensions = [1]
+      %md = arith.subf %m, %m_new : {Vf}
+      %alpha = math.exp %md : {Vf}
+      %accs_init = tensor.empty() : {Tf}
+      %accs = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0)>,
+                                               affine_map<(d0, d1) -> (d0, d1)>],
+                              iterator_types = ["parallel", "parallel"]}}
+          ins(%acc, %alpha : {Tf}, {Vf}) outs(%accs_init : {Tf}) {{
+        ^bb0(%av: f32, %al: f32, %out: f32):
+          %sc = arith.mulf %av, %al : f32
+          linalg.yield %sc : f32
+      }} -> {Tf}
+      %acc_n = linalg.matmul ins(%p, %vf : {Sf}, {Tf}) outs(%accs : {Tf}) -> {Tf}
+      %la = arith.mulf %l, %alpha : {Vf}
+      %l_n = arith.addf %la, %ls : {Vf}
+      scf.yield %m_new, %l_n, %acc_n : {Vf}, {Vf}, {Tf}
+    }}
+    %o_init = tensor.empty() : {Tf}
+    %of = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0)>,
+                                          affine_map<(d0, d1) -> (d0, d1)>],
+                         iterator_types = ["parallel", "parallel"]}}
+        ins(%acc_f, %l_f : {Tf}, {Vf}) outs(%o_init : {Tf}) {{
+      ^bb0(%av: f32, %lv: f32, %out: f32):
+        %q_ = arith.divf %av, %lv : f32
+        linalg.yield %q_ : f32
+    }} -> {Tf}
+    %ob = arith.truncf %of : {Tf} to {Tb}
+    %o4 = tensor.expand_shape %ob [[0, 1, 2], [3]] output_shape [1, 1, {blk}, {D}] : {Tb} into {T4}
+{_tile("o_acc", "o_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, "bf16")}
+    ktdp.store %o4, %o_acc : {T4}, {at}
+    return
+  }}
+}}
+"""

@@ -1,0 +1,1412 @@
+"""NumPy restatement of the reference KTIR interpreter (test oracle only).
+
+TEST INFRASTRUCTURE: imported only by ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s ``cpu_baseline`` leg, never by the product.
+
+Execution model (reference ``interpreter.py:122-194``, ``grid.py:524-623``):
+every simulated core runs the whole function, one core after another in
+core-id order (x fastest, ``grid.py:455-469``); each op is one or a few NumPy
+calls; tensors live in a sparse, byte-addressed HBM (``memory.py:167-352``)
+whose reads past an allocation's end give zeros and whose writes past it are
+dropped.  Pointer arguments are element indices ``stick*128 // bytes``
+(``dtypes.py:79-85``).
+
+How each part is pinned (see ``tests/test_oracle_*.py``):
+- memory read/write/pad/truncate: reference golden vectors
+  (``tests/test_ktir_cpu.py:51-115`` values) + brute-force index checks;
+- load/store/gather/scatter, collisions: reference golden vectors
+  (``tests/test_indirect_access.py:122-441``, ``tests/test_tile.py:175-328``);
+- f16 elementwise: closed form (IEEE RNE of the f64 result);
+- ``_tree_fold``: brute-force pairwise-halving model on small inputs and the
+  reference's exact small values (reduce → 10, outs init → 110);
+- matmul: closed form (f32 sequential-k sum of exact products for f16);
+- transcendentals on f32 tiles and the f32 BLAS matmul order:
+  tolerance-only ("parity unpinned" beyond rtol/atol, as in the reference's
+  own tests);
+- LX-overflow accounting (``grid.py:255-350``): parity unpinned — restated
+  from source text, no reference fixture exercises its exact boundary.
+
+bf16 is an extension (the reference has none, ``dtypes.py:24-39``): bf16
+tiles hold float32 data that is always rounded to the nearest bf16 (RNE);
+HBM stores bf16 as uint16 bit patterns.
+"""
+
+from __future__ import annotations
+
+import bisect
+import math
+import operator
+from dataclasses import dataclass, field
+from typing import Any, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from ktir_cpu_amd.affine import AffineMap, AffineSet, Box, evaluate
+from ktir_cpu_amd.ir import IRModule, Operation
+from ktir_cpu_amd.parser import KTIRParser
+
+STICK_BYTES = 128
+
+# ---------------------------------------------------------------------------
+# dtypes (reference dtypes.py:24-97, plus bf16)
+# ---------------------------------------------------------------------------
+
+_NP = {
+    "f16": np.float16, "fp16": np.float16, "float16": np.float16,
+    "f32": np.float32, "float32": np.float32,
+    "bf16": np.float32,
+    "i1": np.bool_, "i32": np.int32, "si32": np.int32, "index": np.int32,
+    "i64": np.int64, "si64": np.int64, "ui32": np.uint32,
+}
+_BYTES = {"bf16": 2}
+
+
+def to_np_dtype(d: str):
+    if d in ("fp8", "mxfp8"):
+        raise NotImplementedError(f"dtype {d!r} is a placeholder")
+    try:
+        return np.dtype(_NP[d])
+    except KeyError:
+        raise ValueError(f"Unsupported KTIR dtype: {d!r}")
+
+
+def bytes_per_elem(d: str) -> int:
+    return _BYTES.get(d) or int(to_np_dtype(d).itemsize)
+
+
+def to_ktir_dtype(npd) -> str:
+    npd = np.dtype(npd)
+    m = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.int32): "i32",
+         np.dtype(np.int64): "i64", np.dtype(np.uint16): "bf16"}
+    if npd not in m:
+        raise ValueError(f"No KTIR dtype for NumPy dtype: {npd!r}")
+    return m[npd]
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round float32 values to the nearest bf16 (ties to even), as float32."""
+    a = np.asarray(x, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(a), a, out).astype(np.float32)
+
+
+def bf16_bits(x) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Values (reference ir_types.py:52-477)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class OracleTile:
+    data: np.ndarray
+    dtype: str
+    shape: Tuple[int, ...]
+
+    def copy(self):
+        return OracleTile(self.data.copy(), self.dtype, self.shape)
+
+    def size_bytes(self):
+        return self.data.nbytes
+
+
+def _mk(data, dtype, shape) -> OracleTile:
+    if dtype == "bf16":
+        data = bf16_round(data)
+    return OracleTile(data, dtype, tuple(shape))
+
+
+@dataclass
+class MemRef:
+    base_ptr: int
+    shape: Tuple
+    strides: List[int]
+    memory_space: str
+    dtype: str
+    coordinate_set: Any = None
+    lx_core_id: Optional[int] = None
+
+    @property
+    def byte_address(self):
+        return self.base_ptr * bytes_per_elem(self.dtype)
+
+
+@dataclass
+class TileRef:
+    base_ptr: int
+    shape: Tuple
+    strides: List[int]
+    memref: MemRef
+    dtype: str
+
+
+@dataclass
+class AccessTile:
+    parent_ref: TileRef
+    shape: Tuple
+    base_map: AffineMap
+    coordinate_set: Any
+    coordinate_order: Optional[AffineMap]
+
+
+@dataclass
+class IndirectAccessTile:
+    parent_ref: MemRef
+    shape: Tuple
+    dim_subscripts: List[Dict]
+    index_views: List[MemRef]
+    vss: Any
+    vso: Optional[AffineMap]
+
+
+class _Yield:
+    __slots__ = ("values",)
+
+    def __init__(self, values):
+        self.values = values
+
+
+def _unwrap(res):
+    if not isinstance(res, _Yield):
+        return res
+    if not res.values:
+        return None
+    return res.values[0] if len(res.values) == 1 else tuple(res.values)
+
+
+# ---------------------------------------------------------------------------
+# Sparse memory store (reference memory.py:142-306)
+# ---------------------------------------------------------------------------
+
+class _Store(dict):
+    def find(self, ptr: int, elem_size: int):
+        if ptr in self:
+            return ptr, self[ptr], 0
+        if not self:
+            return None
+        keys = sorted(self.keys())
+        i = bisect.bisect_right(keys, ptr) - 1
+        if i >= 0:
+            base = keys[i]
+            data = self[base]
+            end = base + data.size * data.itemsize
+            if base < ptr < end:
+                return base, data, (ptr - base) // elem_size
+        return None
+
+    def read(self, ptr: int, n: int, dtype: str, offsets=None) -> np.ndarray:
+        alloc = self.find(ptr, bytes_per_elem(dtype))
+        if alloc is None:
+            raise ValueError(f"Read from unmapped address 0x{ptr:x} (n_elements={n})")
+        _, data, eo = alloc
+        flat = data.ravel()
+        if offsets is not None:
+            idx = eo + offsets
+            oob = idx >= flat.size
+            if oob.any():
+                idx = np.where(oob, 0, idx)
+                res = flat[idx]
+                res[oob] = 0
+            else:
+                res = flat[idx]
+            return _from_storage(res, dtype)
+        end = eo + n
+        npd = _storage_dtype(dtype)
+        if end <= flat.size:
+            return _from_storage(flat[eo:end].astype(npd, copy=True), dtype)
+        res = np.zeros(n, dtype=npd)
+        avail = flat.size - eo
+        res[:avail] = flat[eo:]
+        return _from_storage(res, dtype)
+
+    def write(self, ptr: int, data: np.ndarray, offsets=None):
+        alloc = self.find(ptr, data.itemsize)
+        if offsets is not None:
+            if alloc is None:
+                raise ValueError(f"Scatter to unmapped address 0x{ptr:x}")
+            _, buf, eo = alloc
+            idx = eo + offsets
+            inb = idx < buf.ravel().size
+            if not inb.all():
+                buf.ravel()[idx[inb]] = data.ravel()[inb]
+            else:
+                buf.ravel()[idx] = data.ravel()
+            return
+        if alloc is not None:
+            base, existing, eo = alloc
+            flat = existing.flatten()
+            src = data.ravel()
+            end = eo + src.size
+            if end <= flat.size:
+                flat[eo:end] = src
+            else:
+                flat[eo:] = src[:flat.size - eo]
+            self[base] = flat.reshape(existing.shape)
+            return
+        self[ptr] = data.flatten()
+
+
+def _storage_dtype(dtype: str):
+    return np.uint16 if dtype == "bf16" else to_np_dtype(dtype)
+
+
+def _from_storage(arr: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16" and arr.dtype == np.uint16:
+        return bf16_from_bits(arr)
+    return arr
+
+
+def _to_storage(arr: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_bits(arr)
+    return arr
+
+
+class _HBM:
+    def __init__(self):
+        self.memory = _Store()
+        self.next_ptr = 0x10000
+
+    def allocate(self, size: int) -> int:
+        ptr = self.next_ptr
+        self.next_ptr = (self.next_ptr + size + STICK_BYTES - 1) & ~(STICK_BYTES - 1)
+        return ptr // STICK_BYTES
+
+
+class _LX:
+    def __init__(self, size_mb: int):
+        self.capacity = size_mb * 1024 * 1024
+        self.used = 0
+        self.memory = _Store()
+        self.next_ptr = 0
+
+
+# ---------------------------------------------------------------------------
+# Per-core context (reference grid.py:41-367)
+# ---------------------------------------------------------------------------
+
+class _Core:
+    def __init__(self, core_id, grid_pos, lx: _LX, hbm: _HBM, lxs):
+        self.core_id = core_id
+        self.grid_pos = grid_pos
+        self.lx = lx
+        self.hbm = hbm
+        self._lxs = lxs
+        self.scopes: List[Dict[str, Any]] = [{}]
+        self.refcount: Dict[int, int] = {}
+        self.uncharged: set = set()
+        self.ptr_stack: List[int] = []
+        self.use_counts: Dict[str, int] = {}
+
+    def push_scope(self):
+        self.ptr_stack.append(self.lx.next_ptr)
+        self.scopes.append({})
+
+    def pop_scope(self):
+        scope = self.scopes.pop()
+        for v in scope.values():
+            if isinstance(v, OracleTile):
+                self._release(v)
+        self.lx.next_ptr = self.ptr_stack.pop()
+
+    def set_value(self, name, value, charge=True):
+        old = self.scopes[-1].get(name)
+        if isinstance(old, OracleTile):
+            self._release(old)
+        self.scopes[-1][name] = value
+        if isinstance(value, OracleTile):
+            vid = id(value)
+            if (not charge) or vid in self.uncharged:
+                self.uncharged.add(vid)
+                self.refcount[vid] = self.refcount.get(vid, 0) + 1
+                return
+            if self.refcount.get(vid, 0) == 0:
+                if self.lx.used + value.size_bytes() > self.lx.capacity:
+                    raise MemoryError(
+                        f"LX scratchpad overflow on core {self.core_id}: requested "
+                        f"{value.size_bytes()} bytes, available {self.lx.capacity - self.lx.used} bytes "
+                        f"(capacity {self.lx.capacity} bytes)")
+                self.lx.used += value.size_bytes()
+            self.refcount[vid] = self.refcount.get(vid, 0) + 1
+
+    def _release(self, t: OracleTile):
+        vid = id(t)
+        unch = vid in self.uncharged
+        self.refcount[vid] -= 1
+        if self.refcount[vid] == 0:
+            del self.refcount[vid]
+            self.uncharged.discard(vid)
+            if not unch:
+                self.lx.used -= t.size_bytes()
+
+    def get_value(self, name, peek=False):
+        for scope in reversed(self.scopes):
+            if name in scope:
+                v = scope[name]
+                if (not peek and isinstance(v, OracleTile) and self.use_counts.get(name, 0) == 1
+                        and scope is self.scopes[-1]):
+                    del scope[name]
+                    self._release(v)
+                return v
+        raise KeyError(f"Value '{name}' not found in core {self.core_id}")
+
+    def has_value(self, name):
+        return any(name in s for s in self.scopes)
+
+    def get_lx(self, core_id):
+        return self.lx if core_id is None or core_id == self.core_id else self._lxs[core_id]
+
+
+def _use_counts(ops: List[Operation]) -> Dict[str, int]:
+    """Textual operand counts over the body and nested regions (parser_utils.py:62-84)."""
+    counts: Dict[str, int] = {}
+    for op in ops:
+        for n in op.operands:
+            counts[n] = counts.get(n, 0) + 1
+        for r in op.regions:
+            for n, c in _use_counts(r.ops).items():
+                counts[n] = counts.get(n, 0) + c
+    return counts
+
+
+# ---------------------------------------------------------------------------
+# Memory tile ops (reference ops/memory_ops.py:611-964)
+# ---------------------------------------------------------------------------
+
+def _is_contiguous(shape, strides) -> bool:
+    exp = 1
+    for dim, st in zip(reversed(shape), reversed(strides)):
+        if st != exp:
+            return False
+        exp *= dim
+    return True
+
+
+def _store_for(ctx: _Core, memref: MemRef) -> _Store:
+    if memref.memory_space == "HBM":
+        return ctx.hbm.memory
+    return ctx.get_lx(memref.lx_core_id).memory
+
+
+def _write_to_lx(ctx: _Core, data: np.ndarray):
+    ptr = ctx.lx.next_ptr
+    ctx.lx.next_ptr = (ctx.lx.next_ptr + data.nbytes + STICK_BYTES - 1) & ~(STICK_BYTES - 1)
+    ctx.lx.memory.write(ptr, np.ascontiguousarray(data).reshape(-1))
+
+
+def _flat_offsets(shape, strides, coords=None) -> np.ndarray:
+    st = np.asarray(strides, dtype=np.int64)
+    if coords is not None:
+        if len(coords) == 0:
+            return np.empty(0, dtype=np.int64)
+        return np.asarray(coords, dtype=np.int64) @ st
+    if not shape:
+        return np.zeros(1, dtype=np.int64)
+    grids = np.indices(shape, dtype=np.int64)
+    return np.tensordot(st, grids, axes=(0, 0)).reshape(-1)
+
+
+def mem_load(ctx, tref: TileRef, coords=None, offsets=None, result_shape=None) -> OracleTile:
+    store = _store_for(ctx, tref.memref)
+    if offsets is None and coords is None and _is_contiguous(tref.shape, tref.strides):
+        n = int(np.prod(tref.shape))
+        data = store.read(tref.base_ptr, n, tref.dtype).reshape(tref.shape)
+        _write_to_lx(ctx, data)
+        return OracleTile(data, tref.dtype, tuple(tref.shape))
+    if offsets is None:
+        offsets = _flat_offsets(tref.shape, tref.strides, coords)
+    data = store.read(tref.base_ptr, len(offsets), tref.dtype, offsets=offsets)
+    out_shape = tuple(result_shape) if result_shape is not None else tuple(tref.shape)
+    data = data.reshape(out_shape)
+    _write_to_lx(ctx, data)
+    return OracleTile(data, tref.dtype, out_shape)
+
+
+def mem_store(ctx, tile: OracleTile, tref: TileRef, coords=None, offsets=None):
+    store = _store_for(ctx, tref.memref)
+    src = _to_storage(tile.data, tref.dtype)
+    if offsets is None and coords is None and _is_contiguous(tref.shape, tref.strides):
+        store.write(tref.base_ptr, src.ravel())
+        return
+    if offsets is None:
+        offsets = _flat_offsets(tref.shape, tref.strides, coords)
+    store.write(tref.base_ptr, src.ravel(), offsets=offsets)
+
+
+def _subtile(tref: TileRef, box: Box) -> TileRef:
+    """Reference ops/memory_ops.py:1101-1124 with partition origin 0."""
+    bpe = bytes_per_elem(tref.dtype)
+    off = sum(l * s for l, s in zip(box.lo, tref.strides)) * bpe
+    return TileRef(tref.base_ptr + off, tuple(h - l for l, h in zip(box.lo, box.hi)),
+                   list(tref.strides), tref.memref, tref.dtype)
+
+
+def _iat_points(iat: IndirectAccessTile) -> np.ndarray:
+    pts = iat.vss.enumerate(iat.shape)
+    if iat.vso is not None:
+        pts = sorted(pts, key=lambda p: iat.vso.eval(p))
+    return np.asarray(pts, dtype=np.int64).reshape(len(pts), len(iat.shape))
+
+
+def _iat_coords(ctx, iat: IndirectAccessTile) -> np.ndarray:
+    """Parent-tensor coordinates for every VSS point in VSO order.
+
+    Same values as reference ``_resolve_idx_reads`` + ``_build_indirect_coords``
+    (``ops/memory_ops.py:491-576``), evaluated with NumPy per dimension.
+    """
+    if iat.vso is not None and not iat.vso.is_permutation():
+        raise ValueError("variables_space_order must permute its input dimensions")
+    pts = _iat_points(iat)
+    cols = [pts[:, k] for k in range(pts.shape[1])]
+    coords = []
+    for sub in iat.dim_subscripts:
+        if sub["kind"] == "direct":
+            coords.append(cols[sub["var_index"]])
+        elif sub["kind"] == "direct_expr":
+            coords.append(np.broadcast_to(np.asarray(evaluate(sub["subscript"], cols), dtype=np.int64),
+                                          (len(pts),)))
+        else:
+            iv = iat.index_views[sub["index_view_idx"]]
+            off = 0
+            for e, s in zip(sub["idx_exprs"], iv.strides):
+                off = off + np.asarray(evaluate(e, cols), dtype=np.int64) * s
+            off = np.broadcast_to(np.asarray(off, dtype=np.int64), (len(pts),))
+            store = _store_for(ctx, iv)
+            # reference read_scattered reads each index at base + off*bpe; one
+            # vectorised gather relative to the view base gives the same values
+            vals = store.read(iv.byte_address, len(off), iv.dtype,
+                              offsets=np.ascontiguousarray(off)).astype(np.int64)
+            if vals.size and (vals < 0).any():
+                raise IndexError(f"indirect index {int(vals.min())} is negative")
+            coords.append(vals)
+    return np.stack(coords, axis=1) if coords else np.zeros((len(pts), 0), np.int64)
+
+
+def indirect_load(ctx, iat: IndirectAccessTile, result_shape=None) -> OracleTile:
+    coords = _iat_coords(ctx, iat)
+    pr = iat.parent_ref
+    tref = TileRef(pr.byte_address, pr.shape, pr.strides, pr, pr.dtype)
+    return mem_load(ctx, tref, coords=coords,
+                    result_shape=result_shape if result_shape is not None else iat.shape)
+
+
+def indirect_store(ctx, tile: OracleTile, iat: IndirectAccessTile):
+    if tuple(tile.shape) != tuple(iat.shape):
+        raise ValueError(f"indirect_store: source tile shape {tuple(tile.shape)} does not match "
+                         f"IAT shape {tuple(iat.shape)}")
+    coords = _iat_coords(ctx, iat)
+    pr = iat.parent_ref
+    tref = TileRef(pr.byte_address, pr.shape, pr.strides, pr, pr.dtype)
+    mem_store(ctx, tile, tref, coords=coords)
+
+
+# ---------------------------------------------------------------------------
+# Elementwise helpers (reference dialects/_helpers.py:39-72, ops/_helpers.py)
+# ---------------------------------------------------------------------------
+
+def _is_scalar(v) -> bool:
+    return isinstance(v, (int, float, np.integer, np.floating, bool, np.bool_))
+
+
+def _float_binop(a, b, fn):
+    if _is_scalar(a) and _is_scalar(b):
+        r = fn(np.float16(a), np.float16(b))
+        return np.float16(r) if not isinstance(r, np.float16) else r
+    if isinstance(a, OracleTile) and isinstance(b, OracleTile):
+        return _mk(fn(a.data, b.data), a.dtype, a.shape)
+    if isinstance(a, OracleTile):
+        return _mk(fn(a.data, np.float16(b)), a.dtype, a.shape)
+    return _mk(fn(np.float16(a), b.data), b.dtype, b.shape)
+
+
+def _int_binop(a, b, fn):
+    if isinstance(a, OracleTile) or isinstance(b, OracleTile):
+        if isinstance(a, OracleTile) and isinstance(b, OracleTile):
+            return OracleTile(fn(a.data, b.data), a.dtype, a.shape)
+        if isinstance(a, OracleTile):
+            return OracleTile(fn(a.data, int(b)), a.dtype, a.shape)
+        return OracleTile(fn(int(a), b.data), b.dtype, b.shape)
+    return fn(a, b)
+
+
+def _tile_binop_int(fn, a, b):
+    if isinstance(a, OracleTile) and isinstance(b, OracleTile):
+        r = fn(a.data, b.data)
+        return OracleTile(r, a.dtype, r.shape)
+    if isinstance(a, OracleTile):
+        r = fn(a.data, int(b))
+        return OracleTile(r, a.dtype, r.shape)
+    if isinstance(b, OracleTile):
+        r = fn(int(a), b.data)
+        return OracleTile(r, b.dtype, r.shape)
+    return int(fn(int(a), int(b)))
+
+
+def _truncdiv(a, b):
+    return np.trunc(a / b).astype(np.asarray(a).dtype)
+
+
+def _truncrem(a, b):
+    return np.asarray(a) - _truncdiv(a, b) * np.asarray(b)
+
+
+def _ceildiv(a, b):
+    if isinstance(a, np.ndarray) or isinstance(b, np.ndarray):
+        r = np.ceil(a / b)
+        return r.astype(a.dtype if isinstance(a, np.ndarray) else b.dtype)
+    return math.ceil(a / b)
+
+
+def _unary_float(fn, v):
+    if isinstance(v, OracleTile):
+        d = fn(v.data).astype(v.data.dtype)
+        return _mk(d, v.dtype, d.shape)
+    cast = type(v) if isinstance(v, (float, np.floating)) else float
+    return cast(fn(v))
+
+
+def _erf(x):
+    a = np.abs(x)
+    t = 1.0 / (1.0 + 0.3275911 * a)
+    poly = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))))
+    return np.sign(x) * (1.0 - poly * np.exp(-a * a))
+
+
+_FLOAT_BIN = {
+    "arith.addf": operator.add, "arith.subf": operator.sub, "arith.mulf": operator.mul,
+    "arith.divf": operator.truediv, "arith.remf": operator.mod,
+}
+_INT_BIN = {
+    "arith.addi": operator.add, "arith.subi": operator.sub, "arith.muli": operator.mul,
+    "arith.divui": operator.floordiv, "arith.divsi": _truncdiv, "arith.floordivsi": operator.floordiv,
+    "arith.remui": operator.mod, "arith.remsi": _truncrem, "arith.andi": operator.and_,
+    "arith.ori": operator.or_, "arith.xori": operator.xor, "arith.shli": operator.lshift,
+    "arith.shrsi": operator.rshift,
+}
+_INT_VIA = {
+    "arith.minsi": np.minimum, "arith.maxsi": np.maximum, "arith.minui": np.minimum,
+    "arith.maxui": np.maximum, "arith.ceildivsi": _ceildiv, "arith.ceildivui": _ceildiv,
+}
+_MINMAX = {
+    "arith.maxf": np.maximum, "arith.maximumf": np.maximum, "arith.maxnumf": np.fmax,
+    "arith.minf": np.minimum, "arith.minimumf": np.minimum, "arith.minnumf": np.fmin,
+}
+_MATH = {
+    "math.exp": np.exp, "math.sqrt": np.sqrt, "math.rsqrt": lambda x: 1.0 / np.sqrt(x),
+    "math.log": np.log, "math.log2": np.log2, "math.log1p": np.log1p, "math.tanh": np.tanh,
+    "math.sin": np.sin, "math.cos": np.cos, "math.erf": _erf, "math.ceil": np.ceil,
+    "math.floor": np.floor,
+}
+_COMBINER_IDENTITY = {
+    "arith.addf": 0.0, "arith.addi": 0, "arith.mulf": 1.0, "arith.muli": 1,
+    "arith.maxf": float("-inf"), "arith.maximumf": float("-inf"),
+    "arith.minf": float("inf"), "arith.minimumf": float("inf"),
+}
+_NO_LX_CHARGE = {"arith.constant"}
+
+
+def _bool_not(x):
+    return ~x if isinstance(x, np.ndarray) else not x
+
+
+def _cmp_operands(a, b):
+    is_tile = isinstance(a, OracleTile) or isinstance(b, OracleTile)
+    if is_tile:
+        lhs = a.data if isinstance(a, OracleTile) else np.full(b.shape, a, dtype=b.data.dtype)
+        rhs = b.data if isinstance(b, OracleTile) else np.full(a.shape, b, dtype=a.data.dtype)
+    else:
+        lhs, rhs = a, b
+    return is_tile, lhs, rhs
+
+
+def _cast(value, target, op_name):
+    """Reference ops/arith_ops.py:38-87 (target np dtype)."""
+    if isinstance(value, OracleTile):
+        if value.data.dtype == target:
+            return value
+        return OracleTile(value.data.astype(target), to_ktir_dtype(target), value.shape)
+    if isinstance(value, target):
+        return value
+    r = target(value)
+    if np.issubdtype(np.dtype(target), np.floating) and np.isinf(r) and not np.isinf(float(value)):
+        raise OverflowError(f"{op_name}: {value} overflows {target.__name__}")
+    return r
+
+
+# ---------------------------------------------------------------------------
+# Interpreter
+# ---------------------------------------------------------------------------
+
+class OracleInterpreter:
+    """``load`` / ``tensor_input_output_sizes`` / ``execute_function`` like the reference."""
+
+    def __init__(self, lx_size_mb: int = 2, parser=None):
+        self.module: Optional[IRModule] = None
+        self._parser = parser or KTIRParser()
+        self.lx_size_mb = lx_size_mb
+        self.hbm: Optional[_HBM] = None
+        self.cores_to_run: Optional[Sequence[int]] = None   # bounded-sample timing
+        self.prepare_hook = None   # callable(self) run after argument placement
+
+    # -- direct HBM access by stick (reference memory.py:354-383) -------------
+    def hbm_write(self, stick: int, data: np.ndarray, intra_byte: int = 0):
+        dt = to_ktir_dtype(data.dtype)
+        self.hbm.memory.write(stick * STICK_BYTES + intra_byte, _to_storage(data, dt).ravel()
+                              if dt != "bf16" else data.ravel())
+
+    def hbm_read(self, stick: int, n: int, dtype: str, intra_byte: int = 0) -> np.ndarray:
+        return self.hbm.memory.read(stick * STICK_BYTES + intra_byte, n, dtype)
+
+    # -- API -----------------------------------------------------------------
+    def load(self, src: str):
+        if "\n" in src or src.lstrip().startswith("module"):
+            self.module = self._parser.parse_module(src)
+        else:
+            self.module = self._parser.parse_file(src)
+
+    def arg_names(self, fn: str) -> List[str]:
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        return self.module.get_function(fn).arg_names
+
+    def tensor_input_output_sizes(self, fn: str):
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        return self.module.get_function(fn).tensor_sizes
+
+    def execute_function(self, fn_name: str, **kwargs) -> Dict[str, np.ndarray]:
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        fn = self.module.get_function(fn_name)
+        declared = fn.arg_names
+        if kwargs and declared and not any(k in declared for k in kwargs):
+            if len(kwargs) == len(declared):
+                kwargs = dict(zip(declared, kwargs.values()))
+        self.hbm = _HBM()
+        nx, ny, nz = fn.grid
+        ncores = nx * ny * nz
+        lxs = [_LX(self.lx_size_mb) for _ in range(ncores)]
+        byte_ptrs, ptrs = {}, {}
+        for name, t in kwargs.items():
+            if isinstance(t, np.ndarray):
+                dt = to_ktir_dtype(t.dtype)
+                stick = self.hbm.allocate(t.nbytes)
+                addr = stick * STICK_BYTES
+                self.hbm.memory.write(addr, t.flatten())
+                byte_ptrs[name] = addr
+                ptrs[name] = (stick * STICK_BYTES) // bytes_per_elem(dt)
+            else:
+                ptrs[name] = t
+        if self.prepare_hook is not None:
+            self.prepare_hook(self)
+        counts = _use_counts(fn.operations)
+        order = range(ncores) if self.cores_to_run is None else self.cores_to_run
+        for cid in order:
+            z = cid // (nx * ny)
+            rem = cid % (nx * ny)
+            ctx = _Core(cid, (rem % nx, rem // nx, z), lxs[cid], self.hbm, lxs)
+            ctx.use_counts = counts
+            for name, v in ptrs.items():
+                ctx.set_value("%" + name, v)
+            self._run(fn.operations, ctx)
+        out = {}
+        for name, t in kwargs.items():
+            if isinstance(t, np.ndarray):
+                dt = to_ktir_dtype(t.dtype)
+                n = int(np.prod(t.shape))
+                data = self.hbm.memory.read(byte_ptrs[name], n, dt)
+                if dt == "bf16":
+                    data = bf16_bits(data)
+                out[name] = data.reshape(t.shape)
+        return out
+
+    # -- execution -----------------------------------------------------------
+    def _run(self, ops, ctx):
+        res = None
+        for op in ops:
+            res = self._exec(op, ctx)
+        return res
+
+    def _exec(self, op: Operation, ctx: _Core):
+        h = getattr(self, "_h_" + op.op_type.replace(".", "_"), None)
+        if h is None:
+            if op.op_type in _FLOAT_BIN:
+                a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+                res = _float_binop(a, b, _FLOAT_BIN[op.op_type])
+            elif op.op_type in _INT_BIN:
+                a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+                res = _int_binop(a, b, _INT_BIN[op.op_type])
+            elif op.op_type in _INT_VIA:
+                a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+                res = _tile_binop_int(_INT_VIA[op.op_type], a, b)
+            elif op.op_type in _MINMAX:
+                a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+                f = _MINMAX[op.op_type]
+                if isinstance(a, OracleTile) and isinstance(b, OracleTile):
+                    res = _mk(f(a.data, b.data), a.dtype, a.shape)
+                elif isinstance(a, OracleTile):
+                    res = _mk(f(a.data, b), a.dtype, a.shape)
+                elif isinstance(b, OracleTile):
+                    res = _mk(f(a, b.data), b.dtype, b.shape)
+                else:
+                    res = f(a, b)
+            elif op.op_type in _MATH:
+                res = _unary_float(_MATH[op.op_type], ctx.get_value(op.operands[0]))
+            else:
+                raise ValueError(f"Unknown operation: {op.op_type}")
+        else:
+            res = h(op, ctx)
+        if op.results and res is not None:
+            vals = res if isinstance(res, tuple) else (res,)
+            if len(vals) != len(op.results):
+                raise RuntimeError(f"{op.op_type}: expected {len(op.results)} result(s), got {len(vals)}")
+            charge = op.op_type not in _NO_LX_CHARGE
+            for n, v in zip(op.results, vals):
+                ctx.set_value(n, v, charge=charge)
+        return res
+
+    def _region(self, ops, ctx):
+        return self._run(ops, ctx)
+
+    # ktdp --------------------------------------------------------------------
+    def _h_ktdp_get_compute_tile_id(self, op, ctx):
+        n = max(1, len(op.results))
+        return ctx.grid_pos[0] if n == 1 else tuple(ctx.grid_pos[d] for d in range(n))
+
+    def _h_ktdp_construct_memory_view(self, op, ctx):
+        a = op.attributes
+        ptr = ctx.get_value(op.operands[0])
+        shape = tuple(ctx.get_value(s) if isinstance(s, str) else s for s in a["shape"])
+        strides = [ctx.get_value(s) if isinstance(s, str) else s for s in a["strides"]]
+        cs = a.get("coordinate_set")
+        if isinstance(cs, Box) and not cs.is_concrete:
+            cs = cs.specialize(tuple(ctx.get_value(s) for s in a["shape"] if isinstance(s, str)))
+        lx = a.get("lx_core_id") if a["memory_space"] == "LX" else None
+        return MemRef(ptr, shape, strides, a["memory_space"], a["dtype"], cs, lx)
+
+    def _h_ktdp_construct_access_tile(self, op, ctx):
+        parent = ctx.get_value(op.operands[0])
+        idx = [ctx.get_value(o) for o in op.operands[1:]]
+        a = op.attributes
+        cs = a["coordinate_set"]
+        if isinstance(cs, Box) and not cs.is_concrete:
+            raise NotImplementedError("construct_access_tile: symbolic access_tile_set is not supported")
+        base = a["base_map"].eval(idx)
+        bpe = bytes_per_elem(parent.dtype)
+        off = sum(int(c) * int(s) for c, s in zip(base, parent.strides))
+        tref = TileRef(parent.byte_address + off * bpe, tuple(a["shape"]), list(parent.strides),
+                       parent, parent.dtype)
+        return AccessTile(tref, tuple(a["shape"]), a["base_map"], cs, a.get("coordinate_order"))
+
+    def _h_ktdp_construct_indirect_access_tile(self, op, ctx):
+        parent = ctx.get_value(op.operands[0])
+        views = [ctx.get_value(n) for n in op.operands[1:]]
+        ivars = op.attributes["intermediate_vars"]
+
+        def resolve(e):
+            tag = e[0]
+            if tag == "ssa":
+                return ("const", int(ctx.get_value(e[1])))
+            if tag == "dim":
+                nm = "%" + ivars[e[1]] if e[1] < len(ivars) else None
+                if nm is not None and ctx.has_value(nm):
+                    try:
+                        return ("const", int(ctx.get_value(nm)))
+                    except TypeError:
+                        pass
+                return e
+            if tag == "const":
+                return e
+            return (tag,) + tuple(resolve(c) if isinstance(c, tuple) else c for c in e[1:])
+
+        subs = []
+        for s in op.attributes["dim_subscripts"]:
+            s = dict(s)
+            if "idx_exprs" in s:
+                s["idx_exprs"] = [resolve(e) for e in s["idx_exprs"]]
+            elif s["kind"] == "direct_expr":
+                s["subscript"] = resolve(s["subscript"])
+            subs.append(s)
+        shape = tuple(op.attributes["shape"])
+        vss = op.attributes["variables_space_set"]
+        for i, v in enumerate(ivars):
+            if ctx.has_value("%" + v):
+                if any(p[i] != 0 for p in vss.enumerate(shape)):
+                    raise ValueError(
+                        f"construct_indirect_access_tile: intermediate variable %{v} (index {i}) is an "
+                        f"outer SSA value but its dimension in variables_space_set has a non-zero range.")
+        return IndirectAccessTile(parent, shape, subs, views, vss, op.attributes.get("variables_space_order"))
+
+    def _h_ktdp_load(self, op, ctx):
+        at = ctx.get_value(op.operands[0])
+        rs = op.attributes.get("_result_shape")
+        if isinstance(at, IndirectAccessTile):
+            return indirect_load(ctx, at, rs if rs is not None else at.shape)
+        cs, co = at.coordinate_set, at.coordinate_order
+        if isinstance(cs, Box) and co is None:
+            return mem_load(ctx, _subtile(at.parent_ref, cs))
+        coords = cs.enumerate(at.shape)
+        if co is not None:
+            coords = [co.eval(p) for p in coords]
+        return mem_load(ctx, at.parent_ref, coords=coords, result_shape=rs if rs is not None else at.shape)
+
+    def _h_ktdp_store(self, op, ctx):
+        val = ctx.get_value(op.operands[0])
+        if not isinstance(val, OracleTile):
+            raise TypeError(f"ktdp.store expects a Tile, got {type(val)}")
+        at = ctx.get_value(op.operands[1])
+        if isinstance(at, IndirectAccessTile):
+            indirect_store(ctx, val, at)
+            return None
+        cs, co = at.coordinate_set, at.coordinate_order
+        if isinstance(cs, Box) and co is None:
+            mem_store(ctx, val, _subtile(at.parent_ref, cs))
+            return None
+        coords = cs.enumerate(at.shape)
+        if co is not None:
+            coords = [co.eval(p) for p in coords]
+        mem_store(ctx, val, at.parent_ref, coords=coords)
+        return None
+
+    # arith --------------------------------------------------------------------
+    def _h_arith_constant(self, op, ctx):
+        a = op.attributes
+        v = a.get("value", 0)
+        if a.get("is_tensor"):
+            dt = a.get("dtype", "f16")
+            npd = to_np_dtype(dt)
+            if a.get("dense_list"):
+                return _mk(np.array(v, dtype=npd).reshape(a["shape"]), dt, a["shape"])
+            return _mk(np.full(a["shape"], v, dtype=npd), dt, a["shape"])
+        return v
+
+    def _h_arith_cmpi(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        is_tile, l, r = _cmp_operands(a, b)
+        p = op.attributes["predicate"]
+        fns = {"slt": operator.lt, "ult": operator.lt, "sle": operator.le, "ule": operator.le,
+               "sgt": operator.gt, "ugt": operator.gt, "sge": operator.ge, "uge": operator.ge,
+               "eq": operator.eq, "ne": operator.ne}
+        if p not in fns:
+            raise NotImplementedError(f"arith.cmpi: unsupported predicate '{p}'")
+        res = fns[p](l, r)
+        return OracleTile(res, "i1", res.shape) if is_tile else res
+
+    def _h_arith_cmpf(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        is_tile, l, r = _cmp_operands(a, b)
+        if not is_tile:
+            l, r = float(l), float(r)
+        nan = lambda: np.isnan(l) | np.isnan(r)
+        fns = {
+            "false": lambda: np.zeros_like(l, dtype=bool) if is_tile else False,
+            "oeq": lambda: l == r, "one": lambda: (l != r) & _bool_not(nan()),
+            "olt": lambda: l < r, "ole": lambda: l <= r, "ogt": lambda: l > r, "oge": lambda: l >= r,
+            "ueq": lambda: (l == r) | nan(), "une": lambda: l != r, "ult": lambda: (l < r) | nan(),
+            "ule": lambda: (l <= r) | nan(), "ugt": lambda: (l > r) | nan(), "uge": lambda: (l >= r) | nan(),
+            "ord": lambda: _bool_not(nan()), "uno": nan,
+            "true": lambda: np.ones_like(l, dtype=bool) if is_tile else True,
+        }
+        p = op.attributes["predicate"]
+        if p not in fns:
+            raise NotImplementedError(f"arith.cmpf: unsupported predicate '{p}'")
+        res = fns[p]()
+        return OracleTile(res, "i1", res.shape) if is_tile else res
+
+    def _h_arith_select(self, op, ctx):
+        c = ctx.get_value(op.operands[0])
+        t = ctx.get_value(op.operands[1])
+        f = ctx.get_value(op.operands[2])
+        if isinstance(c, (OracleTile, np.ndarray)):
+            cd = c.data if isinstance(c, OracleTile) else c
+            td = t.data if isinstance(t, OracleTile) else t
+            fd = f.data if isinstance(f, OracleTile) else f
+            res = np.where(cd, td, fd)
+            ref = t if isinstance(t, OracleTile) else f
+            dt = ref.dtype if isinstance(ref, OracleTile) else "f16"
+            shape = ref.shape if isinstance(ref, OracleTile) else res.shape
+            return OracleTile(res, dt, shape)
+        return t if c else f
+
+    def _h_arith_negf(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(-v.data, v.dtype, v.shape) if isinstance(v, OracleTile) else -v
+
+    def _h_arith_absf(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(np.abs(v.data), v.dtype, v.shape) if isinstance(v, OracleTile) else abs(v)
+
+    _h_math_absf = _h_arith_absf
+
+    def _h_arith_extf(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        if isinstance(v, OracleTile) and v.dtype == "bf16":
+            return OracleTile(v.data.astype(np.float32), "f32", v.shape)
+        return _cast(v, np.float32, "extf")
+
+    def _h_arith_truncf(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        rt = op.result_type
+        if getattr(rt, "elem", getattr(rt, "name", None)) == "bf16":
+            if isinstance(v, OracleTile):
+                return _mk(v.data.astype(np.float32), "bf16", v.shape)
+            return np.float32(bf16_round(np.float32(v)))
+        return _cast(v, np.float16, "truncf")
+
+    def _h_arith_extsi(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(v.data.astype(np.int64), "i64", v.shape) if isinstance(v, OracleTile) else int(v)
+
+    _h_arith_extui = _h_arith_extsi
+
+    def _h_arith_trunci(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(v.data.astype(np.int32), "i32", v.shape) if isinstance(v, OracleTile) else int(v)
+
+    def _h_arith_fptosi(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(v.data.astype(np.int32), "i32", v.shape) if isinstance(v, OracleTile) else int(v)
+
+    _h_arith_fptoui = _h_arith_fptosi
+
+    def _h_arith_sitofp(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        rt = op.result_type
+        dt = getattr(rt, "elem", None) or getattr(rt, "name", None) or "f32"
+        npd = to_np_dtype(dt)
+        if isinstance(v, OracleTile):
+            return _mk(v.data.astype(npd), dt, v.shape)
+        return npd.type(v)
+
+    def _h_arith_uitofp(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(v.data.astype(np.float32), "f32", v.shape) if isinstance(v, OracleTile) else float(v)
+
+    def _h_arith_index_cast(self, op, ctx):
+        return int(ctx.get_value(op.operands[0]))
+
+    _h_arith_index_castui = _h_arith_index_cast
+
+    def _h_arith_bitcast(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        dst = op.attributes.get("dst_type", "f32")
+        if isinstance(v, OracleTile):
+            if dst == "f32":
+                return OracleTile(v.data.view(np.float32), "f32", v.shape)
+            if dst in ("i32", "si32"):
+                return OracleTile(v.data.view(np.int32), "i32", v.shape)
+            raise NotImplementedError(f"arith.bitcast: unsupported dst_type '{dst}' for Tile")
+        if dst == "f32":
+            return float(np.frombuffer(int(v).to_bytes(4, "little", signed=(v < 0)), dtype=np.float32)[0])
+        if dst in ("i32", "si32"):
+            return int(np.frombuffer(np.float32(v).tobytes(), dtype=np.int32)[0])
+        raise NotImplementedError(f"arith.bitcast: unsupported dst_type '{dst}' for scalar")
+
+    def _h_arith_shrui(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        if isinstance(a, OracleTile):
+            bb = b.data if isinstance(b, OracleTile) else int(b)
+            return OracleTile(a.data.view(np.uint32) >> bb, a.dtype, a.shape)
+        if isinstance(b, OracleTile):
+            return OracleTile(np.array(a, dtype=np.int32).view(np.uint32) >> b.data, b.dtype, b.shape)
+        return int(np.array(a, dtype=np.int32).view(np.uint32) >> np.uint32(b))
+
+    # math ---------------------------------------------------------------------
+    def _h_math_absi(self, op, ctx):
+        v = ctx.get_value(op.operands[0])
+        return OracleTile(np.abs(v.data), v.dtype, v.shape) if isinstance(v, OracleTile) else type(v)(abs(int(v)))
+
+    def _h_math_powf(self, op, ctx):
+        b, e = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        if isinstance(b, OracleTile):
+            ed = e.data if isinstance(e, OracleTile) else e
+            d = np.power(b.data.astype(np.float32), np.asarray(ed).astype(np.float32)).astype(b.data.dtype)
+            return _mk(d, b.dtype, b.shape)
+        return type(b)(float(b) ** float(e))
+
+    def _h_math_fma(self, op, ctx):
+        a, b, c = (ctx.get_value(o) for o in op.operands[:3])
+        if isinstance(a, OracleTile):
+            d = (a.data.astype(np.float32) * b.data.astype(np.float32) + c.data.astype(np.float32))
+            return _mk(d.astype(a.data.dtype), a.dtype, a.shape)
+        return type(a)(float(a) * float(b) + float(c))
+
+    # linalg -------------------------------------------------------------------
+    def _combine(self, region, lhs, rhs, ctx):
+        """Run a 2-argument combiner region once (reference linalg_ops.py:59-83)."""
+        ctx.push_scope()
+        try:
+            names = [n for n, _ in region.args]
+            if names:
+                ctx.set_value(names[0], lhs)
+            if len(names) > 1:
+                ctx.set_value(names[1], rhs)
+            res = self._region(region.ops, ctx)
+        finally:
+            ctx.pop_scope()
+        return res.values[0] if isinstance(res, _Yield) else res
+
+    def _tree_fold(self, tile: OracleTile, dim, region, ctx) -> np.ndarray:
+        """Pairwise halving fold (reference linalg_ops.py:86-133)."""
+        data = tile.data
+        if dim is None:
+            data = data.reshape(-1)
+            dim = 0
+        n = data.shape[dim]
+
+        def sl(arr, lo, hi):
+            idx = [slice(None)] * arr.ndim
+            idx[dim] = slice(lo, hi)
+            return arr[tuple(idx)]
+
+        acc = data
+        while n > 1:
+            half = n // 2
+            left, right = sl(acc, 0, half), sl(acc, half, 2 * half)
+            comb = self._combine(region, _mk(left.copy(), tile.dtype, left.shape),
+                                 _mk(right.copy(), tile.dtype, right.shape), ctx)
+            comb = comb.data if isinstance(comb, OracleTile) else np.asarray(comb)
+            if n % 2:
+                comb = np.concatenate([comb, sl(acc, 2 * half, n)], axis=dim)
+            acc = comb
+            n = acc.shape[dim]
+        return acc
+
+    def _h_linalg_reduce(self, op, ctx):
+        tile = ctx.get_value(op.operands[0])
+        region = op.regions[0]
+        dims = op.attributes.get("dimensions")
+        outs = op.attributes.get("outs") or []
+        outs_var = outs[0] if outs else None
+        outs_tile = ctx.get_value(outs_var) if outs_var else None
+        if isinstance(tile, OracleTile):
+            if dims is None:
+                folded = self._tree_fold(tile, None, region, ctx)
+                reduced = folded.reshape(()).astype(tile.data.dtype)
+            else:
+                folded = tile.data
+                for d in sorted(dims, reverse=True):
+                    folded = self._tree_fold(OracleTile(folded, tile.dtype, folded.shape), d, region, ctx)
+                reduced = folded
+                for d in sorted(dims, reverse=True):
+                    reduced = np.squeeze(reduced, axis=d)
+                reduced = reduced.astype(tile.data.dtype)
+            if isinstance(outs_tile, OracleTile):
+                comb = self._combine(region, OracleTile(reduced.copy(), tile.dtype, reduced.shape),
+                                     outs_tile, ctx)
+                reduced = comb.data if isinstance(comb, OracleTile) else np.asarray(comb)
+            result = reduced.item() if reduced.ndim == 0 else _mk(reduced, tile.dtype, reduced.shape)
+        else:
+            result = tile
+        if outs_var and result is not None:
+            ctx.set_value(outs_var, result)
+        return result
+
+    def _h_linalg_add(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        return _mk(a.data + b.data, a.dtype, a.shape)
+
+    def _h_linalg_max(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        return _mk(np.maximum(a.data, b.data), a.dtype, a.shape)
+
+    def _h_linalg_fill(self, op, ctx):
+        s = ctx.get_value(op.operands[0])
+        out = ctx.get_value(op.operands[1])
+        return _mk(np.full(out.shape, float(s), dtype=out.data.dtype), out.dtype, out.shape)
+
+    def _h_linalg_broadcast(self, op, ctx):
+        inp = ctx.get_value(op.operands[0])
+        out = ctx.get_value(op.operands[1])
+        data = inp.data
+        for d in sorted(op.attributes.get("dimensions", [])):
+            data = np.expand_dims(data, axis=d)
+        return OracleTile(np.broadcast_to(data, out.shape).copy(), inp.dtype, tuple(out.shape))
+
+    def _h_linalg_transpose(self, op, ctx):
+        inp = ctx.get_value(op.operands[0])
+        perm = op.attributes.get("permutation")
+        if perm is None:
+            raise ValueError("linalg.transpose: missing permutation attribute")
+        return OracleTile(np.transpose(inp.data, perm).copy(), inp.dtype, tuple(inp.shape[i] for i in perm))
+
+    def _accumulate(self, acc: OracleTile, res: OracleTile, ctx) -> OracleTile:
+        if id(acc) in ctx.uncharged:
+            acc = acc.copy()
+        acc.data += res.data
+        if acc.dtype == "bf16":
+            acc.data[...] = bf16_round(acc.data)
+        return acc
+
+    def _h_linalg_matmul(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        data = np.matmul(a.data, b.data).astype(a.data.dtype)
+        res = _mk(data, a.dtype, (a.shape[0], b.shape[1]))
+        if len(op.operands) > 2:
+            acc = ctx.get_value(op.operands[2])
+            if isinstance(acc, OracleTile):
+                return self._accumulate(acc, res, ctx)
+        return res
+
+    def _h_linalg_batch_matmul(self, op, ctx):
+        a, b = ctx.get_value(op.operands[0]), ctx.get_value(op.operands[1])
+        p = a.data @ b.data
+        res = _mk(p, a.dtype, p.shape)
+        if len(op.operands) > 2:
+            acc = ctx.get_value(op.operands[2])
+            if isinstance(acc, OracleTile):
+                return self._accumulate(acc, res, ctx)
+        return res
+
+    def _h_linalg_index(self, op, ctx):
+        dim = op.attributes.get("dim", 0)
+        shape = ctx.get_value("__linalg_shape__")
+        idx = np.arange(shape[dim], dtype=np.int64)
+        rs = [1] * len(shape)
+        rs[dim] = shape[dim]
+        return OracleTile(idx.reshape(rs), "index", tuple(rs))
+
+    def _h_linalg_generic(self, op, ctx):
+        """Reference linalg_ops.py:467-585."""
+        n_ins = op.attributes.get("n_ins", 0)
+        maps = op.attributes.get("indexing_maps", [])
+        it = op.attributes.get("iterator_types")
+        ins = [ctx.get_value(op.operands[i]) for i in range(n_ins)]
+        outs_val = ctx.get_value(op.operands[n_ins])
+        region = op.regions[0]
+        names = [n for n, _ in region.args]
+        body = region.ops
+        if not isinstance(outs_val, OracleTile):
+            raise TypeError("linalg.generic: outs must be a Tile")
+        out_shape = outs_val.shape
+        out_np = outs_val.data.dtype
+        red = [i for i, t in enumerate(it or []) if t == "reduction"]
+        if not red:
+            iter_shape = tuple(out_shape)
+        else:
+            shapes = [v.shape for v in ins if isinstance(v, OracleTile)] + [out_shape]
+            ext = [None] * maps[0].n_dims
+            for m, s in zip(maps[:len(shapes)], shapes):
+                for k, e in enumerate(m.exprs):
+                    if e[0] == "dim" and ext[e[1]] is None:
+                        ext[e[1]] = s[k]
+            if any(e is None for e in ext):
+                raise ValueError("linalg.generic: cannot infer iteration extents")
+            iter_shape = tuple(ext)
+        ctx.push_scope()
+        ctx.set_value("__linalg_shape__", iter_shape)
+        for i, (v, m) in enumerate(zip(ins, maps[:n_ins])):
+            arg = OracleTile(_gather_input(v.data, m, iter_shape), v.dtype, iter_shape) \
+                if isinstance(v, OracleTile) else v
+            if i < len(names):
+                ctx.set_value(names[i], arg)
+        if not red:
+            if n_ins < len(names):
+                ctx.set_value(names[n_ins], OracleTile(outs_val.data.copy(), outs_val.dtype, out_shape))
+            res = self._region(body, ctx)
+            ctx.pop_scope()
+            od = _unwrap(res)
+            if isinstance(od, OracleTile):
+                d = np.broadcast_to(od.data, out_shape).copy().astype(out_np)
+                return _mk(d, outs_val.dtype, out_shape)
+            return _mk(np.full(out_shape, od, dtype=out_np), outs_val.dtype, out_shape)
+        outs_name = names[n_ins] if n_ins < len(names) else None
+        y = next((o for o in body if o.op_type == "linalg.yield"), None)
+        comb = None
+        if y is not None:
+            yn = y.operands[0] if y.operands else None
+            comb = next((o for o in body if o.result == yn and outs_name in o.operands), None)
+        if comb is None:
+            raise ValueError("linalg.generic: cannot identify combiner op for reduction")
+        if comb.op_type not in _COMBINER_IDENTITY:
+            raise ValueError(f"linalg.generic: unsupported combiner '{comb.op_type}' for reduction")
+        from ktir_cpu_amd.ir import Region
+        cregion = Region([("%__fold_lhs__", None), ("%__fold_rhs__", None)], [
+            Operation(comb.op_type, ["%__fold_combined__"], ["%__fold_lhs__", "%__fold_rhs__"],
+                      dict(comb.attributes), list(comb.result_types)),
+            Operation("linalg.yield", [], ["%__fold_combined__"])])
+        if n_ins < len(names):
+            ctx.set_value(names[n_ins], OracleTile(np.full(iter_shape, _COMBINER_IDENTITY[comb.op_type],
+                                                           dtype=out_np), outs_val.dtype, iter_shape))
+        res = self._region(body, ctx)
+        ctx.pop_scope()
+        od = _unwrap(res)
+        if not isinstance(od, OracleTile):
+            od = OracleTile(np.full(iter_shape, od, dtype=out_np), outs_val.dtype, iter_shape)
+        folded = od.data
+        for d in sorted(red, reverse=True):
+            folded = self._tree_fold(OracleTile(folded, outs_val.dtype, folded.shape), d, cregion, ctx)
+        for d in sorted(red, reverse=True):
+            folded = np.squeeze(folded, axis=d)
+        rt = OracleTile(folded.astype(out_np), outs_val.dtype, folded.shape)
+        c = self._combine(cregion, rt, outs_val, ctx)
+        final = c.data if isinstance(c, OracleTile) else np.asarray(c)
+        return _mk(final.astype(out_np), outs_val.dtype, out_shape)
+
+    def _h_linalg_yield(self, op, ctx):
+        return _Yield([ctx.get_value(n) for n in op.operands])
+
+    _h_scf_yield = _h_linalg_yield
+    _h_tensor_yield = _h_linalg_yield
+
+    # tensor -------------------------------------------------------------------
+    def _h_tensor_empty(self, op, ctx):
+        shape = op.attributes.get("shape", (1,))
+        dt = op.attributes.get("dtype", "f16")
+        return OracleTile(np.zeros(shape, dtype=to_np_dtype(dt)), dt, tuple(shape))
+
+    def _h_tensor_splat(self, op, ctx):
+        s = ctx.get_value(op.operands[0])
+        if isinstance(s, OracleTile):
+            s = s.data.flat[0]
+        shape = tuple(op.attributes.get("shape", ()))
+        dt = op.attributes.get("dtype", "f16")
+        if not shape:
+            shape = (1,)
+        if isinstance(s, (np.integer, int)) and not isinstance(s, bool):
+            npd, dt = np.int32, "i32"
+        else:
+            npd = to_np_dtype(dt)
+        return _mk(np.full(shape, s, dtype=npd), dt, shape)
+
+    def _h_tensor_extract(self, op, ctx):
+        src = ctx.get_value(op.operands[0])
+        idx = [ctx.get_value(o) for o in op.operands[1:]]
+        if isinstance(src, OracleTile):
+            v = src.data.flat[0] if not idx else src.data[tuple(int(i) for i in idx)]
+            return np.float32(v) if src.dtype == "bf16" else v
+        return src
+
+    def _reshape(self, op, ctx):
+        src = ctx.get_value(op.operands[0])
+        ts = op.attributes.get("target_shape")
+        if ts is None:
+            raise ValueError(f"{op.op_type}: missing 'target_shape' attribute")
+        if not isinstance(src, OracleTile):
+            return src
+        return OracleTile(src.data.reshape(ts), src.dtype, tuple(ts))
+
+    _h_tensor_expand_shape = _reshape
+    _h_tensor_collapse_shape = _reshape
+    _h_tensor_reshape = _reshape
+
+    def _h_tensor_from_elements(self, op, ctx):
+        shape = tuple(op.attributes["shape"])
+        dt = op.attributes["dtype"]
+        vals = []
+        for n in op.operands:
+            v = ctx.get_value(n)
+            vals.append(v.data.flat[0] if isinstance(v, OracleTile) else v)
+        return _mk(np.array(vals, dtype=to_np_dtype(dt)).reshape(shape), dt, shape)
+
+    def _slice_params(self, op, ctx, first_dyn):
+        a = op.attributes
+        K = -(1 << 63)
+        dyn = iter(op.operands[first_dyn:])
+
+        def res(lst):
+            return [int(ctx.get_value(next(dyn))) if v == K else int(v) for v in lst]
+
+        return res(a["static_offsets"]), res(a["static_sizes"]), res(a["static_strides"])
+
+    def _h_tensor_extract_slice(self, op, ctx):
+        src = ctx.get_value(op.operands[0])
+        offs, sizes, strides = self._slice_params(op, ctx, 1)
+        idx = tuple(slice(o, o + s * st, st) for o, s, st in zip(offs, sizes, strides))
+        rs = tuple(op.attributes["result_shape"])
+        return OracleTile(src.data[idx].reshape(rs), op.attributes["dtype"], rs)
+
+    def _h_tensor_insert_slice(self, op, ctx):
+        src = ctx.get_value(op.operands[0])
+        dst = ctx.get_value(op.operands[1])
+        offs, sizes, strides = self._slice_params(op, ctx, 2)
+        idx = tuple(slice(o, o + s * st, st) for o, s, st in zip(offs, sizes, strides))
+        d = dst.data.copy()
+        d[idx] = src.data.reshape(sizes)
+        rs = tuple(op.attributes["result_shape"])
+        return OracleTile(d, op.attributes["dtype"], rs)
+
+    def _h_tensor_generate(self, op, ctx):
+        shape = tuple(op.attributes["shape"])
+        dt = op.attributes["dtype"]
+        region = op.regions[0]
+        grids = np.meshgrid(*(np.arange(s) for s in shape), indexing="ij")
+        ctx.push_scope()
+        for (n, _), g in zip(region.args, grids):
+            ctx.set_value(n, OracleTile(g, "index", shape))
+        res = self._region(region.ops, ctx)
+        if isinstance(res, _Yield):
+            res = res.values[0]
+        ctx.pop_scope()
+        if isinstance(res, OracleTile):
+            return _mk(res.data.astype(to_np_dtype(dt)), dt, shape)
+        return _mk(np.full(shape, res, dtype=to_np_dtype(dt)), dt, shape)
+
+    # scf ----------------------------------------------------------------------
+    def _h_scf_for(self, op, ctx):
+        lb = ctx.get_value(op.operands[0])
+        ub = ctx.get_value(op.operands[1])
+        st = ctx.get_value(op.operands[2])
+        iv = op.attributes["iter_var"]
+        names = op.attributes.get("iter_args", [])
+        inits = []
+        for n in op.operands[3:]:
+            v = ctx.get_value(n, peek=True)
+            inits.append(v.copy() if isinstance(v, OracleTile) else v)
+        cur = list(inits)
+        for n, v in zip(names, cur):
+            ctx.set_value(n, v)
+        body = op.regions[0].ops
+        for i in range(int(lb), int(ub), max(int(st), 1)):
+            ctx.push_scope()
+            ctx.set_value(iv, i)
+            res = self._region(body, ctx)
+            ctx.pop_scope()
+            if isinstance(res, _Yield) and names:
+                for n, v in zip(names, res.values):
+                    ctx.set_value(n, v)
+                cur = res.values
+        if not cur:
+            return None
+        return cur[0] if len(cur) == 1 else tuple(cur)
+
+    def _h_scf_if(self, op, ctx):
+        c = ctx.get_value(op.operands[0])
+        regions = op.regions
+        region = regions[0] if c else (regions[1] if len(regions) > 1 else None)
+        if region is None or not region.ops:
+            return None
+        ctx.push_scope()
+        res = self._region(region.ops, ctx)
+        ctx.pop_scope()
+        return _unwrap(res)
+
+    def _h_return(self, op, ctx):
+        return ctx.get_value(op.operands[0]) if op.operands else None
+
+    _h_func_return = _h_return
+
+
+def _gather_input(data, imap: AffineMap, target):
+    """Reference linalg_ops.py:400-419."""
+    exprs = imap.exprs
+    if all(e[0] == "dim" for e in exprs):
+        plain = [e[1] for e in exprs]
+        srt = sorted(plain)
+        if plain != srt:
+            data = np.transpose(data, [plain.index(d) for d in srt])
+        for d in range(len(target)):
+            if d not in plain:
+                data = np.expand_dims(data, axis=d)
+        return np.broadcast_to(data, target).copy()
+    out = np.empty(target, dtype=data.dtype)
+    for idx in np.ndindex(*target):
+        out[idx] = data[imap.eval(list(idx))]
+    return out
