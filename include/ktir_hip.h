@@ -1,0 +1,272 @@
+/*
+ * ktir_hip.h — C ABI of the MI355X (gfx950) execution backend for KTIR.
+ *
+ * This is the drop-in boundary under the Python `KTIRInterpreter`
+ * (reference `ktir_cpu/interpreter.py:40-395`).  The reference executes each
+ * simulated Spyre core one after another and every tile op as NumPy calls on
+ * a simulated HBM (`ktir_cpu/memory.py:311-398`).  Here the simulated HBM is one
+ * device arena, tile values are device buffers, and tile ops run as the gfx950
+ * kernels below.  Only plain integers, doubles and device addresses cross this
+ * boundary; every entry point returns 0 on success or a negative KTIR_E_* code,
+ * with a message available from ktir_last_error().
+ *
+ * Terminology (from the reference): a *lane* is one instance of the KTIR
+ * function body executing in lockstep with others: one simulated grid core
+ * (`ktir_cpu/grid.py:434-469`), or one (core, loop-iteration) pair when the
+ * host runs independent `scf.for` iterations side by side.  A *leaf* is one
+ * strided or offset-list view of device memory read or written by a kernel.
+ */
+#ifndef KTIR_HIP_H
+#define KTIR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (mapped to Python exceptions by the host runtime) ---- */
+#define KTIR_OK 0
+#define KTIR_E_HIP -1        /* HIP runtime error                  -> RuntimeError */
+#define KTIR_E_ARG -2        /* invalid descriptor / argument       -> ValueError   */
+#define KTIR_E_INDEX -3      /* negative indirect index (reference ops/memory_ops.py:378-382) -> IndexError */
+#define KTIR_E_UNSUPPORTED -4 /* shape / dtype not handled          -> NotImplementedError */
+
+/* ---- element types (reference dtypes.py:24-39; bf16 is an extension) ---- */
+#define KTIR_F16 0
+#define KTIR_BF16 1
+#define KTIR_F32 2
+#define KTIR_I1 3   /* stored as one byte, like numpy bool */
+#define KTIR_I32 4  /* also `index` (reference maps index to int32) */
+#define KTIR_I64 5
+#define KTIR_I8 6
+#define KTIR_I16 7
+
+/* ---- fused-program opcodes ----
+ * A program is a straight-line list of instructions over 8 virtual registers
+ * of 32-bit values (f32 for f16/bf16/f32 data, int32 for integer data).
+ * Each float op rounds its result to the instruction's dtype, which reproduces
+ * NumPy's f16 arithmetic (compute in f32, round to nearest even). */
+#define KTIR_OP_NOP 0
+#define KTIR_OP_LD 1          /* dst <- leaf[aux] at the current element */
+#define KTIR_OP_ST 2          /* leaf[aux] <- a (converted to the leaf dtype) */
+#define KTIR_OP_CONST 3       /* dst <- imm (as dt) */
+#define KTIR_OP_LANE 4        /* dst <- lane_scalars[lane * n_lane_scalars + aux] (as dt) */
+#define KTIR_OP_IDX 5         /* dst <- iteration index along dim aux (int) */
+#define KTIR_OP_RED 6         /* row mode: deposit a into the row reduction buffer */
+#define KTIR_OP_FOLD 7        /* row mode: dst <- pairwise-halving fold of the buffer with binop aux */
+#define KTIR_OP_ELEM 8        /* row mode: begin element loop; i = pc of matching KTIR_OP_ENDELEM */
+#define KTIR_OP_ENDELEM 9
+#define KTIR_OP_CAST 10       /* dst(dt) <- a(aux = source dtype) : ext/trunc/sitofp/fptosi/... */
+#define KTIR_OP_BITCAST 11    /* dst <- a reinterpreted (32-bit) */
+#define KTIR_OP_SELECT 12     /* dst <- a ? b : c */
+#define KTIR_OP_FMA 13        /* dst <- a * b + c (f32 then round to dt) */
+#define KTIR_OP_CMPF 14       /* dst(i1) <- pred aux (a, b) over floats */
+#define KTIR_OP_CMPI 15       /* dst(i1) <- pred aux (a, b) over ints */
+/* unary float 20..39 */
+#define KTIR_OP_NEGF 20
+#define KTIR_OP_ABSF 21
+#define KTIR_OP_EXP 22
+#define KTIR_OP_LOG 23
+#define KTIR_OP_LOG2 24
+#define KTIR_OP_LOG1P 25
+#define KTIR_OP_SQRT 26
+#define KTIR_OP_RSQRT 27
+#define KTIR_OP_TANH 28
+#define KTIR_OP_SIN 29
+#define KTIR_OP_COS 30
+#define KTIR_OP_ERF 31
+#define KTIR_OP_CEIL 32
+#define KTIR_OP_FLOOR 33
+#define KTIR_OP_NOTI 34       /* i1 logical not */
+#define KTIR_OP_ABSI 35
+/* binary float 40..59 */
+#define KTIR_OP_ADDF 40
+#define KTIR_OP_SUBF 41
+#define KTIR_OP_MULF 42
+#define KTIR_OP_DIVF 43
+#define KTIR_OP_REMF 44       /* Python/NumPy modulo: sign of the divisor */
+#define KTIR_OP_MAXIMUMF 45   /* NaN-propagating max (np.maximum) */
+#define KTIR_OP_MINIMUMF 46
+#define KTIR_OP_MAXNUMF 47    /* NaN-ignoring max (np.fmax) */
+#define KTIR_OP_MINNUMF 48
+#define KTIR_OP_POWF 49
+/* binary int 60..89 */
+#define KTIR_OP_ADDI 60
+#define KTIR_OP_SUBI 61
+#define KTIR_OP_MULI 62
+#define KTIR_OP_DIVSI 63      /* truncating */
+#define KTIR_OP_REMSI 64      /* truncating remainder */
+#define KTIR_OP_FLOORDIVSI 65
+#define KTIR_OP_FLOORREMSI 66 /* Python modulo */
+#define KTIR_OP_CEILDIVSI 67
+#define KTIR_OP_ANDI 68
+#define KTIR_OP_ORI 69
+#define KTIR_OP_XORI 70
+#define KTIR_OP_SHLI 71
+#define KTIR_OP_SHRSI 72
+#define KTIR_OP_SHRUI 73
+#define KTIR_OP_MAXSI 74
+#define KTIR_OP_MINSI 75
+
+/* comparison predicates (arith.cmpf / arith.cmpi) */
+#define KTIR_CMP_FALSE 0
+#define KTIR_CMP_OEQ 1
+#define KTIR_CMP_OGT 2
+#define KTIR_CMP_OGE 3
+#define KTIR_CMP_OLT 4
+#define KTIR_CMP_OLE 5
+#define KTIR_CMP_ONE 6
+#define KTIR_CMP_ORD 7
+#define KTIR_CMP_UEQ 8
+#define KTIR_CMP_UGT 9
+#define KTIR_CMP_UGE 10
+#define KTIR_CMP_ULT 11
+#define KTIR_CMP_ULE 12
+#define KTIR_CMP_UNE 13
+#define KTIR_CMP_UNO 14
+#define KTIR_CMP_TRUE 15
+#define KTIR_CMP_EQ 16
+#define KTIR_CMP_NE 17
+#define KTIR_CMP_SLT 18
+#define KTIR_CMP_SLE 19
+#define KTIR_CMP_SGT 20
+#define KTIR_CMP_SGE 21
+#define KTIR_CMP_ULTI 22
+#define KTIR_CMP_ULEI 23
+#define KTIR_CMP_UGTI 24
+#define KTIR_CMP_UGEI 25
+
+#define KTIR_MAX_DIMS 4
+#define KTIR_MAX_LEAVES 10
+#define KTIR_MAX_INSTR 112
+#define KTIR_NREG 8
+#define KTIR_MAX_ROW 16384   /* longest row a row-mode program can fold in LDS */
+
+/* leaf flags */
+#define KTIR_LEAF_VEC 1      /* inner stride 1 and every vector start aligned: use wide accesses */
+
+/* One strided (or offset-list) view of device memory.
+ * Element address for lane l at iteration index (i0..i3):
+ *   ptr + bpe * (lane_off(l) + sum_d i_d * strides[d])               (strided)
+ *   ptr + bpe * (lane_off(l) + offsets[l * offsets_lane_stride + flat]) (offset list)
+ * with lane_off(l) = lane_base ? lane_base[l] : base + l * lane_stride.
+ * Element offsets outside [lo, hi) read as zero and are not written: the
+ * reference's zero-pad-on-over-read and truncate-on-over-write for an
+ * allocation (memory.py:243-259, :281-305). */
+typedef struct ktir_leaf {
+  uint64_t ptr;
+  int64_t base;
+  int64_t lane_stride;
+  uint64_t lane_base;            /* const int64_t* [lanes] or 0 */
+  uint64_t offsets;              /* const int64_t* or 0 */
+  int64_t offsets_lane_stride;
+  int64_t strides[KTIR_MAX_DIMS];
+  int64_t lo, hi;
+  uint64_t winner;               /* const int32_t*: last-writer-wins table for scatters, or 0 */
+  int64_t winner_base;           /* element offset of winner[0] */
+  int32_t dtype;
+  int32_t flags;
+} ktir_leaf_t;
+
+typedef struct ktir_instr {
+  int8_t op, dst, a, b, c, dt;
+  int16_t aux;       /* leaf / dim / predicate / source dtype / lane-scalar slot / pc of ENDELEM */
+  int32_t imm;       /* CONST bits: float32 bits for float dtypes, int32 otherwise */
+} ktir_instr_t;
+
+/* A fused tile program over the iteration space [lanes, shape[0..ndim-1]].
+ * mode 0 (flat): every element independently (elementwise chains, copies,
+ *   broadcasts, transposes, casts, gathers, scatters).
+ * mode 1 (rows): one workgroup per row (all dims but the last); ELEM blocks
+ *   loop over the row, RED/FOLD implement the reference's pairwise-halving
+ *   reduction (dialects/linalg_ops.py:86-133) in LDS; instructions outside
+ *   ELEM blocks compute per-row values. */
+typedef struct ktir_prog {
+  int32_t mode, ndim, n_instr, n_leaves;
+  int64_t lanes;
+  int64_t shape[KTIR_MAX_DIMS];
+  uint64_t lane_scalars;          /* const double* [lanes * n_lane_scalars] or 0 */
+  int64_t n_lane_scalars;
+  ktir_leaf_t leaves[KTIR_MAX_LEAVES];
+  ktir_instr_t instr[KTIR_MAX_INSTR];
+} ktir_prog_t;
+
+/* ---- runtime (reference: interpreter.py:95-120 builds the simulated HBM) ---- */
+const char* ktir_last_error(void);
+int ktir_init(int device);
+int ktir_device_info(int* cu_count, int* clock_khz, int64_t* hbm_bytes, char* name, int name_len);
+int ktir_malloc(uint64_t bytes, uint64_t* dptr);
+int ktir_free(uint64_t dptr);
+int ktir_memcpy_h2d(uint64_t dst, const void* src, uint64_t bytes);
+int ktir_memcpy_d2h(void* dst, uint64_t src, uint64_t bytes);
+int ktir_memcpy_d2d(uint64_t dst, uint64_t src, uint64_t bytes);
+int ktir_memset(uint64_t dst, int value, uint64_t bytes);
+int ktir_sync(void);
+int ktir_check_error_flag(void);  /* device-side errors (negative indices) raised since the last call */
+/* HIP events on the library's stream, for timing launches */
+int ktir_event_create(uint64_t* ev);
+int ktir_event_record(uint64_t ev);
+int ktir_event_elapsed_ms(uint64_t start, uint64_t stop, float* ms);
+int ktir_event_destroy(uint64_t ev);
+
+/* ---- fused tile programs ----
+ * Replaces the per-op NumPy tile kernels of the reference: MemoryOps.load /
+ * store (ops/memory_ops.py:724-865), the arith/math elementwise handlers
+ * (dialects/_helpers.py:39-54, ops/arith_ops.py, ops/math_ops.py:27-138),
+ * linalg.broadcast/transpose/fill/generic (dialects/linalg_ops.py:272-614),
+ * linalg.reduce (:137-246) and the tensor reshapes (dialects/tensor_ops.py).
+ * The descriptor travels by value in the kernel arguments (no host-device
+ * copy per launch), so launches stay asynchronous on the library stream. */
+int ktir_launch_program(const ktir_prog_t* prog);
+
+/* ---- last-writer-wins scatter support ----
+ * Reference memory.py:281-291 writes duplicates in enumeration order, so the
+ * last position wins.  ktir_scatter_winners fills winner[off - winner_base]
+ * with the largest flat position (lane * n + i) that writes each offset; a
+ * following program whose store leaf carries `winner` writes only winners. */
+int ktir_scatter_winners(const ktir_leaf_t* leaf, int64_t lanes, int64_t n, uint64_t winner);
+
+/* ---- indirect access tiles (reference ops/memory_ops.py:224-576, 868-964) ----
+ * out[l * n + p] = dir[l * dir_ls + p] + sum_k idx_k(l, p) * stride_k where
+ * idx_k(l, p) = index value read from index view k at element
+ * pos_k[l * pos_ls_k + p] (+ pos_lane_k[l]).  A negative index raises
+ * KTIR_E_INDEX on the next ktir_check_error_flag().  Up to 4 indirect dims. */
+typedef struct ktir_iat {
+  int64_t lanes, n;
+  uint64_t dir;          /* const int64_t* direct part */
+  int64_t dir_ls;
+  int32_t n_ind, pad;
+  uint64_t idx_ptr[4];   /* device address of each index view's element 0 */
+  int32_t idx_dtype[4];
+  int64_t idx_hi[4];     /* valid element window of the index allocation */
+  int64_t idx_lo[4];
+  uint64_t pos[4];       /* const int64_t* */
+  int64_t pos_ls[4];
+  uint64_t pos_lane[4];  /* const int64_t* [lanes] or 0 */
+  int64_t stride[4];
+  uint64_t out;          /* int64_t* [lanes * n] */
+} ktir_iat_t;
+int ktir_iat_offsets(const ktir_iat_t* d);
+
+/* ---- matmul tiles (reference dialects/linalg_ops.py:307-369, ops/arith_ops.py:324-340) ----
+ * For every lane: C = A @ B (+ C0 when accumulate), A [M,K], B [K,N].
+ * The K loop may be a fused `scf.for` reduction loop: `ksteps` steps, each
+ * advancing A and B by a_kstep / b_kstep elements (the K-loop GEMM of
+ * examples/triton-ktir/matmul_fwd_ktir.mlir:33-57).  f16 / bf16 operands use
+ * gfx950 MFMA with f32 accumulation; f32 operands use f32 FMA. */
+typedef struct ktir_mm {
+  int64_t lanes, M, N, K, ksteps;
+  ktir_leaf_t a, b;       /* strides[0] = row stride, strides[1] = column stride */
+  int64_t a_kstep, b_kstep;
+  ktir_leaf_t c;          /* result (f32 / f16 / bf16), strides[0..1] */
+  ktir_leaf_t c0;         /* accumulator input when accumulate != 0 */
+  int32_t accumulate;
+  int32_t round_dt;       /* dtype the product is rounded to before accumulating (the KTIR operand dtype) */
+} ktir_mm_t;
+int ktir_launch_matmul(const ktir_mm_t* d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KTIR_HIP_H */

@@ -1,0 +1,83 @@
+// Shared device helpers for the KTIR gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/ktir_hip.h"
+
+namespace ktir {
+
+// Status plumbing shared by every translation unit (defined in ktir_runtime.hip).
+int set_error(int code, const char* fmt, ...);
+hipStream_t stream();
+int* device_error_flag();   // device int: 1 = negative indirect index seen
+
+#define KTIR_HIP_CHECK(expr)                                                        \
+  do {                                                                              \
+    hipError_t _e = (expr);                                                         \
+    if (_e != hipSuccess)                                                           \
+      return ::ktir::set_error(KTIR_E_HIP, "%s failed: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+// ---- element conversions -------------------------------------------------
+
+__device__ __forceinline__ float round_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return __uint_as_float(u | 0x400000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ float round_f16(float x) { return (float)(_Float16)x; }
+
+// Round a float result to the KTIR dtype it is declared with.
+__device__ __forceinline__ float round_to(float x, int dt) {
+  if (dt == KTIR_F16) return round_f16(x);
+  if (dt == KTIR_BF16) return round_bf16(x);
+  return x;
+}
+
+__device__ __forceinline__ bool is_float_dt(int dt) { return dt <= KTIR_F32; }
+
+__device__ __forceinline__ int elem_bytes(int dt) {
+  switch (dt) {
+    case KTIR_F16: case KTIR_BF16: case KTIR_I16: return 2;
+    case KTIR_F32: case KTIR_I32: return 4;
+    case KTIR_I64: return 8;
+    default: return 1;
+  }
+}
+
+// Read one element of dtype dt at element offset off from ptr, as a 32-bit
+// register value (float bits for float types, int32 for integer types).
+__device__ __forceinline__ float load_elem(uint64_t ptr, int64_t off, int dt) {
+  switch (dt) {
+    case KTIR_F16: return (float)((const _Float16*)ptr)[off];
+    case KTIR_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)ptr)[off]) << 16);
+    case KTIR_F32: return ((const float*)ptr)[off];
+    case KTIR_I1: return __int_as_float(((const uint8_t*)ptr)[off] ? 1 : 0);
+    case KTIR_I8: return __int_as_float((int)((const int8_t*)ptr)[off]);
+    case KTIR_I16: return __int_as_float((int)((const int16_t*)ptr)[off]);
+    case KTIR_I32: return __int_as_float(((const int32_t*)ptr)[off]);
+    case KTIR_I64: return __int_as_float((int32_t)((const int64_t*)ptr)[off]);
+  }
+  return 0.f;
+}
+
+__device__ __forceinline__ void store_elem(uint64_t ptr, int64_t off, int dt, float v) {
+  switch (dt) {
+    case KTIR_F16: ((_Float16*)ptr)[off] = (_Float16)v; break;
+    case KTIR_BF16: ((uint16_t*)ptr)[off] = (uint16_t)(__float_as_uint(round_bf16(v)) >> 16); break;
+    case KTIR_F32: ((float*)ptr)[off] = v; break;
+    case KTIR_I1: ((uint8_t*)ptr)[off] = __float_as_int(v) ? 1 : 0; break;
+    case KTIR_I8: ((int8_t*)ptr)[off] = (int8_t)__float_as_int(v); break;
+    case KTIR_I16: ((int16_t*)ptr)[off] = (int16_t)__float_as_int(v); break;
+    case KTIR_I32: ((int32_t*)ptr)[off] = __float_as_int(v); break;
+    case KTIR_I64: ((int64_t*)ptr)[off] = (int64_t)__float_as_int(v); break;
+  }
+}
+
+__device__ __forceinline__ int64_t lane_offset(const ktir_leaf_t& L, int64_t lane) {
+  return L.lane_base ? ((const int64_t*)L.lane_base)[lane] : L.base + lane * L.lane_stride;
+}
+
+}  // namespace ktir

@@ -1,0 +1,152 @@
+"""`KTIRInterpreter`: the drop-in API of the reference, executed on an MI355X.
+
+Same surface as the reference's ``ktir_cpu/interpreter.py:40-395``:
+``load``, ``arg_names``, ``tensor_input_output_sizes``, ``execute_function``
+(returns every ndarray argument read back after the run, inputs included)
+and ``get_latency_report``.  The arguments are laid out in a device arena at
+the byte addresses the reference's HBM simulator gives them
+(``interpreter.py:161-172``: one stick-aligned allocation per array, pointer
+argument = element index), the function runs through the lockstep executor
+(``walker.Executor``) and the results are copied back into fresh arrays.
+There is no CPU execution path: a missing library or GPU raises.
+"""
+
+from __future__ import annotations
+
+import time
+from typing import Any, Dict, List, Optional
+
+import numpy as np
+
+from . import runtime as rt
+from .executor import Arena, NeedEager, Plan, Pool, STICK_BYTES
+from .ir import IRModule
+from .parser import KTIRParser
+from .walker import Executor
+
+_NP_TO_KTIR = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.int32): "i32",
+               np.dtype(np.int64): "i64", np.dtype(np.uint16): "bf16", np.dtype(np.bool_): "i1",
+               np.dtype(np.int8): "i8", np.dtype(np.int16): "i16"}
+
+
+def ktir_dtype_of(arr: np.ndarray) -> str:
+    """KTIR dtype of a host array; bf16 tensors travel as uint16 bit patterns."""
+    try:
+        return _NP_TO_KTIR[arr.dtype]
+    except KeyError:
+        raise ValueError(f"Unsupported array dtype {arr.dtype} (reference dtypes.py:24-39 plus bf16 as uint16)")
+
+
+class Prepared:
+    """Arguments resident on the device plus the launch plan of one function:
+    `run()` replays the device work only (no host walk, no copies)."""
+
+    def __init__(self, interp: "KTIRInterpreter", fn_name: str, names: List[str], plan: Plan, arena: Arena,
+                 arrays: Dict[str, np.ndarray]):
+        self.interp = interp
+        self.fn_name = fn_name
+        self.names = names
+        self.plan = plan
+        self.arena = arena
+        self.arrays = arrays
+
+    def run(self):
+        self.plan.run()
+
+    def reset_inputs(self):
+        for a in self.arena.allocs:
+            arr = self.arrays[a.name]
+            self.arena.buf.upload(np.ascontiguousarray(arr).reshape(-1).view(np.uint8), a.off)
+
+    def outputs(self) -> Dict[str, np.ndarray]:
+        rt.sync()
+        out = {}
+        for a in self.arena.allocs:
+            src = self.arrays[a.name]
+            raw = self.arena.buf.download(a.nbytes, a.off)
+            out[a.name] = np.frombuffer(raw.tobytes(), dtype=src.dtype).reshape(src.shape).copy()
+        return out
+
+
+class KTIRInterpreter:
+    """Drop-in for the reference ``KTIRInterpreter`` running on one MI355X."""
+
+    def __init__(self, latency_config=None, trace_latency: bool = False, parser=None, lx_size_mb: Optional[int] = None):
+        self.module: Optional[IRModule] = None
+        self._parser = parser or KTIRParser()
+        self.latency_config = latency_config
+        self.trace_latency = trace_latency
+        if lx_size_mb is None:
+            lx_size_mb = int(getattr(latency_config, "lx_size_mb", 2) or 2) if latency_config is not None else 2
+        self.lx_size_mb = lx_size_mb
+        self.last_plan: Optional[Plan] = None
+        self._arena = Arena()
+        self._pool = None
+        self._latency_report = None
+
+    # -- reference API ------------------------------------------------------
+    def load(self, src: str):
+        """Path to a .mlir file, or inline KTIR text (reference interpreter.py:81-93)."""
+        if "\n" in src or src.lstrip().startswith("module"):
+            self.module = self._parser.parse_module(src)
+        else:
+            self.module = self._parser.parse_file(src)
+
+    def arg_names(self, fn: str) -> List[str]:
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        return self.module.get_function(fn).arg_names
+
+    def tensor_input_output_sizes(self, fn: str):
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        return self.module.get_function(fn).tensor_sizes
+
+    def get_latency_report(self):
+        return self._latency_report
+
+    def execute_function(self, fn_name: str, **kwargs) -> Dict[str, np.ndarray]:
+        """Run `fn_name` on the GPU; returns every ndarray argument (reference interpreter.py:122-194)."""
+        prep = self.prepare(fn_name, **kwargs)
+        return prep.outputs()
+
+    # -- GPU-specific ---------------------------------------------------------
+    def prepare(self, fn_name: str, **kwargs) -> Prepared:
+        """Place the arguments on the device, walk the function once, launch
+        it, and return a handle that can replay the device work."""
+        if not self.module:
+            raise RuntimeError("No module loaded. Call load() first.")
+        fn = self.module.get_function(fn_name)
+        declared = fn.arg_names
+        if kwargs and declared and not any(k in declared for k in kwargs):
+            if len(kwargs) == len(declared):
+                kwargs = dict(zip(declared, kwargs.values()))
+        rt.lib()
+        arrays = {k: v for k, v in kwargs.items() if isinstance(v, np.ndarray)}
+        specs = [(k, ktir_dtype_of(v), int(v.nbytes), tuple(v.shape)) for k, v in arrays.items()]
+        if self._pool is not None:
+            self._pool.free_all()
+        self._pool = Pool()
+        arena = Arena()
+        arena.layout(specs)
+        self._arena = arena
+        args: Dict[str, Any] = {}
+        for a in arena.allocs:
+            v = arrays[a.name]
+            arena.buf.upload(np.ascontiguousarray(v).reshape(-1).view(np.uint8), a.off)
+            args[a.name] = np.int64(a.addr // rt.ELEM_BYTES[a.dtype])
+        for k, v in kwargs.items():
+            if not isinstance(v, np.ndarray):
+                args[k] = np.asarray(v)
+        plan = None
+        try:
+            ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb)
+            plan = ex.run()
+            plan.run()
+        except NeedEager as why:
+            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb)
+            plan = ex.run()
+            plan.fallback_reason = str(why)
+        rt.sync()
+        self.last_plan = plan
+        return Prepared(self, fn_name, list(arrays), plan, arena, arrays)

@@ -1,0 +1,56 @@
+"""Seeded inputs for the five benchmark kernels at sizes the oracle finishes
+in seconds (the same generators run at full size in bench.py)."""
+import math
+
+import numpy as np
+
+from ktir_cpu_amd import configs
+from oracle.interp import bf16_bits
+
+
+def vector_add(n=4096, block=128, cores=32, seed=42):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n).astype(np.float16)
+    y = rng.standard_normal(n).astype(np.float16)
+    return (configs.vector_add(n, block, cores), "add_kernel",
+            dict(x_ptr=x, y_ptr=y, output_ptr=np.zeros(n, np.float16), BLOCK_SIZE=block))
+
+
+def gather_scatter_add(rows=1024, dim=32, n_idx=512, cores=4, chunk=32, seed=42, dup_frac=0.1):
+    rng = np.random.default_rng(seed)
+    table = rng.standard_normal((rows, dim)).astype(np.float16)
+    n_dup = int(n_idx * dup_frac)
+    uniq = rng.choice(rows, n_idx - n_dup, replace=False)
+    dup = rng.choice(uniq, n_dup)
+    idx = rng.permutation(np.concatenate([uniq, dup])).astype(np.int32)
+    return (configs.gather_scatter_add(rows, dim, n_idx, cores, chunk), "gather_scatter_add",
+            dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((rows, dim), np.float32)))
+
+
+def softmax(rows=64, cols=256, cores=8, rblk=4, seed=42):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float16)
+    return configs.softmax(rows, cols, cores, rblk), "softmax_kernel", dict(x_ptr=x, y_ptr=np.zeros_like(x))
+
+
+def rmsnorm(rows=64, cols=256, cores=8, rblk=4, seed=42):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float16)
+    return (configs.rmsnorm(rows, cols, cores, rblk), "rmsnorm_kernel",
+            dict(x_ptr=x, w_ptr=w, y_ptr=np.zeros_like(x), eps=1e-6))
+
+
+def gemm(M=256, N=256, K=256, bm=64, bn=64, bk=32, gm=2, gn=2, seed=42):
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal((M, K)) * K ** -0.5).astype(np.float16)
+    b = (rng.standard_normal((K, N)) * K ** -0.5).astype(np.float16)
+    return (configs.gemm(M, N, K, bm, bn, bk, gm, gn), "gemm_kernel",
+            dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16)))
+
+
+def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42):
+    rng = np.random.default_rng(seed)
+    q, k, v = (bf16_bits(rng.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    return (configs.flash_attention(B, H, S, D, blk), "flash_attention",
+            dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D)))
