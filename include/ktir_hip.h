@@ -144,7 +144,8 @@ extern "C" {
 #define KTIR_MAX_ROW 16384   /* longest row a row-mode program can fold in LDS */
 
 /* leaf flags */
-#define KTIR_LEAF_VEC 1      /* inner stride 1 and every vector start aligned: use wide accesses */
+#define KTIR_LEAF_VEC 1      /* inner stride 1, every 4-element vector start aligned: wide accesses */
+#define KTIR_LEAF_VEC8 2     /* same for 8-element vectors */
 
 /* One strided (or offset-list) view of device memory.
  * Element address for lane l at iteration index (i0..i3):
@@ -265,6 +266,34 @@ typedef struct ktir_mm {
   int32_t round_dt;       /* dtype the product is rounded to before accumulating (the KTIR operand dtype) */
 } ktir_mm_t;
 int ktir_launch_matmul(const ktir_mm_t* d);
+
+/* ---- ordered indirect read-modify-write of rows ----
+ * Replaces, for a whole `scf.for` over index chunks, the reference's sequence
+ *   g = ktdp.load src[ind(idx[p + k]), c]     (ops/memory_ops.py:868-915)
+ *   o = ktdp.load dst[ind(idx[q + k]), c]
+ *   ktdp.store f(o, g), dst[ind(idx[q + k]), c] (ops/memory_ops.py:918-964, memory.py:281-291)
+ * run instance after instance (instances = (core, iteration) in the
+ * reference's order, grid.py:595-616).  Results are bit-exact: inside one
+ * instance a repeated destination row keeps only its last position; across
+ * instances the updates of one row are applied one after another in order.
+ * f is  dst = round_dt(op(dst, src))  (order 0) or  round_dt(op(src, dst))  (order 1). */
+typedef struct ktir_rmw {
+  int64_t n_inst, K, D;
+  uint64_t dst_pos;        /* const int64_t* [n_inst]: index-tensor element of row 0's dst index */
+  uint64_t src_pos;        /* const int64_t* [n_inst]: index-tensor element of row 0's src index */
+  uint64_t dst_idx_ptr, src_idx_ptr;   /* index tensors (element 0) */
+  int32_t dst_idx_dtype, src_idx_dtype;
+  int64_t dst_idx_hi, src_idx_hi;      /* valid element window [0, hi) of the index tensors */
+  uint64_t dst_ptr, src_ptr;           /* dst / src allocations (element 0) */
+  int32_t dst_dtype, src_dtype;
+  int64_t dst_base, dst_row, dst_col, dst_hi;  /* view origin, row and column strides, allocation size (elements) */
+  int64_t src_base, src_row, src_col, src_hi;
+  int32_t op, order, dt, pad;
+  int64_t n_rows;          /* destination rows covered by the head table */
+  uint64_t head;           /* int32_t [n_rows] scratch (set to -1 by the call) */
+  uint64_t link;           /* int32_t [n_inst * K] scratch */
+} ktir_rmw_t;
+int ktir_launch_row_rmw(const ktir_rmw_t* d);
 
 #ifdef __cplusplus
 }

@@ -202,6 +202,33 @@ __device__ __forceinline__ void leaf_load(const ktir_leaf_t& L, int nd, int64_t 
     for (int v = 0; v < V; ++v) out[v] = x;
     return;
   }
+  if (V == 8 && (L.flags & KTIR_LEAF_VEC8) && e0 >= L.lo && e0 + V <= L.hi) {
+    switch (L.dtype) {
+      case KTIR_F16: {
+        uint4 w = *(const uint4*)((const _Float16*)L.ptr + e0);
+        const _Float16* h = (const _Float16*)&w;
+        for (int v = 0; v < V; ++v) out[v] = (float)h[v];
+        return;
+      }
+      case KTIR_BF16: {
+        uint4 w = *(const uint4*)((const uint16_t*)L.ptr + e0);
+        const uint32_t* u = (const uint32_t*)&w;
+        for (int v = 0; v < 4; ++v) {
+          out[2 * v] = __uint_as_float(u[v] << 16);
+          out[2 * v + 1] = __uint_as_float(u[v] & 0xffff0000u);
+        }
+        return;
+      }
+      case KTIR_F32: case KTIR_I32: {
+        float4 w0 = *(const float4*)((const float*)L.ptr + e0);
+        float4 w1 = *(const float4*)((const float*)L.ptr + e0 + 4);
+        out[0] = w0.x; out[1] = w0.y; out[2] = w0.z; out[3] = w0.w;
+        out[4] = w1.x; out[5] = w1.y; out[6] = w1.z; out[7] = w1.w;
+        return;
+      }
+      default: break;
+    }
+  }
   if (V == 4 && (L.flags & KTIR_LEAF_VEC) && e0 >= L.lo && e0 + V <= L.hi) {
     switch (L.dtype) {
       case KTIR_F16: {
@@ -250,6 +277,28 @@ __device__ __forceinline__ void leaf_store(const ktir_leaf_t& L, int nd, int64_t
   }
   int64_t e0 = lo;
   for (int d = 0; d < nd; ++d) e0 += idx[d] * L.strides[d];
+  if (V == 8 && nv == V && !L.winner && (L.flags & KTIR_LEAF_VEC8) && e0 >= L.lo && e0 + V <= L.hi) {
+    switch (L.dtype) {
+      case KTIR_F16: {
+        _Float16 h[8];
+        for (int v = 0; v < 8; ++v) h[v] = (_Float16)val[v];
+        *(uint4*)((_Float16*)L.ptr + e0) = *(const uint4*)h;
+        return;
+      }
+      case KTIR_BF16: {
+        uint32_t b[8];
+        for (int v = 0; v < 8; ++v) b[v] = __float_as_uint(round_bf16(val[v])) >> 16;
+        *(uint4*)((uint16_t*)L.ptr + e0) =
+            make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+        return;
+      }
+      case KTIR_F32: case KTIR_I32:
+        *(float4*)((float*)L.ptr + e0) = make_float4(val[0], val[1], val[2], val[3]);
+        *(float4*)((float*)L.ptr + e0 + 4) = make_float4(val[4], val[5], val[6], val[7]);
+        return;
+      default: break;
+    }
+  }
   if (V == 4 && nv == V && !L.winner && (L.flags & KTIR_LEAF_VEC) && e0 >= L.lo && e0 + V <= L.hi) {
     switch (L.dtype) {
       case KTIR_F16: {
@@ -285,8 +334,8 @@ __device__ __forceinline__ void leaf_store(const ktir_leaf_t& L, int nd, int64_t
 
 // Execute one instruction for V elements.  `rowctx` marks per-row code in row
 // mode: loads broadcast the element at inner index 0 and stores write once.
-template <int V>
-__device__ __forceinline__ void exec(const ktir_prog_t& P, const ktir_instr_t in, float (&r)[KTIR_NREG][V],
+template <int V, int NR>
+__device__ __forceinline__ void exec(const ktir_prog_t& P, const ktir_instr_t in, float (&r)[NR][V],
                                      int64_t lane, const int64_t* idx, int64_t flat, int64_t per_lane,
                                      bool rowctx, bool writer, float* red, int64_t red_pos, int64_t inner) {
   const int op = in.op;
@@ -350,30 +399,51 @@ __device__ __forceinline__ void exec(const ktir_prog_t& P, const ktir_instr_t in
   }
 }
 
-template <int V>
-__global__ __launch_bounds__(256) void prog_flat(const ktir_prog_t P, int64_t total_vecs) {
+// Division by a launch-invariant divisor with one multiply-high (n < 2^31).
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+static FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.s = s;
+  f.m = (uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+struct FlatDivs {
+  FastDiv nvi;                     // vectors per row
+  FastDiv dim[KTIR_MAX_DIMS];      // extents of the outer dims
+  uint32_t rows_per_lane;
+};
+
+template <int V, int NR>
+__global__ __launch_bounds__(256) void prog_flat(const ktir_prog_t P, const FlatDivs D, uint32_t total_vecs) {
   const int nd = P.ndim;
   const int64_t inner = P.shape[nd - 1];
-  const int64_t nvi = (inner + V - 1) / V;
   int64_t per_lane = 1;
   for (int d = 0; d < nd; ++d) per_lane *= P.shape[d];
-  const int64_t vecs_per_lane = per_lane / inner * nvi;
-  for (int64_t vid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; vid < total_vecs;
-       vid += (int64_t)gridDim.x * blockDim.x) {
-    int64_t lane = vid / vecs_per_lane;
-    int64_t rem = vid - lane * vecs_per_lane;
+  for (uint32_t vid = blockIdx.x * blockDim.x + threadIdx.x; vid < total_vecs; vid += gridDim.x * blockDim.x) {
+    const uint32_t row = fdiv(vid, D.nvi);
     int64_t idx[KTIR_MAX_DIMS];
-    int64_t row = rem / nvi;
-    idx[nd - 1] = (rem - row * nvi) * V;
+    idx[nd - 1] = (int64_t)(vid - row * D.nvi.d) * V;
+    uint32_t t = row;
     for (int d = nd - 2; d >= 0; --d) {
-      int64_t q = row / P.shape[d];
-      idx[d] = row - q * P.shape[d];
-      row = q;
+      uint32_t q = fdiv(t, D.dim[d]);
+      idx[d] = t - q * D.dim[d].d;
+      t = q;
     }
-    int64_t flat = (rem / nvi) * inner + idx[nd - 1];
-    float r[KTIR_NREG][V];
+    const int64_t lane = t;
+    const int64_t flat = (int64_t)(row - t * D.rows_per_lane) * inner + idx[nd - 1];
+    float r[NR][V];
     for (int pc = 0; pc < P.n_instr; ++pc)
-      exec<V>(P, P.instr[pc], r, lane, idx, flat, per_lane, false, true, nullptr, 0, inner);
+      exec<V, NR>(P, P.instr[pc], r, lane, idx, flat, per_lane, false, true, nullptr, 0, inner);
   }
 }
 
@@ -423,7 +493,7 @@ __global__ __launch_bounds__(256) void prog_rows(const ktir_prog_t P, int64_t to
         for (int64_t c0 = (int64_t)threadIdx.x * V; c0 < inner; c0 += (int64_t)blockDim.x * V) {
           idx[nd - 1] = c0;
           for (int p = pc + 1; p < end; ++p)
-            exec<V>(P, P.instr[p], r, lane, idx, rr * inner + c0, per_lane, false, true, red, c0, inner);
+            exec<V, KTIR_NREG>(P, P.instr[p], r, lane, idx, rr * inner + c0, per_lane, false, true, red, c0, inner);
         }
         pc = end + 1;
         continue;
@@ -435,7 +505,7 @@ __global__ __launch_bounds__(256) void prog_rows(const ktir_prog_t P, int64_t to
         FOR_V r[in.dst][v] = x;
       } else {
         idx[nd - 1] = 0;
-        exec<V>(P, in, r, lane, idx, rr * inner, per_lane, true, threadIdx.x == 0, red, 0, inner);
+        exec<V, KTIR_NREG>(P, in, r, lane, idx, rr * inner, per_lane, true, threadIdx.x == 0, red, 0, inner);
       }
       ++pc;
     }
@@ -458,13 +528,31 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
   const int64_t inner = P->shape[P->ndim - 1];
   const bool v4 = (inner % 4) == 0;
   if (P->mode == 0) {
-    int64_t vecs = P->lanes * (per_lane / inner) * (v4 ? inner / 4 : inner);
+    // registers the program uses decide the vector width: 4 x 8 or 8 x 4
+    int nreg = 0;
+    for (int i = 0; i < P->n_instr; ++i) {
+      const ktir_instr_t& in = P->instr[i];
+      if (in.op != KTIR_OP_ST && in.dst + 1 > nreg) nreg = in.dst + 1;
+    }
+    // 8-wide registers spill to scratch on gfx950 with this interpreter: use 4
+    int V = inner % 4 == 0 ? 4 : 1;
+    (void)nreg;
+    int64_t rows = P->lanes * (per_lane / inner);
+    int64_t vecs = rows * (inner / V);
+    if (vecs >= (int64_t)0x7fffffff || inner / V >= (int64_t)0x7fffffff)
+      return set_error(KTIR_E_UNSUPPORTED, "program over %lld vectors", (long long)vecs);
+    FlatDivs D;
+    D.nvi = make_fastdiv((uint32_t)(inner / V));
+    for (int d = 0; d < KTIR_MAX_DIMS; ++d) D.dim[d] = make_fastdiv(d < P->ndim - 1 ? (uint32_t)P->shape[d] : 1);
+    D.rows_per_lane = (uint32_t)(per_lane / inner);
     int64_t blocks = (vecs + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (v4)
-      hipLaunchKernelGGL(prog_flat<4>, dim3((unsigned)blocks), dim3(256), 0, stream(), *P, vecs);
+    if (blocks > 1048576) blocks = 1048576;
+    if (V == 8)
+      hipLaunchKernelGGL((prog_flat<8, 4>), dim3((unsigned)blocks), dim3(256), 0, stream(), *P, D, (uint32_t)vecs);
+    else if (V == 4)
+      hipLaunchKernelGGL((prog_flat<4, 8>), dim3((unsigned)blocks), dim3(256), 0, stream(), *P, D, (uint32_t)vecs);
     else
-      hipLaunchKernelGGL(prog_flat<1>, dim3((unsigned)blocks), dim3(256), 0, stream(), *P, vecs);
+      hipLaunchKernelGGL((prog_flat<1, 8>), dim3((unsigned)blocks), dim3(256), 0, stream(), *P, D, (uint32_t)vecs);
   } else {
     if (inner > KTIR_MAX_ROW)
       return set_error(KTIR_E_UNSUPPORTED, "row program: row of %lld elements exceeds %d", (long long)inner,

@@ -213,8 +213,10 @@ class IATile:
     ssa: Dict[str, np.ndarray]  # per-lane values of outer SSA names in the subscripts
 
     def take(self, idx):
+        ssa = {k: ({i: a[idx] for i, a in v.items()} if isinstance(v, dict) else v[idx])
+               for k, v in self.ssa.items()}
         return IATile(self.parent.take(idx), self.shape, self.subs, [v.take(idx) for v in self.views],
-                      self.vss, self.vso, {k: v[idx] for k, v in self.ssa.items()})
+                      self.vss, self.vso, ssa)
 
 
 class Tile:
@@ -263,6 +265,7 @@ class Access:
     shape: Tuple[int, ...]
     strides: Tuple[int, ...]
     whole: bool = False         # data-dependent addresses: the whole allocation
+    group: Optional[int] = None # accesses of one fused launch that orders its lanes itself
 
 
 class Instances:
@@ -317,6 +320,9 @@ def verify(accesses: List[Access], insts: Instances) -> Optional[str]:
         if not any(a.store for a in lst):
             continue
         name = lst[0].alloc.name
+        groups = {a.group for a in lst}
+        if len(groups) == 1 and None not in groups:
+            continue
         all_insts = np.concatenate([a.inst for a in lst])
         if len(np.unique(all_insts)) == 1:
             continue

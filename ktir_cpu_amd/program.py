@@ -507,14 +507,17 @@ def _fill_leaf(dst: rt.Leaf, L: LeafSpec, lanes: int, ndim: int, keep: list):
         dst.winner = L.winner.ptr
         dst.winner_base = L.winner_base
         keep.append(L.winner)
-    # wide accesses: inner stride 1 and every 4-element vector start aligned
-    vec = L.offsets is None and st[-1] == 1 and all(s % 4 == 0 for s in st[:-1])
-    if vec:
-        if starts is not None:
-            vec = bool(np.all(starts % 4 == 0))
-        else:
-            vec = L.lane.base % 4 == 0 and L.lane.stride % 4 == 0
-        bpe = rt.ELEM_BYTES[L.dtype]
-        vec = vec and (L.ptr % (4 * bpe) == 0)
-    dst.flags = rt.K["KTIR_LEAF_VEC"] if vec else 0
+    # wide accesses: inner stride 1 and every 4- (8-) element vector start aligned
+    flags = 0
+    bpe = rt.ELEM_BYTES[L.dtype]
+    for w, bit in ((4, rt.K["KTIR_LEAF_VEC"]), (8, rt.K["KTIR_LEAF_VEC8"])):
+        ok = L.offsets is None and st[-1] == 1 and all(s % w == 0 for s in st[:-1]) and L.ptr % (w * bpe) == 0
+        if ok:
+            if starts is not None:
+                ok = bool(np.all(starts % w == 0))
+            else:
+                ok = L.lane.base % w == 0 and L.lane.stride % w == 0
+        if ok:
+            flags |= bit
+    dst.flags = flags
     keep.extend(L.keep)

@@ -90,6 +90,18 @@ class MM(C.Structure):
                 ("round_dt", C.c_int32)]
 
 
+class RMW(C.Structure):
+    _fields_ = [("n_inst", C.c_int64), ("K", C.c_int64), ("D", C.c_int64), ("dst_pos", C.c_uint64),
+                ("src_pos", C.c_uint64), ("dst_idx_ptr", C.c_uint64), ("src_idx_ptr", C.c_uint64),
+                ("dst_idx_dtype", C.c_int32), ("src_idx_dtype", C.c_int32), ("dst_idx_hi", C.c_int64),
+                ("src_idx_hi", C.c_int64), ("dst_ptr", C.c_uint64), ("src_ptr", C.c_uint64),
+                ("dst_dtype", C.c_int32), ("src_dtype", C.c_int32), ("dst_base", C.c_int64),
+                ("dst_row", C.c_int64), ("dst_col", C.c_int64), ("dst_hi", C.c_int64), ("src_base", C.c_int64),
+                ("src_row", C.c_int64), ("src_col", C.c_int64), ("src_hi", C.c_int64), ("op", C.c_int32),
+                ("order", C.c_int32), ("dt", C.c_int32), ("pad", C.c_int32), ("n_rows", C.c_int64),
+                ("head", C.c_uint64), ("link", C.c_uint64)]
+
+
 class KTIRDeviceError(RuntimeError):
     pass
 
@@ -113,7 +125,8 @@ def lib():
                      "ktir_memcpy_d2d", "ktir_memset", "ktir_sync", "ktir_check_error_flag",
                      "ktir_launch_program", "ktir_scatter_winners", "ktir_iat_offsets",
                      "ktir_launch_matmul", "ktir_event_create", "ktir_event_record",
-                     "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info"):
+                     "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info",
+                     "ktir_launch_row_rmw"):
             getattr(L, name).restype = C.c_int
         L.ktir_malloc.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.ktir_free.argtypes = [C.c_uint64]
@@ -125,6 +138,7 @@ def lib():
         L.ktir_scatter_winners.argtypes = [C.POINTER(Leaf), C.c_int64, C.c_int64, C.c_uint64]
         L.ktir_iat_offsets.argtypes = [C.POINTER(IAT)]
         L.ktir_launch_matmul.argtypes = [C.POINTER(MM)]
+        L.ktir_launch_row_rmw.argtypes = [C.POINTER(RMW)]
         L.ktir_event_create.argtypes = [C.POINTER(C.c_uint64)]
         L.ktir_event_record.argtypes = [C.c_uint64]
         L.ktir_event_elapsed_ms.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_float)]

@@ -417,11 +417,11 @@ class Executor:
         spec = LeafSpec(self.arena.ptr_of(a), view.dtype, LaneOff.from_array(rel), strides, 0, a.n_elems, alloc=a)
         return spec, a, rel
 
-    def log(self, alloc, store, base, shape, strides, whole=False):
+    def log(self, alloc, store, base, shape, strides, whole=False, group=None):
         if self.sequential:
             return
         self.accesses.append(Access(alloc, store, self.lanes.inst.copy(), np.asarray(base, dtype=np.int64),
-                                    tuple(shape), tuple(strides), whole))
+                                    tuple(shape), tuple(strides), whole, group))
 
     def materialize(self, t: Tile, dest: Optional[LeafSpec] = None) -> Tile:
         """Evaluate `t` into a fresh contiguous temporary (or into `dest`)."""

@@ -33,7 +33,20 @@ def test_vector_add_bit_exact(n, block, cores):
 
 
 def test_gather_scatter_add_bit_exact():
-    ref, out, _ = _run(_cases.gather_scatter_add())
+    ref, out, g = _run(_cases.gather_scatter_add())
+    np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    assert g.last_plan.counts() == {"rmw": 1}
+
+
+@pytest.mark.parametrize("rows", [16, 3])
+def test_gather_scatter_add_heavy_duplicates(rows):
+    """Many repeats inside one chunk (last writer wins) and long per-row chains
+    across chunks and cores (sequential accumulation order)."""
+    src, fn, kw = _cases.gather_scatter_add(rows=1024, dim=32, n_idx=512, cores=4, chunk=32)
+    rng = np.random.default_rng(7)
+    kw["idx_ptr"] = rng.integers(0, rows, 512).astype(np.int32)
+    kw["out_ptr"] = rng.standard_normal((1024, 32)).astype(np.float32)
+    ref, out, _ = _run((src, fn, kw))
     np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
 
 
