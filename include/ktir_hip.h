@@ -146,6 +146,8 @@ extern "C" {
 /* leaf flags */
 #define KTIR_LEAF_VEC 1      /* inner stride 1, every 4-element vector start aligned: wide accesses */
 #define KTIR_LEAF_VEC8 2     /* same for 8-element vectors */
+#define KTIR_LEAF_CHECKED 4  /* matmul operand: the host verified that every lane's reads stay inside
+                                [lo, hi) and that every lane offset is a multiple of 8 elements */
 
 /* One strided (or offset-list) view of device memory.
  * Element address for lane l at iteration index (i0..i3):
@@ -185,6 +187,10 @@ typedef struct ktir_instr {
  *   ELEM blocks compute per-row values. */
 typedef struct ktir_prog {
   int32_t mode, ndim, n_instr, n_leaves;
+  /* flat mode: registers 0..n_pf-1 are preloaded from leaves pf_leaf[0..n_pf-1]
+   * before the instructions run, so all of a vector's loads are in flight at once */
+  int32_t n_pf;
+  int8_t pf_leaf[4];
   int64_t lanes;
   int64_t shape[KTIR_MAX_DIMS];
   uint64_t lane_scalars;          /* const double* [lanes * n_lane_scalars] or 0 */
@@ -261,8 +267,8 @@ typedef struct ktir_mm {
   ktir_leaf_t a, b;       /* strides[0] = row stride, strides[1] = column stride */
   int64_t a_kstep, b_kstep;
   ktir_leaf_t c;          /* result (f32 / f16 / bf16), strides[0..1] */
-  ktir_leaf_t c0;         /* accumulator input when accumulate != 0 */
-  int32_t accumulate;
+  ktir_leaf_t c0;         /* accumulator input when accumulate == 1 */
+  int32_t accumulate;     /* 0: C = A@B; 1: C = C0 + A@B; 2: C = 0.0 + A@B (outs is a zero splat) */
   int32_t round_dt;       /* dtype the product is rounded to before accumulating (the KTIR operand dtype) */
 } ktir_mm_t;
 int ktir_launch_matmul(const ktir_mm_t* d);
@@ -292,6 +298,9 @@ typedef struct ktir_rmw {
   int64_t n_rows;          /* destination rows covered by the head table */
   uint64_t head;           /* int32_t [n_rows] scratch (set to -1 by the call) */
   uint64_t link;           /* int32_t [n_inst * K] scratch */
+  uint64_t rows;           /* int32_t [n_inst * K] scratch: destination row of each entry */
+  uint64_t srcs;           /* int32_t [n_inst * K] scratch: source row of each entry */
+  uint64_t owners;         /* int32_t [n_inst * K + 1] scratch: owner count, then owner entries */
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
 

@@ -1,0 +1,246 @@
+// Streaming kernels for the most common fused program: one or two strided
+// inputs, a chain of register ops, one strided output (an elementwise map,
+// a copy, a cast, a broadcast).  Leaf and output dtypes are template
+// parameters, so the memory path is straight-line code: each thread moves
+// 8-element chunks with 16-byte accesses and has all its chunks' loads in
+// flight before it computes.  The register ops still come from the
+// program, evaluated per element with the same semantics as the general
+// interpreter (ktir_program.hip).
+#include "ktir_program_impl.h"
+
+namespace ktir {
+
+template <int DT>
+__device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* out) {
+  if (e0 >= L.lo && e0 + 8 <= L.hi) {
+    if (DT == KTIR_F16) {
+      uint4 w = *(const uint4*)((const _Float16*)L.ptr + e0);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xffffu));
+        out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+      }
+    } else if (DT == KTIR_BF16) {
+      uint4 w = *(const uint4*)((const uint16_t*)L.ptr + e0);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = __uint_as_float(u[i] << 16);
+        out[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+      }
+    } else {
+      float4 w0 = *(const float4*)((const float*)L.ptr + e0);
+      float4 w1 = *(const float4*)((const float*)L.ptr + e0 + 4);
+      out[0] = w0.x; out[1] = w0.y; out[2] = w0.z; out[3] = w0.w;
+      out[4] = w1.x; out[5] = w1.y; out[6] = w1.z; out[7] = w1.w;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t e = e0 + i;
+    out[i] = (e >= L.lo && e < L.hi) ? load_elem(L.ptr, e, DT) : 0.f;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(const ktir_leaf_t& L, int64_t e0, const float* v) {
+  if (e0 >= L.lo && e0 + 8 <= L.hi) {
+    if (DT == KTIR_F16) {
+      uint32_t u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        u[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1]) << 16);
+      *(uint4*)((_Float16*)L.ptr + e0) = make_uint4(u[0], u[1], u[2], u[3]);
+    } else if (DT == KTIR_BF16) {
+      uint32_t u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        u[i] = (__float_as_uint(round_bf16(v[2 * i])) >> 16) | (__float_as_uint(round_bf16(v[2 * i + 1])) & 0xffff0000u);
+      *(uint4*)((uint16_t*)L.ptr + e0) = make_uint4(u[0], u[1], u[2], u[3]);
+    } else {
+      *(float4*)((float*)L.ptr + e0) = make_float4(v[0], v[1], v[2], v[3]);
+      *(float4*)((float*)L.ptr + e0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t e = e0 + i;
+    if (e >= L.lo && e < L.hi) store_elem(L.ptr, e, DT, v[i]);
+  }
+}
+
+// Four named registers selected by the (uniform) register number: no array,
+// so nothing is spilled to scratch.
+struct Reg4 {
+  float r0, r1, r2, r3;
+  __device__ __forceinline__ float get(int i) const { return i == 0 ? r0 : (i == 1 ? r1 : (i == 2 ? r2 : r3)); }
+  __device__ __forceinline__ void set(int i, float v) {
+    r0 = i == 0 ? v : r0;
+    r1 = i == 1 ? v : r1;
+    r2 = i == 2 ? v : r2;
+    r3 = i == 3 ? v : r3;
+  }
+};
+
+__device__ __forceinline__ void exec_reg4(const ktir_prog_t& P, const ktir_instr_t in, Reg4& R, int64_t lane) {
+  const int op = in.op;
+  const float a = R.get(in.a), b = R.get(in.b);
+  float v;
+  if (op >= KTIR_OP_NEGF && op < KTIR_OP_ADDF) {
+    v = unop_simple(op, in.dt, a);
+  } else if (op >= KTIR_OP_ADDF && op < KTIR_OP_ADDI) {
+    v = binop_f_simple(op, in.dt, a, b);
+  } else if (op >= KTIR_OP_ADDI) {
+    v = __int_as_float(binop_i_simple(op, __float_as_int(a), __float_as_int(b)));
+  } else {
+    switch (op) {
+      case KTIR_OP_CONST: v = __int_as_float(in.imm); break;
+      case KTIR_OP_LANE: {
+        double d = ((const double*)P.lane_scalars)[lane * P.n_lane_scalars + in.aux];
+        v = is_float_dt(in.dt) ? round_to((float)d, in.dt) : __int_as_float((int)(long long)d);
+        break;
+      }
+      case KTIR_OP_CAST: v = cast_val(a, in.aux, in.dt); break;
+      case KTIR_OP_BITCAST: v = a; break;
+      case KTIR_OP_SELECT: v = __float_as_int(a) ? b : R.get(in.c); break;
+      case KTIR_OP_FMA: v = round_to(__fadd_rn(__fmul_rn(a, b), R.get(in.c)), in.dt); break;
+      case KTIR_OP_CMPF: v = __int_as_float(cmp_f(in.aux, a, b)); break;
+      case KTIR_OP_CMPI: v = __int_as_float(cmp_i(in.aux, __float_as_int(a), __float_as_int(b))); break;
+      default: v = 0.f;
+    }
+  }
+  R.set(in.dst, v);
+}
+
+template <int DA, int DB, int DO, int NIN>
+__global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatDivs D, uint32_t total, int st_leaf) {
+  const ktir_leaf_t& LA = P.leaves[P.pf_leaf[0]];
+  const ktir_leaf_t& LB = P.leaves[NIN == 2 ? P.pf_leaf[1] : P.pf_leaf[0]];
+  const ktir_leaf_t& LO = P.leaves[st_leaf];
+  const int nd = P.ndim;
+  const int n_ops = P.n_instr - 1;
+  const int out_reg = P.instr[n_ops].a;
+  const uint32_t nth = gridDim.x * blockDim.x;
+  for (uint32_t vid = blockIdx.x * blockDim.x + threadIdx.x; vid < total; vid += nth) {
+    // coordinates of the chunk: c[d] for the outer dims d < nd-1, col inner
+    uint32_t c[KTIR_MAX_DIMS] = {0, 0, 0, 0};
+    const uint32_t row = fdiv(vid, D.nvi);
+    const int64_t col = (int64_t)(vid - row * D.nvi.d) * 8;
+    uint32_t t = row;
+#pragma unroll
+    for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+      if (d < nd - 1) {
+        uint32_t q = fdiv(t, D.dim[d]);
+        c[d] = t - q * D.dim[d].d;
+        t = q;
+      }
+    }
+    // inner strides are 1 on this path (checked at launch)
+    int64_t ea = lane_offset(LA, t) + col;
+    int64_t eb = lane_offset(LB, t) + col;
+    int64_t eo = lane_offset(LO, t) + col;
+#pragma unroll
+    for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) {
+      if (d < nd - 1) {
+        ea += (int64_t)c[d] * LA.strides[d];
+        eb += (int64_t)c[d] * LB.strides[d];
+        eo += (int64_t)c[d] * LO.strides[d];
+      }
+    }
+    float a[8], b[8];
+    load8<DA>(LA, ea, a);
+    if (NIN == 2) load8<DB>(LB, eb, b);
+    Reg4 R[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R[e] = Reg4{a[e], NIN == 2 ? b[e] : 0.f, 0.f, 0.f};
+    for (int pc = 0; pc < n_ops; ++pc) {
+      const ktir_instr_t in = P.instr[pc];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) exec_reg4(P, in, R[e], t);
+    }
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = R[e].get(out_reg);
+    store8<DO>(LO, eo, out);
+  }
+}
+
+template <int DA, int DB, int DO, int NIN>
+static void launch_map(const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, int st_leaf) {
+  int64_t blocks = ((int64_t)total + 255) / 256;
+  if (blocks > 1048576) blocks = 1048576;
+  hipLaunchKernelGGL((prog_map<DA, DB, DO, NIN>), dim3((unsigned)blocks), dim3(256), 0, stream(), Q, D, total,
+                     st_leaf);
+}
+
+template <int DA, int DB, int NIN>
+static bool pick_out(int dout, const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, int st) {
+  switch (dout) {
+    case KTIR_F16: launch_map<DA, DB, KTIR_F16, NIN>(Q, D, total, st); return true;
+    case KTIR_BF16: launch_map<DA, DB, KTIR_BF16, NIN>(Q, D, total, st); return true;
+    case KTIR_F32: launch_map<DA, DB, KTIR_F32, NIN>(Q, D, total, st); return true;
+  }
+  return false;
+}
+
+template <int DA, int NIN>
+static bool pick_b(int db, int dout, const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, int st) {
+  if (NIN == 1) return pick_out<DA, DA, 1>(dout, Q, D, total, st);
+  switch (db) {
+    case KTIR_F16: return pick_out<DA, KTIR_F16, 2>(dout, Q, D, total, st);
+    case KTIR_BF16: return pick_out<DA, KTIR_BF16, 2>(dout, Q, D, total, st);
+    case KTIR_F32: return pick_out<DA, KTIR_F32, 2>(dout, Q, D, total, st);
+  }
+  return false;
+}
+
+// Launch `Q` through a map kernel if it has the supported form.
+bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner) {
+  if (Q.mode != 0 || Q.n_pf < 1 || Q.n_pf > 2 || Q.n_instr < 1 || inner % 8) return false;
+  const ktir_instr_t& st = Q.instr[Q.n_instr - 1];
+  if (st.op != KTIR_OP_ST || st.a > 3) return false;
+  for (int i = 0; i < Q.n_instr - 1; ++i) {
+    const ktir_instr_t& in = Q.instr[i];
+    const int op = in.op;
+    if (op == KTIR_OP_LD || op == KTIR_OP_ST || op == KTIR_OP_IDX || !simple_op(op)) return false;
+    if (in.dst > 3 || in.a > 3 || in.b > 3 || in.c > 3) return false;   // four registers
+  }
+  const int nd = Q.ndim;
+  auto ok_leaf = [nd](const ktir_leaf_t& L) {
+    return L.offsets == 0 && L.winner == 0 && L.strides[nd - 1] == 1 && (L.flags & KTIR_LEAF_VEC8) &&
+           (L.dtype == KTIR_F16 || L.dtype == KTIR_BF16 || L.dtype == KTIR_F32);
+  };
+  for (int k = 0; k < Q.n_pf; ++k)
+    if (!ok_leaf(Q.leaves[Q.pf_leaf[k]])) return false;
+  if (!ok_leaf(Q.leaves[st.aux])) return false;
+  const int64_t chunks = rows * (inner / 8);
+  if (chunks >= (int64_t)0x7fffffff || inner / 8 >= (int64_t)0x7fffffff) return false;
+  FlatDivs D;
+  D.nvi = make_fastdiv((uint32_t)(inner / 8));
+  for (int d = 0; d < KTIR_MAX_DIMS; ++d) D.dim[d] = make_fastdiv(d < Q.ndim - 1 ? (uint32_t)Q.shape[d] : 1);
+  D.rows_per_lane = 0;
+  const int da = Q.leaves[Q.pf_leaf[0]].dtype;
+  const int db = Q.n_pf == 2 ? Q.leaves[Q.pf_leaf[1]].dtype : da;
+  const int dout = Q.leaves[st.aux].dtype;
+  const uint32_t total = (uint32_t)chunks;
+  if (Q.n_pf == 1) {
+    switch (da) {
+      case KTIR_F16: return pick_b<KTIR_F16, 1>(db, dout, Q, D, total, st.aux);
+      case KTIR_BF16: return pick_b<KTIR_BF16, 1>(db, dout, Q, D, total, st.aux);
+      case KTIR_F32: return pick_b<KTIR_F32, 1>(db, dout, Q, D, total, st.aux);
+    }
+  } else {
+    switch (da) {
+      case KTIR_F16: return pick_b<KTIR_F16, 2>(db, dout, Q, D, total, st.aux);
+      case KTIR_BF16: return pick_b<KTIR_BF16, 2>(db, dout, Q, D, total, st.aux);
+      case KTIR_F32: return pick_b<KTIR_F32, 2>(db, dout, Q, D, total, st.aux);
+    }
+  }
+  return false;
+}
+
+}  // namespace ktir

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void mm_generic(const ktir_mm_t d) {
       }
     }
     const int64_t cbase = lane_offset(d.c, lane);
-    const int64_t c0base = d.accumulate ? lane_offset(d.c0, lane) : 0;
+    const int64_t c0base = d.accumulate == 1 ? lane_offset(d.c0, lane) : 0;
     for (int i = 0; i < 4; ++i) {
       int64_t gm = m0 + ty * 4 + i;
       if (gm >= d.M) continue;
@@ -70,10 +70,12 @@ __global__ __launch_bounds__(256) void mm_generic(const ktir_mm_t d) {
         // np.matmul(...).astype(a.dtype): round the product to the result dtype
         // first, then accumulate into outs (the reference's two roundings).
         float v = round_to(acc[i][j], d.round_dt);
-        if (d.accumulate) {
+        if (d.accumulate == 1) {
           int64_t e0 = c0base + gm * d.c0.strides[0] + gn * d.c0.strides[1];
           float prev = (e0 >= d.c0.lo && e0 < d.c0.hi) ? load_elem(d.c0.ptr, e0, d.c0.dtype) : 0.f;
           v = round_to(__fadd_rn(prev, v), d.c.dtype);
+        } else if (d.accumulate == 2) {
+          v = round_to(__fadd_rn(0.f, v), d.c.dtype);
         }
         int64_t e = cbase + gm * d.c.strides[0] + gn * d.c.strides[1];
         if (e >= d.c.lo && e < d.c.hi) store_elem(d.c.ptr, e, d.c.dtype, v);

@@ -1,8 +1,200 @@
-// gfx950 MFMA matmul tiles (f16 / bf16 operands, f32 accumulation).
+// gfx950 MFMA matmul tiles: f16 / bf16 operands, f32 accumulation.
+//
+// One workgroup (4 wavefronts) computes one 128x128 output tile of one lane;
+// each wavefront owns a 64x64 quadrant made of 2x2 v_mfma_f32_32x32x16
+// tiles.  The K dimension (the fused scf.for steps times the tile's own K)
+// advances 64 at a time through double-buffered LDS: A is staged row-major,
+// B transposed (k contiguous) so both MFMA operands are 16-byte LDS reads.
+// Global loads for step t+1 are issued before the MFMAs of step t.
+// Block ids are remapped so consecutive tiles (which share A rows) land on
+// the same XCD and its L2.
+//
+// Operand layout of v_mfma_f32_32x32x16_{f16,bf16} (64 lanes):
+//   A (32 x 16): lane l holds row l%32, k = 8*(l/32) .. +8
+//   B (16 x 32): lane l holds col l%32, k = 8*(l/32) .. +8
+//   D (32 x 32): lane l holds col l%32, rows 8*(i/4) + 4*(l/32) + i%4, i < 16
 #include "ktir_common.h"
 
+namespace ktir {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bfx8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int MT = 128, NT = 128, BK = 64, LDK = BK + 8;   // LDS row: 72 halfs (pad breaks bank conflicts)
+
+// 16-bit element i (0..7) of a 128-bit register group
+__device__ __forceinline__ uint32_t half_of(const uint4& v, int i) {
+  const uint32_t w = i < 2 ? v.x : (i < 4 ? v.y : (i < 6 ? v.z : v.w));
+  return (i & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma32(const uint4& a, const uint4& b, f32x16 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bfx8, a), __builtin_bit_cast(bfx8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void mm_mfma(const ktir_mm_t d, int64_t tiles_m, int64_t tiles_n) {
+  __shared__ __align__(16) uint16_t As[2][MT * LDK];
+  __shared__ __align__(16) uint16_t Bs[2][NT * LDK];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t nblk = gridDim.x;
+  int64_t bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int64_t per_lane = tiles_m * tiles_n;
+  const int64_t ln = bid / per_lane, t = bid - ln * per_lane;
+  const int64_t m0 = (t / tiles_n) * MT, n0 = (t % tiles_n) * NT;
+  const uint16_t* A = (const uint16_t*)d.a.ptr;
+  const uint16_t* B = (const uint16_t*)d.b.ptr;
+  const int64_t a_row = d.a.strides[0], b_row = d.b.strides[0];
+  const int64_t abase = lane_offset(d.a, ln) + m0 * a_row;
+  const int64_t bbase = lane_offset(d.b, ln) + n0;
+  const int64_t kt_per_step = d.K / BK;
+  const int64_t nk = d.ksteps * kt_per_step;
+  // global -> register assignment
+  const int a_r = tid >> 3, a_k = (tid & 7) * 8;      // A rows a_r + 32 j, k-group a_k
+  const int b_k = (tid >> 4) * 4, b_n = (tid & 15) * 8; // B rows b_k + r, cols b_n .. +8
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define GLOAD(kt)                                                                   \
+  do {                                                                              \
+    const int64_t s_ = (kt) / kt_per_step, kk0_ = ((kt) - s_ * kt_per_step) * BK;     \
+    const uint16_t* pa = A + abase + s_ * d.a_kstep + kk0_ + a_k + (int64_t)a_r * a_row; \
+    ra0 = *(const uint4*)(pa);                                                      \
+    ra1 = *(const uint4*)(pa + 32 * a_row);                                         \
+    ra2 = *(const uint4*)(pa + 64 * a_row);                                         \
+    ra3 = *(const uint4*)(pa + 96 * a_row);                                         \
+    const uint16_t* pb = B + bbase + s_ * d.b_kstep + (kk0_ + b_k) * b_row + b_n;   \
+    rb0 = *(const uint4*)(pb);                                                      \
+    rb1 = *(const uint4*)(pb + b_row);                                              \
+    rb2 = *(const uint4*)(pb + 2 * b_row);                                          \
+    rb3 = *(const uint4*)(pb + 3 * b_row);                                          \
+  } while (0)
+#define SWRITE(buf)                                                                  \
+  do {                                                                               \
+    uint16_t* as = &As[buf][a_r * LDK + a_k];                                        \
+    *(uint4*)(as) = ra0;                                                             \
+    *(uint4*)(as + 32 * LDK) = ra1;                                                  \
+    *(uint4*)(as + 64 * LDK) = ra2;                                                  \
+    *(uint4*)(as + 96 * LDK) = ra3;                                                  \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                  \
+      uint2 v = make_uint2(half_of(rb0, i) | (half_of(rb1, i) << 16), half_of(rb2, i) | (half_of(rb3, i) << 16)); \
+      *(uint2*)&Bs[buf][(b_n + i) * LDK + b_k] = v;                                  \
+    }                                                                                \
+  } while (0)
+  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  f32x16 acc00 = zero16, acc01 = zero16, acc10 = zero16, acc11 = zero16;
+  GLOAD(0);
+  SWRITE(0);
+  __syncthreads();
+  const int frag_r = lane & 31, frag_k = (lane >> 5) * 8;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) GLOAD(kt + 1);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      const uint4 a0 = *(const uint4*)&As[cur][(wr * 64 + frag_r) * LDK + kk + frag_k];
+      const uint4 a1 = *(const uint4*)&As[cur][(wr * 64 + 32 + frag_r) * LDK + kk + frag_k];
+      const uint4 b0 = *(const uint4*)&Bs[cur][(wc * 64 + frag_r) * LDK + kk + frag_k];
+      const uint4 b1 = *(const uint4*)&Bs[cur][(wc * 64 + 32 + frag_r) * LDK + kk + frag_k];
+      acc00 = mfma32<BF16>(a0, b0, acc00);
+      acc01 = mfma32<BF16>(a0, b1, acc01);
+      acc10 = mfma32<BF16>(a1, b0, acc10);
+      acc11 = mfma32<BF16>(a1, b1, acc11);
+    }
+    if (kt + 1 < nk) SWRITE(cur ^ 1);
+    __syncthreads();
+  }
+#undef GLOAD
+#undef SWRITE
+  // epilogue: round the product to the operand dtype of the KTIR matmul,
+  // then accumulate into the outs tile (the reference's two roundings)
+  const int64_t cbase = lane_offset(d.c, ln);
+  if (d.c.dtype == KTIR_F32 && d.round_dt == KTIR_F32 && d.accumulate != 1 && d.c.strides[1] == 1) {
+    // f32 result, outs absent or a zero splat (accumulate == 2: x + 0.0)
+    float* C = (float*)d.c.ptr + cbase;
+    const int64_t cs = d.c.strides[0];
+    const float z = d.accumulate == 2 ? 0.f : -0.f;
+#define EPI(a, i, j)                                                                               \
+  do {                                                                                             \
+    float* c = C + (m0 + wr * 64 + (i) * 32 + 4 * (lane >> 5)) * cs + n0 + wc * 64 + (j) * 32 + (lane & 31); \
+    _Pragma("unroll") for (int e = 0; e < 16; ++e) c[(8 * (e >> 2) + (e & 3)) * cs] = __fadd_rn(a[e], z); \
+  } while (0)
+    EPI(acc00, 0, 0);
+    EPI(acc01, 0, 1);
+    EPI(acc10, 1, 0);
+    EPI(acc11, 1, 1);
+#undef EPI
+    return;
+  }
+  const int64_t c0base = d.accumulate == 1 ? lane_offset(d.c0, ln) : 0;
+  for (int q = 0; q < 4; ++q) {
+    const int i = q >> 1, j = q & 1;
+    const f32x16 a = q == 0 ? acc00 : (q == 1 ? acc01 : (q == 2 ? acc10 : acc11));
+    for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int64_t col = n0 + wc * 64 + j * 32 + (lane & 31);
+        float v = round_to(a[e], d.round_dt);
+        if (d.accumulate == 1) {
+          const int64_t e0 = c0base + row * d.c0.strides[0] + col * d.c0.strides[1];
+          v = round_to(__fadd_rn(load_elem(d.c0.ptr, e0, d.c0.dtype), v), d.c.dtype);
+        } else if (d.accumulate == 2) {
+          v = round_to(__fadd_rn(0.f, v), d.c.dtype);
+        }
+        store_elem(d.c.ptr, cbase + row * d.c.strides[0] + col * d.c.strides[1], d.c.dtype, v);
+    }
+  }
+}
+
+}  // namespace ktir
+
+using namespace ktir;
+
+// Host-side eligibility: f16/bf16 operands, row-major with unit inner strides,
+// 16-byte aligned rows, M and N multiples of 128, K a multiple of 64.  The
+// caller (the lockstep executor) has already checked that every lane's
+// operand range lies inside its allocation.
 int ktir_launch_matmul_mfma(const ktir_mm_t* d, bool* handled) {
-  (void)d;
   *handled = false;
+  const bool f16 = d->a.dtype == KTIR_F16 && d->b.dtype == KTIR_F16;
+  const bool bf16 = d->a.dtype == KTIR_BF16 && d->b.dtype == KTIR_BF16;
+  if (!(f16 || bf16)) return KTIR_OK;
+  if (d->M % MT || d->N % NT || d->K % BK) return KTIR_OK;
+  if (d->a.strides[1] != 1 || d->b.strides[1] != 1) return KTIR_OK;
+  if (d->a.offsets || d->b.offsets) return KTIR_OK;
+  auto al8 = [](int64_t x) { return (x & 7) == 0; };
+  if (!al8(d->a.strides[0]) || !al8(d->b.strides[0]) || !al8(d->a_kstep) || !al8(d->b_kstep) ||
+      (d->a.ptr & 15) || (d->b.ptr & 15))
+    return KTIR_OK;
+  // per-lane offset arrays: the host has checked bounds and alignment
+  const bool checked = (d->a.flags & KTIR_LEAF_CHECKED) && (d->b.flags & KTIR_LEAF_CHECKED);
+  if ((d->a.lane_base || d->b.lane_base) && !checked) return KTIR_OK;
+  if (!checked && (!al8(d->a.base) || !al8(d->a.lane_stride) || !al8(d->b.base) || !al8(d->b.lane_stride)))
+    return KTIR_OK;
+  // every element the kernel reads must be inside [lo, hi) for every lane
+  const int64_t L = d->lanes;
+  auto span_ok = [&](const ktir_leaf_t& l, int64_t rows, int64_t cols, int64_t kstep) {
+    int64_t first = l.base, last_lane = l.base + (L - 1) * l.lane_stride;
+    int64_t lo = first < last_lane ? first : last_lane, hi = first < last_lane ? last_lane : first;
+    int64_t ext = (rows - 1) * l.strides[0] + (cols - 1) + (d->ksteps - 1) * kstep;
+    if (ext < 0 || kstep < 0 || l.strides[0] < 0) return false;
+    return lo >= l.lo && hi + ext < l.hi;
+  };
+  if (!checked && (!span_ok(d->a, d->M, d->K, d->a_kstep) || !span_ok(d->b, d->K, d->N, d->b_kstep)))
+    return KTIR_OK;
+  const int64_t tm = d->M / MT, tn = d->N / NT;
+  const int64_t blocks = L * tm * tn;
+  if (blocks >= (int64_t)0x7fffffff) return KTIR_OK;
+  if (f16)
+    hipLaunchKernelGGL((mm_mfma<false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
+  else
+    hipLaunchKernelGGL((mm_mfma<true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
+  KTIR_HIP_CHECK(hipGetLastError());
+  *handled = true;
   return KTIR_OK;
 }

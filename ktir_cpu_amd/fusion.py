@@ -310,9 +310,11 @@ def _row_rmw(ex, op, lb, st, trips):
     n_rows = max(1, -(-(ad.n_elems - int(bd[0])) // max(int(vd.strides[0]), 1)))
     d.n_rows = n_rows
     head = ex.pool.temp(n_rows * 4)
-    link = ex.pool.temp(max(1, n_inst * K) * 4)
-    d.head, d.link = head.ptr, link.ptr
-    keep += [head, link]
+    scratch = [ex.pool.temp(max(1, n_inst * K) * 4) for _ in range(3)]
+    owners = ex.pool.temp((n_inst * K + 1) * 4)
+    d.head, d.link, d.rows, d.srcs = head.ptr, scratch[0].ptr, scratch[1].ptr, scratch[2].ptr
+    d.owners = owners.ptr
+    keep += [head, owners] + scratch
     grp = id(d)
     z = np.zeros(L, np.int64)
     ex.log(ad, True, z, (1,), (1,), whole=True, group=grp)

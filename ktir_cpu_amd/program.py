@@ -338,9 +338,16 @@ def compile_program(root: Expr, lanes: int, dest: LeafSpec) -> Tuple[rt.Prog, li
     O = _ops()
     if not root.has_fold:
         space = root.shape if root.shape else (1,)
+        nodes = topo(root)
+        lds = [n for n in nodes if n.kind == "ld"]
+        if 0 < len(lds) <= 4 and len({id(n.attr) for n in lds}) == len(lds):
+            try:
+                return _compile_flat(root, nodes, lds, lanes, dest, space)
+            except CompileError:
+                pass
         b = _Builder(lanes, space, 0)
         regs: Dict[int, int] = {}
-        _emit_block(b, topo(root), regs, {id(root)})
+        _emit_block(b, nodes, regs, {id(root)})
         b.emit(O["ST"], 0, regs[id(root)], dt=root.dtype, aux=b.leaf(dest))
         return _finish(b, lanes, space)
 
@@ -426,6 +433,44 @@ def compile_program(root: Expr, lanes: int, dest: LeafSpec) -> Tuple[rt.Prog, li
     if row_root:
         b.emit(O["ST"], 0, regs[id(root)], dt=root.dtype, aux=b.leaf(row_leaf(dest)))
     return _finish(b, lanes, space)
+
+
+def _compile_flat(root, nodes, lds, lanes, dest, space):
+    """Flat program whose leaf loads are prefetched into registers 0..n-1."""
+    O = _ops()
+    b = _Builder(lanes, space, 0)
+    regs: Dict[int, int] = {}
+    pf = []
+    for n in lds:
+        r = b.alloc()
+        regs[id(n)] = r
+        pf.append(b.leaf(n.attr))
+    rest = [n for n in nodes if n.kind != "ld"]
+    uses: Dict[int, int] = {}
+    for n in nodes:
+        for a in n.args:
+            uses[id(a)] = uses.get(id(a), 0) + 1
+    uses[id(root)] = uses.get(id(root), 0) + 1
+    held = {id(n): regs[id(n)] for n in lds if uses.get(id(n), 0) > 0}
+    for n in rest:
+        args = [regs[id(a)] for a in n.args]
+        for a in n.args:
+            uses[id(a)] -= 1
+            if uses[id(a)] == 0 and id(a) in held:
+                b.release(held.pop(id(a)))
+        d = b.alloc()
+        _emit_one(b, n, args, d)
+        regs[id(n)] = d
+        if uses.get(id(n), 0) > 0:
+            held[id(n)] = d
+        else:
+            b.release(d)
+    b.emit(O["ST"], 0, regs[id(root)], dt=root.dtype, aux=b.leaf(dest))
+    prog, keep = _finish(b, lanes, space)
+    prog.n_pf = len(pf)
+    for i, l in enumerate(pf):
+        prog.pf_leaf[i] = l
+    return prog, keep
 
 
 def topo_stop(root: Expr) -> List[Expr]:

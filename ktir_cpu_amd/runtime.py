@@ -71,7 +71,7 @@ class Instr(C.Structure):
 
 class Prog(C.Structure):
     _fields_ = [("mode", C.c_int32), ("ndim", C.c_int32), ("n_instr", C.c_int32), ("n_leaves", C.c_int32),
-                ("lanes", C.c_int64), ("shape", C.c_int64 * MAX_DIMS), ("lane_scalars", C.c_uint64),
+                ("n_pf", C.c_int32), ("pf_leaf", C.c_int8 * 4), ("lanes", C.c_int64), ("shape", C.c_int64 * MAX_DIMS), ("lane_scalars", C.c_uint64),
                 ("n_lane_scalars", C.c_int64), ("leaves", Leaf * MAX_LEAVES), ("instr", Instr * MAX_INSTR)]
 
 
@@ -99,7 +99,8 @@ class RMW(C.Structure):
                 ("dst_row", C.c_int64), ("dst_col", C.c_int64), ("dst_hi", C.c_int64), ("src_base", C.c_int64),
                 ("src_row", C.c_int64), ("src_col", C.c_int64), ("src_hi", C.c_int64), ("op", C.c_int32),
                 ("order", C.c_int32), ("dt", C.c_int32), ("pad", C.c_int32), ("n_rows", C.c_int64),
-                ("head", C.c_uint64), ("link", C.c_uint64)]
+                ("head", C.c_uint64), ("link", C.c_uint64), ("rows", C.c_uint64), ("srcs", C.c_uint64),
+                ("owners", C.c_uint64)]
 
 
 class KTIRDeviceError(RuntimeError):

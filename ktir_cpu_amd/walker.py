@@ -1425,11 +1425,22 @@ class Executor:
         d.a.dtype = rt.DTYPE_CODE[dta]
         d.b.dtype = rt.DTYPE_CODE[dtb]
         d.a_kstep, d.b_kstep = a_k, b_k
+        # bounds / alignment of every lane's operand reads, for the MFMA path
+        for leaf, spec, rows, cols, ks in ((d.a, la, M, K, a_k), (d.b, lb, K, N, b_k)):
+            st0, st1 = spec.strides[-2], spec.strides[-1]
+            offs = spec.lane.values(L)
+            if st0 >= 0 and st1 == 1 and ks >= 0 and len(offs):
+                ext = (rows - 1) * st0 + (cols - 1) + (ksteps - 1) * ks
+                if offs.min() >= spec.lo and offs.max() + ext < spec.hi and np.all(offs % 8 == 0):
+                    leaf.flags |= rt.K["KTIR_LEAF_CHECKED"]
         n = M * N
         buf = self.pool.temp(max(1, L * n * rt.ELEM_BYTES[_store_dt(out_dt)]))
         cspec = LeafSpec(buf.ptr, _store_dt(out_dt), LaneOff(0, n), (N, 1), 0, L * n, keep=(buf,))
         _fill_leaf(d.c, cspec, L, 2, keep)
-        if acc is not None:
+        if acc is not None and acc.e.kind == "const" and float(acc.e.attr) == 0.0 \
+                and tuple(acc.shape) == (M, N):
+            d.accumulate = 2          # outs is a zero splat: C = 0.0 + A@B
+        elif acc is not None:
             lc, _ = self._mm_leaf(acc) if not (acc.e.kind == "const") else (None, None)
             if lc is None:
                 lc = self.materialize(acc).e.attr

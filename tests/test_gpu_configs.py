@@ -62,8 +62,11 @@ def test_rmsnorm(cols):
     np.testing.assert_allclose(out["y_ptr"].astype(np.float32), ref["y_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
-def test_gemm():
-    ref, out, _ = _run(_cases.gemm())
+@pytest.mark.parametrize("shape", [(256, 256, 256, 64, 64, 32, 2, 2),      # generic tile path
+                                   (256, 256, 512, 128, 128, 64, 2, 2),    # MFMA path, one tile per core
+                                   (512, 256, 256, 128, 128, 64, 2, 1)])   # MFMA path, 2x2 tiles per core
+def test_gemm(shape):
+    ref, out, g = _run(_cases.gemm(*shape))
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
