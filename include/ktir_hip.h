@@ -300,7 +300,7 @@ typedef struct ktir_rmw {
   uint64_t link;           /* int32_t [n_inst * K] scratch */
   uint64_t rows;           /* int32_t [n_inst * K] scratch: destination row of each entry */
   uint64_t srcs;           /* int32_t [n_inst * K] scratch: source row of each entry */
-  uint64_t owners;         /* int32_t [n_inst * K + 1] scratch: owner count, then owner entries */
+  uint64_t owners;         /* int32_t [4 + 4 * n_inst * K] scratch: owner count, then {entry, row, src, -} records */
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
 

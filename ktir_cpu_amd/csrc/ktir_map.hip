@@ -116,6 +116,32 @@ __device__ __forceinline__ void exec_reg4(const ktir_prog_t& P, const ktir_instr
   R.set(in.dst, v);
 }
 
+// One instruction over the 8 elements of a chunk; the opcode switch is
+// taken once (it is uniform), the common ops run as straight loops.
+__device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t in, Reg4 (&R)[8], int64_t lane) {
+  const int op = in.op, dt = in.dt;
+#define EACH(expr)                                                          \
+  _Pragma("unroll") for (int e = 0; e < 8; ++e) {                           \
+    const float x = R[e].get(in.a), y = R[e].get(in.b);                     \
+    (void)x; (void)y;                                                       \
+    R[e].set(in.dst, (expr));                                               \
+  }                                                                         \
+  return;
+  switch (op) {
+    case KTIR_OP_ADDF: EACH(round_to(__fadd_rn(x, y), dt))
+    case KTIR_OP_SUBF: EACH(round_to(__fsub_rn(x, y), dt))
+    case KTIR_OP_MULF: EACH(round_to(__fmul_rn(x, y), dt))
+    case KTIR_OP_DIVF: EACH(round_to(__fdiv_rn(x, y), dt))
+    case KTIR_OP_CAST: EACH(cast_val(x, in.aux, dt))
+    case KTIR_OP_CONST: EACH(__int_as_float(in.imm))
+    case KTIR_OP_EXP: EACH(round_to(expf(x), dt))
+    default: break;
+  }
+#undef EACH
+#pragma unroll
+  for (int e = 0; e < 8; ++e) exec_reg4(P, in, R[e], lane);
+}
+
 template <int DA, int DB, int DO, int NIN>
 __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatDivs D, uint32_t total, int st_leaf) {
   const ktir_leaf_t& LA = P.leaves[P.pf_leaf[0]];
@@ -157,11 +183,7 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
     Reg4 R[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) R[e] = Reg4{a[e], NIN == 2 ? b[e] : 0.f, 0.f, 0.f};
-    for (int pc = 0; pc < n_ops; ++pc) {
-      const ktir_instr_t in = P.instr[pc];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) exec_reg4(P, in, R[e], t);
-    }
+    for (int pc = 0; pc < n_ops; ++pc) exec8(P, P.instr[pc], R, t);
     float out[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[e] = R[e].get(out_reg);

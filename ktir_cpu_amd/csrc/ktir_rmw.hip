@@ -85,7 +85,10 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
       int32_t base = 0;
       if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(&owners[0], __popcll(mask));
       base = __shfl(base, leader);
-      if (own) owners[1 + base + rank] = (int32_t)e;
+      if (own) {
+        int32_t* rec = owners + 4 + 4 * (int64_t)(base + rank);   // {entry, row, src, -}
+        *(int4*)rec = make_int4((int32_t)e, r, ((int32_t*)d.srcs)[e], 0);
+      }
     }
   }
   if (bad) *err = 1;
@@ -113,56 +116,96 @@ __device__ __forceinline__ void apply_src(const ktir_rmw_t& d, int64_t s, int64_
   for (int i = 0; i < 4; ++i) v[i] = combine(d.op, d.order, d.dt, v[i], g[i]);
 }
 
-// One half-wavefront (32 lanes) per owner; each lane covers 4 columns per step.
+// Two owners per half-wavefront (32 lanes x 4 columns cover a 128-wide row
+// per step): the owner records, the chain heads and both rows of both owners
+// are requested before anything is combined.
+__device__ __forceinline__ void load4(const ktir_rmw_t& d, bool dst, int64_t e0, int64_t c, bool vec, float* v) {
+  const uint64_t ptr = dst ? d.dst_ptr : d.src_ptr;
+  const int dt = dst ? d.dst_dtype : d.src_dtype;
+  const int64_t hi = dst ? d.dst_hi : d.src_hi, cs = dst ? d.dst_col : d.src_col;
+  if (vec && e0 >= 0 && e0 + 4 <= hi) {
+    if (dt == KTIR_F16) {
+      uint2 w = *(const uint2*)((const _Float16*)ptr + e0);
+      v[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x & 0xffffu));
+      v[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x >> 16));
+      v[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y & 0xffffu));
+      v[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y >> 16));
+    } else {
+      float4 w = *(const float4*)((const float*)ptr + e0);
+      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+    }
+    return;
+  }
+  for (int i = 0; i < 4; ++i) {
+    int64_t x = e0 + i * cs;
+    v[i] = (c + i < d.D && x >= 0 && x < hi) ? load_elem(ptr, x, dt) : 0.f;
+  }
+}
+
+__device__ __forceinline__ void store4(const ktir_rmw_t& d, int64_t e0, int64_t c, bool vec, const float* v) {
+  if (vec && e0 >= 0 && e0 + 4 <= d.dst_hi) {
+    *(float4*)((float*)d.dst_ptr + e0) = make_float4(v[0], v[1], v[2], v[3]);
+    return;
+  }
+  for (int i = 0; i < 4; ++i) {
+    int64_t x = e0 + i * d.dst_col;
+    if (c + i < d.D && x >= 0 && x < d.dst_hi) store_elem(d.dst_ptr, x, d.dst_dtype, v[i]);
+  }
+}
+
+__device__ __forceinline__ void apply_chain(const ktir_rmw_t& d, int32_t head, int64_t drow, int64_t c, bool vec,
+                                         float* v) {
+  const int32_t* link = (const int32_t*)d.link;
+  const int32_t* srcs = (const int32_t*)d.srcs;
+  int32_t prev = -1;
+  while (true) {
+    int32_t ent = 0x7fffffff;
+    for (int32_t x = head; x >= 0; x = link[x])
+      if (x > prev && x < ent) ent = x;
+    if (ent == 0x7fffffff) break;
+    prev = ent;
+    float g[4];
+    load4(d, false, d.src_base + (int64_t)srcs[ent] * d.src_row + c * d.src_col, c, vec, g);
+    for (int i = 0; i < 4; ++i) v[i] = combine(d.op, d.order, d.dt, v[i], g[i]);
+  }
+}
+
 __global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d) {
   const int32_t* owners = (const int32_t*)d.owners;
   const int32_t n_owners = owners[0];
-  const int32_t* link = (const int32_t*)d.link;
-  const int32_t* rows = (const int32_t*)d.rows;
-  const int32_t* srcs = (const int32_t*)d.srcs;
   const int half = threadIdx.x / 32, hl = threadIdx.x % 32;
   const bool vec = d.dst_col == 1 && d.src_col == 1 && d.dst_dtype == KTIR_F32 &&
                    (d.src_dtype == KTIR_F16 || d.src_dtype == KTIR_F32) &&
                    (d.dst_base % 4 == 0) && (d.dst_row % 4 == 0) && (d.src_base % 4 == 0) && (d.src_row % 4 == 0);
-  for (int64_t o = (int64_t)blockIdx.x * 8 + half; o < n_owners; o += (int64_t)gridDim.x * 8) {
-    const int32_t e = owners[1 + o];
-    const int32_t r = rows[e];
-    const int32_t head = ((const int32_t*)d.head)[r];
-    const int64_t drow = d.dst_base + (int64_t)r * d.dst_row;
+  const int64_t step = (int64_t)gridDim.x * 16;
+  for (int64_t o0 = (int64_t)blockIdx.x * 16 + half * 2; o0 < n_owners; o0 += step) {
+    const bool two = o0 + 1 < n_owners;
+    const int4 ra = *(const int4*)(owners + 4 + 4 * o0);
+    const int4 rb = two ? *(const int4*)(owners + 4 + 4 * (o0 + 1)) : ra;
+    const int32_t ha = ((const int32_t*)d.head)[ra.y];
+    const int32_t hb = ((const int32_t*)d.head)[rb.y];
+    const int64_t da = d.dst_base + (int64_t)ra.y * d.dst_row, db = d.dst_base + (int64_t)rb.y * d.dst_row;
     for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
-      const int64_t de = drow + c * d.dst_col;
-      float v[4];
-      const bool dvec = vec && de >= 0 && de + 4 <= d.dst_hi;
-      if (dvec) {
-        float4 w = *(const float4*)((const float*)d.dst_ptr + de);
-        v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
-      } else {
-        for (int i = 0; i < 4; ++i) {
-          int64_t x = de + i * d.dst_col;
-          v[i] = (c + i < d.D && x >= 0 && x < d.dst_hi) ? load_elem(d.dst_ptr, x, d.dst_dtype) : 0.f;
-        }
+      float va[4], vb[4], ga[4], gb[4];
+      load4(d, true, da + c * d.dst_col, c, vec, va);
+      load4(d, false, d.src_base + (int64_t)ra.z * d.src_row + c * d.src_col, c, vec, ga);
+      if (two) {
+        load4(d, true, db + c * d.dst_col, c, vec, vb);
+        load4(d, false, d.src_base + (int64_t)rb.z * d.src_row + c * d.src_col, c, vec, gb);
       }
-      if (head == e) {
-        apply_src(d, srcs[e], c, v, vec);          // the row's only entry
+      if (ha == ra.x) {   // the row's only entry
+        for (int i = 0; i < 4; ++i) va[i] = combine(d.op, d.order, d.dt, va[i], ga[i]);
       } else {
-        // entries of the chain in ascending order (repeated selection)
-        int32_t prev = -1;
-        while (true) {
-          int32_t ent = 0x7fffffff;
-          for (int32_t x = head; x >= 0; x = link[x])
-            if (x > prev && x < ent) ent = x;
-          if (ent == 0x7fffffff) break;
-          prev = ent;
-          apply_src(d, srcs[ent], c, v, vec);
-        }
+        apply_chain(d, ha, da, c, vec, va);
       }
-      if (dvec) {
-        *(float4*)((float*)d.dst_ptr + de) = make_float4(v[0], v[1], v[2], v[3]);
-      } else {
-        for (int i = 0; i < 4; ++i) {
-          int64_t x = de + i * d.dst_col;
-          if (c + i < d.D && x >= 0 && x < d.dst_hi) store_elem(d.dst_ptr, x, d.dst_dtype, v[i]);
+      store4(d, da + c * d.dst_col, c, vec, va);
+      if (two) {
+        if (hb == rb.x) {
+          for (int i = 0; i < 4; ++i) vb[i] = combine(d.op, d.order, d.dt, vb[i], gb[i]);
+        } else {
+          apply_chain(d, hb, db, c, vec, vb);
         }
+        store4(d, db + c * d.dst_col, c, vec, vb);
       }
     }
   }
@@ -183,7 +226,7 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
   int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());
   int64_t total = d->n_inst * d->K;
-  int64_t blocks = (total + 7) / 8;
+  int64_t blocks = (total + 15) / 16;
   if (blocks > 16384) blocks = 16384;
   hipLaunchKernelGGL(rmw_apply, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
   KTIR_HIP_CHECK(hipGetLastError());

@@ -311,7 +311,7 @@ def _row_rmw(ex, op, lb, st, trips):
     d.n_rows = n_rows
     head = ex.pool.temp(n_rows * 4)
     scratch = [ex.pool.temp(max(1, n_inst * K) * 4) for _ in range(3)]
-    owners = ex.pool.temp((n_inst * K + 1) * 4)
+    owners = ex.pool.temp((4 + 4 * n_inst * K) * 4)
     d.head, d.link, d.rows, d.srcs = head.ptr, scratch[0].ptr, scratch[1].ptr, scratch[2].ptr
     d.owners = owners.ptr
     keep += [head, owners] + scratch

@@ -1,0 +1,117 @@
+"""Host-side logic of the executor that needs no GPU: the cross-lane hazard
+check, view reshapes, lane offsets, and the oracle's pairwise-halving fold."""
+import numpy as np
+import pytest
+
+from ktir_cpu_amd.executor import Access, Alloc, Instances, verify
+from ktir_cpu_amd.program import LaneOff
+from ktir_cpu_amd.walker import _reshape_strides
+
+
+def _acc(alloc, store, inst, base, shape=(2, 2), strides=(8, 1), **kw):
+    return Access(alloc, store, np.asarray(inst, np.int64), np.asarray(base, np.int64), shape, strides, **kw)
+
+
+def test_verify_disjoint_tiles_pass():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(4)
+    # 4 cores each storing its own 2x2 tile of an 8x8 tensor (grid-aligned)
+    acc = [_acc(a, True, [0, 1, 2, 3], [0, 2, 16, 18])]
+    assert verify(acc, ins) is None
+
+
+def test_verify_overlapping_stores_fail():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(2)
+    acc = [_acc(a, True, [0, 1], [0, 0])]
+    assert verify(acc, ins) is not None
+
+
+def test_verify_read_after_write_across_cores_fails():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(2)
+    acc = [_acc(a, True, [0, 1], [0, 2]), _acc(a, False, [0, 1], [2, 0])]
+    assert verify(acc, ins) is not None
+
+
+def test_verify_same_lane_in_place_update_passes():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(2)
+    acc = [_acc(a, False, [0, 1], [0, 2]), _acc(a, True, [0, 1], [0, 2])]
+    assert verify(acc, ins) is None
+
+
+def test_verify_loop_iterations_are_instances():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(1)
+    it = ins.new(np.array([0, 0]))           # two iterations of core 0
+    # both iterations store the same tile: a loop-carried dependence through HBM
+    acc = [_acc(a, True, it, [0, 0])]
+    assert verify(acc, ins) is not None
+    # a core-level access and its own iterations are ordered (ancestor chain)
+    acc = [_acc(a, True, [0], [0]), _acc(a, False, it[:1], [0])]
+    assert verify(acc, ins) is None
+
+
+def test_verify_data_dependent_store_needs_one_lane():
+    a = Alloc("y", "f16", 0x10000, 128, (8, 8))
+    ins = Instances(2)
+    assert verify([_acc(a, True, [0, 1], [0, 0], whole=True)], ins) is not None
+    assert verify([_acc(a, True, [0], [0], whole=True)], ins) is None
+    # an internally ordered fused launch is accepted
+    assert verify([_acc(a, True, [0, 1], [0, 0], whole=True, group=7)], ins) is None
+
+
+@pytest.mark.parametrize("strides,old,new,expect", [
+    ((8192 * 128, 128, 1), (1, 128, 128), (128, 128), (128, 1)),
+    ((4096, 1), (8, 4096), (8 * 4096,), (1,)),
+    ((4096, 1), (8, 16), (128,), None),                 # rows not contiguous
+    ((1,), (128,), (1, 128), (0, 1)),
+    ((64, 1), (4, 64), (2, 2, 64), (128, 64, 1)),
+])
+def test_reshape_strides(strides, old, new, expect):
+    assert _reshape_strides(strides, old, new) == expect
+
+
+def test_lane_offsets_affine_detection():
+    lo = LaneOff.from_array(np.array([4, 12, 20, 28]))
+    assert lo.arr is None and (lo.base, lo.stride) == (4, 8)
+    lo = LaneOff.from_array(np.array([0, 128, 0, 128]))
+    assert lo.arr is not None
+    np.testing.assert_array_equal(lo.take(np.array([1, 3])).values(2), [128, 128])
+
+
+def _tree_fold_reference(x):
+    """Brute-force restatement of pairwise halving with odd-tail carry on a list."""
+    acc = list(x)
+    while len(acc) > 1:
+        half = len(acc) // 2
+        nxt = [acc[i] + acc[i + half] for i in range(half)]
+        if len(acc) % 2:
+            nxt.append(acc[-1])
+        acc = nxt
+    return acc[0]
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 7, 8, 13, 64, 100])
+def test_oracle_tree_fold_order(n):
+    """The oracle's linalg.reduce follows the pairwise-halving order exactly
+    (f16 data, where the order changes the rounding)."""
+    from oracle.interp import OracleInterpreter
+    from ktir_cpu_amd.configs import _tile, _view
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 100).astype(np.float16)
+    src = ("module {\n  func.func @f(%x_ptr: index, %o_ptr: index) attributes {grid = [1, 1]} {\n"
+           + _view("X", "x_ptr", [1, n], [n, 1], "f16") + "\n" + _view("O", "o_ptr", [1], [1], "f16") + "\n"
+           "    %c0 = arith.constant 0 : index\n"
+           + _tile("xt", "X", ["%c0", "%c0"], [1, n], [1, n], "f16") + "\n"
+           + _tile("ot", "O", ["%c0"], [1], [1], "f16") + "\n"
+           f"    %v = ktdp.load %xt : !ktdp.access_tile<1x{n}xindex> -> tensor<1x{n}xf16>\n"
+           "    %z = arith.constant 0.0 : f16\n    %acc = tensor.splat %z : tensor<1xf16>\n"
+           f"    %s = linalg.reduce {{ arith.addf }} ins(%v : tensor<1x{n}xf16>) outs(%acc : tensor<1xf16>) dimensions = [1]\n"
+           "    ktdp.store %s, %ot : tensor<1xf16>, !ktdp.access_tile<1xindex>\n    return\n  }\n}\n")
+    o = OracleInterpreter()
+    o.load(src)
+    out = o.execute_function("f", x_ptr=x, o_ptr=np.zeros(1, np.float16))
+    expect = np.float16(_tree_fold_reference([np.float16(v) for v in x]) + np.float16(0))
+    assert out["o_ptr"][0] == expect
