@@ -304,6 +304,37 @@ typedef struct ktir_rmw {
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
 
+/* ---- fused online-softmax attention loop ----
+ * Replaces a whole KV `scf.for` of the flash-attention form (the reference's
+ * examples/triton-ktir/paged_attention.mlir:191-396 and
+ * notebooks/demo_gen_mlir.py:471-567 build the same loop from these ops):
+ *   S = scale * (Q @ K_j^T), optional causal select(pred(kpos, qpos), S, neg),
+ *   m' = max(m, rowmax S), P = exp(S - m'), alpha = exp(m - m'),
+ *   acc' = acc * alpha + P @ V_j,  l' = l * alpha + rowsum P
+ * with loop-carried f32 m, l (per row) and acc.  One lane = one query block
+ * of M rows; lane l runs trips[l] iterations, the K tile of iteration j
+ * starts at k_base[l] + j * k_step (V: v_base[l] + j * v_step).  M = N = D = 128, bf16 or f16
+ * Q/K/V, MFMA with f32 accumulation; P enters the P @ V product as a
+ * hi + lo pair of operand-type values (about 16 significant bits). */
+typedef struct ktir_attn {
+  int64_t lanes, M, N, D;
+  uint64_t q_ptr, k_ptr, v_ptr;        /* element 0 of each tensor */
+  uint64_t q_base, k_base, v_base;     /* const int64_t* [lanes] element offsets (iteration 0 for k, v) */
+  int64_t q_row, k_row, v_row;         /* row strides in elements (column stride 1) */
+  int64_t k_step, v_step;              /* element offset per iteration */
+  uint64_t trips;                      /* const int32_t* [lanes] */
+  uint64_t order;                      /* const int32_t* [lanes]: workgroup -> lane, or 0 */
+  uint64_t qpos0;                      /* const int64_t* [lanes]: position of query row 0 */
+  uint64_t kpos0;                      /* const int64_t* [lanes]: position of key 0 at iteration 0 */
+  int64_t kpos_step;                   /* key position increment per iteration */
+  float scale, neg;                    /* S multiplier; value of masked scores */
+  int32_t causal, pred;                /* mask on (KTIR_CMP_* predicate keep = pred(kpos, qpos)) */
+  int32_t dtype;                       /* KTIR_BF16 or KTIR_F16 */
+  int32_t pad;
+  uint64_t m_out, l_out, acc_out;      /* f32 [lanes, M], [lanes, M], [lanes, M, D] final state */
+} ktir_attn_t;
+int ktir_launch_attention(const ktir_attn_t* d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -308,23 +308,44 @@ def gemm(M: int = 8192, N: int = 8192, K: int = 8192, bm: int = 128, bn: int = 1
 # 5. Flash attention (causal)
 # ---------------------------------------------------------------------------
 
-def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: int = 128) -> str:
+_FA_MASK = """      %sm_init = tensor.empty() : {Sf}
+      %sm = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>],
+                            iterator_types = ["parallel", "parallel"]}}
+          ins(%s : {Sf}) outs(%sm_init : {Sf}) {{
+        ^bb0(%sv: f32, %out: f32):
+          %row = linalg.index 0 : index
+          %col = linalg.index 1 : index
+          %qpos = arith.addi %q0, %row : index
+          %kpos = arith.addi %k0, %col : index
+          %keep = arith.cmpi ule, %kpos, %qpos : index
+          %r = arith.select %keep, %sv, %neg_inf : f32
+          linalg.yield %r : f32
+      }} -> {Sf}
+"""
+
+
+def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: int = 128, dt: str = "bf16",
+                    causal: bool = True) -> str:
     """O = softmax(Q K^T * scale, causal) V with online softmax over KV tiles.
 
     Grid [S/blk, H, B]; core (qb, h, b) owns query rows [qb*blk, (qb+1)*blk)
-    of head (b, h) and visits KV tiles 0..qb (the causal prefix).
+    of head (b, h) and visits KV tiles 0..qb (the causal prefix), or all
+    S/blk tiles when `causal` is False.
     """
     nq = S // blk
     shp = [B, H, S, D]
     strides = [H * S * D, S * D, D, 1]
-    T4 = _t([1, 1, blk, D], "bf16")
-    Tb, Tf = _t([blk, D], "bf16"), _t([blk, D], "f32")
+    T4 = _t([1, 1, blk, D], dt)
+    Tb, Tf = _t([blk, D], dt), _t([blk, D], "f32")
     Sf = _t([blk, blk], "f32")
     Vf = _t([blk], "f32")
     at = f"!ktdp.access_tile<1x1x{blk}x{D}xindex>"
+    n_kv = "arith.addi %qb, %c1 : index" if causal else f"arith.constant {nq} : index"
+    sm = "%sm" if causal else "%s"
+    mask = _FA_MASK.format(Sf=Sf) if causal else ""
 
     def tile(name, view, row):
-        return _tile(name, view, ["%b", "%h", row, "%c0"], [1, 1, blk, D], shp, "bf16", "      ")
+        return _tile(name, view, ["%b", "%h", row, "%c0"], [1, 1, blk, D], shp, dt, "      ")
 
     return f"""module {{
   func.func @flash_attention(%q_ptr: index, %k_ptr: index, %v_ptr: index, %o_ptr: index, %scale: f32)
@@ -335,12 +356,12 @@ def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: i
     %BLK = arith.constant {blk} : index
     %zero = arith.constant 0.0 : f32
     %neg_inf = arith.constant 0xFF800000 : f32
-{_view("q_view", "q_ptr", shp, strides, "bf16")}
-{_view("k_view", "k_ptr", shp, strides, "bf16")}
-{_view("v_view", "v_ptr", shp, strides, "bf16")}
-{_view("o_view", "o_ptr", shp, strides, "bf16")}
+{_view("q_view", "q_ptr", shp, strides, dt)}
+{_view("k_view", "k_ptr", shp, strides, dt)}
+{_view("v_view", "v_ptr", shp, strides, dt)}
+{_view("o_view", "o_ptr", shp, strides, dt)}
     %q0 = arith.muli %qb, %BLK : index
-{_tile("q_acc", "q_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, "bf16")}
+{_tile("q_acc", "q_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, dt)}
     %q4 = ktdp.load %q_acc : {at} -> {T4}
     %q2 = tensor.collapse_shape %q4 [[0, 1, 2], [3]] : {T4} into {Tb}
     %q = arith.extf %q2 : {Tb} to {Tf}
@@ -348,7 +369,7 @@ def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: i
     %m_init = tensor.splat %neg_inf : {Vf}
     %l_init = tensor.splat %zero : {Vf}
     %acc_init = tensor.splat %zero : {Tf}
-    %n_kv = arith.addi %qb, %c1 : index
+    %n_kv = {n_kv}
     %m_f, %l_f, %acc_f = scf.for %j = %c0 to %n_kv step %c1
         iter_args(%m = %m_init, %l = %l_init, %acc = %acc_init) -> ({Vf}, {Vf}, {Tf}) {{
       %k0 = arith.muli %j, %BLK : index
@@ -365,27 +386,14 @@ def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: i
       %s_init = tensor.splat %zero : {Sf}
       %qk = linalg.matmul ins(%q, %kt : {Tf}, {_t([D, blk], "f32")}) outs(%s_init : {Sf}) -> {Sf}
       %s = arith.mulf %scale_t, %qk : {Sf}
-      %sm_init = tensor.empty() : {Sf}
-      %sm = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>],
-                            iterator_types = ["parallel", "parallel"]}}
-          ins(%s : {Sf}) outs(%sm_init : {Sf}) {{
-        ^bb0(%sv: f32, %out: f32):
-          %row = linalg.index 0 : index
-          %col = linalg.index 1 : index
-          %qpos = arith.addi %q0, %row : index
-          %kpos = arith.addi %k0, %col : index
-          %keep = arith.cmpi ule, %kpos, %qpos : index
-          %r = arith.select %keep, %sv, %neg_inf : f32
-          linalg.yield %r : f32
-      }} -> {Sf}
-      %rm_init = tensor.splat %neg_inf : {Vf}
-      %rm = linalg.reduce {{ arith.maximumf }} ins(%sm : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
+{mask}      %rm_init = tensor.splat %neg_inf : {Vf}
+      %rm = linalg.reduce {{ arith.maximumf }} ins({sm} : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
       %m_new = arith.maximumf %m, %rm : {Vf}
       %p_init = tensor.empty() : {Sf}
       %p = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0)>,
                                             affine_map<(d0, d1) -> (d0, d1)>],
                            iterator_types = ["parallel", "parallel"]}}
-          ins(%sm, %m_new : {Sf}, {Vf}) outs(%p_init : {Sf}) {{
+          ins({sm}, %m_new : {Sf}, {Vf}) outs(%p_init : {Sf}) {{
         ^bb0(%sv: f32, %mv: f32, %out: f32):
           %dd = arith.subf %sv, %mv : f32
           %ee = math.exp %dd : f32
@@ -420,7 +428,7 @@ def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: i
     }} -> {Tf}
     %ob = arith.truncf %of : {Tf} to {Tb}
     %o4 = tensor.expand_shape %ob [[0, 1, 2], [3]] output_shape [1, 1, {blk}, {D}] : {Tb} into {T4}
-{_tile("o_acc", "o_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, "bf16")}
+{_tile("o_acc", "o_view", ["%b", "%h", "%q0", "%c0"], [1, 1, blk, D], shp, dt)}
     ktdp.store %o4, %o_acc : {T4}, {at}
     return
   }}

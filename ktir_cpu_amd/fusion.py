@@ -7,6 +7,10 @@
   and ``notebooks/demo_gen_mlir.py:139-152``).  The reference runs one
   `np.matmul` per iteration (``dialects/linalg_ops.py:325-347``); here the
   loop becomes the K dimension of one batched matmul launch.
+* Ordered indirect row read-modify-write: a loop of row gathers combined into
+  row scatters (``tests/test_indirect_access.py:405-441`` collision order).
+* Online-softmax attention: the flash-attention KV loop with loop-carried
+  (m, l, acc) becomes one fused MFMA kernel.
 """
 
 from __future__ import annotations
@@ -30,6 +34,8 @@ def try_fuse_loop(ex, op, lb, st, trips, inits) -> Optional[List]:
         return _kloop_matmul(ex, op, lb, st, trips, inits[0])
     if not names:
         return _row_rmw(ex, op, lb, st, trips)
+    if len(names) == 3:
+        return _attention_loop(ex, op, lb, st, trips, inits)
     return None
 
 
@@ -322,3 +328,458 @@ def _row_rmw(ex, op, lb, st, trips):
     ex.log(ia_d, False, z, (1,), (1,), whole=True, group=grp)
     ex.launch("rmw", d, keep)
     return []
+
+
+# ---------------------------------------------------------------------------
+# online-softmax attention loop (flash attention over KV tiles)
+# ---------------------------------------------------------------------------
+
+_EW_BIN = {"arith.addf", "arith.subf", "arith.mulf", "arith.divf", "arith.maximumf", "arith.minimumf"}
+_EW_UN = {"math.exp"}
+_COMM = {"arith.addf", "arith.mulf", "arith.maximumf", "arith.minimumf"}
+_SWAP = {"EQ": "EQ", "NE": "NE", "SLT": "SGT", "SGT": "SLT", "SLE": "SGE", "SGE": "SLE",
+         "ULTI": "UGTI", "UGTI": "ULTI", "ULEI": "UGEI", "UGEI": "ULEI"}
+_NOT = {"EQ": "NE", "NE": "EQ", "SLT": "SGE", "SGE": "SLT", "SLE": "SGT", "SGT": "SLE",
+        "ULTI": "UGEI", "UGEI": "ULTI", "ULEI": "UGTI", "UGTI": "ULEI"}
+
+
+def _is_tensor(op) -> bool:
+    t = op.result_types[0] if op.result_types else None
+    return getattr(t, "kind", None) == "tensor"
+
+
+class _Norm:
+    """Elementwise normal form of loop-body values.
+
+    Tensor-level arith/math ops and all-parallel ``linalg.generic`` ops whose
+    bodies are built from the same ops normalise to one tree form, so the two
+    spellings of the online-softmax update (whole-tensor ops as in the
+    reference's ``notebooks/demo_gen_mlir.py:471-567`` and generics as in
+    ``examples/triton-ktir/paged_attention.mlir:273-392``) match alike.
+    ``("v", name)`` is an opaque value, ``("bc", t)`` broadcasts a row vector
+    along the columns, ``("red", fn, t)`` reduces the columns of t,
+    ``("mask", name)`` is a position-mask generic."""
+
+    def __init__(self, body):
+        self.by_res = {r: o for o in body for r in o.results}
+        self.used = set()
+        self.reduce_inits = []       # (combiner, init SSA name)
+        self.masks = {}
+
+    @staticmethod
+    def mk(op, *args):
+        if op in _COMM:
+            args = tuple(sorted(args, key=repr))
+        return (op,) + tuple(args)
+
+    def __call__(self, name):
+        o = self.by_res.get(name)
+        if o is None:
+            return ("v", name)
+        t = o.op_type
+        if t in _EW_BIN and len(o.operands) == 2 and _is_tensor(o):
+            self.used.add(id(o))
+            return self.mk(t, self(o.operands[0]), self(o.operands[1]))
+        if t in _EW_UN and len(o.operands) == 1 and _is_tensor(o):
+            self.used.add(id(o))
+            return self.mk(t, self(o.operands[0]))
+        if t == "linalg.reduce" and o.attributes.get("n_ins") == 1 and list(o.attributes.get("dimensions", [])) == [1] \
+                and o.attributes.get("reduce_fn") in ("arith.maximumf", "arith.addf") and len(o.operands) == 2:
+            self.used.add(id(o))
+            self.reduce_inits.append((o.attributes["reduce_fn"], o.operands[1]))
+            return ("red", o.attributes["reduce_fn"], self(o.operands[0]))
+        if t == "linalg.generic":
+            g = self._generic(o)
+            if g is not None:
+                self.used.add(id(o))
+                return g
+        return ("v", name)
+
+    def _generic(self, o):
+        a = o.attributes
+        n_ins = a.get("n_ins", 0)
+        maps = a.get("indexing_maps", [])
+        if any(x != "parallel" for x in a.get("iterator_types") or []) or len(maps) != n_ins + 1:
+            return None
+        region = o.regions[0]
+        args = [n for n, _ in region.args]
+        if len(args) != n_ins + 1:
+            return None
+        nd = maps[-1].n_dims
+        ident = tuple(("dim", i) for i in range(nd))
+        if tuple(maps[-1].exprs) != ident:
+            return None
+        ops = region.ops
+        if any(x.op_type == "linalg.index" for x in ops):
+            if n_ins == 1 and tuple(maps[0].exprs) == ident and nd == 2:
+                self.masks[o.results[0]] = o
+                return ("mask", o.results[0])
+            return None
+        env = {}
+        for i in range(n_ins):
+            ex = tuple(maps[i].exprs)
+            if ex == ident:
+                env[args[i]] = self(o.operands[i])
+            elif nd == 2 and ex == (("dim", 0),):
+                env[args[i]] = ("bc", self(o.operands[i]))
+            else:
+                return None
+        for x in ops:
+            if x.op_type == "linalg.yield":
+                return env.get(x.operands[0]) if len(x.operands) == 1 else None
+            if any(n not in env for n in x.operands):
+                return None
+            if x.op_type in _EW_BIN and len(x.operands) == 2:
+                env[x.results[0]] = self.mk(x.op_type, env[x.operands[0]], env[x.operands[1]])
+            elif x.op_type in _EW_UN and len(x.operands) == 1:
+                env[x.results[0]] = self.mk(x.op_type, env[x.operands[0]])
+            else:
+                return None
+        return None
+
+
+def _peel(by_res, name):
+    """Follow extf / collapse_shape / transpose back to a ktdp.load."""
+    ops, n_tr, ext = [], 0, False
+    while True:
+        o = by_res.get(name)
+        if o is None:
+            return None
+        ops.append(o)
+        t = o.op_type
+        if t == "ktdp.load":
+            return o, ops, n_tr, ext
+        if t == "arith.extf":
+            ext = True
+        elif t == "tensor.collapse_shape":
+            pass
+        elif t == "linalg.transpose":
+            if list(o.attributes.get("permutation", [])) != [1, 0]:
+                return None
+            n_tr += 1
+        else:
+            return None
+        name = o.operands[0]
+
+
+def _mask_lin(ex, mask_op, L):
+    """Evaluate a causal-mask generic body on the host.
+
+    Index values are kept as ``c[lane] + a*row + b*col``; the body must be
+    ``select(cmpi(pred, kpos, qpos), s, neg)`` (either operand order of the
+    compare and of the select) with kpos = c_k + col and qpos = c_q + row.
+    Returns (pred, c_k, c_q, neg) or None."""
+    region = mask_op.regions[0]
+    sv = region.args[0][0]
+    env = {}
+
+    def val(n):
+        if n in env:
+            return env[n]
+        v = ex.get_value(n, peek=True)
+        if isinstance(v, Tile) or v is None:
+            raise NeedEager("mask operand")
+        arr = np.broadcast_to(np.asarray(v), (L,))
+        if not np.issubdtype(arr.dtype, np.integer):
+            raise NeedEager("mask operand")
+        return (arr.astype(np.int64), 0, 0)
+
+    cmp = None
+    try:
+        for x in region.ops:
+            t, r = x.op_type, (x.results[0] if x.results else None)
+            if t == "linalg.index":
+                env[r] = (np.zeros(L, np.int64), 1, 0) if x.attributes.get("dim") == 0 else (np.zeros(L, np.int64), 0, 1)
+            elif t == "arith.constant" and isinstance(x.attributes.get("value"), int) \
+                    and not isinstance(x.attributes.get("value"), bool):
+                env[r] = (np.full(L, x.attributes["value"], np.int64), 0, 0)
+            elif t in ("arith.addi", "arith.subi"):
+                a, b = val(x.operands[0]), val(x.operands[1])
+                sg = 1 if t == "arith.addi" else -1
+                env[r] = (a[0] + sg * b[0], a[1] + sg * b[1], a[2] + sg * b[2])
+            elif t == "arith.muli":
+                a, b = val(x.operands[0]), val(x.operands[1])
+                if a[1] == 0 and a[2] == 0 and np.all(a[0] == a[0][0]):
+                    a, b = b, a
+                if b[1] != 0 or b[2] != 0 or not np.all(b[0] == b[0][0]):
+                    return None
+                k = int(b[0][0])
+                env[r] = (a[0] * k, a[1] * k, a[2] * k)
+            elif t in ("arith.index_cast", "arith.index_castui"):
+                env[r] = val(x.operands[0])
+            elif t == "arith.cmpi":
+                from .walker import CMPI
+                p = CMPI.get(x.attributes.get("predicate"))
+                if p is None or cmp is not None:
+                    return None
+                a, b = val(x.operands[0]), val(x.operands[1])
+                cmp = (r, p, a, b)
+            elif t == "arith.select":
+                if cmp is None or x.operands[0] != cmp[0]:
+                    return None
+                _, p, a, b = cmp
+                if (a[1], a[2], b[1], b[2]) == (0, 1, 1, 0):
+                    kp, qp = a, b
+                elif (a[1], a[2], b[1], b[2]) == (1, 0, 0, 1):
+                    kp, qp, p = b, a, _SWAP[p]
+                else:
+                    return None
+                if x.operands[1] == sv:
+                    neg_n = x.operands[2]
+                elif x.operands[2] == sv:
+                    neg_n, p = x.operands[1], _NOT[p]
+                else:
+                    return None
+                nv = np.asarray(ex.get_value(neg_n, peek=True), dtype=np.float64).ravel()
+                if nv.size == 0 or np.any(nv != nv[0]) and not np.all(np.isnan(nv)):
+                    return None
+                env[r] = ("sel", p, kp[0], qp[0], float(nv[0]))
+            elif t == "linalg.yield":
+                y = env.get(x.operands[0]) if len(x.operands) == 1 else None
+                if not isinstance(y, tuple) or y[0] != "sel":
+                    return None
+                return y[1:]
+            else:
+                return None
+    except (NeedEager, KeyError):
+        return None
+    return None
+
+
+def _splat_value(ex, name):
+    v = ex.get_value(name, peek=True)
+    if not isinstance(v, Tile) or v.e.kind != "const":
+        return None
+    return float(v.e.attr)
+
+
+def _attention_loop(ex, op, lb, st, trips, inits):
+    """Fuse the online-softmax KV loop of flash attention into one launch
+    (``ktir_launch_attention``).  The reference executes it op by op
+    (``dialects/linalg_ops.py:325-347`` matmuls, ``:400-596`` generics and
+    reductions, ``dialects/math_ops.py`` exp) once per core and iteration."""
+    from . import runtime as rt
+    from .program import LeafSpec, LaneOff, Expr
+    body = op.regions[0].ops
+    names = op.attributes["iter_args"]
+    if not body or body[-1].op_type != "scf.yield" or len(body[-1].operands) != 3:
+        return None
+    nz = _Norm(body)
+    by_res = nz.by_res
+    ys = body[-1].operands
+    ia = [i for i, y in enumerate(ys) if y in by_res and by_res[y].op_type == "linalg.matmul"]
+    if len(ia) != 1:
+        return None
+    ia = ia[0]
+    mm2 = by_res[ys[ia]]
+    if len(mm2.operands) != 3 or mm2.attributes.get("n_ins") != 2:
+        return None
+    p_name, vf_name, accs_name = mm2.operands
+    rest = [i for i in range(3) if i != ia]
+    tm = None
+    for im in rest:
+        t = nz(ys[im])
+        if t[0] == "arith.maximumf" and ("v", names[im]) in t[1:]:
+            tm = t
+            break
+    if tm is None:
+        return None
+    il = rest[0] if im == rest[1] else rest[1]
+    m_arg, l_arg, acc_arg = names[im], names[il], names[ia]
+    red = tm[2] if tm[1] == ("v", m_arg) else tm[1]
+    if red[0] != "red" or red[1] != "arith.maximumf":
+        return None
+    X = red[2]
+    mk = nz.mk
+    p_tree = mk("math.exp", mk("arith.subf", X, ("bc", tm)))
+    alpha = mk("math.exp", mk("arith.subf", ("v", m_arg), tm))
+    if nz(p_name) != p_tree or nz(accs_name) != mk("arith.mulf", ("v", acc_arg), ("bc", alpha)):
+        return None
+    if nz(ys[il]) != mk("arith.addf", mk("arith.mulf", ("v", l_arg), alpha), ("red", "arith.addf", p_tree)):
+        return None
+    mask_op = None
+    s_tree = X
+    if X[0] == "mask":
+        mask_op = nz.masks[X[1]]
+        s_tree = nz(mask_op.operands[0])
+    scale_n = None
+    if s_tree[0] == "v":
+        qk = s_tree[1]
+    elif s_tree[0] == "arith.mulf" and s_tree[1][0] == "v" and s_tree[2][0] == "v":
+        a, b = s_tree[1][1], s_tree[2][1]
+        if a in by_res and by_res[a].op_type == "linalg.matmul":
+            qk, scale_n = a, b
+        else:
+            qk, scale_n = b, a
+    else:
+        return None
+    mm1 = by_res.get(qk)
+    if mm1 is None or mm1.op_type != "linalg.matmul" or len(mm1.operands) != 3 or mm1.attributes.get("n_ins") != 2:
+        return None
+    q_name, kt_name, s_init = mm1.operands
+    if q_name in by_res:
+        return None
+    pk, pv = _peel(by_res, kt_name), _peel(by_res, vf_name)
+    if pk is None or pv is None or pk[2] != 1 or pv[2] != 0 or not pk[3] or not pv[3]:
+        return None
+    matched = set(nz.used) | {id(mm1), id(mm2), id(body[-1])} | {id(o) for o in pk[1] + pv[1]}
+    if mask_op is not None:
+        matched.add(id(mask_op))
+    uses = {}
+    for o in body:
+        for n in o.operands:
+            uses.setdefault(n, []).append(o)
+    for o in body:
+        if id(o) in matched:
+            continue
+        if o.op_type in ("ktdp.construct_access_tile", "tensor.empty", "tensor.splat", "arith.constant") \
+                or (o.op_type.startswith("arith.") and not o.regions and not _is_tensor(o)):
+            continue
+        return None
+    # every intermediate feeds only matched ops (no escaping values)
+    for o in body:
+        if id(o) in matched and o is not body[-1]:
+            for r in o.results:
+                if any(id(u) not in matched for u in uses.get(r, [])):
+                    return None
+    L = ex.L
+    if L == 0:
+        return None
+    # initial state: m = -inf, l = 0, acc = 0
+    def const_of(v):
+        return float(v.e.attr) if isinstance(v, Tile) and v.e.kind == "const" else None
+    if const_of(inits[im]) != -np.inf or const_of(inits[il]) != 0.0 or const_of(inits[ia]) != 0.0:
+        return None
+    q = ex.get_value(q_name, peek=True)
+    if not isinstance(q, Tile):
+        return None
+    qe = q.e
+    if not (qe.kind == "cast" and qe.dtype == "f32" and qe.attr in ("f16", "bf16") and qe.args[0].kind == "ld"
+            and qe.args[0].attr.offsets is None):
+        return None
+    q_leaf = qe.args[0].attr
+    AT = 128
+    if tuple(q.shape) != (AT, AT) or len(q_leaf.strides) < 2 or q_leaf.strides[-1] != 1 \
+            or any(s != 0 for s in q_leaf.strides[:-2]):
+        return None
+    dtype = q_leaf.dtype
+    probe = [o for o in body if id(o) not in matched]
+    iv = op.attributes["iter_var"]
+    k_ld, v_ld = pk[0], pv[0]
+
+    def at(j):
+        ex.push_scope()
+        try:
+            ex.set_value(iv, lb + j * st)
+            for o in probe:
+                ex._exec(o)
+            out = {"k": ex.get_value(k_ld.operands[0], peek=True), "v": ex.get_value(v_ld.operands[0], peek=True)}
+            out["inits"] = [(fn, _splat_value(ex, n)) for fn, n in nz.reduce_inits]
+            out["s_init"] = _splat_value(ex, s_init)
+            out["scale"] = _splat_value(ex, scale_n) if scale_n is not None else 1.0
+            out["mask"] = _mask_lin(ex, mask_op, L) if mask_op is not None else None
+            return out
+        finally:
+            ex.pop_scope()
+
+    tm1 = np.maximum(trips - 1, 0)
+    try:
+        p0 = at(np.zeros(L, np.int64))
+        p1 = at(np.ones(L, np.int64))
+        pl = at(tm1)
+    except NeedEager:
+        return None
+    for fn, v in p0["inits"]:
+        if v != (-np.inf if fn == "arith.maximumf" else 0.0):
+            return None
+    if p0["s_init"] != 0.0 or p0["scale"] is None:
+        return None
+    if mask_op is not None:
+        if p0["mask"] is None or p1["mask"] is None or pl["mask"] is None:
+            return None
+        pred, ck0, cq0, neg = p0["mask"]
+        _, ck1, cq1, _ = p1["mask"]
+        _, ckl, cql, _ = pl["mask"]
+        kstep = ck1 - ck0
+        if np.any(kstep != kstep[0]) or not np.array_equal(cq0, cq1) or not np.array_equal(cq0, cql) \
+                or not np.array_equal(ckl, ck0 + tm1 * kstep[0]):
+            return None
+        kpos_step = int(kstep[0])
+    else:
+        pred, ck0, cq0, neg, kpos_step = "EQ", np.zeros(L, np.int64), np.zeros(L, np.int64), 0.0, 0
+    # K and V tiles: base offsets at iteration 0, uniform step, in bounds for every iteration run
+    tiles = {}
+    for key, ld in (("k", k_ld), ("v", v_ld)):
+        a0, a1, al = p0[key], p1[key], pl[key]
+        if not all(isinstance(x, ATile) for x in (a0, a1, al)):
+            return None
+        if not isinstance(a0.cs, Box) or a0.co is not None:
+            return None
+        if not (np.array_equal(a0.view.base, a1.view.base) and np.array_equal(a0.view.base, al.view.base)):
+            return None
+        d = a1.origin - a0.origin
+        if np.any(d != d.flat[0]) or not np.array_equal(al.origin, a0.origin + tm1 * d.flat[0]):
+            return None
+        v = a0.view
+        if v.dtype != dtype:
+            return None
+        ext = tuple(a0.cs.extent)
+        big = [i for i, e in enumerate(ext) if e != 1]
+        if len(big) != 2 or ext[big[0]] != AT or ext[big[1]] != AT or v.strides[big[1]] != 1:
+            return None
+        lo_off = sum(int(l) * int(s) for l, s in zip(a0.cs.lo, v.strides))
+        spec, alloc, rel = ex._hbm_leaf(v, a0.origin + lo_off, ext, v.strides)
+        row, step = int(v.strides[big[0]]), int(d.flat[0])
+        run = trips > 0
+        lo = rel + np.minimum(0, tm1 * step)
+        hi = rel + np.maximum(0, tm1 * step) + (AT - 1) * row + AT - 1
+        if np.any(run & ((lo < 0) | (hi >= alloc.n_elems) | (rel % 8 != 0))) or row % 8 or step % 8 or row < AT:
+            return None
+        tiles[key] = (alloc, rel, row, step)
+    q_off = q_leaf.lane.values(L)
+    q_row = int(q_leaf.strides[-2])
+    run = trips > 0
+    if np.any(run & ((q_off < q_leaf.lo) | (q_off + (AT - 1) * q_row + AT - 1 >= q_leaf.hi) | (q_off % 8 != 0))) \
+            or q_row % 8 or q_row < AT:
+        return None
+    # launch
+    d = rt.ATTN()
+    d.lanes, d.M, d.N, d.D = L, AT, AT, AT
+    keep = []
+
+    def up(arr):
+        b = ex.pool.upload(np.ascontiguousarray(arr))
+        keep.append(b)
+        return b.ptr
+
+    d.q_ptr = q_leaf.ptr
+    d.k_ptr, d.v_ptr = ex.arena.ptr_of(tiles["k"][0]), ex.arena.ptr_of(tiles["v"][0])
+    d.q_base = up(q_off.astype(np.int64))
+    d.k_base, d.v_base = up(tiles["k"][1].astype(np.int64)), up(tiles["v"][1].astype(np.int64))
+    d.q_row, d.k_row, d.v_row = q_row, tiles["k"][2], tiles["v"][2]
+    d.k_step, d.v_step = tiles["k"][3], tiles["v"][3]
+    d.trips = up(trips.astype(np.int32))
+    d.order = up(np.argsort(-trips, kind="stable").astype(np.int32))
+    d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
+    d.kpos_step = kpos_step
+    d.scale, d.neg = p0["scale"], neg
+    d.causal = 1 if mask_op is not None else 0
+    d.pred = rt.K["KTIR_CMP_" + pred]
+    d.dtype = rt.DTYPE_CODE[dtype]
+    m_buf = ex.pool.temp(L * AT * 4)
+    l_buf = ex.pool.temp(L * AT * 4)
+    a_buf = ex.pool.temp(L * AT * AT * 4)
+    d.m_out, d.l_out, d.acc_out = m_buf.ptr, l_buf.ptr, a_buf.ptr
+    keep += [m_buf, l_buf, a_buf, q_leaf]
+    tmax = max(int(trips.max()), 1)
+    for key in ("k", "v"):
+        alloc, rel, row, step = tiles[key]
+        ex.log(alloc, False, rel, (tmax, AT, AT), (step, row, 1))
+    ex.launch("attn", d, keep)
+    vec = lambda b: Tile(Expr("ld", "f32", (AT,), attr=LeafSpec(b.ptr, "f32", LaneOff(0, AT), (1,), 0, L * AT,
+                                                                  keep=(b,))))
+    res = [None, None, None]
+    res[im], res[il] = vec(m_buf), vec(l_buf)
+    res[ia] = Tile(Expr("ld", "f32", (AT, AT), attr=LeafSpec(a_buf.ptr, "f32", LaneOff(0, AT * AT), (AT, 1), 0,
+                                                               L * AT * AT, keep=(a_buf,))))
+    return res

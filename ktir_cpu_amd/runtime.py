@@ -103,6 +103,18 @@ class RMW(C.Structure):
                 ("owners", C.c_uint64)]
 
 
+class ATTN(C.Structure):
+    _fields_ = [("lanes", C.c_int64), ("M", C.c_int64), ("N", C.c_int64), ("D", C.c_int64),
+                ("q_ptr", C.c_uint64), ("k_ptr", C.c_uint64), ("v_ptr", C.c_uint64),
+                ("q_base", C.c_uint64), ("k_base", C.c_uint64), ("v_base", C.c_uint64),
+                ("q_row", C.c_int64), ("k_row", C.c_int64), ("v_row", C.c_int64),
+                ("k_step", C.c_int64), ("v_step", C.c_int64), ("trips", C.c_uint64), ("order", C.c_uint64),
+                ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64),
+                ("scale", C.c_float), ("neg", C.c_float), ("causal", C.c_int32), ("pred", C.c_int32),
+                ("dtype", C.c_int32), ("pad", C.c_int32),
+                ("m_out", C.c_uint64), ("l_out", C.c_uint64), ("acc_out", C.c_uint64)]
+
+
 class KTIRDeviceError(RuntimeError):
     pass
 
@@ -127,7 +139,7 @@ def lib():
                      "ktir_launch_program", "ktir_scatter_winners", "ktir_iat_offsets",
                      "ktir_launch_matmul", "ktir_event_create", "ktir_event_record",
                      "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info",
-                     "ktir_launch_row_rmw"):
+                     "ktir_launch_row_rmw", "ktir_launch_attention"):
             getattr(L, name).restype = C.c_int
         L.ktir_malloc.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.ktir_free.argtypes = [C.c_uint64]
@@ -140,6 +152,7 @@ def lib():
         L.ktir_iat_offsets.argtypes = [C.POINTER(IAT)]
         L.ktir_launch_matmul.argtypes = [C.POINTER(MM)]
         L.ktir_launch_row_rmw.argtypes = [C.POINTER(RMW)]
+        L.ktir_launch_attention.argtypes = [C.POINTER(ATTN)]
         L.ktir_event_create.argtypes = [C.POINTER(C.c_uint64)]
         L.ktir_event_record.argtypes = [C.c_uint64]
         L.ktir_event_elapsed_ms.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_float)]

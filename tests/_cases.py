@@ -49,8 +49,11 @@ def gemm(M=256, N=256, K=256, bm=64, bn=64, bk=32, gm=2, gn=2, seed=42):
             dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16)))
 
 
-def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42):
+def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42, dt="bf16", causal=True):
     rng = np.random.default_rng(seed)
-    q, k, v = (bf16_bits(rng.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
-    return (configs.flash_attention(B, H, S, D, blk), "flash_attention",
+    if dt == "bf16":
+        q, k, v = (bf16_bits(rng.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    else:
+        q, k, v = (rng.standard_normal((B, H, S, D)).astype(np.float16) for _ in range(3))
+    return (configs.flash_attention(B, H, S, D, blk, dt=dt, causal=causal), "flash_attention",
             dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D)))

@@ -70,6 +70,22 @@ def test_gemm(shape):
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
-def test_flash_attention():
-    ref, out, _ = _run(_cases.flash_attention())
-    np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-2)
+def test_flash_attention_generic_path():
+    """D = 32, 64-row blocks: not the fused kernel's shape, op-by-op launches."""
+    ref, out, g = _run(_cases.flash_attention())
+    assert "attn" not in g.last_plan.counts()
+    np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("args", [dict(S=512, D=128, blk=128),
+                                  dict(S=512, D=128, blk=128, dt="f16"),
+                                  dict(B=2, H=2, S=384, D=128, blk=128, causal=False),
+                                  dict(B=1, H=3, S=1024, D=128, blk=128, seed=3)])
+def test_flash_attention_fused(args):
+    """The whole KV loop in one fused MFMA launch (causal and full, bf16 and f16)."""
+    ref, out, g = _run(_cases.flash_attention(**args))
+    assert g.last_plan.counts().get("attn") == 1
+    f = bf16_from_bits if args.get("dt", "bf16") == "bf16" else (lambda x: x.astype(np.float32))
+    np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+    for k in ("q_ptr", "k_ptr", "v_ptr"):
+        np.testing.assert_array_equal(out[k], ref[k])
