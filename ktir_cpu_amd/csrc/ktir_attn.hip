@@ -38,19 +38,23 @@ __device__ __forceinline__ f32x16_t mfma_at(const uint4& a, const uint4& b, f32x
                                                   0, 0, 0);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// (a, b) rounded to nearest-even in the operand type, packed low/high
 template <bool BF16>
-__device__ __forceinline__ float to_op(float a) {   // value of a rounded to the operand type
-  if constexpr (BF16) return round_bf16(a);
-  else return (float)(_Float16)a;
+__device__ __forceinline__ uint32_t cvt2(float a, float b) {
+  const f32x2_t v = {a, b};
+  if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
 }
 
+// the two operand-type values of a packed word, back in f32
 template <bool BF16>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {   // a, b already representable
-  if constexpr (BF16) {
-    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
-  } else {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
-  }
+__device__ __forceinline__ f32x2_t uncvt2(uint32_t w) {
+  if constexpr (BF16) return f32x2_t{__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
+  else return __builtin_convertvector(__builtin_bit_cast(f16x2_t, w), f32x2_t);
 }
 
 // P is carried into the P @ V product as hi + lo, both in the operand type
@@ -58,11 +62,11 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {   // a, b already 
 // 16 significant bits of P instead of the operand type's 8 (bf16) / 11 (f16).
 template <bool BF16>
 __device__ __forceinline__ void split4(const float* p, uint32_t& h0, uint32_t& h1, uint32_t& l0, uint32_t& l1) {
-  const float a = to_op<BF16>(p[0]), b = to_op<BF16>(p[1]), c = to_op<BF16>(p[2]), d = to_op<BF16>(p[3]);
-  h0 = pack2<BF16>(a, b);
-  h1 = pack2<BF16>(c, d);
-  l0 = pack2<BF16>(to_op<BF16>(__fsub_rn(p[0], a)), to_op<BF16>(__fsub_rn(p[1], b)));
-  l1 = pack2<BF16>(to_op<BF16>(__fsub_rn(p[2], c)), to_op<BF16>(__fsub_rn(p[3], d)));
+  h0 = cvt2<BF16>(p[0], p[1]);
+  h1 = cvt2<BF16>(p[2], p[3]);
+  const f32x2_t a = uncvt2<BF16>(h0), b = uncvt2<BF16>(h1);
+  l0 = cvt2<BF16>(__fsub_rn(p[0], a.x), __fsub_rn(p[1], a.y));
+  l1 = cvt2<BF16>(__fsub_rn(p[2], b.x), __fsub_rn(p[3], b.y));
 }
 
 __device__ __forceinline__ uint32_t half16(const uint4& v, int i) {
@@ -82,7 +86,7 @@ __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(
 
 template <bool BF16>
 // The position mask keeps score (row, key) iff ((lo <= kpos - qpos <= hi) != inv).
-__global__ __launch_bounds__(256) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
+__global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
   __shared__ __align__(16) uint16_t Ks[AT * LDP];   // K tile, [key][d]
   __shared__ __align__(16) uint16_t Vt[AT * LDP];   // V tile transposed, [d][key]
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, r32 = l & 31;
@@ -115,10 +119,12 @@ __global__ __launch_bounds__(256) void attn_kernel(const ktir_attn_t d, int mlo,
       const int c = tid + 256 * i, key = c >> 4, dc = (c & 15) * 8;
       *(uint4*)&Ks[key * LDP + dc] = *(const uint4*)(K + kb + (int64_t)key * d.k_row + dc);
     }
-    // V transposed: units of 4 keys x 8 d, 2 per thread
+    // V transposed: units of 4 keys x 8 d, 2 per thread.  Consecutive lanes
+    // take consecutive key quads, so each transposed 8-byte LDS write of a
+    // wave covers 256 contiguous bytes per 32 lanes (no bank conflicts).
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i, kq = (u >> 4) * 4, dc = (u & 15) * 8;
+      const int u = tid + 256 * i, kq = (u & 31) * 4, dc = (u >> 5) * 8;
       const uint16_t* vr = V + vb + (int64_t)kq * d.v_row + dc;
       const uint4 v0 = *(const uint4*)(vr), v1 = *(const uint4*)(vr + d.v_row);
       const uint4 v2 = *(const uint4*)(vr + 2 * d.v_row), v3 = *(const uint4*)(vr + 3 * d.v_row);

@@ -553,6 +553,44 @@ def _splat_value(ex, name):
     return float(v.e.attr)
 
 
+N_XCD = 8    # MI355X: workgroup i of a launch runs on XCD i % 8, each XCD with its own L2
+
+
+def _xcd_order(trips, k_base, v_base, n_xcd=N_XCD):
+    """Workgroup -> lane map for the attention launch.
+
+    Lanes reading the same K/V stream (same bases: one attention head) go to
+    the same XCD, so the KV tiles they share are fetched into that XCD's L2
+    once; streams are spread over the XCDs by total trip count (longest
+    first), and inside a stream lanes run longest first, so concurrently
+    resident workgroups of one head sweep the same tiles together and the
+    short ones fill the tail."""
+    L = len(trips)
+    if L == 0:
+        return np.zeros(0, np.int32)
+    _, grp = np.unique(np.stack([k_base, v_base], 1), axis=0, return_inverse=True)
+    grp = grp.reshape(-1)
+    work = np.bincount(grp, weights=trips.astype(np.float64) + 1.0)
+    bins = [[] for _ in range(n_xcd)]
+    load = np.zeros(n_xcd)
+    for g in np.argsort(-work, kind="stable"):
+        x = int(np.argmin(load))
+        bins[x].append(int(g))
+        load[x] += work[g]
+    by_grp = {}
+    for lane in np.lexsort((-trips, grp)):
+        by_grp.setdefault(int(grp[lane]), []).append(int(lane))
+    seqs = [[ln for g in b for ln in by_grp[g]] for b in bins]
+    out = []
+    pos = [0] * n_xcd
+    while len(out) < L:
+        for x in range(n_xcd):
+            if pos[x] < len(seqs[x]):
+                out.append(seqs[x][pos[x]])
+                pos[x] += 1
+    return np.asarray(out, np.int32)
+
+
 def _attention_loop(ex, op, lb, st, trips, inits):
     """Fuse the online-softmax KV loop of flash attention into one launch
     (``ktir_launch_attention``).  The reference executes it op by op
@@ -759,7 +797,7 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     d.q_row, d.k_row, d.v_row = q_row, tiles["k"][2], tiles["v"][2]
     d.k_step, d.v_step = tiles["k"][3], tiles["v"][3]
     d.trips = up(trips.astype(np.int32))
-    d.order = up(np.argsort(-trips, kind="stable").astype(np.int32))
+    d.order = up(_xcd_order(trips, tiles["k"][1], tiles["v"][1]))
     d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
     d.kpos_step = kpos_step
     d.scale, d.neg = p0["scale"], neg
