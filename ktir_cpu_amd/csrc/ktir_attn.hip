@@ -6,12 +6,20 @@
 //                   B = Q^T fragments kept in registers, so the D layout puts
 //                   one query row per lane (lanes l and l^32 share a row):
 //                   lane l holds row l%32, keys 8g + 4h + t (h = l/32).
-//   row max / row sum: 64 values in the lane + one swap with lane l^32.
-//   O^T += V_j^T P^T  with A = V^T rows from LDS (V is staged transposed)
-//                   and B = P^T fragments: the 8 consecutive keys a lane
-//                   needs are 4 of its own values and 4 of lane l^32's.
+//   row max / row sum: 64 values in the lane + one v_permlane32_swap.
+//   O^T += V_j^T P^T  with A = V^T fragments read from the row-major V tile
+//                   by ds_read_b64_tr_b16 (gfx950 LDS transpose read) and
+//                   B = P^T fragments: the 8 consecutive keys a lane needs
+//                   are 4 of its own values and 4 of lane l^32's, which one
+//                   v_permlane32_swap per packed word delivers.
 // so O rows also live in lanes and the per-row rescale by alpha needs no
-// communication.  Semantics follow the KTIR loop body (see ktir_hip.h):
+// communication.  K and V tiles move HBM -> LDS with global_load_lds_dwordx4
+// (no registers): the next K tile streams in while P @ V runs, the next V
+// tile while the next scores are computed.  In LDS a tile row is 256 bytes
+// with its 16-byte chunk c stored at slot c ^ 2 (row % 8), so the 8 rows of
+// a ds_read_b128 phase and the 4 rows of a ds_read_b64_tr_b16 phase hit
+// distinct banks.
+// Semantics follow the KTIR loop body (see ktir_hip.h):
 // m' = max(m, rowmax S) (NaN-propagating like arith.maximumf),
 // P = exp(S - m'), alpha = exp(m - m'), acc' = acc*alpha + P@V,
 // l' = l*alpha + rowsum P, all in f32.
@@ -24,9 +32,13 @@ namespace ktir {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int AT = 128;            // M = N = D
-constexpr int LDP = AT + 8;        // padded LDS row (elements)
+constexpr float LOG2E = 1.44269504088896341f;
 
 template <bool BF16>
 __device__ __forceinline__ f32x16_t mfma_at(const uint4& a, const uint4& b, f32x16_t c) {
@@ -37,10 +49,6 @@ __device__ __forceinline__ f32x16_t mfma_at(const uint4& a, const uint4& b, f32x
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
                                                   0, 0, 0);
 }
-
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 // (a, b) rounded to nearest-even in the operand type, packed low/high
 template <bool BF16>
@@ -69,150 +77,230 @@ __device__ __forceinline__ void split4(const float* p, uint32_t& h0, uint32_t& h
   l1 = cvt2<BF16>(__fsub_rn(p[2], b.x), __fsub_rn(p[3], b.y));
 }
 
-__device__ __forceinline__ uint32_t half16(const uint4& v, int i) {
-  const uint32_t w = i < 2 ? v.x : (i < 4 ? v.y : (i < 6 ? v.z : v.w));
-  return (i & 1) ? (w >> 16) : (w & 0xffffu);
+// v_permlane32_swap: lanes 32-63 of a trade places with lanes 0-31 of b, so
+// afterwards lanes 0-31 hold a of both half-waves (own in a, the other
+// half's in b) and lanes 32-63 hold b of both (the other half's in a)
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+// value of the other half-wave's lane l ^ 32
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// a workgroup-uniform value (loaded through a pointer) into scalar registers
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // arith.maximumf: NaN-propagating maximum (v_maximum3_f32 on gfx950)
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32)
-__device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(__fmul_rn(x, 1.44269504088896341f)); }
+__device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(__fmul_rn(x, LOG2E)); }
 
-#define AT_S_LOOP(BODY)                     \
-  _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) { \
+// ds_read_b64_tr_b16: in each 16-lane group, member t receives element t % 4
+// of the 4-element chunks addressed by members 4s + t / 4, s = 0..3
+__device__ __forceinline__ uint2 ds_tr16(const uint16_t* p) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Wave w (uniform) copies rows 32w .. 32w+31 of a 128 x 128 tile into LDS: 8
+// blocks of 4 rows (1 KB), lane l filling slot l % 16 of row 4b + l / 16 of
+// block b.  buffer_load ... lds: a scalar buffer base per wave, a scalar
+// offset per block and a 32-bit lane offset that depends only on the block's
+// parity (vo0 even, vo1 odd).
+__device__ __forceinline__ void tile_to_lds(const uint16_t* src, int64_t row_stride, uint16_t* lds, int wu,
+                                            uint32_t vo0, uint32_t vo1) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(src + (int64_t)(32 * wu) * row_stride), (short)0, (int)((31 * row_stride + AT) * 2), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds + 512 * (8 * wu + i)),
+                                             16, (i & 1) ? vo1 : vo0, (int)(i * 8 * row_stride), 0, 0);
+}
+
+// byte offset of lane l's chunk in a block of parity `odd` (row l / 16 of the block)
+__device__ __forceinline__ uint32_t tile_lane_off(int l, int64_t row_stride, int odd) {
+  const int r = l >> 4, c = (l & 15) ^ (2 * ((4 * odd + r) & 7));
+  return (uint32_t)((r * row_stride + 8 * c) * 2);
+}
+
+#define AT_S_LOOP(BODY)                                      \
+  _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) {         \
     _Pragma("unroll") for (int i = 0; i < 16; ++i) { BODY; } }
 
-template <bool BF16>
 // The position mask keeps score (row, key) iff ((lo <= kpos - qpos <= hi) != inv).
+template <bool BF16>
 __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
-  __shared__ __align__(16) uint16_t Ks[AT * LDP];   // K tile, [key][d]
-  __shared__ __align__(16) uint16_t Vt[AT * LDP];   // V tile transposed, [d][key]
+  __shared__ __align__(16) uint16_t Ks[AT * AT];    // K tile, [key][d] (chunk-swizzled rows)
+  __shared__ __align__(16) uint16_t Vs[AT * AT];    // V tile, [key][d] (chunk-swizzled rows)
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, r32 = l & 31;
-  const int64_t lane = d.order ? ((const int32_t*)d.order)[blockIdx.x] : blockIdx.x;
-  const int T = ((const int32_t*)d.trips)[lane];
+  const int64_t lane = uni(d.order ? ((const int32_t*)d.order)[blockIdx.x] : (int)blockIdx.x);
+  const int T = uni(((const int32_t*)d.trips)[lane]);
   const uint16_t* Q = (const uint16_t*)d.q_ptr;
   const uint16_t* K = (const uint16_t*)d.k_ptr;
   const uint16_t* V = (const uint16_t*)d.v_ptr;
   const int row = w * 32 + r32;                      // this lane's query row
-  // Q^T fragments: for d-step s, Q[row][16 s + 8 h .. + 8]
-  uint4 qf[8];
+  const int64_t kb0 = uni(((const int64_t*)d.k_base)[lane]), vb0 = uni(((const int64_t*)d.v_base)[lane]);
+  uint4 qf[8];                                       // Q^T fragments: Q[row][16 s + 8 h .. + 8]
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint32_t ko0 = tile_lane_off(l, d.k_row, 0), ko1 = tile_lane_off(l, d.k_row, 1);
+  const uint32_t vo0 = tile_lane_off(l, d.v_row, 0), vo1 = tile_lane_off(l, d.v_row, 1);
   if (T > 0) {
-    const uint16_t* qr = Q + ((const int64_t*)d.q_base)[lane] + (int64_t)row * d.q_row + 8 * h;
+    const uint16_t* qr = Q + uni(((const int64_t*)d.q_base)[lane]) + (int64_t)row * d.q_row + 8 * h;
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = *(const uint4*)(qr + 16 * s);
+    tile_to_lds(K + kb0, d.k_row, Ks, wu, ko0, ko1);
+    tile_to_lds(V + vb0, d.v_row, Vs, wu, vo0, vo1);
+    __builtin_amdgcn_s_waitcnt(0);
   }
-  const int64_t kb0 = ((const int64_t*)d.k_base)[lane], vb0 = ((const int64_t*)d.v_base)[lane];
-  const int64_t qpos = ((const int64_t*)d.qpos0)[lane] + row;
-  const int64_t kpos00 = ((const int64_t*)d.kpos0)[lane];
+  __syncthreads();
+  const int64_t qpos = uni(((const int64_t*)d.qpos0)[lane]) + row;
+  const int64_t kpos00 = uni(((const int64_t*)d.kpos0)[lane]);
+  const bool pos_scale = d.scale > 0.f;
+  const float c1 = __fmul_rn(d.scale, LOG2E);
   const f32x16_t z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   f32x16_t o0 = z16, o1 = z16, o2 = z16, o3 = z16;   // O^T tiles: d = 32 dt + 8g + 4h + t, row r32
   float m = -__builtin_inff(), lsum = 0.f;
-  // staging assignment
+  // K^T A-fragments: row 32 kt + r32, chunk 2 s + h at slot (2 s + h) ^ 2 (r32 % 8)
+  const int k_off = r32 * AT + 8 * h;
+  const int k_x = r32 & 7;
+  // V^T fragment rows d = 32 dt + l % 32, keys 16 ks + 8 h + [0..8): member tj of
+  // 16-lane group tg addresses key 8 (tg / 2) + tj / 4 (+4), d 16 (tg % 2) + 4 (tj % 4)
+  const int tg = l >> 4, tj = l & 15;
+  const int v_row0 = 8 * (tg >> 1) + (tj >> 2);
+  const int v_c = 2 * (tg & 1) + ((tj >> 1) & 1), v_in = 4 * (tj & 1);
+  int v_off[2][4];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      v_off[hi][dt] = (v_row0 + 4 * hi) * AT + 8 * ((4 * dt + v_c) ^ (2 * ((v_row0 + 4 * hi) & 7))) + v_in;
   for (int j = 0; j < T; ++j) {
-    const int64_t kb = kb0 + (int64_t)j * d.k_step, vb = vb0 + (int64_t)j * d.v_step;
-    __syncthreads();   // the previous iteration has finished reading Ks / Vt
-    // K: 128 keys x 16 chunks of 8 elements, 8 chunks per thread, row-major into Ks
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, key = c >> 4, dc = (c & 15) * 8;
-      *(uint4*)&Ks[key * LDP + dc] = *(const uint4*)(K + kb + (int64_t)key * d.k_row + dc);
-    }
-    // V transposed: units of 4 keys x 8 d, 2 per thread.  Consecutive lanes
-    // take consecutive key quads, so each transposed 8-byte LDS write of a
-    // wave covers 256 contiguous bytes per 32 lanes (no bank conflicts).
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i, kq = (u & 31) * 4, dc = (u >> 5) * 8;
-      const uint16_t* vr = V + vb + (int64_t)kq * d.v_row + dc;
-      const uint4 v0 = *(const uint4*)(vr), v1 = *(const uint4*)(vr + d.v_row);
-      const uint4 v2 = *(const uint4*)(vr + 2 * d.v_row), v3 = *(const uint4*)(vr + 3 * d.v_row);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *(uint2*)&Vt[(dc + e) * LDP + kq] =
-            make_uint2(half16(v0, e) | (half16(v1, e) << 16), half16(v2, e) | (half16(v3, e) << 16));
-    }
-    __syncthreads();
+    const bool more = j + 1 < T;
     // S^T = K Q^T: 4 key tiles x 8 d-steps
     f32x16_t s0 = z16, s1 = z16, s2 = z16, s3 = z16;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int dofs = 16 * s + 8 * h;
-      s0 = mfma_at<BF16>(*(const uint4*)&Ks[(0 * 32 + r32) * LDP + dofs], qf[s], s0);
-      s1 = mfma_at<BF16>(*(const uint4*)&Ks[(1 * 32 + r32) * LDP + dofs], qf[s], s1);
-      s2 = mfma_at<BF16>(*(const uint4*)&Ks[(2 * 32 + r32) * LDP + dofs], qf[s], s2);
-      s3 = mfma_at<BF16>(*(const uint4*)&Ks[(3 * 32 + r32) * LDP + dofs], qf[s], s3);
+      const uint16_t* kp = &Ks[k_off + 16 * (s ^ k_x)];
+      s0 = mfma_at<BF16>(*(const uint4*)(kp + 0 * 32 * AT), qf[s], s0);
+      s1 = mfma_at<BF16>(*(const uint4*)(kp + 1 * 32 * AT), qf[s], s1);
+      s2 = mfma_at<BF16>(*(const uint4*)(kp + 2 * 32 * AT), qf[s], s2);
+      s3 = mfma_at<BF16>(*(const uint4*)(kp + 3 * 32 * AT), qf[s], s3);
     }
-    // scale, causal mask; lane value (kt, i) is key kt*32 + 8(i/4) + 4h + i%4 of row `row`
-    const int64_t kpos_j = kpos00 + (int64_t)j * d.kpos_step;
+    // lane value (kt, i) is key kt*32 + 8(i/4) + 4h + i%4 of row `row`
     float sv[4][16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      sv[0][i] = __fmul_rn(d.scale, s0[i]);
-      sv[1][i] = __fmul_rn(d.scale, s1[i]);
-      sv[2][i] = __fmul_rn(d.scale, s2[i]);
-      sv[3][i] = __fmul_rn(d.scale, s3[i]);
+      sv[0][i] = s0[i];
+      sv[1][i] = s1[i];
+      sv[2][i] = s2[i];
+      sv[3][i] = s3[i];
     }
-    if (d.causal) {
-      // kpos - qpos of this lane's key 0; its keys add 0 .. 127 (the 4h lane offset included below)
-      const int dbase = (int)(kpos_j - qpos);
-      const bool all_keep = minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi);
-      if (!__all(all_keep)) {
+    const int64_t kpos_j = kpos00 + (int64_t)j * d.kpos_step;
+    const int dbase = (int)(kpos_j - qpos);          // kpos - qpos of this lane's key 0; keys add 0 .. 127
+    const bool all_keep = !d.causal ||
+        (minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi));
+    float mn, ls;
+    if (pos_scale && __all(all_keep)) {
+      // no masked score in the wave: rowmax S = scale * rowmax(QK) (rounding is
+      // monotonic for scale > 0) and P = 2^(QK * scale log2e - m' log2e)
+      float x0 = fmax_nan(sv[0][0], sv[0][1]), x1 = fmax_nan(sv[1][0], sv[1][1]);
+      float x2 = fmax_nan(sv[2][0], sv[2][1]), x3 = fmax_nan(sv[3][0], sv[3][1]);
+#pragma unroll
+      for (int i = 2; i < 16; i += 2) {
+        x0 = fmax_nan(x0, fmax_nan(sv[0][i], sv[0][i + 1]));
+        x1 = fmax_nan(x1, fmax_nan(sv[1][i], sv[1][i + 1]));
+        x2 = fmax_nan(x2, fmax_nan(sv[2][i], sv[2][i + 1]));
+        x3 = fmax_nan(x3, fmax_nan(sv[3][i], sv[3][i + 1]));
+      }
+      float xm = fmax_nan(fmax_nan(x0, x1), fmax_nan(x2, x3));
+      xm = fmax_nan(xm, other_half(xm));
+      mn = fmax_nan(m, __fmul_rn(d.scale, xm));
+      const float c0 = -__fmul_rn(mn, LOG2E);
+      AT_S_LOOP(sv[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kt][i], c1, c0)))
+    } else {
+      AT_S_LOOP(sv[kt][i] = __fmul_rn(d.scale, sv[kt][i]))
+      if (d.causal) {
         AT_S_LOOP({
           const int df = dbase + kt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
           if ((df >= mlo && df <= mhi) == (bool)minv) sv[kt][i] = d.neg;
         })
       }
+      float xm = -__builtin_inff();
+      AT_S_LOOP(xm = fmax_nan(xm, sv[kt][i]))
+      xm = fmax_nan(xm, other_half(xm));
+      mn = fmax_nan(m, xm);
+      AT_S_LOOP(sv[kt][i] = exp_f(__fsub_rn(sv[kt][i], mn)))
     }
-    float rm = -__builtin_inff();
-    AT_S_LOOP(rm = fmax_nan(rm, sv[kt][i]))
-    rm = fmax_nan(rm, __shfl_xor(rm, 32));
-    const float mn = fmax_nan(m, rm);
-    float ls = 0.f;
-    AT_S_LOOP({
-      sv[kt][i] = exp_f(__fsub_rn(sv[kt][i], mn));
-      ls = __fadd_rn(ls, sv[kt][i]);
-    })
-    ls = __fadd_rn(ls, __shfl_xor(ls, 32));
-    const float alpha = exp_f(__fsub_rn(m, mn));
+    {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      o0[i] = __fmul_rn(o0[i], alpha);
-      o1[i] = __fmul_rn(o1[i], alpha);
-      o2[i] = __fmul_rn(o2[i], alpha);
-      o3[i] = __fmul_rn(o3[i], alpha);
+      for (int i = 0; i < 16; ++i) {
+        a0 = __fadd_rn(a0, sv[0][i]);
+        a1 = __fadd_rn(a1, sv[1][i]);
+        a2 = __fadd_rn(a2, sv[2][i]);
+        a3 = __fadd_rn(a3, sv[3][i]);
+      }
+      ls = __fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3));
+      ls = __fadd_rn(ls, other_half(ls));
+    }
+    const float alpha = exp_f(__fsub_rn(m, mn));
+    if (!__all(alpha == 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] = __fmul_rn(o0[i], alpha);
+        o1[i] = __fmul_rn(o1[i], alpha);
+        o2[i] = __fmul_rn(o2[i], alpha);
+        o3[i] = __fmul_rn(o3[i], alpha);
+      }
     }
     lsum = __fadd_rn(__fmul_rn(lsum, alpha), ls);
     m = mn;
+    __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of V_j has landed
+    __syncthreads();                                  // every wave: done with Ks, V_j in LDS
+    if (more) tile_to_lds(K + kb0 + (int64_t)(j + 1) * d.k_step, d.k_row, Ks, wu, ko0, ko1);
     // O^T += V^T P^T over 8 key-steps of 16 keys
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      // lane half h owns 4-key group g = 2 (ks & 1) + h of key tile ks / 2 and sends the other one
+      // lane half h holds key groups g0 (a*) and g0 + 1 (b*) of key tile ks / 2;
+      // after the swaps both halves hold keys 16 ks + 8 h + [0..8) in order
       const int kt = ks >> 1, g0 = 2 * (ks & 1);
       uint32_t ah0, ah1, al0, al1, bh0, bh1, bl0, bl1;
       split4<BF16>(&sv[kt][4 * g0], ah0, ah1, al0, al1);
       split4<BF16>(&sv[kt][4 * g0 + 4], bh0, bh1, bl0, bl1);
-      const uint32_t oh0 = h ? bh0 : ah0, oh1 = h ? bh1 : ah1, ol0 = h ? bl0 : al0, ol1 = h ? bl1 : al1;
-      const uint32_t rh0 = __shfl_xor(h ? ah0 : bh0, 32), rh1 = __shfl_xor(h ? ah1 : bh1, 32);
-      const uint32_t rl0 = __shfl_xor(h ? al0 : bl0, 32), rl1 = __shfl_xor(h ? al1 : bl1, 32);
-      // keys 16 ks + 8 h + [0..3] come from lane half 0, [4..7] from half 1
-      const uint4 ph = h == 0 ? make_uint4(oh0, oh1, rh0, rh1) : make_uint4(rh0, rh1, oh0, oh1);
-      const uint4 pl = h == 0 ? make_uint4(ol0, ol1, rl0, rl1) : make_uint4(rl0, rl1, ol0, ol1);
-      const int kofs = 16 * ks + 8 * h;
-      const uint4 a0 = *(const uint4*)&Vt[(0 * 32 + r32) * LDP + kofs];
-      const uint4 a1 = *(const uint4*)&Vt[(1 * 32 + r32) * LDP + kofs];
-      const uint4 a2 = *(const uint4*)&Vt[(2 * 32 + r32) * LDP + kofs];
-      const uint4 a3 = *(const uint4*)&Vt[(3 * 32 + r32) * LDP + kofs];
-      o0 = mfma_at<BF16>(a0, ph, o0);
-      o1 = mfma_at<BF16>(a1, ph, o1);
-      o2 = mfma_at<BF16>(a2, ph, o2);
-      o3 = mfma_at<BF16>(a3, ph, o3);
-      o0 = mfma_at<BF16>(a0, pl, o0);
-      o1 = mfma_at<BF16>(a1, pl, o1);
-      o2 = mfma_at<BF16>(a2, pl, o2);
-      o3 = mfma_at<BF16>(a3, pl, o3);
+      swap32(ah0, bh0);
+      swap32(ah1, bh1);
+      swap32(al0, bl0);
+      swap32(al1, bl1);
+      const uint4 ph = make_uint4(ah0, ah1, bh0, bh1), pl = make_uint4(al0, al1, bl0, bl1);
+      const uint16_t* vt = &Vs[16 * ks * AT];
+      uint4 a[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint2 lo = ds_tr16(vt + v_off[0][dt]), hi = ds_tr16(vt + v_off[1][dt]);
+        a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+      o0 = mfma_at<BF16>(a[0], ph, o0);
+      o1 = mfma_at<BF16>(a[1], ph, o1);
+      o2 = mfma_at<BF16>(a[2], ph, o2);
+      o3 = mfma_at<BF16>(a[3], ph, o3);
+      o0 = mfma_at<BF16>(a[0], pl, o0);
+      o1 = mfma_at<BF16>(a[1], pl, o1);
+      o2 = mfma_at<BF16>(a[2], pl, o2);
+      o3 = mfma_at<BF16>(a[3], pl, o3);
     }
+    __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of K_{j+1} has landed
+    __syncthreads();                                  // every wave: done with Vs, K_{j+1} in LDS
+    if (more) tile_to_lds(V + vb0 + (int64_t)(j + 1) * d.v_step, d.v_row, Vs, wu, vo0, vo1);
   }
   // final state
   if (h == 0) {

@@ -1,6 +1,6 @@
 // Streaming kernels for the most common fused program: one or two strided
-// inputs, a chain of register ops, one strided output (an elementwise map,
-// a copy, a cast, a broadcast).  Leaf and output dtypes are template
+// inputs (unit or zero inner stride), a chain of register ops, one strided
+// output (an elementwise map, a copy, a cast, a broadcast).  Leaf and output dtypes are template
 // parameters, so the memory path is straight-line code: each thread moves
 // 8-element chunks with 16-byte accesses and has all its chunks' loads in
 // flight before it computes.  The register ops still come from the
@@ -11,7 +11,13 @@
 namespace ktir {
 
 template <int DT>
-__device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* out) {
+__device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* out, bool bcast) {
+  if (bcast) {   // inner stride 0: one element for the whole chunk
+    const float v = (e0 >= L.lo && e0 < L.hi) ? load_elem(L.ptr, e0, DT) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = v;
+    return;
+  }
   if (e0 >= L.lo && e0 + 8 <= L.hi) {
     if (DT == KTIR_F16) {
       uint4 w = *(const uint4*)((const _Float16*)L.ptr + e0);
@@ -150,6 +156,7 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
   const int nd = P.ndim;
   const int n_ops = P.n_instr - 1;
   const int out_reg = P.instr[n_ops].a;
+  const bool bca = LA.strides[nd - 1] == 0, bcb = LB.strides[nd - 1] == 0;
   const uint32_t nth = gridDim.x * blockDim.x;
   for (uint32_t vid = blockIdx.x * blockDim.x + threadIdx.x; vid < total; vid += nth) {
     // coordinates of the chunk: c[d] for the outer dims d < nd-1, col inner
@@ -165,9 +172,9 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
         t = q;
       }
     }
-    // inner strides are 1 on this path (checked at launch)
-    int64_t ea = lane_offset(LA, t) + col;
-    int64_t eb = lane_offset(LB, t) + col;
+    // inner strides are 1 (or 0 for a broadcast input) on this path (checked at launch)
+    int64_t ea = lane_offset(LA, t) + (bca ? 0 : col);
+    int64_t eb = lane_offset(LB, t) + (bcb ? 0 : col);
     int64_t eo = lane_offset(LO, t) + col;
 #pragma unroll
     for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) {
@@ -178,8 +185,8 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
       }
     }
     float a[8], b[8];
-    load8<DA>(LA, ea, a);
-    if (NIN == 2) load8<DB>(LB, eb, b);
+    load8<DA>(LA, ea, a, bca);
+    if (NIN == 2) load8<DB>(LB, eb, b, bcb);
     Reg4 R[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) R[e] = Reg4{a[e], NIN == 2 ? b[e] : 0.f, 0.f, 0.f};
@@ -232,13 +239,14 @@ bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner) {
     if (in.dst > 3 || in.a > 3 || in.b > 3 || in.c > 3) return false;   // four registers
   }
   const int nd = Q.ndim;
-  auto ok_leaf = [nd](const ktir_leaf_t& L) {
-    return L.offsets == 0 && L.winner == 0 && L.strides[nd - 1] == 1 && (L.flags & KTIR_LEAF_VEC8) &&
+  auto ok_leaf = [nd](const ktir_leaf_t& L, bool input) {
+    const bool inner = (L.strides[nd - 1] == 1 && (L.flags & KTIR_LEAF_VEC8)) || (input && L.strides[nd - 1] == 0);
+    return L.offsets == 0 && L.winner == 0 && inner &&
            (L.dtype == KTIR_F16 || L.dtype == KTIR_BF16 || L.dtype == KTIR_F32);
   };
   for (int k = 0; k < Q.n_pf; ++k)
-    if (!ok_leaf(Q.leaves[Q.pf_leaf[k]])) return false;
-  if (!ok_leaf(Q.leaves[st.aux])) return false;
+    if (!ok_leaf(Q.leaves[Q.pf_leaf[k]], true)) return false;
+  if (!ok_leaf(Q.leaves[st.aux], false)) return false;
   const int64_t chunks = rows * (inner / 8);
   if (chunks >= (int64_t)0x7fffffff || inner / 8 >= (int64_t)0x7fffffff) return false;
   FlatDivs D;
