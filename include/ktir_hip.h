@@ -331,7 +331,14 @@ typedef struct ktir_attn {
   int32_t causal, pred;                /* mask on (KTIR_CMP_* predicate keep = pred(kpos, qpos)) */
   int32_t dtype;                       /* KTIR_BF16 or KTIR_F16 */
   int32_t pad;
-  uint64_t m_out, l_out, acc_out;      /* f32 [lanes, M], [lanes, M], [lanes, M, D] final state */
+  uint64_t m_out, l_out, acc_out;      /* f32 [lanes, M], [lanes, M], [lanes, M, D] final state
+                                          (acc_out 0: not written) */
+  /* optional fused epilogue O = acc / l (the division of the reference's
+   * examples/triton-ktir/paged_attention.mlir:400-420 and its store), rounded
+   * to o_dtype and written at o_ptr + o_base[l] + row * o_row + d */
+  uint64_t o_ptr, o_base;              /* 0: no epilogue; o_base: const int64_t* [lanes] */
+  int64_t o_row;
+  int32_t o_dtype, pad2;
 } ktir_attn_t;
 int ktir_launch_attention(const ktir_attn_t* d);
 

@@ -307,13 +307,36 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     ((float*)d.m_out)[lane * AT + row] = m;
     ((float*)d.l_out)[lane * AT + row] = lsum;
   }
-  float* orow = (float*)d.acc_out + (lane * AT + row) * AT + 4 * h;
+  if (d.acc_out) {
+    float* orow = (float*)d.acc_out + (lane * AT + row) * AT + 4 * h;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    *(float4*)(orow + 0 * 32 + 8 * g) = make_float4(o0[4 * g], o0[4 * g + 1], o0[4 * g + 2], o0[4 * g + 3]);
-    *(float4*)(orow + 1 * 32 + 8 * g) = make_float4(o1[4 * g], o1[4 * g + 1], o1[4 * g + 2], o1[4 * g + 3]);
-    *(float4*)(orow + 2 * 32 + 8 * g) = make_float4(o2[4 * g], o2[4 * g + 1], o2[4 * g + 2], o2[4 * g + 3]);
-    *(float4*)(orow + 3 * 32 + 8 * g) = make_float4(o3[4 * g], o3[4 * g + 1], o3[4 * g + 2], o3[4 * g + 3]);
+    for (int g = 0; g < 4; ++g) {
+      *(float4*)(orow + 0 * 32 + 8 * g) = make_float4(o0[4 * g], o0[4 * g + 1], o0[4 * g + 2], o0[4 * g + 3]);
+      *(float4*)(orow + 1 * 32 + 8 * g) = make_float4(o1[4 * g], o1[4 * g + 1], o1[4 * g + 2], o1[4 * g + 3]);
+      *(float4*)(orow + 2 * 32 + 8 * g) = make_float4(o2[4 * g], o2[4 * g + 1], o2[4 * g + 2], o2[4 * g + 3]);
+      *(float4*)(orow + 3 * 32 + 8 * g) = make_float4(o3[4 * g], o3[4 * g + 1], o3[4 * g + 2], o3[4 * g + 3]);
+    }
+  }
+  if (d.o_ptr) {
+    // O = acc / l (f32, correctly rounded), then rounded to the output type
+    const int64_t ob = uni(((const int64_t*)d.o_base)[lane]) + (int64_t)row * d.o_row + 4 * h;
+#define AT_EPI(o, dt)                                                                            \
+    _Pragma("unroll") for (int g = 0; g < 4; ++g) {                                              \
+      const float q0 = __fdiv_rn(o[4 * g], lsum), q1 = __fdiv_rn(o[4 * g + 1], lsum);            \
+      const float q2 = __fdiv_rn(o[4 * g + 2], lsum), q3 = __fdiv_rn(o[4 * g + 3], lsum);        \
+      const int64_t e = ob + 32 * dt + 8 * g;                                                    \
+      if (d.o_dtype == KTIR_F32)                                                                 \
+        *(float4*)((float*)d.o_ptr + e) = make_float4(q0, q1, q2, q3);                           \
+      else if (d.o_dtype == KTIR_BF16)                                                           \
+        *(uint2*)((uint16_t*)d.o_ptr + e) = make_uint2(cvt2<true>(q0, q1), cvt2<true>(q2, q3));   \
+      else                                                                                       \
+        *(uint2*)((uint16_t*)d.o_ptr + e) = make_uint2(cvt2<false>(q0, q1), cvt2<false>(q2, q3)); \
+    }
+    AT_EPI(o0, 0)
+    AT_EPI(o1, 1)
+    AT_EPI(o2, 2)
+    AT_EPI(o3, 3)
+#undef AT_EPI
   }
 }
 
@@ -328,6 +351,8 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
     return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_attention: bf16 or f16 operands");
   if ((d->q_ptr | d->k_ptr | d->v_ptr) & 15 || (d->q_row | d->k_row | d->v_row | d->k_step | d->v_step) & 7)
     return set_error(KTIR_E_ARG, "ktir_launch_attention: operands must be 16-byte aligned");
+  if (d->o_ptr && (d->o_dtype != KTIR_F32 && d->o_dtype != KTIR_BF16 && d->o_dtype != KTIR_F16))
+    return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_attention: output dtype %d", d->o_dtype);
   if (d->lanes == 0) return KTIR_OK;
   // predicate keep = pred(kpos, qpos) as a range test on kpos - qpos
   int lo = 0, hi = 0, inv = 0;

@@ -420,7 +420,9 @@ class Plan:
         self.fallback_reason = None
 
     def add(self, kind, desc, keep=()):
-        self.launches.append((kind, desc, tuple(keep)))
+        # a list stays shared with the caller, who may still append buffers
+        # that a later rewrite of `desc` points at
+        self.launches.append((kind, desc, keep if isinstance(keep, list) else tuple(keep)))
 
     def run(self):
         L = rt.lib()

@@ -814,6 +814,8 @@ def _attention_loop(ex, op, lb, st, trips, inits):
         alloc, rel, row, step = tiles[key]
         ex.log(alloc, False, rel, (tmax, AT, AT), (step, row, 1))
     ex.launch("attn", d, keep)
+    ex.attn_pending = dict(desc=d, keep=keep, acc=a_buf, l=l_buf, lanes=L, level=len(ex.levels),
+                           body_names=set(names))
     vec = lambda b: Tile(Expr("ld", "f32", (AT,), attr=LeafSpec(b.ptr, "f32", LaneOff(0, AT), (1,), 0, L * AT,
                                                                   keep=(b,))))
     res = [None, None, None]
@@ -821,3 +823,71 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     res[ia] = Tile(Expr("ld", "f32", (AT, AT), attr=LeafSpec(a_buf.ptr, "f32", LaneOff(0, AT * AT), (AT, 1), 0,
                                                                L * AT * AT, keep=(a_buf,))))
     return res
+
+
+def _plain_ld(e, ptr, inner):
+    """`e` reads a whole attention state buffer at `ptr`: lane stride = one
+    lane's block, the two inner strides `inner`, any leading dims of extent 1."""
+    if e.kind != "ld" or e.attr.ptr != ptr or e.attr.offsets is not None or e.attr.winner is not None:
+        return False
+    sh, stv = tuple(e.shape), tuple(e.attr.strides)
+    if len(sh) < 2 or any(x != 1 for x in sh[:-2]) or tuple(sh[-2:]) != (128, 128):
+        return False
+    return stv[-2:] == inner and e.attr.lane.arr is None and e.attr.lane.base == 0
+
+
+def attention_epilogue(ex, e, dest) -> bool:
+    """Fold ``store(cast(acc / l))`` of the loop results of the last fused
+    attention launch into that launch (its kernel writes O directly), when
+    nothing else still reads acc.  Same operations and roundings as the
+    store's own program: f32 division, then rounding to the store type."""
+    from . import runtime as rt
+    from .walker import _reads
+    pend = ex.attn_pending
+    if pend is None or ex.eager or ex.L != pend["lanes"] or len(ex.levels) != pend["level"]:
+        return False
+    x = e
+    if x.kind == "cast" and x.attr == "f32":
+        x = x.args[0]
+    if x.kind != "bin" or x.attr != rt.op("DIVF") or x.dtype != "f32" or len(x.args) != 2:
+        return False
+    acc_buf, l_buf = pend["acc"], pend["l"]
+    a, b = x.args
+    if not (_plain_ld(a, acc_buf.ptr, (128, 1)) and a.attr.lane.stride == 128 * 128
+            and _plain_ld(b, l_buf.ptr, (1, 0)) and b.attr.lane.stride == 128):
+        return False
+    if dest.dtype not in ("f32", "bf16", "f16") or dest.offsets is not None or dest.winner is not None:
+        return False
+    dsh = tuple(e.shape)
+    dst = tuple(dest.strides)
+    if len(dst) != len(dsh) or dst[-1] != 1 or any(s_ != 1 for s_ in dsh[:-2]):
+        return False
+    L = ex.L
+    o_row = int(dst[-2])
+    offs = dest.lane.values(L)
+    if np.any(offs < dest.lo) or np.any(offs + 127 * o_row + 127 >= dest.hi) or np.any(offs % 8) or o_row % 8 \
+            or o_row < 128:
+        return False
+    d = pend["desc"]
+    # acc stays needed if any live value other than this store still reads it
+    # (the loop's own iter_args are not visible after the loop)
+    acc_live = False
+    for fr in ex.frames:
+        for name, v in fr.vals.items():
+            if name in pend["body_names"] or not isinstance(v, Tile) or v.e is e:
+                continue
+            if any(n.attr.ptr == acc_buf.ptr for n in _walk_ld(v.e)):
+                acc_live = True
+    ob = ex.pool.upload(np.ascontiguousarray(offs.astype(np.int64)))
+    pend["keep"].extend([ob, dest])
+    d.o_ptr, d.o_base, d.o_row = dest.ptr, ob.ptr, o_row
+    d.o_dtype = rt.DTYPE_CODE[dest.dtype]
+    if not acc_live:
+        d.acc_out = 0
+    ex.attn_pending = None
+    return True
+
+
+def _walk_ld(e):
+    from .program import walk
+    return [n for n in walk(e) if n.kind == "ld"]

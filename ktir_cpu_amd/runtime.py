@@ -112,7 +112,9 @@ class ATTN(C.Structure):
                 ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64),
                 ("scale", C.c_float), ("neg", C.c_float), ("causal", C.c_int32), ("pred", C.c_int32),
                 ("dtype", C.c_int32), ("pad", C.c_int32),
-                ("m_out", C.c_uint64), ("l_out", C.c_uint64), ("acc_out", C.c_uint64)]
+                ("m_out", C.c_uint64), ("l_out", C.c_uint64), ("acc_out", C.c_uint64),
+                ("o_ptr", C.c_uint64), ("o_base", C.c_uint64), ("o_row", C.c_int64), ("o_dtype", C.c_int32),
+                ("pad2", C.c_int32)]
 
 
 class KTIRDeviceError(RuntimeError):

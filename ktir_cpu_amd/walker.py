@@ -236,6 +236,7 @@ class Executor:
         self.pool = pool
         self.sequential = sequential
         self.eager = sequential
+        self.attn_pending = None     # last fused attention launch whose epilogue may still fold in
         self.allow_expand = allow_expand and not sequential
         self.plan = Plan(pool)
         self.plan.mode = "sequential" if sequential else "lockstep"
@@ -643,6 +644,9 @@ class Executor:
             e = self.materialize(Tile(e)).e
         if e.dtype != dest.dtype and not (is_float(e.dtype) and is_float(dest.dtype)):
             e = Expr("cast", dest.dtype, e.shape, [e], e.dtype)
+        from .fusion import attention_epilogue
+        if attention_epilogue(self, e, dest):
+            return
         self.materialize(Tile(e), dest=dest)
 
     def _winners(self, spec: LeafSpec, n: int):

@@ -89,3 +89,12 @@ def test_flash_attention_fused(args):
     np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
     for k in ("q_ptr", "k_ptr", "v_ptr"):
         np.testing.assert_array_equal(out[k], ref[k])
+
+
+def test_flash_attention_unfused_epilogue():
+    """An epilogue other than acc / l stays a separate program after the fused loop."""
+    src, fn, kw = _cases.flash_attention(S=256, D=128, blk=128)
+    src = src.replace("%q_ = arith.divf %av, %lv : f32", "%q_ = arith.mulf %av, %lv : f32")
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts() == {"attn": 1, "prog": 1}
+    np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
