@@ -37,6 +37,16 @@ def _vector_add():
                 workload=f"vector_add n={n} f16 grid={cores} BLOCK={block}")
 
 
+def _copy():
+    from ktir_cpu_amd import configs
+    n, block, cores = 64 * 1024 * 1024, 32768, 2048
+    x = np.random.default_rng(42).standard_normal(n, dtype=np.float32)
+    kw = dict(x_ptr=x, output_ptr=np.zeros(n, np.float32))
+    return dict(src=configs.vector_copy(n, block, cores, "f32"), fn="copy_kernel", kw=kw, cores=cores,
+                bytes=8 * n, flops=0, bound="hbm", dtype="f32",
+                workload=f"copy n={n} f32 grid={cores} BLOCK={block} (HBM traffic calibration)")
+
+
 def _gather():
     from ktir_cpu_amd import configs
     rows, dim, n_idx, cores, chunk = 1 << 20, 128, 262144, 64, 128
@@ -101,8 +111,20 @@ def _attention():
                 workload=f"flash_attention causal B={B} H={H} S={S} D={D} kv_tile=128")
 
 
-CONFIGS = {"vector_add": _vector_add, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
+CONFIGS = {"vector_add": _vector_add, "copy": _copy, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
            "gemm": _gemm, "attention": _attention}
+
+
+def _traffic(config):
+    """HBM bytes per launch of the config's dominant launch, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (profiles/traffic.json,
+    scaled by a copy kernel of known size), or None when not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            t = json.load(f)["configs"].get(config)
+    except (OSError, ValueError, KeyError):
+        return None
+    return round(t["traffic_bytes"]) if t else None
 
 
 def cpu_baseline(cfg, budget_s=15.0):
@@ -212,7 +234,7 @@ def main():
         "config": {"workload": cfg["workload"], "launches_per_step": len(plan.launches),
                    "plan_mode": plan.mode, "host_walk_s": round(walk_s, 3)},
         "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": None,
+                     "frac": round(achieved / peak, 4), "traffic": _traffic(args.config),
                      "dominant_launch": plan.launches[dom][0] if plan.launches else None,
                      "dominant_ms": round(dom_ms, 6)},
     }

@@ -88,6 +88,28 @@ def vector_add(n: int = 4096, block: int = 128, cores: int = 32) -> str:
 """
 
 
+def vector_copy(n: int = 1 << 26, block: int = 32768, cores: int = 2048, dtype: str = "f32") -> str:
+    """out[i] = x[i]: a plain copy of known size (HBM traffic calibration)."""
+    assert n % (cores * block) == 0 and n // (cores * block) == 1
+    at = f"!ktdp.access_tile<{block}xindex>"
+    return f"""module {{
+  func.func @copy_kernel(%x_ptr: index, %output_ptr: index)
+      attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %BLOCK = arith.constant {block} : index
+{_view("x_view", "x_ptr", [n], [1], dtype)}
+{_view("out_view", "output_ptr", [n], [1], dtype)}
+    %offset = arith.muli %core_id, %BLOCK : index
+{_tile("x_tile", "x_view", ["%offset"], [block], [n], dtype)}
+    %x = ktdp.load %x_tile : {at} -> {_t([block], dtype)}
+{_tile("out_tile", "out_view", ["%offset"], [block], [n], dtype)}
+    ktdp.store %x, %out_tile : {_t([block], dtype)}, {at}
+    return
+  }}
+}}
+"""
+
+
 # ---------------------------------------------------------------------------
 # 2. indirect gather + scatter-add
 # ---------------------------------------------------------------------------
