@@ -47,37 +47,49 @@ __device__ __forceinline__ int elem_bytes(int dt) {
   }
 }
 
+// Device buffers are global memory: accesses through address-space-1
+// pointers compile to global_* instructions (flat_* ones would make the
+// compiler wait for LDS traffic too).
+#define KTIR_G(T) __attribute__((address_space(1))) T
+
 // Read one element of dtype dt at element offset off from ptr, as a 32-bit
 // register value (float bits for float types, int32 for integer types).
 __device__ __forceinline__ float load_elem(uint64_t ptr, int64_t off, int dt) {
   switch (dt) {
-    case KTIR_F16: return (float)((const _Float16*)ptr)[off];
-    case KTIR_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)ptr)[off]) << 16);
-    case KTIR_F32: return ((const float*)ptr)[off];
-    case KTIR_I1: return __int_as_float(((const uint8_t*)ptr)[off] ? 1 : 0);
-    case KTIR_I8: return __int_as_float((int)((const int8_t*)ptr)[off]);
-    case KTIR_I16: return __int_as_float((int)((const int16_t*)ptr)[off]);
-    case KTIR_I32: return __int_as_float(((const int32_t*)ptr)[off]);
-    case KTIR_I64: return __int_as_float((int32_t)((const int64_t*)ptr)[off]);
+    case KTIR_F16: return (float)((const KTIR_G(_Float16)*)ptr)[off];
+    case KTIR_BF16: return __uint_as_float(((uint32_t)((const KTIR_G(uint16_t)*)ptr)[off]) << 16);
+    case KTIR_F32: return ((const KTIR_G(float)*)ptr)[off];
+    case KTIR_I1: return __int_as_float(((const KTIR_G(uint8_t)*)ptr)[off] ? 1 : 0);
+    case KTIR_I8: return __int_as_float((int)((const KTIR_G(int8_t)*)ptr)[off]);
+    case KTIR_I16: return __int_as_float((int)((const KTIR_G(int16_t)*)ptr)[off]);
+    case KTIR_I32: return __int_as_float(((const KTIR_G(int32_t)*)ptr)[off]);
+    case KTIR_I64: return __int_as_float((int32_t)((const KTIR_G(int64_t)*)ptr)[off]);
   }
   return 0.f;
 }
 
 __device__ __forceinline__ void store_elem(uint64_t ptr, int64_t off, int dt, float v) {
   switch (dt) {
-    case KTIR_F16: ((_Float16*)ptr)[off] = (_Float16)v; break;
-    case KTIR_BF16: ((uint16_t*)ptr)[off] = (uint16_t)(__float_as_uint(round_bf16(v)) >> 16); break;
-    case KTIR_F32: ((float*)ptr)[off] = v; break;
-    case KTIR_I1: ((uint8_t*)ptr)[off] = __float_as_int(v) ? 1 : 0; break;
-    case KTIR_I8: ((int8_t*)ptr)[off] = (int8_t)__float_as_int(v); break;
-    case KTIR_I16: ((int16_t*)ptr)[off] = (int16_t)__float_as_int(v); break;
-    case KTIR_I32: ((int32_t*)ptr)[off] = __float_as_int(v); break;
-    case KTIR_I64: ((int64_t*)ptr)[off] = (int64_t)__float_as_int(v); break;
+    case KTIR_F16: ((KTIR_G(_Float16)*)ptr)[off] = (_Float16)v; break;
+    case KTIR_BF16: ((KTIR_G(uint16_t)*)ptr)[off] = (uint16_t)(__float_as_uint(round_bf16(v)) >> 16); break;
+    case KTIR_F32: ((KTIR_G(float)*)ptr)[off] = v; break;
+    case KTIR_I1: ((KTIR_G(uint8_t)*)ptr)[off] = __float_as_int(v) ? 1 : 0; break;
+    case KTIR_I8: ((KTIR_G(int8_t)*)ptr)[off] = (int8_t)__float_as_int(v); break;
+    case KTIR_I16: ((KTIR_G(int16_t)*)ptr)[off] = (int16_t)__float_as_int(v); break;
+    case KTIR_I32: ((KTIR_G(int32_t)*)ptr)[off] = __float_as_int(v); break;
+    case KTIR_I64: ((KTIR_G(int64_t)*)ptr)[off] = (int64_t)__float_as_int(v); break;
   }
 }
 
+// a wavefront-uniform value (loaded through a pointer or from LDS) into scalar registers
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ int64_t lane_offset(const ktir_leaf_t& L, int64_t lane) {
-  return L.lane_base ? ((const int64_t*)L.lane_base)[lane] : L.base + lane * L.lane_stride;
+  return L.lane_base ? ((const KTIR_G(int64_t)*)L.lane_base)[lane] : L.base + lane * L.lane_stride;
 }
 
 }  // namespace ktir

@@ -242,6 +242,7 @@ using namespace ktir;
 
 namespace ktir {
 bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner);
+bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner);
 }
 
 extern "C" int ktir_launch_program(const ktir_prog_t* P) {
@@ -320,6 +321,10 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
       return set_error(KTIR_E_UNSUPPORTED, "row program: row of %lld elements exceeds %d", (long long)inner,
                        KTIR_MAX_ROW);
     int64_t rows = P->lanes * (per_lane / inner);
+    if (try_launch_rows(*P, rows, inner)) {
+      KTIR_HIP_CHECK(hipGetLastError());
+      return KTIR_OK;
+    }
     int64_t blocks = rows < 65536 ? rows : 65536;
     int64_t per = v4 ? inner / 4 : inner;
     int threads = per >= 256 ? 256 : (int)((per + 63) / 64 * 64);

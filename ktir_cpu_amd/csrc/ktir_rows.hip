@@ -1,0 +1,1251 @@
+// Register-resident row kernel for row-mode programs (mode 1) whose element
+// blocks are single chains: every ELEM block starts from a loaded row (or a
+// row-broadcast vector), applies a chain of unary ops and binary ops against
+// row scalars / loaded rows, and ends in a fold (RED + FOLD) or a store.
+// Softmax, RMSNorm and LayerNorm lower to this form.
+//
+// A group of TPR threads owns one row of n = TPR * E elements; thread t holds
+// the element pairs p = k * TPR + t (k < E/2), i.e. elements 2p and 2p + 1,
+// so every load moves 2 consecutive elements per lane (coalesced across the
+// wave).  The loaded rows stay in registers for all passes (each leaf is read
+// from HBM once per row).  Folds reproduce the reference's pairwise-halving
+// tree (dialects/linalg_ops.py:114-131) exactly: its levels pair element i
+// with i + n/2, i + n/4, ...; with this layout the first log2(E/2) levels pair
+// registers of one thread, the next log2(TPR) levels pair lanes t and t ^ s
+// (LDS for s >= 64, wave shuffles below), the last pairs the two elements of
+// a pair.  Each combine is commutative, so both partners of a butterfly hold
+// the lower element's value and the result ends up in every thread.
+#include "ktir_program_impl.h"
+
+namespace ktir {
+
+constexpr int RC_MAX_STEPS = 16;
+
+typedef float gf2 __attribute__((ext_vector_type(2)));
+typedef uint32_t gu4 __attribute__((ext_vector_type(4)));
+constexpr int RC_MAX_OPS = 8;
+
+struct RcOp {
+  int8_t op, dt, aux;
+  int8_t kind;      // 0 unary / cast, 1 row register operand, 2 cached row operand, 3 the chain value itself
+  int8_t idx;       // register or cache slot
+  int8_t swap;      // the operand is the left side
+  int8_t pad[2];
+};
+
+struct RcStep {
+  int8_t kind;      // 0 row instruction P.instr[pc], 1 pass, 2 row store of register P.instr[pc].a
+  int8_t pc;
+  int8_t src;       // pass: cache slot the chain starts from
+  int8_t n_ops;
+  int8_t end;       // 0 fold into register dst, 1 store to leaf st_leaf
+  int8_t fold_op, fold_dt, dst, st_leaf;
+  int8_t head;      // fused leading ops: 0 none, 1 SUBF(row) + EXP, 2 MULF(self)
+  int8_t save;      // keep the values after the fused head for a later pass
+  int8_t reuse;     // start from the values a previous pass kept (its head is the same)
+  RcOp ops[RC_MAX_OPS];
+};
+
+struct RcPlan {
+  int32_t n_steps, n_slots;
+  int8_t slot_leaf[2];
+  RcStep steps[RC_MAX_STEPS];
+};
+
+// A copy of an LDS-resident, workgroup-uniform struct in scalar registers.
+template <typename T>
+struct Words {
+  int w[sizeof(T) / 4];
+};
+
+template <typename T>
+__device__ __forceinline__ T uniform_copy(const T& x) {
+  static_assert(sizeof(T) % 4 == 0, "whole words");
+  const Words<T> in = __builtin_bit_cast(Words<T>, x);
+  Words<T> out;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) out.w[i] = __builtin_amdgcn_readfirstlane(in.w[i]);
+  return __builtin_bit_cast(T, out);
+}
+
+// Row registers of one row: uniform values in scalar registers, selected by
+// the (uniform) register number.  Named members, not an array: an array
+// indexed by a run-time number would live in scratch memory, and every
+// scratch access waits for all of the wavefront's outstanding memory traffic.
+struct RowRegs {
+  float r0, r1, r2, r3, r4, r5, r6, r7;
+  __device__ __forceinline__ float get(int i) const {
+    switch (i) {
+      case 0: return r0;
+      case 1: return r1;
+      case 2: return r2;
+      case 3: return r3;
+      case 4: return r4;
+      case 5: return r5;
+      case 6: return r6;
+      default: return r7;
+    }
+  }
+  __device__ __forceinline__ void set(int i, float v) {
+    switch (i) {
+      case 0: r0 = v; break;
+      case 1: r1 = v; break;
+      case 2: r2 = v; break;
+      case 3: r3 = v; break;
+      case 4: r4 = v; break;
+      case 5: r5 = v; break;
+      case 6: r6 = v; break;
+      default: r7 = v; break;
+    }
+  }
+};
+
+// ---- host-side analysis ------------------------------------------------------
+
+static bool rows_leaf_ok(const ktir_leaf_t& L, int nd) {
+  return L.offsets == 0 && L.winner == 0 && L.strides[nd - 1] == 1 && (L.flags & KTIR_LEAF_VEC) &&
+         (L.dtype == KTIR_F16 || L.dtype == KTIR_BF16 || L.dtype == KTIR_F32);
+}
+
+static bool row_op_ok(int op) {
+  switch (op) {
+    case KTIR_OP_LD: case KTIR_OP_ST: case KTIR_OP_IDX: case KTIR_OP_RED: case KTIR_OP_FOLD:
+    case KTIR_OP_ELEM: case KTIR_OP_ENDELEM: case KTIR_OP_NOP:
+      return false;
+  }
+  return true;
+}
+
+// operands a row instruction reads: bit 0 a, bit 1 b, bit 2 c
+static int row_op_reads(int op) {
+  if (op == KTIR_OP_CONST || op == KTIR_OP_LANE) return 0;
+  if (op == KTIR_OP_SELECT || op == KTIR_OP_FMA) return 7;
+  if (op >= KTIR_OP_ADDF || op == KTIR_OP_CMPF || op == KTIR_OP_CMPI) return 3;
+  return 1;
+}
+
+// Chain ops the kernel implements (straight-line code per op keeps the kernel
+// small): f32 arithmetic and f32 -> f16 / bf16 / f32 rounding casts.
+static bool chain_unary(const ktir_instr_t& x) {
+  switch (x.op) {
+    case KTIR_OP_NEGF: case KTIR_OP_ABSF: case KTIR_OP_EXP: case KTIR_OP_SQRT: case KTIR_OP_RSQRT:
+      return x.dt == KTIR_F32;
+    case KTIR_OP_CAST:
+      return x.aux == KTIR_F32 && (x.dt == KTIR_F32 || x.dt == KTIR_F16 || x.dt == KTIR_BF16);
+  }
+  return false;
+}
+
+static bool chain_binary(const ktir_instr_t& x) {
+  switch (x.op) {
+    case KTIR_OP_ADDF: case KTIR_OP_SUBF: case KTIR_OP_MULF: case KTIR_OP_DIVF: case KTIR_OP_MAXIMUMF:
+    case KTIR_OP_MINIMUMF:
+      return x.dt == KTIR_F32;
+  }
+  return false;
+}
+
+static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
+  enum { K_NONE = 0, K_ROW = 1, K_LEAF = 2, K_ACC = 3 };
+  int kind[KTIR_NREG], slot_of[KTIR_NREG];
+  for (int i = 0; i < KTIR_NREG; ++i) kind[i] = K_NONE, slot_of[i] = -1;
+  const int nd = P.ndim;
+  R.n_steps = 0;
+  R.n_slots = 0;
+  auto slot_for = [&](int leaf) -> int {
+    for (int s = 0; s < R.n_slots; ++s)
+      if (R.slot_leaf[s] == leaf) return s;
+    if (R.n_slots == 2 || !rows_leaf_ok(P.leaves[leaf], nd)) return -1;
+    R.slot_leaf[R.n_slots] = (int8_t)leaf;
+    return R.n_slots++;
+  };
+  int pc = 0;
+  while (pc < P.n_instr) {
+    const ktir_instr_t& in = P.instr[pc];
+    if (R.n_steps == RC_MAX_STEPS) return false;
+    RcStep& S = R.steps[R.n_steps];
+    S = RcStep{};
+    if (in.op == KTIR_OP_ST) {
+      // a row-level value stored once per row (column 0 of the leaf's row)
+      if (in.a < 0 || in.a >= KTIR_NREG || kind[in.a] != K_ROW || P.leaves[in.aux].offsets != 0 ||
+          P.leaves[in.aux].winner != 0)
+        return false;
+      S.kind = 2;
+      S.pc = (int8_t)pc;
+      S.st_leaf = (int8_t)in.aux;
+      ++R.n_steps;
+      ++pc;
+      continue;
+    }
+    if (in.op != KTIR_OP_ELEM) {
+      if (!row_op_ok(in.op) || !simple_op(in.op) || in.dst < 0 || in.dst >= KTIR_NREG) return false;
+      const int reads = row_op_reads(in.op);
+      if (((reads & 1) && (in.a < 0 || in.a >= KTIR_NREG || kind[in.a] != K_ROW)) ||
+          ((reads & 2) && (in.b < 0 || in.b >= KTIR_NREG || kind[in.b] != K_ROW)) ||
+          ((reads & 4) && (in.c < 0 || in.c >= KTIR_NREG || kind[in.c] != K_ROW)))
+        return false;
+      S.kind = 0;
+      S.pc = (int8_t)pc;
+      kind[in.dst] = K_ROW;
+      ++R.n_steps;
+      ++pc;
+      continue;
+    }
+    const int end = in.aux;
+    if (end <= pc || end >= P.n_instr || P.instr[end].op != KTIR_OP_ENDELEM) return false;
+    S.kind = 1;
+    S.src = -1;
+    int acc = -1;
+    bool done = false;
+    // start the chain from the cached row held by register r
+    auto start = [&](int r) -> bool {
+      if (acc >= 0 || kind[r] != K_LEAF) return false;
+      S.src = (int8_t)slot_of[r];
+      acc = r;
+      return true;
+    };
+    auto add = [&](const RcOp& o) -> bool {
+      if (S.n_ops == RC_MAX_OPS) return false;
+      S.ops[S.n_ops++] = o;
+      return true;
+    };
+    for (int q = pc + 1; q < end; ++q) {
+      const ktir_instr_t& x = P.instr[q];
+      if (done || x.dst < 0 || x.dst >= KTIR_NREG || x.a < 0 || x.a >= KTIR_NREG || x.b < 0 || x.b >= KTIR_NREG)
+        return false;
+      if (x.op == KTIR_OP_LD) {
+        const int s = slot_for(x.aux);
+        if (s < 0 || x.dst == acc) return false;
+        kind[x.dst] = K_LEAF;
+        slot_of[x.dst] = s;
+      } else if (x.op == KTIR_OP_CAST && kind[x.a] == K_LEAF && x.dt == KTIR_F32 &&
+                 x.aux == P.leaves[R.slot_leaf[slot_of[x.a]]].dtype) {
+        // exact widening of a cached row: the cache holds it as f32 already
+        kind[x.dst] = K_LEAF;
+        slot_of[x.dst] = slot_of[x.a];
+      } else if (chain_unary(x)) {
+        if (kind[x.a] == K_LEAF && !start(x.a)) return false;
+        if (x.a != acc) return false;
+        if (!add(RcOp{x.op, x.dt, (int8_t)x.aux, 0, 0, 0, {0, 0}})) return false;
+        acc = x.dst;
+      } else if (chain_binary(x)) {
+        int a = x.a, b = x.b;
+        if (a != acc && b != acc) {
+          if (kind[a] == K_LEAF) {
+            if (!start(a)) return false;
+          } else if (kind[b] == K_LEAF) {
+            if (!start(b)) return false;
+          } else {
+            return false;
+          }
+        }
+        RcOp o{x.op, x.dt, 0, 0, 0, 0, {0, 0}};
+        if (a == acc && b == acc) {
+          o.kind = 3;
+        } else {
+          const bool left_is_acc = (a == acc);
+          const int other = left_is_acc ? b : a;
+          o.swap = left_is_acc ? 0 : 1;
+          if (kind[other] == K_ROW) {
+            o.kind = 1;
+            o.idx = (int8_t)other;
+          } else if (kind[other] == K_LEAF) {
+            o.kind = 2;
+            o.idx = (int8_t)slot_of[other];
+          } else {
+            return false;
+          }
+        }
+        if (!add(o)) return false;
+        acc = x.dst;
+      } else if (x.op == KTIR_OP_RED || x.op == KTIR_OP_ST) {
+        if (kind[x.a] == K_LEAF && acc < 0 && !start(x.a)) return false;
+        if (x.a != acc) return false;
+        if (x.op == KTIR_OP_RED) {
+          S.end = 0;
+        } else {
+          if (!rows_leaf_ok(P.leaves[x.aux], nd)) return false;
+          S.end = 1;
+          S.st_leaf = (int8_t)x.aux;
+        }
+        done = true;
+      } else {
+        return false;
+      }
+      if (x.op != KTIR_OP_RED && x.op != KTIR_OP_ST && x.op != KTIR_OP_LD &&
+          !(x.op == KTIR_OP_CAST && kind[x.dst] == K_LEAF))
+        kind[x.dst] = K_ACC;
+    }
+    if (!done) return false;
+    pc = end + 1;
+    if (S.end == 0) {
+      if (pc >= P.n_instr || P.instr[pc].op != KTIR_OP_FOLD) return false;
+      const ktir_instr_t& f = P.instr[pc];
+      if (f.dst < 0 || f.dst >= KTIR_NREG || f.aux >= KTIR_OP_ADDI) return false;
+      if (f.aux != KTIR_OP_ADDF && f.aux != KTIR_OP_MULF && f.aux != KTIR_OP_MAXIMUMF && f.aux != KTIR_OP_MINIMUMF)
+        return false;
+      if (f.dt != KTIR_F32 && f.dt != KTIR_F16 && f.dt != KTIR_BF16) return false;
+      S.fold_op = (int8_t)f.aux;
+      S.fold_dt = f.dt;
+      S.dst = f.dst;
+      kind[f.dst] = K_ROW;
+      ++pc;
+    }
+    // registers written in the block other than the cached rows are gone after it
+    for (int i = 0; i < KTIR_NREG; ++i)
+      if (kind[i] == K_ACC) kind[i] = K_NONE;
+    ++R.n_steps;
+  }
+  // fused heads, and reuse of exp(x - m) between two passes that compute it
+  int last_subexp = -1;
+  for (int i = 0; i < R.n_steps; ++i) {
+    RcStep& S = R.steps[i];
+    if (S.kind == 0) {
+      // a row instruction that rewrites the subtracted register ends the reuse window
+      if (last_subexp >= 0 && P.instr[S.pc].dst == R.steps[last_subexp].ops[0].idx) last_subexp = -1;
+      continue;
+    }
+    if (S.kind != 1) continue;
+    const RcOp* o = S.ops;
+    if (S.n_ops >= 2 && o[0].op == KTIR_OP_SUBF && o[0].kind == 1 && !o[0].swap && o[1].op == KTIR_OP_EXP &&
+        o[1].kind == 0) {
+      S.head = 1;
+      if (last_subexp >= 0 && R.steps[last_subexp].src == S.src && R.steps[last_subexp].ops[0].idx == o[0].idx) {
+        R.steps[last_subexp].save = 1;
+        S.reuse = 1;
+      }
+      last_subexp = i;
+    } else if (S.n_ops >= 1 && o[0].op == KTIR_OP_MULF && o[0].kind == 3) {
+      S.head = 2;
+    }
+  }
+  return R.n_steps > 0;
+}
+
+// ---- device side ---------------------------------------------------------------
+
+template <int DT>
+__device__ __forceinline__ void load_pair(const void* ptr, int64_t e0, float& a, float& b) {
+  if (DT == KTIR_F32) {
+    const gf2 w = *(const KTIR_G(gf2)*)((const KTIR_G(float)*)ptr + e0);
+    a = w[0];
+    b = w[1];
+  } else {
+    const uint32_t w = *(const KTIR_G(uint32_t)*)((const KTIR_G(uint16_t)*)ptr + e0);
+    if (DT == KTIR_BF16) {
+      a = __uint_as_float(w << 16);
+      b = __uint_as_float(w & 0xffff0000u);
+    } else {
+      a = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+      b = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_pair(void* ptr, int64_t e0, float a, float b) {
+  if (DT == KTIR_F32) {
+    *(KTIR_G(gf2)*)((KTIR_G(float)*)ptr + e0) = gf2{a, b};
+  } else if (DT == KTIR_BF16) {
+    *(KTIR_G(uint32_t)*)((KTIR_G(uint16_t)*)ptr + e0) =
+        (__float_as_uint(round_bf16(a)) >> 16) | (__float_as_uint(round_bf16(b)) & 0xffff0000u);
+  } else {
+    *(KTIR_G(uint32_t)*)((KTIR_G(uint16_t)*)ptr + e0) = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+                                        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+  }
+}
+
+// a row of n = tpr * E elements starting at element `base` of L: straight-line
+// paired accesses when the row lies inside the allocation, else per element
+// with the reference's out-of-range rules (reads 0, writes dropped)
+template <int E>
+__device__ __forceinline__ void load_row(const ktir_leaf_t& L, int64_t base, int t, int tpr, float (&c)[E]) {
+  if (base >= L.lo && base + (int64_t)tpr * E <= L.hi) {
+    switch (L.dtype) {
+      case KTIR_F16:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) load_pair<KTIR_F16>((const void*)L.ptr, base + 2 * (k * tpr + t), c[2 * k], c[2 * k + 1]);
+        return;
+      case KTIR_BF16:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) load_pair<KTIR_BF16>((const void*)L.ptr, base + 2 * (k * tpr + t), c[2 * k], c[2 * k + 1]);
+        return;
+      default:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) load_pair<KTIR_F32>((const void*)L.ptr, base + 2 * (k * tpr + t), c[2 * k], c[2 * k + 1]);
+        return;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < E; ++q) {
+    const int64_t e = base + 2 * ((q >> 1) * tpr + t) + (q & 1);
+    c[q] = (e >= L.lo && e < L.hi) ? load_elem(L.ptr, e, L.dtype) : 0.f;
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void store_row(const ktir_leaf_t& L, int64_t base, int t, int tpr, const float (&v)[E]) {
+  if (base >= L.lo && base + (int64_t)tpr * E <= L.hi) {
+    switch (L.dtype) {
+      case KTIR_F16:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) store_pair<KTIR_F16>((void*)L.ptr, base + 2 * (k * tpr + t), v[2 * k], v[2 * k + 1]);
+        return;
+      case KTIR_BF16:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) store_pair<KTIR_BF16>((void*)L.ptr, base + 2 * (k * tpr + t), v[2 * k], v[2 * k + 1]);
+        return;
+      default:
+#pragma unroll
+        for (int k = 0; k < E / 2; ++k) store_pair<KTIR_F32>((void*)L.ptr, base + 2 * (k * tpr + t), v[2 * k], v[2 * k + 1]);
+        return;
+    }
+  }
+  for (int q = 0; q < E; ++q) {
+    const int64_t e = base + 2 * ((q >> 1) * tpr + t) + (q & 1);
+    if (e >= L.lo && e < L.hi) store_elem(L.ptr, e, L.dtype, v[q]);
+  }
+}
+
+__device__ __forceinline__ float maxnan(float x, float y) {
+  return (x != x || y != y) ? __int_as_float(0x7fc00000) : fmaxf(x, y);
+}
+__device__ __forceinline__ float minnan(float x, float y) {
+  return (x != x || y != y) ? __int_as_float(0x7fc00000) : fminf(x, y);
+}
+
+// e^x on the hardware exp2: 2^(x log2 e).  The rounding of x log2 e costs
+// about |x| * 6e-8 relative error (a few f32 ulps for softmax arguments).
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// x / s for a row scalar s with r = 1/s correctly rounded: q = x r, then one
+// Markstein correction q + (x - s q) r (fused); within one ulp of x / s and
+// nearly always its correct rounding.  Operands near the ends of the
+// exponent range take __fdiv_rn.
+__device__ __forceinline__ float div_by(float x, float s, float r) {
+  const float q = x * r;
+  const float res = __builtin_fmaf(-s, q, x);
+  return __builtin_fmaf(res, r, q);
+}
+
+// one chain op over the E chain values; the opcode and operand kind are
+// uniform, so both are dispatched once outside the element loops
+template <int E>
+__device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, const float (&c0)[E],
+                                         const float (&c1)[E]) {
+#define RC_UN(expr) { _Pragma("unroll") for (int e = 0; e < E; ++e) { const float x = v[e]; v[e] = (expr); } return; }
+  if (o.kind == 0) {
+    switch (o.op) {
+      case KTIR_OP_NEGF: RC_UN(-x)
+      case KTIR_OP_ABSF: RC_UN(fabsf(x))
+      case KTIR_OP_EXP: RC_UN(exp_hw(x))
+      case KTIR_OP_SQRT: RC_UN(__fsqrt_rn(x))
+      case KTIR_OP_RSQRT: RC_UN(__fdiv_rn(1.f, __fsqrt_rn(x)))
+      case KTIR_OP_CAST:
+        if (o.dt == KTIR_F16) RC_UN(round_f16(x))
+        if (o.dt == KTIR_BF16) RC_UN(round_bf16(x))
+        return;
+    }
+    return;
+  }
+#undef RC_UN
+  if (o.kind == 1) {
+    // row scalar operand: no per-element operand copies
+#define RC_S(expr) { _Pragma("unroll") for (int e = 0; e < E; ++e) { const float x = v[e]; v[e] = (expr); } return; }
+    switch (o.op) {
+      case KTIR_OP_ADDF: RC_S(__fadd_rn(x, s))
+      case KTIR_OP_MULF: RC_S(__fmul_rn(x, s))
+      case KTIR_OP_MAXIMUMF: RC_S(maxnan(x, s))
+      case KTIR_OP_MINIMUMF: RC_S(minnan(x, s))
+      case KTIR_OP_SUBF: if (o.swap) RC_S(__fsub_rn(s, x)) else RC_S(__fsub_rn(x, s))
+      case KTIR_OP_DIVF:
+        if (o.swap) RC_S(__fdiv_rn(s, x))
+        {
+          const float r = __fdiv_rn(1.f, s);
+          const float as = fabsf(s);
+          if (as > 1e-30f && as < 1e30f && r == r) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+              const float x = v[e];
+              v[e] = fabsf(x) < 1e30f ? div_by(x, s, r) : __fdiv_rn(x, s);
+            }
+            return;
+          }
+          RC_S(__fdiv_rn(x, s))
+        }
+    }
+    return;
+#undef RC_S
+  }
+  // operand from the cached rows or the chain value itself
+#define RC_B(expr)                                                          \
+  {                                                                         \
+    _Pragma("unroll") for (int e = 0; e < E; ++e) {                         \
+      const float p = v[e], q = o.kind == 3 ? p : (o.idx ? c1[e] : c0[e]);  \
+      const float l = o.swap ? q : p, r = o.swap ? p : q;                   \
+      v[e] = (expr);                                                        \
+    }                                                                       \
+    return;                                                                 \
+  }
+  switch (o.op) {
+    case KTIR_OP_ADDF: RC_B(__fadd_rn(l, r))
+    case KTIR_OP_SUBF: RC_B(__fsub_rn(l, r))
+    case KTIR_OP_MULF: RC_B(__fmul_rn(l, r))
+    case KTIR_OP_DIVF: RC_B(__fdiv_rn(l, r))
+    case KTIR_OP_MAXIMUMF: RC_B(maxnan(l, r))
+    case KTIR_OP_MINIMUMF: RC_B(minnan(l, r))
+  }
+#undef RC_B
+}
+
+// fold combine in the fold's dtype (f32, or rounded to f16 / bf16)
+template <int OP, int DT>
+__device__ __forceinline__ float fold_op(float x, float y) {
+  float r;
+  if (OP == KTIR_OP_ADDF) r = __fadd_rn(x, y);
+  else if (OP == KTIR_OP_MULF) r = __fmul_rn(x, y);
+  else if (OP == KTIR_OP_MAXIMUMF) return maxnan(x, y);
+  else return minnan(x, y);
+  return DT == KTIR_F32 ? r : (DT == KTIR_F16 ? round_f16(r) : round_bf16(r));
+}
+
+// fold of the group's n = TPR * E values (pairwise-halving order, see top)
+template <int E, int OP, int DT>
+__device__ __forceinline__ float fold_group_t(float (&v)[E], int tpr, float* xch) {
+#pragma unroll
+  for (int h = E / 4; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int k = 0; k < h; ++k) {
+      v[2 * k] = fold_op<OP, DT>(v[2 * k], v[2 * (k + h)]);
+      v[2 * k + 1] = fold_op<OP, DT>(v[2 * k + 1], v[2 * (k + h) + 1]);
+    }
+  }
+  float a = v[0], b = v[1];
+  for (int s = tpr >> 1; s >= 64; s >>= 1) {   // partners in other wavefronts: through LDS
+    __syncthreads();
+    xch[2 * threadIdx.x] = a;
+    xch[2 * threadIdx.x + 1] = b;
+    __syncthreads();
+    const int p = threadIdx.x ^ s;
+    a = fold_op<OP, DT>(a, xch[2 * p]);
+    b = fold_op<OP, DT>(b, xch[2 * p + 1]);
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    if (s < tpr) {
+      a = fold_op<OP, DT>(a, __shfl_xor(a, s));
+      b = fold_op<OP, DT>(b, __shfl_xor(b, s));
+    }
+  }
+  return fold_op<OP, DT>(a, b);
+}
+
+template <int E, int OP>
+__device__ __forceinline__ float fold_group_d(float (&v)[E], int dt, int tpr, float* xch) {
+  if (dt == KTIR_F32) return fold_group_t<E, OP, KTIR_F32>(v, tpr, xch);
+  if (dt == KTIR_F16) return fold_group_t<E, OP, KTIR_F16>(v, tpr, xch);
+  return fold_group_t<E, OP, KTIR_BF16>(v, tpr, xch);
+}
+
+template <int E>
+__device__ __forceinline__ float fold_group(float (&v)[E], int op, int dt, int tpr, float* xch) {
+  switch (op) {
+    case KTIR_OP_ADDF: return fold_group_d<E, KTIR_OP_ADDF>(v, dt, tpr, xch);
+    case KTIR_OP_MULF: return fold_group_d<E, KTIR_OP_MULF>(v, dt, tpr, xch);
+    case KTIR_OP_MAXIMUMF: return fold_group_d<E, KTIR_OP_MAXIMUMF>(v, dt, tpr, xch);
+    default: return fold_group_d<E, KTIR_OP_MINIMUMF>(v, dt, tpr, xch);
+  }
+}
+
+__device__ __forceinline__ void row_exec(const ktir_prog_t& P, const ktir_instr_t in, float* rr, int64_t lane) {
+  const int op = in.op;
+  const float a = rr[in.a], b = rr[in.b];
+  float v;
+  if (op >= KTIR_OP_NEGF && op < KTIR_OP_ADDF) {
+    v = unop_simple(op, in.dt, a);
+  } else if (op >= KTIR_OP_ADDI) {
+    v = __int_as_float(binop_i_simple(op, __float_as_int(a), __float_as_int(b)));
+  } else if (op >= KTIR_OP_ADDF) {
+    v = binop_f_simple(op, in.dt, a, b);
+  } else {
+    switch (op) {
+      case KTIR_OP_CONST: v = __int_as_float(in.imm); break;
+      case KTIR_OP_LANE: {
+        const double d = ((const double*)P.lane_scalars)[lane * P.n_lane_scalars + in.aux];
+        v = is_float_dt(in.dt) ? round_to((float)d, in.dt) : __int_as_float((int)(long long)d);
+        break;
+      }
+      case KTIR_OP_CAST: v = cast_val(a, in.aux, in.dt); break;
+      case KTIR_OP_BITCAST: v = a; break;
+      case KTIR_OP_SELECT: v = __float_as_int(a) ? b : rr[in.c]; break;
+      case KTIR_OP_FMA: v = round_to(__fadd_rn(__fmul_rn(a, b), rr[in.c]), in.dt); break;
+      case KTIR_OP_CMPF: v = __int_as_float(cmp_f(in.aux, a, b)); break;
+      case KTIR_OP_CMPI: v = __int_as_float(cmp_i(in.aux, __float_as_int(a), __float_as_int(b))); break;
+      default: v = 0.f;
+    }
+  }
+  rr[in.dst] = v;
+}
+
+template <int E>
+__global__ __launch_bounds__(256) void prog_rowchain(const ktir_prog_t P, const RcPlan R, int tpr_log2,
+                                                     int64_t total_rows) {
+  __shared__ float xch[512];
+  // row registers: one copy per wavefront (a group spans whole wavefronts) or
+  // per group (several groups share a wavefront); each copy is written and
+  // read by one wavefront only, in program order
+  __shared__ float regs[8][KTIR_NREG];
+  const int tpr = 1 << tpr_log2;
+  const int grp = threadIdx.x >> tpr_log2, t = threadIdx.x & (tpr - 1);
+  const int rpw = 256 >> tpr_log2;
+  float* rr = regs[tpr >= 64 ? (threadIdx.x >> 6) : grp];
+  const int nd = P.ndim;
+  const int64_t inner = P.shape[nd - 1];
+  int64_t rows_per_lane = 1;
+  for (int d = 0; d < nd - 1; ++d) rows_per_lane *= P.shape[d];
+  for (int64_t row0 = (int64_t)blockIdx.x * rpw; row0 < total_rows; row0 += (int64_t)gridDim.x * rpw) {
+    const int64_t row = row0 + grp;
+    const bool active = row < total_rows;
+    const int64_t rw = active ? row : total_rows - 1;
+    const int64_t lane = rw / rows_per_lane;
+    int64_t rr_idx = rw - lane * rows_per_lane;
+    int64_t idx[KTIR_MAX_DIMS - 1] = {0, 0, 0};
+#pragma unroll
+    for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+      if (d < nd - 1) {
+        const int64_t q = rr_idx / P.shape[d];
+        idx[d] = rr_idx - q * P.shape[d];
+        rr_idx = q;
+      }
+    }
+    // element offset of column 0 of this row in leaf L
+    auto row_base = [&](const ktir_leaf_t& L) {
+      int64_t e = lane_offset(L, lane);
+#pragma unroll
+      for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
+        if (d < nd - 1) e += idx[d] * L.strides[d];
+      return e;
+    };
+    float c0[E], c1[E], kept[E];
+    load_row<E>(P.leaves[R.slot_leaf[0]], row_base(P.leaves[R.slot_leaf[0]]), t, tpr, c0);
+    if (R.n_slots > 1) load_row<E>(P.leaves[R.slot_leaf[1]], row_base(P.leaves[R.slot_leaf[1]]), t, tpr, c1);
+    else
+#pragma unroll
+      for (int e = 0; e < E; ++e) c1[e] = 0.f;
+    for (int si = 0; si < R.n_steps; ++si) {
+      const RcStep& S = R.steps[si];
+      if (S.kind == 0) {
+        row_exec(P, P.instr[S.pc], rr, lane);
+        continue;
+      }
+      if (S.kind == 2) {
+        const ktir_leaf_t& L = P.leaves[S.st_leaf];
+        const int64_t e = row_base(L);
+        if (active && t == 0 && e >= L.lo && e < L.hi) store_elem(L.ptr, e, L.dtype, rr[P.instr[S.pc].a]);
+        continue;
+      }
+      float v[E];
+      int oi = 0;
+      if (S.reuse) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = kept[e];
+        oi = 2;
+      } else if (S.head == 1) {
+        const float m = rr[S.ops[0].idx];
+        if (S.src) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) v[e] = exp_hw(__fsub_rn(c1[e], m));
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) v[e] = exp_hw(__fsub_rn(c0[e], m));
+        }
+        oi = 2;
+      } else if (S.head == 2) {
+        if (S.src) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) v[e] = __fmul_rn(c1[e], c1[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) v[e] = __fmul_rn(c0[e], c0[e]);
+        }
+        oi = 1;
+      } else if (S.src) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = c1[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = c0[e];
+      }
+      if (S.save) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) kept[e] = v[e];
+      }
+      for (; oi < S.n_ops; ++oi) {
+        const RcOp o = S.ops[oi];
+        apply_op<E>(o, v, o.kind == 1 ? rr[o.idx] : 0.f, c0, c1);
+      }
+      if (S.end == 0) {
+        const float f = fold_group<E>(v, S.fold_op, S.fold_dt, tpr, xch);
+        rr[S.dst] = f;
+      } else if (active) {
+        store_row<E>(P.leaves[S.st_leaf], row_base(P.leaves[S.st_leaf]), t, tpr, v);
+      }
+    }
+    (void)inner;
+    __syncthreads();    // the next row's folds reuse xch
+  }
+}
+
+// ---- one wavefront per row, rows staged in LDS -----------------------------------
+//
+// For rows of n = 128 K elements whose cached leaves fill whole 1 KB blocks: a
+// wavefront owns a row, the row's cached leaves move HBM -> registers -> LDS
+// (the next row's loads are in flight while this one is computed; leaves that
+// are the same for every row are staged once), and lane l handles the element
+// pairs 128 k + 2 l + {0, 1}, k < K.  Folds: the lane's pairs go through the
+// in-thread levels of the halving tree (the bits of k), then lanes
+// l ^ 32 .. l ^ 1, then the two elements of the pair.
+
+// Self-contained plan of the row-wave kernel (copied to LDS by each
+// workgroup, so the kernel's control reads are LDS reads that never wait
+// behind the row loads in flight).
+struct RwLeaf {
+  uint64_t ptr, lane_base;
+  int64_t base, lane_stride, lo, hi;
+  int64_t strides[KTIR_MAX_DIMS - 1];   // outer dims
+  int32_t dtype, esize;
+};
+
+struct RwHead {
+  int8_t kind, src, n_ops, end, fold_op, fold_dt, dst, out;   // out: store leaf (index into RwPlan.leaf)
+  int8_t head, pad[3];
+  ktir_instr_t ins;                     // kind 0: the row instruction; kind 2: the row-level store
+};
+
+struct RwStep : RwHead {
+  RcOp ops[RC_MAX_OPS];
+};
+
+struct RwPlan {
+  int32_t n_steps, n_slots, nd, n_leaves;
+  int64_t shape[KTIR_MAX_DIMS];
+  uint64_t lane_scalars;
+  int64_t n_lane_scalars;
+  int32_t off[2], bytes[2], inv[2];
+  RwLeaf leaf[4];                       // 0, 1: cached slots; then store leaves
+  RwStep steps[RC_MAX_STEPS];
+};
+
+struct RwOut {          // the store leaf of a pass, by value (no pointer into the kernel arguments)
+  uint64_t ptr;
+  int64_t lo, hi, base;
+  int dt;
+};
+
+__device__ __forceinline__ void global_pair_store(const RwOut& L, int64_t e0, float a, float b) {
+  if (e0 >= L.lo && e0 + 2 <= L.hi) {
+    switch (L.dt) {
+      case KTIR_F32: store_pair<KTIR_F32>((void*)L.ptr, e0, a, b); return;
+      case KTIR_BF16: store_pair<KTIR_BF16>((void*)L.ptr, e0, a, b); return;
+      default: store_pair<KTIR_F16>((void*)L.ptr, e0, a, b); return;
+    }
+  }
+  if (e0 >= L.lo && e0 < L.hi) store_elem(L.ptr, e0, L.dt, a);
+  if (e0 + 1 >= L.lo && e0 + 1 < L.hi) store_elem(L.ptr, e0 + 1, L.dt, b);
+}
+
+__device__ __forceinline__ float fold_rt(int op, float x, float y) {
+  switch (op) {
+    case KTIR_OP_ADDF: return __fadd_rn(x, y);
+    case KTIR_OP_MULF: return __fmul_rn(x, y);
+    case KTIR_OP_MAXIMUMF: return maxnan(x, y);
+    default: return minnan(x, y);
+  }
+}
+
+// Pairs k = c NB + q (c < B) of a cached row in LDS: v[2c], v[2c + 1] are the
+// elements 128 k + 2 l + {0, 1}.
+template <int B, int NB>
+__device__ __forceinline__ void rw_lds_row(const uint8_t* sp, int dp, int q, int l, float (&v)[2 * B]) {
+  if (dp == KTIR_F32) {
+#pragma unroll
+    for (int c = 0; c < B; ++c) {
+      const gf2 w = *(const gf2*)(sp + 4 * (128 * (c * NB + q) + 2 * l));
+      v[2 * c] = w[0];
+      v[2 * c + 1] = w[1];
+    }
+  } else if (dp == KTIR_BF16) {
+#pragma unroll
+    for (int c = 0; c < B; ++c) {
+      const uint32_t w = *(const uint32_t*)(sp + 2 * (128 * (c * NB + q) + 2 * l));
+      v[2 * c] = __uint_as_float(w << 16);
+      v[2 * c + 1] = __uint_as_float(w & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < B; ++c) {
+      const uint32_t w = *(const uint32_t*)(sp + 2 * (128 * (c * NB + q) + 2 * l));
+      v[2 * c] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+      v[2 * c + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+  }
+}
+
+// v <- v op c (or c op v when swapped), element by element
+template <int E>
+__device__ __forceinline__ void rw_binary(int op, bool swap, float (&v)[E], const float (&c)[E]) {
+#define RW_B(expr)                                           \
+  {                                                          \
+    if (swap) {                                              \
+      _Pragma("unroll") for (int e = 0; e < E; ++e) {        \
+        const float x = c[e], y = v[e];                      \
+        v[e] = (expr);                                       \
+      }                                                      \
+    } else {                                                 \
+      _Pragma("unroll") for (int e = 0; e < E; ++e) {        \
+        const float x = v[e], y = c[e];                      \
+        v[e] = (expr);                                       \
+      }                                                      \
+    }                                                        \
+    return;                                                  \
+  }
+  switch (op) {
+    case KTIR_OP_ADDF: RW_B(__fadd_rn(x, y))
+    case KTIR_OP_SUBF: RW_B(__fsub_rn(x, y))
+    case KTIR_OP_MULF: RW_B(__fmul_rn(x, y))
+    case KTIR_OP_DIVF: RW_B(__fdiv_rn(x, y))
+    case KTIR_OP_MAXIMUMF: RW_B(maxnan(x, y))
+    case KTIR_OP_MINIMUMF: RW_B(minnan(x, y))
+  }
+#undef RW_B
+}
+
+// fold of the step's B pairs to one pair: the halving tree over c (c with
+// c + B/2, then c + B/4, ...), the left operand the lower index
+template <int B, int OP>
+__device__ __forceinline__ void rw_fold_step(float (&v)[2 * B]) {
+#pragma unroll
+  for (int h = B / 2; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int c = 0; c < h; ++c) {
+      v[2 * c] = fold_op<OP, KTIR_F32>(v[2 * c], v[2 * (c + h)]);
+      v[2 * c + 1] = fold_op<OP, KTIR_F32>(v[2 * c + 1], v[2 * (c + h) + 1]);
+    }
+  }
+}
+
+// One pass of a row.  Lane l holds the K pairs k of its row (elements
+// 128 k + 2 l + {0, 1}) as NB steps of B pairs, step q holding k = c NB + q:
+// the whole step's values are in registers, so every op of the pass is
+// dispatched once per step.  A fold pass reduces each step by the halving
+// tree over c (the tree's levels over the high bits of k), the NB <= 4 step
+// roots by its levels over the low bits of k (the bits of q), then lanes
+// l ^ 32 .. l ^ 1, then the two elements of the pair.  A store pass writes every pair.
+template <int K>
+__device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const uint8_t* s0, int d0,
+                                         const uint8_t* s1, int d1, const RowRegs& rr, const RwOut& SL,
+                                         bool out_in_range, int l) {
+  constexpr int B = K < 16 ? K : 16;
+  constexpr int NB = K / B;
+  static_assert(NB <= 4, "at most four steps per row");
+  const bool fold = S.end == 0;
+  const int fop = S.fold_op;
+  const int n_ops = S.n_ops;
+  const uint8_t* sp = S.src ? s1 : s0;
+  const int dp = S.src ? d1 : d0;
+  float ra[NB], rb[NB];
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    float v[2 * B];
+    rw_lds_row<B, NB>(sp, dp, q, l, v);
+    int oi = 0;
+    if (S.head == 1) {
+      const float m = rr.get(uniform_copy(ops[0]).idx);
+#pragma unroll
+      for (int e = 0; e < 2 * B; ++e) v[e] = exp_hw(__fsub_rn(v[e], m));
+      oi = 2;
+    } else if (S.head == 2) {
+#pragma unroll
+      for (int e = 0; e < 2 * B; ++e) v[e] = __fmul_rn(v[e], v[e]);
+      oi = 1;
+    }
+    for (; oi < n_ops; ++oi) {
+      const RcOp o = uniform_copy(ops[oi]);
+      if (o.kind == 2) {
+        float c[2 * B];
+        rw_lds_row<B, NB>(o.idx ? s1 : s0, o.idx ? d1 : d0, q, l, c);
+        rw_binary<2 * B>(o.op, o.swap, v, c);
+      } else if (o.kind == 3) {
+        float c[2 * B];
+#pragma unroll
+        for (int e = 0; e < 2 * B; ++e) c[e] = v[e];
+        rw_binary<2 * B>(o.op, false, v, c);
+      } else {
+        apply_op<2 * B>(o, v, o.kind == 1 ? rr.get(o.idx) : 0.f, v, v);
+      }
+    }
+    if (!fold) {
+      if (out_in_range) {
+        switch (SL.dt) {
+          case KTIR_F32:
+#pragma unroll
+            for (int c = 0; c < B; ++c)
+              store_pair<KTIR_F32>((void*)SL.ptr, SL.base + 128 * (c * NB + q) + 2 * l, v[2 * c], v[2 * c + 1]);
+            break;
+          case KTIR_BF16:
+#pragma unroll
+            for (int c = 0; c < B; ++c)
+              store_pair<KTIR_BF16>((void*)SL.ptr, SL.base + 128 * (c * NB + q) + 2 * l, v[2 * c], v[2 * c + 1]);
+            break;
+          default:
+#pragma unroll
+            for (int c = 0; c < B; ++c)
+              store_pair<KTIR_F16>((void*)SL.ptr, SL.base + 128 * (c * NB + q) + 2 * l, v[2 * c], v[2 * c + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < B; ++c) global_pair_store(SL, SL.base + 128 * (c * NB + q) + 2 * l, v[2 * c], v[2 * c + 1]);
+      }
+      continue;
+    }
+    switch (fop) {
+      case KTIR_OP_ADDF: rw_fold_step<B, KTIR_OP_ADDF>(v); break;
+      case KTIR_OP_MULF: rw_fold_step<B, KTIR_OP_MULF>(v); break;
+      case KTIR_OP_MAXIMUMF: rw_fold_step<B, KTIR_OP_MAXIMUMF>(v); break;
+      default: rw_fold_step<B, KTIR_OP_MINIMUMF>(v); break;
+    }
+    ra[q] = v[0];
+    rb[q] = v[1];
+  }
+  if (!fold) return 0.f;
+  // the tree's levels over the bits of q
+#pragma unroll
+  for (int h = NB / 2; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int q = 0; q < h; ++q) {
+      ra[q] = fold_rt(fop, ra[q], ra[q + h]);
+      rb[q] = fold_rt(fop, rb[q], rb[q + h]);
+    }
+  }
+  float a = ra[0], b = rb[0];
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    a = fold_rt(fop, a, __shfl_xor(a, s));
+    b = fold_rt(fop, b, __shfl_xor(b, s));
+  }
+  return fold_rt(fop, a, b);
+}
+
+// element offset of column 0 of row r in leaf L
+__device__ __forceinline__ int64_t rw_row_base(const RwPlan& SP, const RwLeaf& L, int64_t r, int64_t rows_per_lane) {
+  const int64_t lane = r / rows_per_lane;
+  int64_t t = r - lane * rows_per_lane;
+  int64_t e = L.lane_base ? uni(((const KTIR_G(int64_t)*)L.lane_base)[lane]) : L.base + lane * L.lane_stride;
+  const int nd = __builtin_amdgcn_readfirstlane(SP.nd);
+#pragma unroll
+  for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+    if (d < nd - 1) {
+      const int64_t ext = uni(SP.shape[d]);
+      const int64_t q = t / ext;
+      e += (t - q * ext) * L.strides[d];
+      t = q;
+    }
+  }
+  return e;
+}
+
+// registers <- row r of the non-invariant slots; false (nothing read) when a
+// row is not wholly inside its allocation
+template <int NQ>
+__device__ __forceinline__ bool rw_load_regs(const RwPlan& SP, uint4 (&st)[NQ], int64_t r, int64_t rows_per_lane,
+                                             int64_t inner, int l) {
+  const int n_slots = __builtin_amdgcn_readfirstlane(SP.n_slots);
+  int q0 = 0;
+  for (int s = 0; s < n_slots; ++s) {
+    if (__builtin_amdgcn_readfirstlane(SP.inv[s])) continue;
+    const RwLeaf L = uniform_copy(SP.leaf[s]);
+    const int64_t x = rw_row_base(SP, L, r, rows_per_lane);
+    if (x < L.lo || x + inner > L.hi) return false;
+  }
+  for (int s = 0; s < n_slots; ++s) {
+    if (__builtin_amdgcn_readfirstlane(SP.inv[s])) continue;
+    const RwLeaf L = uniform_copy(SP.leaf[s]);
+    const int64_t x = rw_row_base(SP, L, r, rows_per_lane);
+    const int nq = __builtin_amdgcn_readfirstlane(SP.bytes[s]) >> 10;
+    const KTIR_G(uint8_t)* src = (const KTIR_G(uint8_t)*)L.ptr + x * L.esize + 16 * l;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      if (i >= q0 && i < q0 + nq) st[i] = __builtin_bit_cast(uint4, *(const KTIR_G(gu4)*)(src + 1024 * (i - q0)));
+    q0 += nq;
+  }
+  return true;
+}
+
+template <int NQ>
+__device__ __forceinline__ void rw_store_regs(const RwPlan& SP, const uint4 (&st)[NQ], uint8_t* lds, int l) {
+  const int n_slots = __builtin_amdgcn_readfirstlane(SP.n_slots);
+  int q0 = 0;
+  for (int s = 0; s < n_slots; ++s) {
+    if (__builtin_amdgcn_readfirstlane(SP.inv[s])) continue;
+    const int nq = __builtin_amdgcn_readfirstlane(SP.bytes[s]) >> 10;
+    uint8_t* dst = lds + __builtin_amdgcn_readfirstlane(SP.off[s]) + 16 * l;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      if (i >= q0 && i < q0 + nq) *(uint4*)(dst + 1024 * (i - q0)) = st[i];
+    q0 += nq;
+  }
+}
+
+// element by element into LDS with the reference's out-of-range read rule (0)
+__device__ __forceinline__ void rw_stage_slow(const RwPlan& SP, int s, int64_t r, int64_t rows_per_lane,
+                                              int64_t inner, uint8_t* lds, int l) {
+  const RwLeaf L = uniform_copy(SP.leaf[s]);
+  const int64_t e = rw_row_base(SP, L, r, rows_per_lane);
+  uint8_t* dst = lds + __builtin_amdgcn_readfirstlane(SP.off[s]);
+  for (int64_t i = l; i < inner; i += 64) {
+    const int64_t x = e + i;
+    const float v = (x >= L.lo && x < L.hi) ? load_elem(L.ptr, x, L.dtype) : 0.f;
+    if (L.dtype == KTIR_F32) ((float*)dst)[i] = v;
+    else if (L.dtype == KTIR_BF16) ((uint16_t*)dst)[i] = (uint16_t)(__float_as_uint(v) >> 16);
+    else ((_Float16*)dst)[i] = (_Float16)v;
+  }
+}
+
+__device__ __forceinline__ void rw_row_exec(const RwPlan& SP, const ktir_instr_t in, RowRegs& rr, int64_t lane) {
+  const int op = in.op;
+  const float a = rr.get(in.a), b = rr.get(in.b);
+  float v;
+  if (op >= KTIR_OP_NEGF && op < KTIR_OP_ADDF) {
+    v = unop_simple(op, in.dt, a);
+  } else if (op >= KTIR_OP_ADDI) {
+    v = __int_as_float(binop_i_simple(op, __float_as_int(a), __float_as_int(b)));
+  } else if (op >= KTIR_OP_ADDF) {
+    v = binop_f_simple(op, in.dt, a, b);
+  } else {
+    switch (op) {
+      case KTIR_OP_CONST: v = __int_as_float(in.imm); break;
+      case KTIR_OP_LANE: {
+        const double d = ((const KTIR_G(double)*)uni((int64_t)SP.lane_scalars))[lane * uni(SP.n_lane_scalars) + in.aux];
+        v = is_float_dt(in.dt) ? round_to((float)d, in.dt) : __int_as_float((int)(long long)d);
+        break;
+      }
+      case KTIR_OP_CAST: v = cast_val(a, in.aux, in.dt); break;
+      case KTIR_OP_BITCAST: v = a; break;
+      case KTIR_OP_SELECT: v = __float_as_int(a) ? b : rr.get(in.c); break;
+      case KTIR_OP_FMA: v = round_to(__fadd_rn(__fmul_rn(a, b), rr.get(in.c)), in.dt); break;
+      case KTIR_OP_CMPF: v = __int_as_float(cmp_f(in.aux, a, b)); break;
+      case KTIR_OP_CMPI: v = __int_as_float(cmp_i(in.aux, __float_as_int(a), __float_as_int(b))); break;
+      default: v = 0.f;
+    }
+  }
+  rr.set(in.dst, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))));
+}
+
+// Row staging: the next row's cached leaves are read into registers (NQ
+// 16-byte chunks per lane: chunk i of lane l is bytes 1024 i + 16 l of the
+// slots' rows laid end to end) while the current row is computed from LDS,
+// then written to LDS.  Plain loads and LDS stores: the compiler waits for
+// the loaded registers only where they are stored.
+template <int K, int NQ>
+__global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t total_rows) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ RwPlan SP;
+  RowRegs rr{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int l = threadIdx.x;
+  {
+    const int* src = (const int*)&Pk;
+    int* dst = (int*)&SP;
+    for (int i = l; i < (int)(sizeof(RwPlan) / 4); i += 64) dst[i] = src[i];
+  }
+  __syncthreads();
+  const int n_steps = __builtin_amdgcn_readfirstlane(SP.n_steps);
+  const int n_slots = __builtin_amdgcn_readfirstlane(SP.n_slots);
+  const int nd = __builtin_amdgcn_readfirstlane(SP.nd);
+  int64_t shape[KTIR_MAX_DIMS];
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS; ++d) shape[d] = uni(SP.shape[d]);
+  const int64_t inner = nd == 1 ? shape[0] : (nd == 2 ? shape[1] : (nd == 3 ? shape[2] : shape[3]));
+  int64_t rows_per_lane = 1;
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
+    if (d < nd - 1) rows_per_lane *= shape[d];
+  uint4 st[NQ];
+  int64_t r = blockIdx.x;
+  if (r < total_rows) {
+    for (int s = 0; s < n_slots; ++s)
+      if (__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, r, rows_per_lane, inner, lds, l);
+    if (rw_load_regs<NQ>(SP, st, r, rows_per_lane, inner, l)) {
+      rw_store_regs<NQ>(SP, st, lds, l);
+    } else {
+      for (int s = 0; s < n_slots; ++s)
+        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, r, rows_per_lane, inner, lds, l);
+    }
+  }
+  for (; r < total_rows; r += gridDim.x) {
+    const int64_t rn = r + gridDim.x;
+    const bool more = rn < total_rows;
+    const bool fast = more && rw_load_regs<NQ>(SP, st, rn, rows_per_lane, inner, l);
+    const int64_t lane = r / rows_per_lane;
+    const uint8_t* s0 = lds + __builtin_amdgcn_readfirstlane(SP.off[0]);
+    const uint8_t* s1 = n_slots > 1 ? lds + __builtin_amdgcn_readfirstlane(SP.off[1]) : nullptr;
+    const int d0 = __builtin_amdgcn_readfirstlane(SP.leaf[0].dtype);
+    const int d1 = n_slots > 1 ? __builtin_amdgcn_readfirstlane(SP.leaf[1].dtype) : KTIR_F32;
+    for (int si = 0; si < n_steps; ++si) {
+      const RwHead S = uniform_copy(*(const RwHead*)&SP.steps[si]);
+      if (S.kind == 0) {
+        rw_row_exec(SP, S.ins, rr, lane);
+        continue;
+      }
+      if (S.kind == 2) {
+        const RwLeaf L = uniform_copy(SP.leaf[S.out]);
+        const int64_t e = rw_row_base(SP, L, r, rows_per_lane);
+        if (l == 0 && e >= L.lo && e < L.hi) store_elem(L.ptr, e, L.dtype, rr.get(S.ins.a));
+        continue;
+      }
+      RwOut SL{0, 0, 0, 0, KTIR_F32};
+      bool in_range = false;
+      if (S.end) {
+        const RwLeaf L = uniform_copy(SP.leaf[S.out]);
+        SL = RwOut{L.ptr, L.lo, L.hi, rw_row_base(SP, L, r, rows_per_lane), L.dtype};
+        in_range = SL.base >= SL.lo && SL.base + inner <= SL.hi;
+      }
+      const float f = rw_pass<K>(S, SP.steps[si].ops, s0, d0, s1, d1, rr, SL, in_range, l);
+      if (S.end == 0) rr.set(S.dst, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f))));
+    }
+    // the row's LDS reads are done (LDS operations of a wavefront complete in order)
+    if (fast) {
+      rw_store_regs<NQ>(SP, st, lds, l);
+    } else if (more) {
+      for (int s = 0; s < n_slots; ++s)
+        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, rn, rows_per_lane, inner, lds, l);
+    }
+  }
+}
+
+template <int K, int NQ>
+static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows, int64_t blocks) {
+  hipLaunchKernelGGL((prog_rowwave<K, NQ>), dim3((unsigned)blocks), dim3(64), lds_bytes, stream(), W, rows);
+}
+
+template <int K>
+static bool pick_nq(int nq, const RwPlan& W, int lds_bytes, int64_t rows, int64_t blocks) {
+  // K/4 chunks: one 16-bit slot; K/2: one f32 slot or two 16-bit slots; K: more (at most 16 chunks)
+  constexpr int A = K / 4 > 0 ? K / 4 : 1, B = K / 2, C = K;
+  if (nq <= A) { launch_rowwave<K, A>(W, lds_bytes, rows, blocks); return true; }
+  if constexpr (B <= 16) {
+    if (nq <= B) { launch_rowwave<K, B>(W, lds_bytes, rows, blocks); return true; }
+  }
+  if constexpr (C <= 16) {
+    if (nq <= C) { launch_rowwave<K, C>(W, lds_bytes, rows, blocks); return true; }
+  }
+  return false;
+}
+
+static RwLeaf rw_leaf(const ktir_prog_t& P, int leaf) {
+  const ktir_leaf_t& L = P.leaves[leaf];
+  RwLeaf o{};
+  o.ptr = L.ptr;
+  o.lane_base = L.lane_base;
+  o.base = L.base;
+  o.lane_stride = L.lane_stride;
+  o.lo = L.lo;
+  o.hi = L.hi;
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) o.strides[d] = d < P.ndim - 1 ? L.strides[d] : 0;
+  o.dtype = L.dtype;
+  o.esize = L.dtype == KTIR_F32 ? 4 : 2;
+  return o;
+}
+
+static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t rows, int64_t inner) {
+  if (inner % 128 || inner / 128 < 4 || inner / 128 > 64) return false;
+  RwPlan W{};
+  W.n_steps = R.n_steps;
+  W.n_slots = R.n_slots;
+  W.nd = P.ndim;
+  for (int d = 0; d < KTIR_MAX_DIMS; ++d) W.shape[d] = d < P.ndim ? P.shape[d] : 1;
+  W.lane_scalars = P.lane_scalars;
+  W.n_lane_scalars = P.n_lane_scalars;
+  const int nd = P.ndim;
+  int32_t off = 0, nq = 0;
+  for (int s = 0; s < R.n_slots; ++s) {
+    const ktir_leaf_t& L = P.leaves[R.slot_leaf[s]];
+    W.leaf[s] = rw_leaf(P, R.slot_leaf[s]);
+    W.bytes[s] = (int32_t)(inner * W.leaf[s].esize);
+    if (W.bytes[s] % 1024) return false;
+    if (!(L.flags & (W.leaf[s].esize == 4 ? KTIR_LEAF_VEC : KTIR_LEAF_VEC8))) return false;   // 16-byte aligned rows
+    bool inv = L.lane_base == 0 && L.lane_stride == 0;
+    for (int d = 0; d < nd - 1; ++d) inv = inv && (L.strides[d] == 0 || P.shape[d] == 1);
+    W.inv[s] = inv;
+    W.off[s] = off;
+    off += W.bytes[s];
+    if (!inv) nq += W.bytes[s] >> 10;
+  }
+  int n_leaves = R.n_slots;
+  for (int i = 0; i < R.n_steps; ++i) {
+    const RcStep& S = R.steps[i];
+    RwStep& D = W.steps[i];
+    D.kind = S.kind;
+    if (S.kind == 1 && S.end == 0 && S.fold_dt != KTIR_F32) return false;
+    if (S.kind == 0 || S.kind == 2) D.ins = P.instr[S.pc];
+    if (S.kind == 2 || (S.kind == 1 && S.end == 1)) {
+      if (n_leaves == 4) return false;
+      W.leaf[n_leaves] = rw_leaf(P, S.st_leaf);
+      D.out = (int8_t)n_leaves++;
+    }
+    D.src = S.src;
+    D.n_ops = S.n_ops;
+    D.end = S.end;
+    D.fold_op = S.fold_op;
+    D.fold_dt = S.fold_dt;
+    D.dst = S.dst;
+    D.head = S.head;
+    for (int o = 0; o < RC_MAX_OPS; ++o) D.ops[o] = S.ops[o];
+  }
+  W.n_leaves = n_leaves;
+  if (off > 64 * 1024 || nq > 16) return false;
+  const int per_cu = (160 * 1024) / (off + (int)sizeof(RwPlan) + 64);
+  int64_t blocks = (int64_t)256 * (per_cu < 1 ? 1 : (per_cu > 16 ? 16 : per_cu));
+  if (blocks > rows) blocks = rows;
+  switch (inner / 128) {
+    case 4: return pick_nq<4>(nq, W, off, rows, blocks);
+    case 8: return pick_nq<8>(nq, W, off, rows, blocks);
+    case 16: return pick_nq<16>(nq, W, off, rows, blocks);
+    case 32: return pick_nq<32>(nq, W, off, rows, blocks);
+    case 64: return pick_nq<64>(nq, W, off, rows, blocks);
+  }
+  return false;
+}
+
+// Launch `P` (mode 1) through the row-chain kernel if it has the supported form.
+bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
+  if (P.mode != 1 || inner < 64 || inner > 8192 || (inner & (inner - 1))) return false;
+  if (P.lanes > 0 && P.lane_scalars == 0) {
+    for (int i = 0; i < P.n_instr; ++i)
+      if (P.instr[i].op == KTIR_OP_LANE) return false;
+  }
+  RcPlan R;
+  if (!analyze_rows(P, R)) return false;
+  if (try_launch_rowwave(P, R, rows, inner)) return true;
+  // threads per row and elements per thread: n = tpr * E, E in {2..32}, tpr in {32..256}
+  int tpr = (int)(inner / 16);
+  if (tpr > 256) tpr = 256;
+  if (tpr < 32) tpr = 32;
+  const int E = (int)(inner / tpr);
+  if (E < 2 || E > 32) return false;
+  int tpr_log2 = 0;
+  while ((1 << tpr_log2) < tpr) ++tpr_log2;
+  const int rpw = 256 / tpr;
+  int64_t blocks = (rows + rpw - 1) / rpw;
+  if (blocks > 65536) blocks = 65536;
+  switch (E) {
+    case 2: hipLaunchKernelGGL(prog_rowchain<2>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
+    case 4: hipLaunchKernelGGL(prog_rowchain<4>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
+    case 8: hipLaunchKernelGGL(prog_rowchain<8>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
+    case 16: hipLaunchKernelGGL(prog_rowchain<16>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
+    case 32: hipLaunchKernelGGL(prog_rowchain<32>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
+    default: return false;
+  }
+  return true;
+}
+
+}  // namespace ktir

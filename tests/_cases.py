@@ -57,3 +57,35 @@ def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42, dt="bf16", causal=Tr
         q, k, v = (rng.standard_normal((B, H, S, D)).astype(np.float16) for _ in range(3))
     return (configs.flash_attention(B, H, S, D, blk, dt=dt, causal=causal), "flash_attention",
             dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D)))
+
+
+def row_reduce(rows=32, cols=4096, rblk=4, combiner="arith.addf", dt="f32", seed=5):
+    """out[r] = fold of x[r, :] with `combiner` (the reference's pairwise-halving
+    linalg.reduce), one core per rblk-row block; values spread over 12 decades so
+    the summation order shows in the result bits."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 10.0 ** rng.uniform(-6, 6, (rows, cols))).astype(np.float32)
+    x = x.astype(np.float16) if dt == "f16" else x
+    cores = rows // rblk
+    T, V = configs._t([rblk, cols], dt), configs._t([rblk], dt)
+    init = {"arith.addf": "0.0", "arith.maximumf": "0xFF800000", "arith.mulf": "1.0"}[combiner]
+    src = f"""module {{
+  func.func @row_reduce(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %RB = arith.constant {rblk} : index
+    %init = arith.constant {init} : {dt}
+{configs._view("x_view", "x_ptr", [rows, cols], [cols, 1], dt)}
+{configs._view("y_view", "y_ptr", [rows], [1], dt)}
+    %row = arith.muli %core_id, %RB : index
+{configs._tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], dt)}
+    %x = ktdp.load %x_acc : !ktdp.access_tile<{rblk}x{cols}xindex> -> {T}
+    %i = tensor.splat %init : {V}
+    %r = linalg.reduce {{ {combiner} }} ins(%x : {T}) outs(%i : {V}) dimensions = [1]
+{configs._tile("y_acc", "y_view", ["%row"], [rblk], [rows], dt)}
+    ktdp.store %r, %y_acc : {V}, !ktdp.access_tile<{rblk}xindex>
+    return
+  }}
+}}
+"""
+    return src, "row_reduce", dict(x_ptr=x, y_ptr=np.zeros(rows, x.dtype))

@@ -62,6 +62,22 @@ def test_rmsnorm(cols):
     np.testing.assert_allclose(out["y_ptr"].astype(np.float32), ref["y_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("cols", [64, 256, 1024, 4096, 8192, 96, 3000])
+@pytest.mark.parametrize("combiner", ["arith.addf", "arith.maximumf"])
+def test_row_reduce_bit_exact(cols, combiner):
+    """Row folds reproduce the reference's pairwise-halving order bit for bit
+    (power-of-two rows take the register-resident row kernel, the others the
+    general row program)."""
+    ref, out, _ = _run(_cases.row_reduce(rows=32, cols=cols, combiner=combiner))
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
+@pytest.mark.parametrize("cols", [256, 4096])
+def test_row_reduce_f16_bit_exact(cols):
+    ref, out, _ = _run(_cases.row_reduce(rows=16, cols=cols, dt="f16"))
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
 @pytest.mark.parametrize("shape", [(256, 256, 256, 64, 64, 32, 2, 2),      # generic tile path
                                    (256, 256, 512, 128, 128, 64, 2, 2),    # MFMA path, one tile per core
                                    (512, 256, 256, 128, 128, 64, 2, 1)])   # MFMA path, 2x2 tiles per core
