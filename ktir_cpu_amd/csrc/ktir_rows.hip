@@ -464,10 +464,19 @@ __device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, c
           const float r = __fdiv_rn(1.f, s);
           const float as = fabsf(s);
           if (as > 1e-30f && as < 1e30f && r == r) {
+            // the corrected product; __fdiv_rn for huge or non-finite operands
+            float mx = 0.f;
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-              const float x = v[e];
-              v[e] = fabsf(x) < 1e30f ? div_by(x, s, r) : __fdiv_rn(x, s);
+            for (int e = 0; e < E; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            if (__all(mx < 1e30f)) {
+#pragma unroll
+              for (int e = 0; e < E; ++e) v[e] = div_by(v[e], s, r);
+            } else {
+#pragma unroll
+              for (int e = 0; e < E; ++e) {
+                const float x = v[e];
+                v[e] = fabsf(x) < 1e30f ? div_by(x, s, r) : __fdiv_rn(x, s);
+              }
             }
             return;
           }
@@ -936,41 +945,57 @@ __device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const
   return fold_rt(fop, a, b);
 }
 
-// element offset of column 0 of row r in leaf L
-__device__ __forceinline__ int64_t rw_row_base(const RwPlan& SP, const RwLeaf& L, int64_t r, int64_t rows_per_lane) {
-  const int64_t lane = r / rows_per_lane;
-  int64_t t = r - lane * rows_per_lane;
-  int64_t e = L.lane_base ? uni(((const KTIR_G(int64_t)*)L.lane_base)[lane]) : L.base + lane * L.lane_stride;
+// Position of row r: its lane (core) and its index in each outer dim.  Rows,
+// lanes and dims are below 2^31 (checked at launch): 32-bit division.
+struct RwPos {
+  int32_t lane;
+  int32_t idx[KTIR_MAX_DIMS - 1];
+};
+
+__device__ __forceinline__ RwPos rw_pos(const RwPlan& SP, int64_t r, int32_t rows_per_lane) {
+  RwPos p;
+  const uint32_t ru = (uint32_t)r, rpl = (uint32_t)rows_per_lane;
+  const uint32_t lane = ru / rpl;
+  uint32_t t = ru - lane * rpl;
+  p.lane = (int32_t)lane;
   const int nd = __builtin_amdgcn_readfirstlane(SP.nd);
 #pragma unroll
   for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+    p.idx[d] = 0;
     if (d < nd - 1) {
-      const int64_t ext = uni(SP.shape[d]);
-      const int64_t q = t / ext;
-      e += (t - q * ext) * L.strides[d];
+      const uint32_t ext = (uint32_t)__builtin_amdgcn_readfirstlane((int)SP.shape[d]);
+      const uint32_t q = t / ext;
+      p.idx[d] = (int32_t)(t - q * ext);
       t = q;
     }
   }
+  return p;
+}
+
+// element offset of column 0 of the row at p in leaf L
+__device__ __forceinline__ int64_t rw_row_base(const RwLeaf& L, const RwPos& p) {
+  int64_t e = L.lane_base ? uni(((const KTIR_G(int64_t)*)L.lane_base)[p.lane]) : L.base + (int64_t)p.lane * L.lane_stride;
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) e += (int64_t)p.idx[d] * L.strides[d];
   return e;
 }
 
 // registers <- row r of the non-invariant slots; false (nothing read) when a
 // row is not wholly inside its allocation
 template <int NQ>
-__device__ __forceinline__ bool rw_load_regs(const RwPlan& SP, uint4 (&st)[NQ], int64_t r, int64_t rows_per_lane,
-                                             int64_t inner, int l) {
+__device__ __forceinline__ bool rw_load_regs(const RwPlan& SP, uint4 (&st)[NQ], const RwPos& p, int64_t inner, int l) {
   const int n_slots = __builtin_amdgcn_readfirstlane(SP.n_slots);
   int q0 = 0;
   for (int s = 0; s < n_slots; ++s) {
     if (__builtin_amdgcn_readfirstlane(SP.inv[s])) continue;
     const RwLeaf L = uniform_copy(SP.leaf[s]);
-    const int64_t x = rw_row_base(SP, L, r, rows_per_lane);
+    const int64_t x = rw_row_base(L, p);
     if (x < L.lo || x + inner > L.hi) return false;
   }
   for (int s = 0; s < n_slots; ++s) {
     if (__builtin_amdgcn_readfirstlane(SP.inv[s])) continue;
     const RwLeaf L = uniform_copy(SP.leaf[s]);
-    const int64_t x = rw_row_base(SP, L, r, rows_per_lane);
+    const int64_t x = rw_row_base(L, p);
     const int nq = __builtin_amdgcn_readfirstlane(SP.bytes[s]) >> 10;
     const KTIR_G(uint8_t)* src = (const KTIR_G(uint8_t)*)L.ptr + x * L.esize + 16 * l;
 #pragma unroll
@@ -997,10 +1022,10 @@ __device__ __forceinline__ void rw_store_regs(const RwPlan& SP, const uint4 (&st
 }
 
 // element by element into LDS with the reference's out-of-range read rule (0)
-__device__ __forceinline__ void rw_stage_slow(const RwPlan& SP, int s, int64_t r, int64_t rows_per_lane,
+__device__ __forceinline__ void rw_stage_slow(const RwPlan& SP, int s, const RwPos& p,
                                               int64_t inner, uint8_t* lds, int l) {
   const RwLeaf L = uniform_copy(SP.leaf[s]);
-  const int64_t e = rw_row_base(SP, L, r, rows_per_lane);
+  const int64_t e = rw_row_base(L, p);
   uint8_t* dst = lds + __builtin_amdgcn_readfirstlane(SP.off[s]);
   for (int64_t i = l; i < inner; i += 64) {
     const int64_t x = e + i;
@@ -1046,8 +1071,12 @@ __device__ __forceinline__ void rw_row_exec(const RwPlan& SP, const ktir_instr_t
 // slots' rows laid end to end) while the current row is computed from LDS,
 // then written to LDS.  Plain loads and LDS stores: the compiler waits for
 // the loaded registers only where they are stored.
+// three wavefronts per SIMD where the registers fit without spilling
 template <int K, int NQ>
-__global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t total_rows) {
+constexpr int rw_waves() { return (K == 32 && NQ == 8) || (K == 16 && NQ == 4) || K <= 8 ? 3 : 2; }
+
+template <int K, int NQ>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(rw_waves<K, NQ>()))) void prog_rowwave(const RwPlan Pk, int64_t total_rows) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ RwPlan SP;
   RowRegs rr{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -1069,23 +1098,25 @@ __global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t tota
 #pragma unroll
   for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
     if (d < nd - 1) rows_per_lane *= shape[d];
+  const int32_t rpl = (int32_t)rows_per_lane;
   uint4 st[NQ];
   int64_t r = blockIdx.x;
+  RwPos pos = rw_pos(SP, r, rpl);
   if (r < total_rows) {
     for (int s = 0; s < n_slots; ++s)
-      if (__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, r, rows_per_lane, inner, lds, l);
-    if (rw_load_regs<NQ>(SP, st, r, rows_per_lane, inner, l)) {
+      if (__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, pos, inner, lds, l);
+    if (rw_load_regs<NQ>(SP, st, pos, inner, l)) {
       rw_store_regs<NQ>(SP, st, lds, l);
     } else {
       for (int s = 0; s < n_slots; ++s)
-        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, r, rows_per_lane, inner, lds, l);
+        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, pos, inner, lds, l);
     }
   }
   for (; r < total_rows; r += gridDim.x) {
     const int64_t rn = r + gridDim.x;
     const bool more = rn < total_rows;
-    const bool fast = more && rw_load_regs<NQ>(SP, st, rn, rows_per_lane, inner, l);
-    const int64_t lane = r / rows_per_lane;
+    const RwPos pn = rw_pos(SP, more ? rn : r, rpl);
+    const bool fast = more && rw_load_regs<NQ>(SP, st, pn, inner, l);
     const uint8_t* s0 = lds + __builtin_amdgcn_readfirstlane(SP.off[0]);
     const uint8_t* s1 = n_slots > 1 ? lds + __builtin_amdgcn_readfirstlane(SP.off[1]) : nullptr;
     const int d0 = __builtin_amdgcn_readfirstlane(SP.leaf[0].dtype);
@@ -1093,12 +1124,12 @@ __global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t tota
     for (int si = 0; si < n_steps; ++si) {
       const RwHead S = uniform_copy(*(const RwHead*)&SP.steps[si]);
       if (S.kind == 0) {
-        rw_row_exec(SP, S.ins, rr, lane);
+        rw_row_exec(SP, S.ins, rr, pos.lane);
         continue;
       }
       if (S.kind == 2) {
         const RwLeaf L = uniform_copy(SP.leaf[S.out]);
-        const int64_t e = rw_row_base(SP, L, r, rows_per_lane);
+        const int64_t e = rw_row_base(L, pos);
         if (l == 0 && e >= L.lo && e < L.hi) store_elem(L.ptr, e, L.dtype, rr.get(S.ins.a));
         continue;
       }
@@ -1106,7 +1137,7 @@ __global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t tota
       bool in_range = false;
       if (S.end) {
         const RwLeaf L = uniform_copy(SP.leaf[S.out]);
-        SL = RwOut{L.ptr, L.lo, L.hi, rw_row_base(SP, L, r, rows_per_lane), L.dtype};
+        SL = RwOut{L.ptr, L.lo, L.hi, rw_row_base(L, pos), L.dtype};
         in_range = SL.base >= SL.lo && SL.base + inner <= SL.hi;
       }
       const float f = rw_pass<K>(S, SP.steps[si].ops, s0, d0, s1, d1, rr, SL, in_range, l);
@@ -1117,26 +1148,44 @@ __global__ __launch_bounds__(64) void prog_rowwave(const RwPlan Pk, int64_t tota
       rw_store_regs<NQ>(SP, st, lds, l);
     } else if (more) {
       for (int s = 0; s < n_slots; ++s)
-        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, rn, rows_per_lane, inner, lds, l);
+        if (!__builtin_amdgcn_readfirstlane(SP.inv[s])) rw_stage_slow(SP, s, pn, inner, lds, l);
     }
+    pos = pn;
   }
 }
 
+// One resident wavefront per row stream: as many workgroups as the device
+// holds at once (so no second, partial round of workgroups), each taking an
+// equal share of the rows.
 template <int K, int NQ>
-static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows, int64_t blocks) {
+static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows) {
+  static int cached_lds = -1, cached_resident = 0;
+  if (cached_lds != lds_bytes) {
+    int per_cu = 0, cus = 0, dev = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prog_rowwave<K, NQ>, 64, lds_bytes) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 || cus < 1) {
+      per_cu = 1;
+      cus = 256;
+    }
+    cached_resident = per_cu * cus;
+    cached_lds = lds_bytes;
+  }
+  const int64_t per_block = (rows + cached_resident - 1) / cached_resident;
+  const int64_t blocks = (rows + per_block - 1) / per_block;
   hipLaunchKernelGGL((prog_rowwave<K, NQ>), dim3((unsigned)blocks), dim3(64), lds_bytes, stream(), W, rows);
 }
 
 template <int K>
-static bool pick_nq(int nq, const RwPlan& W, int lds_bytes, int64_t rows, int64_t blocks) {
+static bool pick_nq(int nq, const RwPlan& W, int lds_bytes, int64_t rows) {
   // K/4 chunks: one 16-bit slot; K/2: one f32 slot or two 16-bit slots; K: more (at most 16 chunks)
   constexpr int A = K / 4 > 0 ? K / 4 : 1, B = K / 2, C = K;
-  if (nq <= A) { launch_rowwave<K, A>(W, lds_bytes, rows, blocks); return true; }
+  if (nq <= A) { launch_rowwave<K, A>(W, lds_bytes, rows); return true; }
   if constexpr (B <= 16) {
-    if (nq <= B) { launch_rowwave<K, B>(W, lds_bytes, rows, blocks); return true; }
+    if (nq <= B) { launch_rowwave<K, B>(W, lds_bytes, rows); return true; }
   }
   if constexpr (C <= 16) {
-    if (nq <= C) { launch_rowwave<K, C>(W, lds_bytes, rows, blocks); return true; }
+    if (nq <= C) { launch_rowwave<K, C>(W, lds_bytes, rows); return true; }
   }
   return false;
 }
@@ -1158,6 +1207,9 @@ static RwLeaf rw_leaf(const ktir_prog_t& P, int leaf) {
 
 static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t rows, int64_t inner) {
   if (inner % 128 || inner / 128 < 4 || inner / 128 > 64) return false;
+  if (rows > INT32_MAX) return false;   // row positions use 32-bit arithmetic
+  for (int d = 0; d < P.ndim; ++d)
+    if (P.shape[d] > INT32_MAX) return false;
   RwPlan W{};
   W.n_steps = R.n_steps;
   W.n_slots = R.n_slots;
@@ -1203,15 +1255,12 @@ static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t ro
   }
   W.n_leaves = n_leaves;
   if (off > 64 * 1024 || nq > 16) return false;
-  const int per_cu = (160 * 1024) / (off + (int)sizeof(RwPlan) + 64);
-  int64_t blocks = (int64_t)256 * (per_cu < 1 ? 1 : (per_cu > 16 ? 16 : per_cu));
-  if (blocks > rows) blocks = rows;
   switch (inner / 128) {
-    case 4: return pick_nq<4>(nq, W, off, rows, blocks);
-    case 8: return pick_nq<8>(nq, W, off, rows, blocks);
-    case 16: return pick_nq<16>(nq, W, off, rows, blocks);
-    case 32: return pick_nq<32>(nq, W, off, rows, blocks);
-    case 64: return pick_nq<64>(nq, W, off, rows, blocks);
+    case 4: return pick_nq<4>(nq, W, off, rows);
+    case 8: return pick_nq<8>(nq, W, off, rows);
+    case 16: return pick_nq<16>(nq, W, off, rows);
+    case 32: return pick_nq<32>(nq, W, off, rows);
+    case 64: return pick_nq<64>(nq, W, off, rows);
   }
   return false;
 }
