@@ -296,11 +296,10 @@ typedef struct ktir_rmw {
   int64_t src_base, src_row, src_col, src_hi;
   int32_t op, order, dt, pad;
   int64_t n_rows;          /* destination rows covered by the head table */
-  uint64_t head;           /* int32_t [n_rows] scratch (set to -1 by the call) */
+  uint64_t head;           /* int32_t [n_rows] scratch: -1 in every entry on entry, and so left on return */
   uint64_t link;           /* int32_t [n_inst * K] scratch */
   uint64_t rows;           /* int32_t [n_inst * K] scratch: destination row of each entry */
   uint64_t srcs;           /* int32_t [n_inst * K] scratch: source row of each entry */
-  uint64_t owners;         /* int32_t [4 + 4 * n_inst * K] scratch: owner count, then {entry, row, src, -} records */
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
 

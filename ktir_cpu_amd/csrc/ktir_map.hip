@@ -10,6 +10,9 @@
 
 namespace ktir {
 
+typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mu4 __attribute__((ext_vector_type(4)));
+
 template <int DT>
 __device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* out, bool bcast) {
   if (bcast) {   // inner stride 0: one element for the whole chunk
@@ -20,7 +23,7 @@ __device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* o
   }
   if (e0 >= L.lo && e0 + 8 <= L.hi) {
     if (DT == KTIR_F16) {
-      uint4 w = *(const uint4*)((const _Float16*)L.ptr + e0);
+      const uint4 w = __builtin_bit_cast(uint4, *(const KTIR_G(mu4)*)((const KTIR_G(uint16_t)*)L.ptr + e0));
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -28,7 +31,7 @@ __device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* o
         out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
       }
     } else if (DT == KTIR_BF16) {
-      uint4 w = *(const uint4*)((const uint16_t*)L.ptr + e0);
+      const uint4 w = __builtin_bit_cast(uint4, *(const KTIR_G(mu4)*)((const KTIR_G(uint16_t)*)L.ptr + e0));
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -36,10 +39,10 @@ __device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* o
         out[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
       }
     } else {
-      float4 w0 = *(const float4*)((const float*)L.ptr + e0);
-      float4 w1 = *(const float4*)((const float*)L.ptr + e0 + 4);
-      out[0] = w0.x; out[1] = w0.y; out[2] = w0.z; out[3] = w0.w;
-      out[4] = w1.x; out[5] = w1.y; out[6] = w1.z; out[7] = w1.w;
+      const mf4 w0 = *(const KTIR_G(mf4)*)((const KTIR_G(float)*)L.ptr + e0);
+      const mf4 w1 = *(const KTIR_G(mf4)*)((const KTIR_G(float)*)L.ptr + e0 + 4);
+      out[0] = w0[0]; out[1] = w0[1]; out[2] = w0[2]; out[3] = w0[3];
+      out[4] = w1[0]; out[5] = w1[1]; out[6] = w1[2]; out[7] = w1[3];
     }
     return;
   }
@@ -59,16 +62,16 @@ __device__ __forceinline__ void store8(const ktir_leaf_t& L, int64_t e0, const f
       for (int i = 0; i < 4; ++i)
         u[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i]) |
                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1]) << 16);
-      *(uint4*)((_Float16*)L.ptr + e0) = make_uint4(u[0], u[1], u[2], u[3]);
+      *(KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0) = mu4{u[0], u[1], u[2], u[3]};
     } else if (DT == KTIR_BF16) {
       uint32_t u[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         u[i] = (__float_as_uint(round_bf16(v[2 * i])) >> 16) | (__float_as_uint(round_bf16(v[2 * i + 1])) & 0xffff0000u);
-      *(uint4*)((uint16_t*)L.ptr + e0) = make_uint4(u[0], u[1], u[2], u[3]);
+      *(KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0) = mu4{u[0], u[1], u[2], u[3]};
     } else {
-      *(float4*)((float*)L.ptr + e0) = make_float4(v[0], v[1], v[2], v[3]);
-      *(float4*)((float*)L.ptr + e0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      *(KTIR_G(mf4)*)((KTIR_G(float)*)L.ptr + e0) = mf4{v[0], v[1], v[2], v[3]};
+      *(KTIR_G(mf4)*)((KTIR_G(float)*)L.ptr + e0 + 4) = mf4{v[4], v[5], v[6], v[7]};
     }
     return;
   }
@@ -148,8 +151,100 @@ __device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t i
   for (int e = 0; e < 8; ++e) exec_reg4(P, in, R[e], lane);
 }
 
+// element offsets of chunk vid in the two inputs and the output
+struct MapOffs {
+  int64_t a, b, o, lane;
+};
+
+__device__ __forceinline__ MapOffs map_offsets(const ktir_prog_t& P, const FlatDivs& D, const ktir_leaf_t& LA,
+                                               const ktir_leaf_t& LB, const ktir_leaf_t& LO, bool bca, bool bcb,
+                                               uint32_t vid) {
+  const int nd = P.ndim;
+  uint32_t c[KTIR_MAX_DIMS] = {0, 0, 0, 0};
+  const uint32_t row = fdiv(vid, D.nvi);
+  const int64_t col = (int64_t)(vid - row * D.nvi.d) * 8;
+  uint32_t t = row;
+#pragma unroll
+  for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+    if (d < nd - 1) {
+      uint32_t q = fdiv(t, D.dim[d]);
+      c[d] = t - q * D.dim[d].d;
+      t = q;
+    }
+  }
+  // inner strides are 1 (or 0 for a broadcast input) on this path (checked at launch)
+  MapOffs m;
+  m.a = lane_offset(LA, t) + (bca ? 0 : col);
+  m.b = lane_offset(LB, t) + (bcb ? 0 : col);
+  m.o = lane_offset(LO, t) + col;
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) {
+    if (d < nd - 1) {
+      m.a += (int64_t)c[d] * LA.strides[d];
+      m.b += (int64_t)c[d] * LB.strides[d];
+      m.o += (int64_t)c[d] * LO.strides[d];
+    }
+  }
+  m.lane = t;
+  return m;
+}
+
+// r = a OP b (or b OP a) over a chunk; the result rounded to dt unless the
+// output store rounds to the same type
+template <int DO>
+__device__ __forceinline__ void map_binop(int op, int dt, bool swap, const float (&a)[8], const float (&b)[8],
+                                          float (&r)[8]) {
+  const bool round = dt != DO && dt != KTIR_F32;
+  float p[8], q[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ae = a[e], be = b[e];
+    p[e] = swap ? be : ae;
+    q[e] = swap ? ae : be;
+  }
+#define MB(expr)                                                 \
+  _Pragma("unroll") for (int e = 0; e < 8; ++e) {                \
+    const float x = p[e], y = q[e];                              \
+    const float v = (expr);                                      \
+    r[e] = round ? round_to(v, dt) : v;                          \
+  }                                                              \
+  return;
+  switch (op) {
+    case KTIR_OP_ADDF: MB(__fadd_rn(x, y))
+    case KTIR_OP_SUBF: MB(__fsub_rn(x, y))
+    case KTIR_OP_MULF: MB(__fmul_rn(x, y))
+    case KTIR_OP_DIVF: MB(__fdiv_rn(x, y))
+  }
+#undef MB
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = binop_f_simple(op, dt, p[e], q[e]);
+}
+
+// compute and store one chunk
+template <int DO, int NIN>
+__device__ __forceinline__ void map_chunk(const ktir_prog_t& P, const ktir_leaf_t& LO, int fast, int n_ops, int out_reg,
+                                          const MapOffs& m, const float (&a)[8], const float (&b)[8]) {
+  float out[8];
+  if (NIN == 2 && fast >= 0) {
+    map_binop<DO>(fast & 0xff, fast >> 16, (fast >> 8) & 1, a, b, out);
+  } else {
+    Reg4 R[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R[e] = Reg4{a[e], NIN == 2 ? b[e] : 0.f, 0.f, 0.f};
+    for (int pc = 0; pc < n_ops; ++pc) exec8(P, P.instr[pc], R, m.lane);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = R[e].get(out_reg);
+  }
+  store8<DO>(LO, m.o, out);
+}
+
+// Two chunks per thread per step (256 chunks apart), both chunks' loads
+// issued before any compute.  `fast` >= 0: the program is one float binary
+// op of the two inputs whose result is stored (op | swap << 8 | dt << 16),
+// applied directly.
 template <int DA, int DB, int DO, int NIN>
-__global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatDivs D, uint32_t total, int st_leaf) {
+__global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatDivs D, uint32_t total, int st_leaf,
+                                                int fast) {
   const ktir_leaf_t& LA = P.leaves[P.pf_leaf[0]];
   const ktir_leaf_t& LB = P.leaves[NIN == 2 ? P.pf_leaf[1] : P.pf_leaf[0]];
   const ktir_leaf_t& LO = P.leaves[st_leaf];
@@ -157,53 +252,40 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
   const int n_ops = P.n_instr - 1;
   const int out_reg = P.instr[n_ops].a;
   const bool bca = LA.strides[nd - 1] == 0, bcb = LB.strides[nd - 1] == 0;
-  const uint32_t nth = gridDim.x * blockDim.x;
-  for (uint32_t vid = blockIdx.x * blockDim.x + threadIdx.x; vid < total; vid += nth) {
-    // coordinates of the chunk: c[d] for the outer dims d < nd-1, col inner
-    uint32_t c[KTIR_MAX_DIMS] = {0, 0, 0, 0};
-    const uint32_t row = fdiv(vid, D.nvi);
-    const int64_t col = (int64_t)(vid - row * D.nvi.d) * 8;
-    uint32_t t = row;
-#pragma unroll
-    for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
-      if (d < nd - 1) {
-        uint32_t q = fdiv(t, D.dim[d]);
-        c[d] = t - q * D.dim[d].d;
-        t = q;
-      }
+  const uint32_t step = gridDim.x * 512;
+  for (uint32_t v0 = blockIdx.x * 512 + threadIdx.x; v0 < total; v0 += step) {
+    const uint32_t v1 = v0 + 256;
+    const bool on1 = v1 < total;
+    float a0[8], b0[8], a1[8], b1[8];
+    const MapOffs m0 = map_offsets(P, D, LA, LB, LO, bca, bcb, v0);
+    const MapOffs m1 = map_offsets(P, D, LA, LB, LO, bca, bcb, on1 ? v1 : v0);
+    load8<DA>(LA, m0.a, a0, bca);
+    if (NIN == 2) load8<DB>(LB, m0.b, b0, bcb);
+    if (on1) {
+      load8<DA>(LA, m1.a, a1, bca);
+      if (NIN == 2) load8<DB>(LB, m1.b, b1, bcb);
     }
-    // inner strides are 1 (or 0 for a broadcast input) on this path (checked at launch)
-    int64_t ea = lane_offset(LA, t) + (bca ? 0 : col);
-    int64_t eb = lane_offset(LB, t) + (bcb ? 0 : col);
-    int64_t eo = lane_offset(LO, t) + col;
-#pragma unroll
-    for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d) {
-      if (d < nd - 1) {
-        ea += (int64_t)c[d] * LA.strides[d];
-        eb += (int64_t)c[d] * LB.strides[d];
-        eo += (int64_t)c[d] * LO.strides[d];
-      }
-    }
-    float a[8], b[8];
-    load8<DA>(LA, ea, a, bca);
-    if (NIN == 2) load8<DB>(LB, eb, b, bcb);
-    Reg4 R[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) R[e] = Reg4{a[e], NIN == 2 ? b[e] : 0.f, 0.f, 0.f};
-    for (int pc = 0; pc < n_ops; ++pc) exec8(P, P.instr[pc], R, t);
-    float out[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = R[e].get(out_reg);
-    store8<DO>(LO, eo, out);
+    map_chunk<DO, NIN>(P, LO, fast, n_ops, out_reg, m0, a0, b0);
+    if (on1) map_chunk<DO, NIN>(P, LO, fast, n_ops, out_reg, m1, a1, b1);
   }
 }
 
 template <int DA, int DB, int DO, int NIN>
 static void launch_map(const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, int st_leaf) {
-  int64_t blocks = ((int64_t)total + 255) / 256;
+  int64_t blocks = ((int64_t)total + 511) / 512;
   if (blocks > 1048576) blocks = 1048576;
+  int fast = -1;
+  if (NIN == 2 && Q.n_instr == 2) {
+    const ktir_instr_t& x = Q.instr[0];
+    const bool fop = x.op == KTIR_OP_ADDF || x.op == KTIR_OP_SUBF || x.op == KTIR_OP_MULF || x.op == KTIR_OP_DIVF ||
+                     x.op == KTIR_OP_MAXIMUMF || x.op == KTIR_OP_MINIMUMF || x.op == KTIR_OP_MAXNUMF ||
+                     x.op == KTIR_OP_MINNUMF;
+    const bool fdt = x.dt == KTIR_F16 || x.dt == KTIR_BF16 || x.dt == KTIR_F32;
+    if (fop && fdt && Q.instr[1].a == x.dst && ((x.a == 0 && x.b == 1) || (x.a == 1 && x.b == 0)))
+      fast = x.op | ((x.a == 1) << 8) | (x.dt << 16);
+  }
   hipLaunchKernelGGL((prog_map<DA, DB, DO, NIN>), dim3((unsigned)blocks), dim3(256), 0, stream(), Q, D, total,
-                     st_leaf);
+                     st_leaf, fast);
 }
 
 template <int DA, int DB, int NIN>

@@ -11,14 +11,22 @@
 //     source indices, find the surviving (last) position of every destination
 //     row inside the instance, and push survivors on the row's chain:
 //     link[e] = atomicExch(&head[row], e).  The entry that finds the chain
-//     empty becomes the row's owner and is appended to a compact owner list.
-//   pass 2 (one half-wavefront per owner): a row with one entry is a single
-//     load-combine-store; a longer chain is applied entry by entry in
-//     ascending e, which is the reference's instance order, so the floating
-//     point accumulation order is exactly the reference's.
+//     empty (link[e] == -1) is the row's owner; entries that do not survive
+//     get link[e] = -2.
+//   pass 2: every row with a chain is applied once.  A row with one entry is
+//     a single load-combine-store; a longer chain is applied entry by entry
+//     in ascending e, which is the reference's instance order, so the
+//     floating point accumulation order is exactly the reference's.  The
+//     common form (f32 rows, f16 / f32 sources) walks the head table in row
+//     order; other forms give each owner entry half a wavefront.  Pass 2
+//     resets every head it reads to -1, so the head table is all -1 between
+//     calls (the caller fills it once).
 #include "ktir_common.h"
 
 namespace ktir {
+
+typedef float gf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gu2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int64_t read_index(uint64_t ptr, int dt, int64_t e, int64_t hi, bool* bad) {
   if (e < 0 || e >= hi) return 0;   // over-read of the index tensor reads zeros
@@ -62,7 +70,6 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
     rows[k] = (r >= 0 && r < d.n_rows) ? (int32_t)r : -1;
   }
   __syncthreads();
-  int32_t* owners = (int32_t*)d.owners;
   for (int k = threadIdx.x; k < d.K; k += blockDim.x) {
     const int64_t e = inst * d.K + k;
     const int32_t r = rows[k];
@@ -76,49 +83,11 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
       prev = atomicExch(&((int32_t*)d.head)[r], (int32_t)e);
     }
     ((int32_t*)d.link)[e] = prev;
-    // append owners (first pushed entry of a row) with one atomic per wavefront
-    const bool own = prev == -1;
-    const uint64_t mask = __ballot(own);
-    if (mask) {
-      const int leader = __ffsll((unsigned long long)mask) - 1;
-      const int rank = __popcll(mask & ((1ull << (threadIdx.x & 63)) - 1));
-      int32_t base = 0;
-      if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(&owners[0], __popcll(mask));
-      base = __shfl(base, leader);
-      if (own) {
-        int32_t* rec = owners + 4 + 4 * (int64_t)(base + rank);   // {entry, row, src, -}
-        *(int4*)rec = make_int4((int32_t)e, r, ((int32_t*)d.srcs)[e], 0);
-      }
-    }
   }
   if (bad) *err = 1;
 }
 
-// Apply one chain entry to the 4 columns [c, c+4) of the running row value.
-__device__ __forceinline__ void apply_src(const ktir_rmw_t& d, int64_t s, int64_t c, float* v, bool vec) {
-  const int64_t se = d.src_base + s * d.src_row + c * d.src_col;
-  float g[4];
-  if (vec && se >= 0 && se + 4 <= d.src_hi) {
-    if (d.src_dtype == KTIR_F16) {
-      uint2 w = *(const uint2*)((const _Float16*)d.src_ptr + se);
-      const _Float16* h = (const _Float16*)&w;
-      for (int i = 0; i < 4; ++i) g[i] = (float)h[i];
-    } else {
-      float4 w = *(const float4*)((const float*)d.src_ptr + se);
-      g[0] = w.x; g[1] = w.y; g[2] = w.z; g[3] = w.w;
-    }
-  } else {
-    for (int i = 0; i < 4; ++i) {
-      int64_t x = se + i * d.src_col;
-      g[i] = (c + i < d.D && x >= 0 && x < d.src_hi) ? load_elem(d.src_ptr, x, d.src_dtype) : 0.f;
-    }
-  }
-  for (int i = 0; i < 4; ++i) v[i] = combine(d.op, d.order, d.dt, v[i], g[i]);
-}
-
-// Two owners per half-wavefront (32 lanes x 4 columns cover a 128-wide row
-// per step): the owner records, the chain heads and both rows of both owners
-// are requested before anything is combined.
+// 4 columns [c, c+4) of a destination (dst) or source row
 __device__ __forceinline__ void load4(const ktir_rmw_t& d, bool dst, int64_t e0, int64_t c, bool vec, float* v) {
   const uint64_t ptr = dst ? d.dst_ptr : d.src_ptr;
   const int dt = dst ? d.dst_dtype : d.src_dtype;
@@ -170,43 +139,117 @@ __device__ __forceinline__ void apply_chain(const ktir_rmw_t& d, int32_t head, i
   }
 }
 
-__global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d) {
-  const int32_t* owners = (const int32_t*)d.owners;
-  const int32_t n_owners = owners[0];
+// RMW_NE entries per half-wavefront (32 lanes x 4 columns cover a 128-wide
+// row per step): the entries' chain records are read together, then, for
+// owners, the chain heads and all rows, before anything is combined.
+constexpr int RMW_NE = 4;
+
+__global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d, int64_t n_entries) {
   const int half = threadIdx.x / 32, hl = threadIdx.x % 32;
   const bool vec = d.dst_col == 1 && d.src_col == 1 && d.dst_dtype == KTIR_F32 &&
                    (d.src_dtype == KTIR_F16 || d.src_dtype == KTIR_F32) &&
                    (d.dst_base % 4 == 0) && (d.dst_row % 4 == 0) && (d.src_base % 4 == 0) && (d.src_row % 4 == 0);
-  const int64_t step = (int64_t)gridDim.x * 16;
-  for (int64_t o0 = (int64_t)blockIdx.x * 16 + half * 2; o0 < n_owners; o0 += step) {
-    const bool two = o0 + 1 < n_owners;
-    const int4 ra = *(const int4*)(owners + 4 + 4 * o0);
-    const int4 rb = two ? *(const int4*)(owners + 4 + 4 * (o0 + 1)) : ra;
-    const int32_t ha = ((const int32_t*)d.head)[ra.y];
-    const int32_t hb = ((const int32_t*)d.head)[rb.y];
-    const int64_t da = d.dst_base + (int64_t)ra.y * d.dst_row, db = d.dst_base + (int64_t)rb.y * d.dst_row;
+  const int32_t* link = (const int32_t*)d.link;
+  const int32_t* rows = (const int32_t*)d.rows;
+  const int32_t* srcs = (const int32_t*)d.srcs;
+  const int32_t* head = (const int32_t*)d.head;
+  const int64_t step = (int64_t)gridDim.x * 8 * RMW_NE;
+  for (int64_t e0 = ((int64_t)blockIdx.x * 8 + half) * RMW_NE; e0 < n_entries; e0 += step) {
+    bool own[RMW_NE];
+    int32_t r[RMW_NE], sr[RMW_NE], h[RMW_NE];
+    // records of entries that do not survive are never read (their rows and
+    // sources were not written): read all, use the owners'
+#pragma unroll
+    for (int j = 0; j < RMW_NE; ++j) {
+      const int64_t e = e0 + j < n_entries ? e0 + j : e0;
+      own[j] = e0 + j < n_entries && link[e] == -1;
+      r[j] = rows[e];
+      sr[j] = srcs[e];
+    }
+#pragma unroll
+    for (int j = 0; j < RMW_NE; ++j) h[j] = own[j] ? head[r[j]] : 0;
+    // the row's owner leaves its head empty again for the next call
+#pragma unroll
+    for (int j = 0; j < RMW_NE; ++j)
+      if (own[j]) ((int32_t*)d.head)[r[j]] = -1;
     for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
-      float va[4], vb[4], ga[4], gb[4];
-      load4(d, true, da + c * d.dst_col, c, vec, va);
-      load4(d, false, d.src_base + (int64_t)ra.z * d.src_row + c * d.src_col, c, vec, ga);
-      if (two) {
-        load4(d, true, db + c * d.dst_col, c, vec, vb);
-        load4(d, false, d.src_base + (int64_t)rb.z * d.src_row + c * d.src_col, c, vec, gb);
+      float v[RMW_NE][4], g[RMW_NE][4];
+#pragma unroll
+      for (int j = 0; j < RMW_NE; ++j) {
+        if (!own[j]) continue;
+        load4(d, true, d.dst_base + (int64_t)r[j] * d.dst_row + c * d.dst_col, c, vec, v[j]);
+        load4(d, false, d.src_base + (int64_t)sr[j] * d.src_row + c * d.src_col, c, vec, g[j]);
       }
-      if (ha == ra.x) {   // the row's only entry
-        for (int i = 0; i < 4; ++i) va[i] = combine(d.op, d.order, d.dt, va[i], ga[i]);
-      } else {
-        apply_chain(d, ha, da, c, vec, va);
-      }
-      store4(d, da + c * d.dst_col, c, vec, va);
-      if (two) {
-        if (hb == rb.x) {
-          for (int i = 0; i < 4; ++i) vb[i] = combine(d.op, d.order, d.dt, vb[i], gb[i]);
+#pragma unroll
+      for (int j = 0; j < RMW_NE; ++j) {
+        if (!own[j]) continue;
+        const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
+        if (h[j] == (int32_t)(e0 + j)) {   // the row's only entry
+          for (int i = 0; i < 4; ++i) v[j][i] = combine(d.op, d.order, d.dt, v[j][i], g[j][i]);
         } else {
-          apply_chain(d, hb, db, c, vec, vb);
+          apply_chain(d, h[j], de, c, vec, v[j]);
         }
-        store4(d, db + c * d.dst_col, c, vec, vb);
+        store4(d, de + c * d.dst_col, c, vec, v[j]);
       }
+    }
+  }
+}
+
+// The common form: f32 destination rows and f16 / f32 source rows, unit
+// column stride, 16-byte aligned rows, D a multiple of 128, f32 result.
+// Destination-row order: wave w covers rows 64 w .. 64 w + 63 (one head
+// entry per lane, read coalesced); the rows with a chain are compacted in
+// LDS with their head entry's link and source, then applied by half
+// wavefronts in ascending row order, so the row reads and writes of
+// neighbouring wavefronts fall on neighbouring addresses.  Each head is reset
+// to -1 once read.
+template <int SDT>
+__device__ __forceinline__ void rmw_src4(const ktir_rmw_t& d, int64_t se, float* g) {
+  if (SDT == KTIR_F16) {
+    const uint2 w = __builtin_bit_cast(uint2, *(const KTIR_G(gu2)*)((const KTIR_G(uint16_t)*)d.src_ptr + se));
+    g[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x & 0xffffu));
+    g[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x >> 16));
+    g[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y & 0xffffu));
+    g[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y >> 16));
+  } else {
+    const gf4 w = *(const KTIR_G(gf4)*)((const KTIR_G(float)*)d.src_ptr + se);
+    g[0] = w[0]; g[1] = w[1]; g[2] = w[2]; g[3] = w[3];
+  }
+}
+
+template <int SDT>
+__global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d) {
+  __shared__ int4 items[4][64];
+  const int wv = threadIdx.x / 64, l = threadIdx.x % 64, half = l / 32, hl = l % 32;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wv) * 64 + l;
+  const int32_t h = r < d.n_rows ? ((const KTIR_G(int32_t)*)d.head)[r] : -1;
+  const uint64_t mask = __ballot(h >= 0);
+  const int n = __popcll(mask);
+  if (h >= 0) {
+    const int rank = __popcll(mask & ((1ull << l) - 1));
+    const int32_t lk = ((const KTIR_G(int32_t)*)d.link)[h];
+    const int32_t sr = ((const KTIR_G(int32_t)*)d.srcs)[h];
+    items[wv][rank] = make_int4((int32_t)r, h, lk, sr);
+    ((KTIR_G(int32_t)*)d.head)[r] = -1;
+  }
+  // the records are written and read by this wavefront only (its LDS
+  // operations complete in order)
+  __builtin_amdgcn_wave_barrier();
+  const KTIR_G(float)* dst = (const KTIR_G(float)*)d.dst_ptr;
+  for (int i = half; i < n; i += 2) {
+    const int4 it = items[wv][i];
+    const int64_t de = d.dst_base + (int64_t)it.x * d.dst_row;
+    for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
+      const gf4 v = *(const KTIR_G(gf4)*)(dst + de + c);
+      float g[4];
+      rmw_src4<SDT>(d, d.src_base + (int64_t)it.w * d.src_row + c, g);
+      float x[4] = {v[0], v[1], v[2], v[3]};
+      if (it.z == -1) {   // the head entry was also the chain's first: one entry
+        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[q]);
+      } else {
+        apply_chain(d, it.y, de, c, true, x);
+      }
+      *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + de + c) = gf4{x[0], x[1], x[2], x[3]};
     }
   }
 }
@@ -221,14 +264,24 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
   if (d->n_inst * d->K >= (int64_t)0x7fffffff || d->n_rows >= (int64_t)0x7fffffff)
     return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_row_rmw: too many entries");
   if (d->n_inst == 0) return KTIR_OK;
-  KTIR_HIP_CHECK(hipMemsetAsync((void*)d->head, 0xff, (size_t)d->n_rows * 4, stream()));
-  KTIR_HIP_CHECK(hipMemsetAsync((void*)d->owners, 0, 4, stream()));
   int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());
-  int64_t total = d->n_inst * d->K;
-  int64_t blocks = (total + 15) / 16;
-  if (blocks > 16384) blocks = 16384;
-  hipLaunchKernelGGL(rmw_apply, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
+  const int64_t total = d->n_inst * d->K;
+  const bool vec = d->dst_col == 1 && d->src_col == 1 && d->dst_dtype == KTIR_F32 && d->dt == KTIR_F32 &&
+                   (d->src_dtype == KTIR_F16 || d->src_dtype == KTIR_F32) && d->D % 128 == 0 &&
+                   d->dst_base % 4 == 0 && d->dst_row % 4 == 0 && d->src_base % 4 == 0 && d->src_row % 4 == 0 &&
+                   d->dst_ptr % 16 == 0 && d->src_ptr % 16 == 0;
+  if (vec) {
+    const int64_t blocks = (d->n_rows + 255) / 256;
+    if (d->src_dtype == KTIR_F16)
+      hipLaunchKernelGGL(rmw_apply_rows<KTIR_F16>, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
+    else
+      hipLaunchKernelGGL(rmw_apply_rows<KTIR_F32>, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
+  } else {
+    int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(rmw_apply, dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+  }
   KTIR_HIP_CHECK(hipGetLastError());
   return KTIR_OK;
 }

@@ -315,12 +315,12 @@ def _row_rmw(ex, op, lb, st, trips):
     d.op, d.order, d.dt = rt.op(_RMW_OPS[val.op_type]), order, rt.DTYPE_CODE[res_dt]
     n_rows = max(1, -(-(ad.n_elems - int(bd[0])) // max(int(vd.strides[0]), 1)))
     d.n_rows = n_rows
-    head = ex.pool.temp(n_rows * 4)
+    # the chain heads: all -1 between calls (the launch resets what it uses)
+    head = rt.DeviceBuffer(n_rows * 4)
+    head.upload(np.full(n_rows, -1, np.int32))
     scratch = [ex.pool.temp(max(1, n_inst * K) * 4) for _ in range(3)]
-    owners = ex.pool.temp((4 + 4 * n_inst * K) * 4)
     d.head, d.link, d.rows, d.srcs = head.ptr, scratch[0].ptr, scratch[1].ptr, scratch[2].ptr
-    d.owners = owners.ptr
-    keep += [head, owners] + scratch
+    keep += [head] + scratch
     grp = id(d)
     z = np.zeros(L, np.int64)
     ex.log(ad, True, z, (1,), (1,), whole=True, group=grp)

@@ -99,8 +99,7 @@ class RMW(C.Structure):
                 ("dst_row", C.c_int64), ("dst_col", C.c_int64), ("dst_hi", C.c_int64), ("src_base", C.c_int64),
                 ("src_row", C.c_int64), ("src_col", C.c_int64), ("src_hi", C.c_int64), ("op", C.c_int32),
                 ("order", C.c_int32), ("dt", C.c_int32), ("pad", C.c_int32), ("n_rows", C.c_int64),
-                ("head", C.c_uint64), ("link", C.c_uint64), ("rows", C.c_uint64), ("srcs", C.c_uint64),
-                ("owners", C.c_uint64)]
+                ("head", C.c_uint64), ("link", C.c_uint64), ("rows", C.c_uint64), ("srcs", C.c_uint64)]
 
 
 class ATTN(C.Structure):
