@@ -220,6 +220,38 @@ __device__ __forceinline__ void map_binop(int op, int dt, bool swap, const float
   for (int e = 0; e < 8; ++e) r[e] = binop_f_simple(op, dt, p[e], q[e]);
 }
 
+// A chunk's 8 elements as raw 16-byte words (one for 16-bit types, two for f32)
+template <int DT>
+struct Raw8 {
+  mu4 w[DT == KTIR_F32 ? 2 : 1];
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> raw_load(uint64_t ptr, int64_t e0) {
+  Raw8<DT> r;
+  const KTIR_G(mu4)* p = (const KTIR_G(mu4)*)((const KTIR_G(uint8_t)*)ptr + e0 * (DT == KTIR_F32 ? 4 : 2));
+  r.w[0] = p[0];
+  if (DT == KTIR_F32) r.w[DT == KTIR_F32 ? 1 : 0] = p[1];
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void raw_decode(const Raw8<DT>& r, float (&out)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (DT == KTIR_F32) {
+      out[i] = __uint_as_float(r.w[0][i]);
+      out[4 + i] = __uint_as_float(r.w[DT == KTIR_F32 ? 1 : 0][i]);
+    } else if (DT == KTIR_BF16) {
+      out[2 * i] = __uint_as_float(r.w[0][i] << 16);
+      out[2 * i + 1] = __uint_as_float(r.w[0][i] & 0xffff0000u);
+    } else {
+      out[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.w[0][i] & 0xffffu));
+      out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.w[0][i] >> 16));
+    }
+  }
+}
+
 // compute and store one chunk
 template <int DO, int NIN>
 __device__ __forceinline__ void map_chunk(const ktir_prog_t& P, const ktir_leaf_t& LO, int fast, int n_ops, int out_reg,
@@ -259,14 +291,93 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
     float a0[8], b0[8], a1[8], b1[8];
     const MapOffs m0 = map_offsets(P, D, LA, LB, LO, bca, bcb, v0);
     const MapOffs m1 = map_offsets(P, D, LA, LB, LO, bca, bcb, on1 ? v1 : v0);
-    load8<DA>(LA, m0.a, a0, bca);
-    if (NIN == 2) load8<DB>(LB, m0.b, b0, bcb);
-    if (on1) {
-      load8<DA>(LA, m1.a, a1, bca);
-      if (NIN == 2) load8<DB>(LB, m1.b, b1, bcb);
+    // one uniform test: every chunk of the wavefront inside its allocations
+    // (then all raw loads are issued before anything is decoded)
+    bool inb = on1 && !bca && (NIN == 1 || !bcb);
+    inb = inb && m0.a >= LA.lo && m0.a + 8 <= LA.hi && m1.a >= LA.lo && m1.a + 8 <= LA.hi;
+    if (NIN == 2) inb = inb && m0.b >= LB.lo && m0.b + 8 <= LB.hi && m1.b >= LB.lo && m1.b + 8 <= LB.hi;
+    if (__all(inb)) {
+      const Raw8<DA> ra0 = raw_load<DA>(LA.ptr, m0.a), ra1 = raw_load<DA>(LA.ptr, m1.a);
+      Raw8<DB> rb0, rb1;
+      if (NIN == 2) {
+        rb0 = raw_load<DB>(LB.ptr, m0.b);
+        rb1 = raw_load<DB>(LB.ptr, m1.b);
+      }
+      raw_decode<DA>(ra0, a0);
+      raw_decode<DA>(ra1, a1);
+      if (NIN == 2) {
+        raw_decode<DB>(rb0, b0);
+        raw_decode<DB>(rb1, b1);
+      }
+    } else {
+      load8<DA>(LA, m0.a, a0, bca);
+      if (NIN == 2) load8<DB>(LB, m0.b, b0, bcb);
+      if (on1) {
+        load8<DA>(LA, m1.a, a1, bca);
+        if (NIN == 2) load8<DB>(LB, m1.b, b1, bcb);
+      }
     }
     map_chunk<DO, NIN>(P, LO, fast, n_ops, out_reg, m0, a0, b0);
     if (on1) map_chunk<DO, NIN>(P, LO, fast, n_ops, out_reg, m1, a1, b1);
+  }
+}
+
+// The single-binary-op form in a kernel of its own (no interpreter, so few
+// registers): MAP_BU chunks per thread per step, 256 chunks apart.  When the
+// whole wavefront's chunks lie inside their allocations (one uniform test)
+// all raw 16-byte loads are issued before anything is decoded; otherwise
+// chunk by chunk with the per-element out-of-range rules.
+constexpr int MAP_BU = 4;
+
+template <int DA, int DB, int DO>
+__global__ __launch_bounds__(256) void prog_map_bin(const ktir_prog_t P, const FlatDivs D, uint32_t total,
+                                                    int st_leaf, int fast) {
+  const ktir_leaf_t& LA = P.leaves[P.pf_leaf[0]];
+  const ktir_leaf_t& LB = P.leaves[P.pf_leaf[1]];
+  const ktir_leaf_t& LO = P.leaves[st_leaf];
+  const int nd = P.ndim;
+  const bool bca = LA.strides[nd - 1] == 0, bcb = LB.strides[nd - 1] == 0;
+  const int op = fast & 0xff, dt = fast >> 16;
+  const bool swap = (fast >> 8) & 1;
+  const uint32_t step = gridDim.x * 256 * MAP_BU;
+  for (uint32_t v0 = blockIdx.x * 256 * MAP_BU + threadIdx.x; v0 < total; v0 += step) {
+    MapOffs m[MAP_BU];
+    bool inb = !bca && !bcb;
+#pragma unroll
+    for (int u = 0; u < MAP_BU; ++u) {
+      const uint32_t v = v0 + 256 * u;
+      m[u] = map_offsets(P, D, LA, LB, LO, bca, bcb, v < total ? v : v0);
+      inb = inb && v < total && m[u].a >= LA.lo && m[u].a + 8 <= LA.hi && m[u].b >= LB.lo && m[u].b + 8 <= LB.hi &&
+            m[u].o >= LO.lo && m[u].o + 8 <= LO.hi;
+    }
+    if (__all(inb)) {
+      Raw8<DA> ra[MAP_BU];
+      Raw8<DB> rb[MAP_BU];
+#pragma unroll
+      for (int u = 0; u < MAP_BU; ++u) {
+        ra[u] = raw_load<DA>(LA.ptr, m[u].a);
+        rb[u] = raw_load<DB>(LB.ptr, m[u].b);
+      }
+#pragma unroll
+      for (int u = 0; u < MAP_BU; ++u) {
+        float a[8], b[8], out[8];
+        raw_decode<DA>(ra[u], a);
+        raw_decode<DB>(rb[u], b);
+        map_binop<DO>(op, dt, swap, a, b, out);
+        store8<DO>(LO, m[u].o, out);
+      }
+      continue;
+    }
+#pragma unroll
+    for (int u = 0; u < MAP_BU; ++u) {
+      if (v0 + 256 * u < total) {
+        float a[8], b[8], out[8];
+        load8<DA>(LA, m[u].a, a, bca);
+        load8<DB>(LB, m[u].b, b, bcb);
+        map_binop<DO>(op, dt, swap, a, b, out);
+        store8<DO>(LO, m[u].o, out);
+      }
+    }
   }
 }
 
@@ -283,6 +394,13 @@ static void launch_map(const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, 
     const bool fdt = x.dt == KTIR_F16 || x.dt == KTIR_BF16 || x.dt == KTIR_F32;
     if (fop && fdt && Q.instr[1].a == x.dst && ((x.a == 0 && x.b == 1) || (x.a == 1 && x.b == 0)))
       fast = x.op | ((x.a == 1) << 8) | (x.dt << 16);
+  }
+  if (fast >= 0) {
+    int64_t nb = ((int64_t)total + 256 * MAP_BU - 1) / (256 * MAP_BU);
+    if (nb > 1048576) nb = 1048576;
+    hipLaunchKernelGGL((prog_map_bin<DA, DB, DO>), dim3((unsigned)nb), dim3(256), 0, stream(), Q, D, total, st_leaf,
+                       fast);
+    return;
   }
   hipLaunchKernelGGL((prog_map<DA, DB, DO, NIN>), dim3((unsigned)blocks), dim3(256), 0, stream(), Q, D, total,
                      st_leaf, fast);
