@@ -38,6 +38,50 @@ __device__ __forceinline__ f32x16 mfma32(const uint4& a, const uint4& b, f32x16 
   }
 }
 
+// Epilogue of a 128 x 128 tile (wavefront (wr, wc) holds the 64 x 64
+// quadrant as 2 x 2 MFMA tiles): round the product to the operand dtype of
+// the KTIR matmul, then accumulate into the outs tile (the reference's two
+// roundings).
+__device__ __forceinline__ void mm_epilogue(const ktir_mm_t& d, int64_t ln, int64_t m0, int64_t n0, int wr, int wc,
+                                            int lane, const f32x16& acc00, const f32x16& acc01, const f32x16& acc10,
+                                            const f32x16& acc11) {
+  const int64_t cbase = lane_offset(d.c, ln);
+  if (d.c.dtype == KTIR_F32 && d.round_dt == KTIR_F32 && d.accumulate != 1 && d.c.strides[1] == 1) {
+    // f32 result, outs absent or a zero splat (accumulate == 2: x + 0.0)
+    float* C = (float*)d.c.ptr + cbase;
+    const int64_t cs = d.c.strides[0];
+    const float z = d.accumulate == 2 ? 0.f : -0.f;
+#define EPI(a, i, j)                                                                               \
+  do {                                                                                             \
+    float* c = C + (m0 + wr * 64 + (i) * 32 + 4 * (lane >> 5)) * cs + n0 + wc * 64 + (j) * 32 + (lane & 31); \
+    _Pragma("unroll") for (int e = 0; e < 16; ++e) c[(8 * (e >> 2) + (e & 3)) * cs] = __fadd_rn(a[e], z); \
+  } while (0)
+    EPI(acc00, 0, 0);
+    EPI(acc01, 0, 1);
+    EPI(acc10, 1, 0);
+    EPI(acc11, 1, 1);
+#undef EPI
+    return;
+  }
+  const int64_t c0base = d.accumulate == 1 ? lane_offset(d.c0, ln) : 0;
+  for (int q = 0; q < 4; ++q) {
+    const int i = q >> 1, j = q & 1;
+    const f32x16 a = q == 0 ? acc00 : (q == 1 ? acc01 : (q == 2 ? acc10 : acc11));
+    for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int64_t col = n0 + wc * 64 + j * 32 + (lane & 31);
+        float v = round_to(a[e], d.round_dt);
+        if (d.accumulate == 1) {
+          const int64_t e0 = c0base + row * d.c0.strides[0] + col * d.c0.strides[1];
+          v = round_to(__fadd_rn(load_elem(d.c0.ptr, e0, d.c0.dtype), v), d.c.dtype);
+        } else if (d.accumulate == 2) {
+          v = round_to(__fadd_rn(0.f, v), d.c.dtype);
+        }
+        store_elem(d.c.ptr, cbase + row * d.c.strides[0] + col * d.c.strides[1], d.c.dtype, v);
+    }
+  }
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(256) void mm_mfma(const ktir_mm_t d, int64_t tiles_m, int64_t tiles_n) {
   __shared__ __align__(16) uint16_t As[2][MT * LDK];
@@ -112,43 +156,158 @@ __global__ __launch_bounds__(256) void mm_mfma(const ktir_mm_t d, int64_t tiles_
   }
 #undef GLOAD
 #undef SWRITE
-  // epilogue: round the product to the operand dtype of the KTIR matmul,
-  // then accumulate into the outs tile (the reference's two roundings)
-  const int64_t cbase = lane_offset(d.c, ln);
-  if (d.c.dtype == KTIR_F32 && d.round_dt == KTIR_F32 && d.accumulate != 1 && d.c.strides[1] == 1) {
-    // f32 result, outs absent or a zero splat (accumulate == 2: x + 0.0)
-    float* C = (float*)d.c.ptr + cbase;
-    const int64_t cs = d.c.strides[0];
-    const float z = d.accumulate == 2 ? 0.f : -0.f;
-#define EPI(a, i, j)                                                                               \
-  do {                                                                                             \
-    float* c = C + (m0 + wr * 64 + (i) * 32 + 4 * (lane >> 5)) * cs + n0 + wc * 64 + (j) * 32 + (lane & 31); \
-    _Pragma("unroll") for (int e = 0; e < 16; ++e) c[(8 * (e >> 2) + (e & 3)) * cs] = __fadd_rn(a[e], z); \
-  } while (0)
-    EPI(acc00, 0, 0);
-    EPI(acc01, 0, 1);
-    EPI(acc10, 1, 0);
-    EPI(acc11, 1, 1);
-#undef EPI
-    return;
-  }
-  const int64_t c0base = d.accumulate == 1 ? lane_offset(d.c0, ln) : 0;
-  for (int q = 0; q < 4; ++q) {
-    const int i = q >> 1, j = q & 1;
-    const f32x16 a = q == 0 ? acc00 : (q == 1 ? acc01 : (q == 2 ? acc10 : acc11));
-    for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int64_t col = n0 + wc * 64 + j * 32 + (lane & 31);
-        float v = round_to(a[e], d.round_dt);
-        if (d.accumulate == 1) {
-          const int64_t e0 = c0base + row * d.c0.strides[0] + col * d.c0.strides[1];
-          v = round_to(__fadd_rn(load_elem(d.c0.ptr, e0, d.c0.dtype), v), d.c.dtype);
-        } else if (d.accumulate == 2) {
-          v = round_to(__fadd_rn(0.f, v), d.c.dtype);
-        }
-        store_elem(d.c.ptr, cbase + row * d.c.strides[0] + col * d.c.strides[1], d.c.dtype, v);
+  mm_epilogue(d, ln, m0, n0, wr, wc, lane, acc00, acc01, acc10, acc11);
+}
+
+// ---- 128 x 128 x 64 tiles staged by LDS DMA -------------------------------------
+//
+// The same tile and wavefront split as mm_mfma, with both operands moving
+// HBM -> LDS by buffer_load ... lds (no registers, no transposition on the
+// way in), double-buffered in four distinct LDS arrays so the DMA of step
+// t + 1 overlaps the MFMAs of step t:
+//   A tile: 128 rows x 64 k, 128-byte rows, 16-byte chunk c of row r at slot
+//           c ^ (r % 8); A fragments are ds_read_b128 (the 8 rows of a read
+//           phase hit distinct banks).
+//   B tile: 64 k-rows x 128 columns, row-major as in HBM, 256-byte rows with
+//           chunk c at slot c ^ 2 (r % 8); B fragments (column l % 32, k
+//           8 (l / 32) .. + 8) are two ds_read_b64_tr_b16 transposing reads.
+typedef short mm_s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 mm_tr16(const uint16_t* p) {
+  const mm_s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) mm_s16x4*)p);
+  return __builtin_bit_cast(uint2, v);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mm_rsrc(const uint16_t* base, int64_t hi_elems) {
+  int64_t bytes = hi_elems * 2;
+  if (bytes < 0) bytes = 0;
+  if (bytes > 0xffffffffll) bytes = 0xffffffffll;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+
+struct MmStage {
+  __amdgpu_buffer_rsrc_t ra, rb;
+  uint32_t ao, bo0, bo1;       // lane byte offsets (A; B even / odd blocks)
+  int64_t a_row, b_row;
+};
+
+// wave w's share of step (koff_a, koff_b): A rows 32 w .. + 32 (4 blocks of 8
+// rows), B k-rows 16 w .. + 16 (4 blocks of 4 rows)
+__device__ __forceinline__ void mm_stage(const MmStage& g, uint16_t* as, uint16_t* bs, int w, int64_t koff_a,
+                                         int64_t koff_b) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(g.ra, (__attribute__((address_space(3))) void*)(as + 64 * (32 * w + 8 * b)),
+                                             16, g.ao, (int)((8 * b * g.a_row + koff_a) * 2), 0, 0);
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(g.rb, (__attribute__((address_space(3))) void*)(bs + 128 * (16 * w + 4 * b)),
+                                             16, (b & 1) ? g.bo1 : g.bo0, (int)((4 * b * g.b_row + koff_b) * 2), 0, 0);
+}
+
+struct MmAcc {
+  f32x16 c00, c01, c10, c11;
+};
+
+template <bool BF16>
+__device__ __forceinline__ void mm_step(MmAcc& acc, const uint16_t* as, const uint16_t* bs, int wr, int wc, int r32,
+                                        int h, const int (&b_off)[2][2]) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int ar0 = wr * 64 + r32, ar1 = ar0 + 32;
+    const int ch = 2 * kk + h;
+    const uint4 a0 = *(const uint4*)&as[ar0 * 64 + 8 * (ch ^ (ar0 & 7))];
+    const uint4 a1 = *(const uint4*)&as[ar1 * 64 + 8 * (ch ^ (ar1 & 7))];
+    const uint16_t* bt = bs + 16 * kk * 128;
+    uint4 b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint2 lo = mm_tr16(bt + b_off[0][j]), hi = mm_tr16(bt + b_off[1][j]);
+      b[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
+    acc.c00 = mfma32<BF16>(a0, b[0], acc.c00);
+    acc.c01 = mfma32<BF16>(a0, b[1], acc.c01);
+    acc.c10 = mfma32<BF16>(a1, b[0], acc.c10);
+    acc.c11 = mfma32<BF16>(a1, b[1], acc.c11);
   }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256, 2) void mm_mfma_dma(const ktir_mm_t d, int64_t tiles_m, int64_t tiles_n) {
+  __shared__ __align__(16) uint16_t As0[MT * BK];
+  __shared__ __align__(16) uint16_t As1[MT * BK];
+  __shared__ __align__(16) uint16_t Bs0[BK * NT];
+  __shared__ __align__(16) uint16_t Bs1[BK * NT];
+  const int tid = threadIdx.x, l = tid & 63, h = l >> 5, r32 = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w >> 1, wc = w & 1;
+  const int64_t nblk = gridDim.x;
+  int64_t bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int64_t per_lane = tiles_m * tiles_n;
+  const int64_t ln = bid / per_lane, t = bid - ln * per_lane;
+  const int64_t m0 = (t / tiles_n) * MT, n0 = (t % tiles_n) * NT;
+  const int64_t a_row = d.a.strides[0], b_row = d.b.strides[0];
+  const int64_t abase = uni(lane_offset(d.a, ln)) + m0 * a_row;
+  const int64_t bbase = uni(lane_offset(d.b, ln)) + n0;
+  MmStage g;
+  const int64_t a0w = abase + 32 * w * a_row, b0w = bbase + 16 * w * b_row;
+  g.ra = mm_rsrc((const uint16_t*)d.a.ptr + a0w, d.a.hi - a0w);
+  g.rb = mm_rsrc((const uint16_t*)d.b.ptr + b0w, d.b.hi - b0w);
+  g.a_row = a_row;
+  g.b_row = b_row;
+  g.ao = (uint32_t)(((l >> 3) * a_row + 8 * ((l & 7) ^ (l >> 3))) * 2);
+  g.bo0 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ (2 * (l >> 4)))) * 2);
+  g.bo1 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ (2 * (4 + (l >> 4))))) * 2);
+  // B fragment offsets inside a 16-row step: member tj of 16-lane group tg
+  // reads k-row 8 (tg / 2) + tj / 4 (+ 4), columns 16 (tg % 2) + 4 (tj % 4)
+  // of the 32-column group 2 wc + j
+  const int tg = l >> 4, tj = l & 15;
+  const int br0 = 8 * (tg >> 1) + (tj >> 2);
+  const int bc = 2 * (tg & 1) + ((tj >> 1) & 1), bin = 4 * (tj & 1);
+  int b_off[2][2];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      b_off[hi][j] = (br0 + 4 * hi) * NT + 8 * ((4 * (2 * wc + j) + bc) ^ (2 * ((br0 + 4 * hi) & 7))) + bin;
+  const int64_t kt_per_step = d.K / BK;
+  const int64_t nk = d.ksteps * kt_per_step;
+  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  MmAcc acc{zero16, zero16, zero16, zero16};
+  // k offsets (elements) of the staged step for A and B
+  int64_t s_ = 0, kk0 = 0;
+  int64_t ka = 0, kb = 0;
+  mm_stage(g, As0, Bs0, w, ka, kb);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; kt += 2) {
+    // even step from buffers 0 while step kt + 1 streams into buffers 1
+    kk0 += BK;
+    if (kk0 == kt_per_step * BK) { kk0 = 0; ++s_; }
+    const bool m1 = kt + 1 < nk;
+    if (m1) {
+      ka = s_ * d.a_kstep + kk0;
+      kb = s_ * d.b_kstep + kk0 * b_row;
+      mm_stage(g, As1, Bs1, w, ka, kb);
+    }
+    mm_step<BF16>(acc, As0, Bs0, wr, wc, r32, h, b_off);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (!m1) break;
+    kk0 += BK;
+    if (kk0 == kt_per_step * BK) { kk0 = 0; ++s_; }
+    const bool m2 = kt + 2 < nk;
+    if (m2) {
+      ka = s_ * d.a_kstep + kk0;
+      kb = s_ * d.b_kstep + kk0 * b_row;
+      mm_stage(g, As0, Bs0, w, ka, kb);
+    }
+    mm_step<BF16>(acc, As1, Bs1, wr, wc, r32, h, b_off);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  mm_epilogue(d, ln, m0, n0, wr, wc, l, acc.c00, acc.c01, acc.c10, acc.c11);
 }
 
 }  // namespace ktir
@@ -190,10 +349,21 @@ int ktir_launch_matmul_mfma(const ktir_mm_t* d, bool* handled) {
   const int64_t tm = d->M / MT, tn = d->N / NT;
   const int64_t blocks = L * tm * tn;
   if (blocks >= (int64_t)0x7fffffff) return KTIR_OK;
-  if (f16)
+  // the DMA kernel addresses each wavefront's rows with 32-bit buffer offsets
+  const int64_t a_span = (31 + 24) * d->a.strides[0] + (d->ksteps - 1) * d->a_kstep + d->K;
+  const int64_t b_span = (15 + 12 + d->K) * d->b.strides[0] + (d->ksteps - 1) * d->b_kstep + NT;
+  const bool dma = a_span >= 0 && b_span >= 0 && a_span * 2 < (int64_t)0x7fffffff && b_span * 2 < (int64_t)0x7fffffff &&
+                   d->a_kstep >= 0 && d->b_kstep >= 0;
+  if (dma) {
+    if (f16)
+      hipLaunchKernelGGL((mm_mfma_dma<false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
+    else
+      hipLaunchKernelGGL((mm_mfma_dma<true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
+  } else if (f16) {
     hipLaunchKernelGGL((mm_mfma<false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
-  else
+  } else {
     hipLaunchKernelGGL((mm_mfma<true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
+  }
   KTIR_HIP_CHECK(hipGetLastError());
   *handled = true;
   return KTIR_OK;
