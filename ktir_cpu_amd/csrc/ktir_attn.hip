@@ -16,9 +16,9 @@
 // communication.  K and V tiles move HBM -> LDS with global_load_lds_dwordx4
 // (no registers): the next K tile streams in while P @ V runs, the next V
 // tile while the next scores are computed.  In LDS a tile row is 256 bytes
-// with its 16-byte chunk c stored at slot c ^ 2 (row % 8), so the 8 rows of
-// a ds_read_b128 phase and the 4 rows of a ds_read_b64_tr_b16 phase hit
-// distinct banks.
+// with its 16-byte chunk c stored at slot c ^ swz16(row % 16) (an XOR of row
+// bits), so every ds_read_b128 and ds_read_b64_tr_b16 phase hits distinct
+// banks (with 32 or 64 LDS banks alike).
 // Semantics follow the KTIR loop body (see ktir_hip.h):
 // m' = max(m, rowmax S) (NaN-propagating like arith.maximumf),
 // P = exp(S - m'), alpha = exp(m - m'), acc' = acc*alpha + P@V,
@@ -105,25 +105,30 @@ __device__ __forceinline__ uint2 ds_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// slot permutation of the 16 chunks of a 256-byte LDS row r
+__device__ __forceinline__ int swz16(int r) {
+  return ((r & 1) ? 4 : 0) ^ ((r & 2) ? 10 : 0) ^ ((r & 4) ? 1 : 0) ^ ((r & 8) ? 8 : 0);
+}
+
+// byte offset of lane l's chunk in a 4-row block whose rows have
+// row % 16 = 4 q + l / 16 (row l / 16 of the block)
+__device__ __forceinline__ uint32_t tile_lane_off(int l, int64_t row_stride, int q) {
+  const int r = l >> 4, c = (l & 15) ^ swz16(4 * q + r);
+  return (uint32_t)((r * row_stride + 8 * c) * 2);
+}
+
 // Wave w (uniform) copies rows 32w .. 32w+31 of a 128 x 128 tile into LDS: 8
 // blocks of 4 rows (1 KB), lane l filling slot l % 16 of row 4b + l / 16 of
 // block b.  buffer_load ... lds: a scalar buffer base per wave, a scalar
-// offset per block and a 32-bit lane offset that depends only on the block's
-// parity (vo0 even, vo1 odd).
-__device__ __forceinline__ void tile_to_lds(const uint16_t* src, int64_t row_stride, uint16_t* lds, int wu,
-                                            uint32_t vo0, uint32_t vo1) {
+// offset per block and a 32-bit lane offset that depends on b % 4 (computed
+// here: a few VALU instructions instead of registers held across the loop).
+__device__ __forceinline__ void tile_to_lds(const uint16_t* src, int64_t row_stride, uint16_t* lds, int wu, int l) {
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(src + (int64_t)(32 * wu) * row_stride), (short)0, (int)((31 * row_stride + AT) * 2), 0x00020000);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds + 512 * (8 * wu + i)),
-                                             16, (i & 1) ? vo1 : vo0, (int)(i * 8 * row_stride), 0, 0);
-}
-
-// byte offset of lane l's chunk in a block of parity `odd` (row l / 16 of the block)
-__device__ __forceinline__ uint32_t tile_lane_off(int l, int64_t row_stride, int odd) {
-  const int r = l >> 4, c = (l & 15) ^ (2 * ((4 * odd + r) & 7));
-  return (uint32_t)((r * row_stride + 8 * c) * 2);
+                                             16, tile_lane_off(l, row_stride, i & 3), (int)(i * 8 * row_stride), 0, 0);
 }
 
 #define AT_S_LOOP(BODY)                                      \
@@ -145,14 +150,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   const int64_t kb0 = uni(((const int64_t*)d.k_base)[lane]), vb0 = uni(((const int64_t*)d.v_base)[lane]);
   uint4 qf[8];                                       // Q^T fragments: Q[row][16 s + 8 h .. + 8]
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  const uint32_t ko0 = tile_lane_off(l, d.k_row, 0), ko1 = tile_lane_off(l, d.k_row, 1);
-  const uint32_t vo0 = tile_lane_off(l, d.v_row, 0), vo1 = tile_lane_off(l, d.v_row, 1);
   if (T > 0) {
     const uint16_t* qr = Q + uni(((const int64_t*)d.q_base)[lane]) + (int64_t)row * d.q_row + 8 * h;
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = *(const uint4*)(qr + 16 * s);
-    tile_to_lds(K + kb0, d.k_row, Ks, wu, ko0, ko1);
-    tile_to_lds(V + vb0, d.v_row, Vs, wu, vo0, vo1);
+    tile_to_lds(K + kb0, d.k_row, Ks, wu, l);
+    tile_to_lds(V + vb0, d.v_row, Vs, wu, l);
     __builtin_amdgcn_s_waitcnt(0);
   }
   __syncthreads();
@@ -163,27 +166,27 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   const f32x16_t z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   f32x16_t o0 = z16, o1 = z16, o2 = z16, o3 = z16;   // O^T tiles: d = 32 dt + 8g + 4h + t, row r32
   float m = -__builtin_inff(), lsum = 0.f;
-  // K^T A-fragments: row 32 kt + r32, chunk 2 s + h at slot (2 s + h) ^ 2 (r32 % 8)
-  const int k_off = r32 * AT + 8 * h;
-  const int k_x = r32 & 7;
+  // K A-fragments: row 32 kt + r32, chunk 2 s + h at slot (2 s + h) ^ swz16(r32 % 16)
+  const int k_off = r32 * AT;
+  const int k_x = swz16(r32 & 15);
   // V^T fragment rows d = 32 dt + l % 32, keys 16 ks + 8 h + [0..8): member tj of
   // 16-lane group tg addresses key 8 (tg / 2) + tj / 4 (+4), d 16 (tg % 2) + 4 (tj % 4)
   const int tg = l >> 4, tj = l & 15;
   const int v_row0 = 8 * (tg >> 1) + (tj >> 2);
   const int v_c = 2 * (tg & 1) + ((tj >> 1) & 1), v_in = 4 * (tj & 1);
-  int v_off[2][4];
-#pragma unroll
-  for (int hi = 0; hi < 2; ++hi)
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-      v_off[hi][dt] = (v_row0 + 4 * hi) * AT + 8 * ((4 * dt + v_c) ^ (2 * ((v_row0 + 4 * hi) & 7))) + v_in;
+  // chunk index bases (4 dt + v_c) ^ swz16(row) = 4 dt ^ (v_c ^ swz16(row)): two per lane
+  const int v_b0 = v_row0 * AT + v_in, v_x0 = v_c ^ swz16(v_row0), v_x1 = v_c ^ swz16(v_row0 + 4);
   for (int j = 0; j < T; ++j) {
     const bool more = j + 1 < T;
+    // fragment addresses are recomputed in the loop from opaque bases (a few
+    // VALU instructions) instead of 16 registers held across it
+    int kx = k_x, vfb = v_b0, vx0 = v_x0, vx1 = v_x1;
+    asm volatile("" : "+v"(kx), "+v"(vfb), "+v"(vx0), "+v"(vx1));
     // S^T = K Q^T: 4 key tiles x 8 d-steps
     f32x16_t s0 = z16, s1 = z16, s2 = z16, s3 = z16;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const uint16_t* kp = &Ks[k_off + 16 * (s ^ k_x)];
+      const uint16_t* kp = &Ks[k_off + 8 * ((2 * s + h) ^ kx)];
       s0 = mfma_at<BF16>(*(const uint4*)(kp + 0 * 32 * AT), qf[s], s0);
       s1 = mfma_at<BF16>(*(const uint4*)(kp + 1 * 32 * AT), qf[s], s1);
       s2 = mfma_at<BF16>(*(const uint4*)(kp + 2 * 32 * AT), qf[s], s2);
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     m = mn;
     __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of V_j has landed
     __syncthreads();                                  // every wave: done with Ks, V_j in LDS
-    if (more) tile_to_lds(K + kb0 + (int64_t)(j + 1) * d.k_step, d.k_row, Ks, wu, ko0, ko1);
+    if (more) tile_to_lds(K + kb0 + (int64_t)(j + 1) * d.k_step, d.k_row, Ks, wu, l);
     // O^T += V^T P^T over 8 key-steps of 16 keys
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
       uint4 a[4];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const uint2 lo = ds_tr16(vt + v_off[0][dt]), hi = ds_tr16(vt + v_off[1][dt]);
+        const uint2 lo = ds_tr16(vt + vfb + 8 * ((4 * dt) ^ vx0)), hi = ds_tr16(vt + vfb + 4 * AT + 8 * ((4 * dt) ^ vx1));
         a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
       o0 = mfma_at<BF16>(a[0], ph, o0);
@@ -293,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     }
     __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of K_{j+1} has landed
     __syncthreads();                                  // every wave: done with Vs, K_{j+1} in LDS
-    if (more) tile_to_lds(V + vb0 + (int64_t)(j + 1) * d.v_step, d.v_row, Vs, wu, vo0, vo1);
+    if (more) tile_to_lds(V + vb0 + (int64_t)(j + 1) * d.v_step, d.v_row, Vs, wu, l);
   }
   // final state
   if (h == 0) {

@@ -166,12 +166,22 @@ __global__ __launch_bounds__(256) void mm_mfma(const ktir_mm_t d, int64_t tiles_
 // way in), double-buffered in four distinct LDS arrays so the DMA of step
 // t + 1 overlaps the MFMAs of step t:
 //   A tile: 128 rows x 64 k, 128-byte rows, 16-byte chunk c of row r at slot
-//           c ^ (r % 8); A fragments are ds_read_b128 (the 8 rows of a read
-//           phase hit distinct banks).
+//           c ^ (r % 8) ^ ((r / 8) % 2); A fragments are ds_read_b128.
 //   B tile: 64 k-rows x 128 columns, row-major as in HBM, 256-byte rows with
-//           chunk c at slot c ^ 2 (r % 8); B fragments (column l % 32, k
+//           chunk c at slot c ^ swz16(r); B fragments (column l % 32, k
 //           8 (l / 32) .. + 8) are two ds_read_b64_tr_b16 transposing reads.
+// Both swizzles make every read phase touch distinct banks (with 32 or 64
+// LDS banks alike).
 typedef short mm_s16x4 __attribute__((ext_vector_type(4)));
+
+// slot permutation of the 16 chunks of a 256-byte LDS row r (an XOR of row
+// bits; conflict-free for ds_read_b64_tr_b16 column reads and ds_read_b128
+// row reads)
+__device__ __forceinline__ int swz16(int r) {
+  return ((r & 1) ? 4 : 0) ^ ((r & 2) ? 10 : 0) ^ ((r & 4) ? 1 : 0) ^ ((r & 8) ? 8 : 0);
+}
+
+__device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 __device__ __forceinline__ uint2 mm_tr16(const uint16_t* p) {
   const mm_s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) mm_s16x4*)p);
@@ -187,7 +197,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mm_rsrc(const uint16_t* base, 
 
 struct MmStage {
   __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t ao, bo0, bo1;       // lane byte offsets (A; B even / odd blocks)
+  uint32_t ao0, ao1;            // lane byte offsets of A blocks (even / odd)
+  uint32_t bo0, bo1, bo2, bo3;  // lane byte offsets of B blocks b % 4
   int64_t a_row, b_row;
 };
 
@@ -198,11 +209,12 @@ __device__ __forceinline__ void mm_stage(const MmStage& g, uint16_t* as, uint16_
 #pragma unroll
   for (int b = 0; b < 4; ++b)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(g.ra, (__attribute__((address_space(3))) void*)(as + 64 * (32 * w + 8 * b)),
-                                             16, g.ao, (int)((8 * b * g.a_row + koff_a) * 2), 0, 0);
+                                             16, (b & 1) ? g.ao1 : g.ao0, (int)((8 * b * g.a_row + koff_a) * 2), 0, 0);
 #pragma unroll
   for (int b = 0; b < 4; ++b)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(g.rb, (__attribute__((address_space(3))) void*)(bs + 128 * (16 * w + 4 * b)),
-                                             16, (b & 1) ? g.bo1 : g.bo0, (int)((4 * b * g.b_row + koff_b) * 2), 0, 0);
+                                             16, b == 0 ? g.bo0 : (b == 1 ? g.bo1 : (b == 2 ? g.bo2 : g.bo3)),
+                                             (int)((4 * b * g.b_row + koff_b) * 2), 0, 0);
 }
 
 struct MmAcc {
@@ -216,8 +228,8 @@ __device__ __forceinline__ void mm_step(MmAcc& acc, const uint16_t* as, const ui
   for (int kk = 0; kk < 4; ++kk) {
     const int ar0 = wr * 64 + r32, ar1 = ar0 + 32;
     const int ch = 2 * kk + h;
-    const uint4 a0 = *(const uint4*)&as[ar0 * 64 + 8 * (ch ^ (ar0 & 7))];
-    const uint4 a1 = *(const uint4*)&as[ar1 * 64 + 8 * (ch ^ (ar1 & 7))];
+    const uint4 a0 = *(const uint4*)&as[ar0 * 64 + 8 * (ch ^ swz_a(ar0))];
+    const uint4 a1 = *(const uint4*)&as[ar1 * 64 + 8 * (ch ^ swz_a(ar1))];
     const uint16_t* bt = bs + 16 * kk * 128;
     uint4 b[2];
 #pragma unroll
@@ -256,9 +268,14 @@ __global__ __launch_bounds__(256, 2) void mm_mfma_dma(const ktir_mm_t d, int64_t
   g.rb = mm_rsrc((const uint16_t*)d.b.ptr + b0w, d.b.hi - b0w);
   g.a_row = a_row;
   g.b_row = b_row;
-  g.ao = (uint32_t)(((l >> 3) * a_row + 8 * ((l & 7) ^ (l >> 3))) * 2);
-  g.bo0 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ (2 * (l >> 4)))) * 2);
-  g.bo1 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ (2 * (4 + (l >> 4))))) * 2);
+  // block b of A: rows 8 b + l / 8 (row % 16 = 8 (b % 2) + l / 8), slot l % 8;
+  // block b of B: k-rows 4 b + l / 16 (row % 16 = 4 b + l / 16), slot l % 16
+  g.ao0 = (uint32_t)(((l >> 3) * a_row + 8 * ((l & 7) ^ swz_a(l >> 3))) * 2);
+  g.ao1 = (uint32_t)(((l >> 3) * a_row + 8 * ((l & 7) ^ swz_a(8 + (l >> 3)))) * 2);
+  g.bo0 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ swz16(l >> 4))) * 2);
+  g.bo1 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ swz16(4 + (l >> 4)))) * 2);
+  g.bo2 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ swz16(8 + (l >> 4)))) * 2);
+  g.bo3 = (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ swz16(12 + (l >> 4)))) * 2);
   // B fragment offsets inside a 16-row step: member tj of 16-lane group tg
   // reads k-row 8 (tg / 2) + tj / 4 (+ 4), columns 16 (tg % 2) + 4 (tj % 4)
   // of the 32-column group 2 wc + j
@@ -270,7 +287,7 @@ __global__ __launch_bounds__(256, 2) void mm_mfma_dma(const ktir_mm_t d, int64_t
   for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      b_off[hi][j] = (br0 + 4 * hi) * NT + 8 * ((4 * (2 * wc + j) + bc) ^ (2 * ((br0 + 4 * hi) & 7))) + bin;
+      b_off[hi][j] = (br0 + 4 * hi) * NT + 8 * ((4 * (2 * wc + j) + bc) ^ swz16(br0 + 4 * hi)) + bin;
   const int64_t kt_per_step = d.K / BK;
   const int64_t nk = d.ksteps * kt_per_step;
   const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
