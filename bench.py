@@ -115,16 +115,26 @@ CONFIGS = {"vector_add": _vector_add, "copy": _copy, "gather": _gather, "softmax
            "gemm": _gemm, "attention": _attention}
 
 
-def _traffic(config):
-    """HBM bytes per launch of the config's dominant launch, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (profiles/traffic.json,
-    scaled by a copy kernel of known size), or None when not measured."""
+# kernels that make up each kind of launch (the HIP kernel names)
+_LAUNCH_KERNELS = {"mm": ("mm_mfma", "mm_generic"), "attn": ("attn_kernel",), "rmw": ("rmw_",),
+                   "prog": ("prog_",)}
+
+
+def _traffic(config, kind):
+    """HBM bytes per launch of the config's dominant launch (of kind `kind`):
+    the summed rocprofv3 FETCH_SIZE / WRITE_SIZE bytes of that launch's
+    kernels, committed in profiles/traffic.json (scaled by a copy kernel of
+    known size), or None when not measured."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             t = json.load(f)["configs"].get(config)
     except (OSError, ValueError, KeyError):
         return None
-    return round(t["traffic_bytes"]) if t else None
+    if not t:
+        return None
+    pats = _LAUNCH_KERNELS.get(kind, ())
+    b = [v["bytes"] for k, v in t.get("kernels", {}).items() if any(p in k for p in pats)]
+    return round(sum(b)) if b else None
 
 
 def cpu_baseline(cfg, budget_s=15.0):
@@ -234,7 +244,7 @@ def main():
         "config": {"workload": cfg["workload"], "launches_per_step": len(plan.launches),
                    "plan_mode": plan.mode, "host_walk_s": round(walk_s, 3)},
         "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": _traffic(args.config),
+                     "frac": round(achieved / peak, 4), "traffic": _traffic(args.config, plan.launches[dom][0] if plan.launches else None),
                      "dominant_launch": plan.launches[dom][0] if plan.launches else None,
                      "dominant_ms": round(dom_ms, 6)},
     }
