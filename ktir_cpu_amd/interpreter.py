@@ -21,6 +21,7 @@ import numpy as np
 from . import runtime as rt
 from .executor import Arena, NeedEager, Plan, Pool, STICK_BYTES
 from .ir import IRModule
+from .latency import LatencyReport, LatencyTracker
 from .parser import KTIRParser
 from .walker import Executor
 
@@ -82,7 +83,9 @@ class KTIRInterpreter:
         self.last_plan: Optional[Plan] = None
         self._arena = Arena()
         self._pool = None
-        self._latency_report = None
+        # latency model (reference interpreter.py:76-78): charged op by op during the run
+        self._latency_tracker = LatencyTracker(latency_config, trace=trace_latency) if latency_config is not None \
+            else None
 
     # -- reference API ------------------------------------------------------
     def load(self, src: str):
@@ -102,8 +105,11 @@ class KTIRInterpreter:
             raise RuntimeError("No module loaded. Call load() first.")
         return self.module.get_function(fn).tensor_sizes
 
-    def get_latency_report(self):
-        return self._latency_report
+    def get_latency_report(self) -> Optional[LatencyReport]:
+        """Latency report of the last run, or None when no latency_config was given."""
+        if self._latency_tracker is None:
+            return None
+        return self._latency_tracker.report()
 
     def execute_function(self, fn_name: str, **kwargs) -> Dict[str, np.ndarray]:
         """Run `fn_name` on the GPU; returns every ndarray argument (reference interpreter.py:122-194)."""
@@ -139,14 +145,25 @@ class KTIRInterpreter:
             if not isinstance(v, np.ndarray):
                 args[k] = np.asarray(v)
         plan = None
-        try:
-            ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb)
+        lat = self._latency_tracker
+        if lat is not None:
+            # the latency model needs every op of every core, with the data
+            # its memory costs depend on: run core by core, op by op, on the GPU
+            nx, ny, nz = fn.grid
+            lat.reset()
+            lat.set_cores_active(nx * ny * nz)
+            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb, latency=lat)
             plan = ex.run()
-            plan.run()
-        except NeedEager as why:
-            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb)
-            plan = ex.run()
-            plan.fallback_reason = str(why)
+            plan.fallback_reason = "latency model"
+        else:
+            try:
+                ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb)
+                plan = ex.run()
+                plan.run()
+            except NeedEager as why:
+                ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb)
+                plan = ex.run()
+                plan.fallback_reason = str(why)
         rt.sync()
         self.last_plan = plan
         return Prepared(self, fn_name, list(arrays), plan, arena, arrays)

@@ -229,8 +229,11 @@ class _Level:
 
 class Executor:
     def __init__(self, fn: IRFunction, arena: Arena, args: Dict[str, Any], pool: Pool, *, sequential: bool,
-                 lx_size_mb: int = 2, allow_expand: bool = True):
+                 lx_size_mb: int = 2, allow_expand: bool = True, latency=None):
         self.fn = fn
+        # latency model (ktir_cpu_amd.latency.LatencyTracker) charged op by op, or None
+        self.lat = latency
+        self._lat_mem: Optional[np.ndarray] = None
         self.arena = arena
         self.args = args
         self.pool = pool
@@ -374,6 +377,11 @@ class Executor:
     def _exec(self, op: Operation):
         h = getattr(self, "h_" + op.op_type.replace(".", "_"), None)
         t = op.op_type
+        lat_ops = None
+        if self.lat is not None:
+            # operands as they were before the op (reference interpreter.py:209-217)
+            lat_ops = [self.get_value(n, peek=True) if self.has_value(n) else None for n in op.operands]
+            self._lat_mem = None
         if h is not None:
             res = h(op)
         elif t in FLOAT_BIN:
@@ -393,7 +401,72 @@ class Executor:
             charge = t not in NO_LX_CHARGE
             for n, v in zip(op.results, vals):
                 self.set_value(n, v, charge=charge)
+        if self.lat is not None:
+            self._lat_record(t, res, lat_ops)
         return res
+
+    # -- latency model (reference latency.py:289-432) -------------------------
+    def _lat_record(self, t: str, res, operands):
+        """Charge op `t` to every active core: HBM bytes of a load / store at
+        stick granularity, M/N/K of a matmul, else the element count of the
+        result (or of the first tile operand)."""
+        from . import latency
+        cat = latency.category_of(t)
+        cores = self.lanes.cores
+        if cat == latency.LC.MEMORY:
+            sticks = self._lat_mem if self._lat_mem is not None else np.zeros(len(cores), np.int64)
+            for c, k in zip(cores, sticks):
+                self.lat.record_op(int(c), t, nbytes=int(k) * latency.STICK_BYTES)
+            return
+        if cat == latency.LC.COMPUTE_MATMUL:
+            tiles = [v for v in (operands or []) if isinstance(v, Tile)]
+            mnk = (1, 1, 1)
+            if len(tiles) >= 2:
+                a, b = tiles[0].shape, tiles[1].shape
+                mnk = (a[0] if len(a) >= 2 else 1, b[1] if len(b) >= 2 else 1, a[1] if len(a) >= 2 else a[0])
+            for c in cores:
+                self.lat.record_op(int(c), t, mnk=mnk)
+            return
+        n = 1
+        if isinstance(res, Tile):
+            n = _prod(res.shape)
+        else:
+            for v in operands or []:
+                if isinstance(v, Tile):
+                    n = _prod(v.shape)
+                    break
+        for c in cores:
+            self.lat.record_op(int(c), t, n_elems=n)
+
+    def _lat_box(self, rel: np.ndarray, shape, strides, bpe: int):
+        """Per-lane unique sticks of a strided box access (element offsets
+        relative to a stick-aligned allocation)."""
+        if self.lat is None:
+            return
+        from .latency import unique_sticks_rows, unique_sticks_elems
+        shape = tuple(int(x) for x in shape) or (1,)
+        strides = tuple(int(x) for x in strides) or (1,)
+        rel = np.asarray(rel, dtype=np.int64).reshape(-1)
+        outer = np.zeros(1, np.int64)
+        for ext, st in zip(shape[:-1], strides[:-1]):
+            outer = (outer[:, None] + np.arange(ext, dtype=np.int64)[None, :] * st).reshape(-1)
+        if strides[-1] == 1:
+            self._lat_mem = np.array([unique_sticks_rows((r + outer) * bpe, shape[-1] * bpe) for r in rel], np.int64)
+        else:
+            full = (outer[:, None] + np.arange(shape[-1], dtype=np.int64)[None, :] * strides[-1]).reshape(-1)
+            self._lat_mem = np.array([unique_sticks_elems((r + full) * bpe) for r in rel], np.int64)
+
+    def _lat_elems(self, rel: np.ndarray, offs: np.ndarray, bpe: int, extra: Optional[np.ndarray] = None):
+        """Per-lane unique sticks of single-element accesses at `offs` (plus `extra` sticks)."""
+        if self.lat is None:
+            return
+        from .latency import unique_sticks_elems
+        rel = np.asarray(rel, dtype=np.int64).reshape(-1)
+        offs = np.asarray(offs, dtype=np.int64)
+        if offs.ndim == 1:
+            offs = np.broadcast_to(offs, (len(rel), offs.size))
+        k = np.array([unique_sticks_elems((r + o) * bpe) for r, o in zip(rel, offs)], np.int64)
+        self._lat_mem = k if extra is None else k + extra
 
     # -- memory helpers -------------------------------------------------------
     def _alloc_of(self, byte_addr: np.ndarray) -> Alloc:
@@ -578,6 +651,7 @@ class Executor:
             shape = cs.extent
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
             self.log(alloc, False, rel, shape, v.strides)
+            self._lat_box(rel, shape, v.strides, rt.ELEM_BYTES[v.dtype])
             return Tile(Expr("ld", v.dtype, shape, attr=spec))
         coords = cs.enumerate(at.shape)
         if co is not None:
@@ -592,6 +666,7 @@ class Executor:
         if len(offs) != _prod(out_shape):
             raise ValueError(f"cannot reshape {len(offs)} loaded elements into {out_shape}")
         spec, alloc, rel = self._hbm_leaf(v, origin, out_shape, _cstrides(out_shape))
+        self._lat_elems(rel, offs, rt.ELEM_BYTES[v.dtype])
         buf = self.pool.upload(offs)
         spec.offsets, spec.offsets_ls = buf, 0
         spec.strides = _cstrides(out_shape) if out_shape else (1,)
@@ -615,6 +690,7 @@ class Executor:
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
             self._store_expr(val, spec, alloc, shape)
             self.log(alloc, True, rel, shape, v.strides)
+            self._lat_box(rel, shape, v.strides, rt.ELEM_BYTES[v.dtype])
             return None
         coords = cs.enumerate(at.shape)
         if co is not None:
@@ -625,6 +701,7 @@ class Executor:
         if len(offs) != n:
             raise ValueError("ktdp.store: tile size does not match the access tile's points")
         spec, alloc, rel = self._hbm_leaf(v, at.origin, val.shape, _cstrides(val.shape))
+        self._lat_elems(rel, offs, rt.ELEM_BYTES[v.dtype])
         spec.offsets, spec.offsets_ls = self.pool.upload(offs), 0
         if len(np.unique(offs)) != len(offs):
             self._winners(spec, n)
@@ -728,11 +805,29 @@ class Executor:
         spec, alloc, rel = self._hbm_leaf(at.parent, np.zeros(L, np.int64), (n,), (1,))
         spec.offsets, spec.offsets_ls = out, n
         spec.keep = spec.keep + (out,)
+        if self.lat is not None:
+            # index-tensor sticks from the positions read, data sticks from the
+            # offsets the GPU computed (the run is eager, so they exist now)
+            from .latency import unique_sticks_elems
+            idx_k = np.zeros(L, np.int64)
+            for iv, pos, _ in ind:
+                ibpe = rt.ELEM_BYTES[iv.dtype]
+                ia = self._alloc_of(iv.base.astype(np.int64) * ibpe)
+                lane_rel = iv.base.astype(np.int64) - ia.addr // ibpe
+                p = np.broadcast_to(pos, (L, n))
+                idx_k += np.array([unique_sticks_elems((lr + pp) * ibpe) for lr, pp in zip(lane_rel, p)], np.int64)
+            rt.sync()
+            raw = out.buf.download(L * n * 8)
+            offs = np.frombuffer(raw.tobytes(), dtype=np.int64).reshape(L, n)
+            self._lat_iat = (rel, offs, rt.ELEM_BYTES[at.parent.dtype], idx_k)
         return out, n, spec, alloc
 
     def indirect_load(self, at: IATile, result_shape):
         _, n, spec, alloc = self._iat_offsets(at)
         self.log(alloc, False, np.zeros(self.L, np.int64), (1,), (1,), whole=True)
+        if self.lat is not None:
+            rel, offs, bpe, idx_k = self._lat_iat
+            self._lat_elems(rel, offs, bpe, extra=idx_k)
         shape = tuple(result_shape)
         if _prod(shape) != n:
             raise ValueError(f"cannot reshape {n} gathered elements into {shape}")
@@ -745,9 +840,15 @@ class Executor:
                              f"IAT shape {tuple(at.shape)}")
         _, n, spec, alloc = self._iat_offsets(at)
         spec.strides = _cstrides(val.shape) if val.shape else (1,)
+        if self.lat is not None:
+            rel, offs, bpe, idx_k = self._lat_iat
+            lat_mem = (rel, offs, bpe, idx_k)
         self._winners(spec, n)
         self.log(alloc, True, np.zeros(self.L, np.int64), (1,), (1,), whole=True)
         self._store_expr(val, spec, alloc, val.shape)
+        if self.lat is not None:
+            rel, offs, bpe, idx_k = lat_mem
+            self._lat_elems(rel, offs, bpe, extra=idx_k)
 
     # ======================================================================
     # arith / math (reference dialects/arith_ops.py, ops/arith_ops.py, ops/math_ops.py)
@@ -1307,6 +1408,15 @@ class Executor:
             perm = [d for d in range(nd) if d != dim] + [dim]
             t = self.transpose(t, perm)
         n = t.shape[-1]
+        if self.lat is not None:
+            # the reference runs the combiner once per halving level on the
+            # two halves (linalg_ops.py:114-131): charge those runs
+            other, m = _prod(t.shape[:-1]), n
+            while m > 1:
+                half = m // 2
+                for c in self.lanes.cores:
+                    self.lat.record_op(int(c), comb, n_elems=other * half)
+                m = half + (m % 2)
         e = t.e
         if e.has_fold and (e._fold != n or len(_fold_space(e)) != len(t.shape)):
             e = self.materialize(t).e
@@ -1650,7 +1760,8 @@ class Executor:
         body = op.regions[0].ops
         inits = [self.get_value(n, peek=True) for n in op.operands[3:]]
         from .fusion import try_fuse_loop
-        fused = try_fuse_loop(self, op, lb, st, trips, inits)
+        # the latency model charges the loop body op by op: no fused loop launches
+        fused = try_fuse_loop(self, op, lb, st, trips, inits) if self.lat is None else None
         if fused is not None:
             res = fused
         elif not names and self.allow_expand and _expandable(body) and L > 0:
