@@ -270,6 +270,13 @@ typedef struct ktir_mm {
   ktir_leaf_t c0;         /* accumulator input when accumulate == 1 */
   int32_t accumulate;     /* 0: C = A@B; 1: C = C0 + A@B; 2: C = 0.0 + A@B (outs is a zero splat) */
   int32_t round_dt;       /* dtype the product is rounded to before accumulating (the KTIR operand dtype) */
+  /* Optional: lanes grouped 2 x 2 into 256 x 256 blocks (M = N = 128 only):
+   * const int32_t* [4 * n_quads] {top-left, top-right, bottom-left,
+   * bottom-right}; the right lane's B starts N columns after the left's with
+   * the same A, the bottom lane's A M rows below the top's with the same B.
+   * 0 / 0: not grouped. */
+  uint64_t quads;
+  int64_t n_quads;
 } ktir_mm_t;
 int ktir_launch_matmul(const ktir_mm_t* d);
 

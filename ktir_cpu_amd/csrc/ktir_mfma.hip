@@ -327,6 +327,160 @@ __global__ __launch_bounds__(256, 2) void mm_mfma_dma(const ktir_mm_t d, int64_t
   mm_epilogue(d, ln, m0, n0, wr, wc, l, acc.c00, acc.c01, acc.c10, acc.c11);
 }
 
+// ---- 256 x 256 blocks of four lanes ------------------------------------------------
+//
+// One workgroup computes a quad of lanes (a 256 x 256 block; the host checks
+// the lanes are adjacent): wavefront (wr, wc) computes lane quad[2 wr + wc]'s
+// whole 128 x 128 tile as 4 x 4 MFMA tiles (the accumulators live in AGPRs),
+// so every byte staged in LDS feeds twice the MFMA work of a 128 x 128 tile
+// and a 64-deep k step is 2048 MFMA cycles per wavefront, enough to cover the
+// next step's DMA.  A stage holds four 16 KB sub-tiles, each staged by one
+// wavefront: A top (rows of the top lanes), A bottom, B left, B right, in the
+// layouts of mm_mfma_dma (A: chunk c of row r at c ^ swz_a(r); B: row-major,
+// chunk c at c ^ swz16(r)); two stages double-buffered in two LDS arrays.
+// Launched for an f32 result without an accumulator input (the K-loop form).
+constexpr int QT = MT * BK;                     // halfs per sub-tile (16 KB)
+
+// fragments of one 16-deep slice: A rows 32 i + r32 (chunk 2 kk + h), B
+// columns 32 j + l % 32 (two transposing reads each)
+__device__ __forceinline__ void q256_frags(const uint16_t* as, const uint16_t* bs, int kk, int r32, int h,
+                                           const int (&b_off)[2][4], uint4 (&a)[4], uint4 (&b)[4]) {
+  const int ch = 2 * kk + h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ar = 32 * i + r32;
+    a[i] = *(const uint4*)&as[ar * BK + 8 * (ch ^ swz_a(ar))];
+  }
+  const uint16_t* bt = bs + 16 * kk * NT;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint2 lo = mm_tr16(bt + b_off[0][j]), hi = mm_tr16(bt + b_off[1][j]);
+    b[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void q256_step(f32x16 (&acc)[4][4], const uint16_t* as, const uint16_t* bs, int r32, int h,
+                                          const int (&b_off)[2][4]) {
+  uint4 a0[4], b0[4], a1[4], b1[4];
+  q256_frags(as, bs, 0, r32, h, b_off, a0, b0);
+#define Q_MFMA16(A, B)                                                                         \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<BF16>(A[i], B[j], acc[i][j]);
+  q256_frags(as, bs, 1, r32, h, b_off, a1, b1);
+  Q_MFMA16(a0, b0)
+  q256_frags(as, bs, 2, r32, h, b_off, a0, b0);
+  Q_MFMA16(a1, b1)
+  q256_frags(as, bs, 3, r32, h, b_off, a1, b1);
+  Q_MFMA16(a0, b0)
+  Q_MFMA16(a1, b1)
+#undef Q_MFMA16
+  // schedule: the first slice's 12 reads, then each later slice's 12 reads
+  // one per MFMA of the slice before it
+  __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+#pragma unroll
+    for (int x = 0; x < 12; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
+  __shared__ __align__(16) uint16_t P0[4 * QT];
+  __shared__ __align__(16) uint16_t P1[4 * QT];
+  const int tid = threadIdx.x, l = tid & 63, h = l >> 5, r32 = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w >> 1, wc = w & 1;
+  const int64_t nblk = gridDim.x;
+  int64_t g = blockIdx.x;
+  if ((nblk & 7) == 0) g = (g & 7) * (nblk >> 3) + (g >> 3);
+  const int32_t* q = (const int32_t*)d.quads + 4 * g;
+  const int64_t q0 = uni(q[0]), q1 = uni(q[1]), q2 = uni(q[2]), q3 = uni(q[3]);
+  const int64_t a_row = d.a.strides[0], b_row = d.b.strides[0];
+  // this wavefront's sub-tile: 0 A top (lane q0), 1 A bottom (q2), 2 B left (q0), 3 B right (q1)
+  const bool is_a = w < 2;
+  const int64_t src_lane = w == 0 ? q0 : (w == 1 ? q2 : (w == 2 ? q0 : q1));
+  const int64_t base = is_a ? uni(lane_offset(d.a, src_lane)) : uni(lane_offset(d.b, src_lane));
+  const __amdgpu_buffer_rsrc_t rs = is_a ? mm_rsrc((const uint16_t*)d.a.ptr + base, d.a.hi - base)
+                                         : mm_rsrc((const uint16_t*)d.b.ptr + base, d.b.hi - base);
+  // lane byte offsets: A blocks of 8 rows (row % 16 = 8 (b % 2) + l / 8), B
+  // blocks of 4 k-rows (row % 16 = 4 (b % 4) + l / 16)
+  uint32_t lo[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    lo[k] = is_a ? (uint32_t)(((l >> 3) * a_row + 8 * ((l & 7) ^ swz_a(8 * (k & 1) + (l >> 3)))) * 2)
+                 : (uint32_t)(((l >> 4) * b_row + 8 * ((l & 15) ^ swz16(4 * k + (l >> 4)))) * 2);
+  const int64_t blk_stride = is_a ? 8 * a_row : 4 * b_row;   // elements per 1 KB block
+  const int tg = l >> 4, tj = l & 15;
+  const int br0 = 8 * (tg >> 1) + (tj >> 2);
+  const int bc = 2 * (tg & 1) + ((tj >> 1) & 1), bin = 4 * (tj & 1);
+  int b_off[2][4];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b_off[hi][j] = (br0 + 4 * hi) * NT + 8 * ((4 * j + bc) ^ swz16(br0 + 4 * hi)) + bin;
+  const int64_t kt_per_step = d.K / BK;
+  const int64_t nk = d.ksteps * kt_per_step;
+  const f32x16 z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = z16;
+  int64_t s_ = 0, kk0 = 0;
+  // stage the next k step's sub-tile w into P (16 blocks of 1 KB)
+#define Q_ISSUE(P)                                                                                     \
+  do {                                                                                                 \
+    const int64_t koff = is_a ? s_ * d.a_kstep + kk0 : s_ * d.b_kstep + kk0 * b_row;                   \
+    uint16_t* dst = (P) + QT * w;                                                                      \
+    _Pragma("unroll") for (int b = 0; b < 16; ++b)                                                     \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * b), 16, \
+                                               lo[b & 3], (int)((b * blk_stride + koff) * 2), 0, 0);   \
+    kk0 += BK;                                                                                         \
+    if (kk0 == kt_per_step * BK) { kk0 = 0; ++s_; }                                                    \
+  } while (0)
+  // one k step from stage P: A sub-tile wr, B sub-tile 2 + wc.  The
+  // fragments of the next 16-deep slice are read while the 16 MFMAs of this
+  // one run (one LDS read between MFMAs), so the matrix pipe does not wait
+  // for LDS latency.
+#define Q_COMPUTE(P) q256_step<BF16>(acc, (P) + QT * wr, (P) + QT * (2 + wc), r32, h, b_off)
+  Q_ISSUE(P0);
+  // nk is even (checked at launch): whole pairs of steps, one exit
+  for (int64_t t = 0; t < nk; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < nk) Q_ISSUE(P1);
+    Q_COMPUTE(P0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < nk) Q_ISSUE(P0);
+    Q_COMPUTE(P1);
+  }
+#undef Q_ISSUE
+#undef Q_COMPUTE
+  // epilogue: this wavefront's lane tile (4 x 4 MFMA tiles; lane l holds
+  // column 32 j + l % 32, rows 32 i + 8 (e / 4) + 4 h + e % 4)
+  const int64_t ln = w == 0 ? q0 : (w == 1 ? q1 : (w == 2 ? q2 : q3));
+  // f32 result, outs absent or a zero splat (the only form launched here)
+  float* C = (float*)d.c.ptr + lane_offset(d.c, ln);
+  const int64_t cs = d.c.strides[0];
+  const float z = d.accumulate == 2 ? 0.f : -0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        C[(32 * i + 8 * (e >> 2) + 4 * h + (e & 3)) * cs + 32 * j + r32] = __fadd_rn(acc[i][j][e], z);
+}
+
 }  // namespace ktir
 
 using namespace ktir;
@@ -335,6 +489,8 @@ using namespace ktir;
 // 16-byte aligned rows, M and N multiples of 128, K a multiple of 64.  The
 // caller (the lockstep executor) has already checked that every lane's
 // operand range lies inside its allocation.
+static int64_t kt_steps(const ktir_mm_t* d) { return d->K / BK; }
+
 int ktir_launch_matmul_mfma(const ktir_mm_t* d, bool* handled) {
   *handled = false;
   const bool f16 = d->a.dtype == KTIR_F16 && d->b.dtype == KTIR_F16;
@@ -371,7 +527,15 @@ int ktir_launch_matmul_mfma(const ktir_mm_t* d, bool* handled) {
   const int64_t b_span = (15 + 12 + d->K) * d->b.strides[0] + (d->ksteps - 1) * d->b_kstep + NT;
   const bool dma = a_span >= 0 && b_span >= 0 && a_span * 2 < (int64_t)0x7fffffff && b_span * 2 < (int64_t)0x7fffffff &&
                    d->a_kstep >= 0 && d->b_kstep >= 0;
-  if (dma) {
+  const bool q256 = dma && d->quads && d->n_quads * 4 == L && d->M == MT && d->N == NT &&
+                    (d->ksteps * kt_steps(d)) % 2 == 0 && d->n_quads < (int64_t)0x7fffffff &&
+                    d->c.dtype == KTIR_F32 && d->round_dt == KTIR_F32 && d->accumulate != 1 && d->c.strides[1] == 1;
+  if (q256) {
+    if (f16)
+      hipLaunchKernelGGL((mm_mfma_256<false>), dim3((unsigned)d->n_quads), dim3(256), 0, stream(), *d);
+    else
+      hipLaunchKernelGGL((mm_mfma_256<true>), dim3((unsigned)d->n_quads), dim3(256), 0, stream(), *d);
+  } else if (dma) {
     if (f16)
       hipLaunchKernelGGL((mm_mfma_dma<false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, tm, tn);
     else

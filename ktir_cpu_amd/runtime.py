@@ -87,7 +87,7 @@ class MM(C.Structure):
     _fields_ = [("lanes", C.c_int64), ("M", C.c_int64), ("N", C.c_int64), ("K", C.c_int64),
                 ("ksteps", C.c_int64), ("a", Leaf), ("b", Leaf), ("a_kstep", C.c_int64),
                 ("b_kstep", C.c_int64), ("c", Leaf), ("c0", Leaf), ("accumulate", C.c_int32),
-                ("round_dt", C.c_int32)]
+                ("round_dt", C.c_int32), ("quads", C.c_uint64), ("n_quads", C.c_int64)]
 
 
 class RMW(C.Structure):

@@ -194,6 +194,36 @@ def remap_lanes(e: Expr, idx: np.ndarray, memo=None) -> Expr:
     return r
 
 
+def _mm_quads(la, lb, L: int, M: int, N: int) -> Optional[np.ndarray]:
+    """Group the lanes of a 128 x 128 matmul 2 x 2 into 256 x 256 blocks:
+    {top-left, top-right, bottom-left, bottom-right} with the right lane's B
+    N columns after the left's (same A) and the bottom lane's A M rows below
+    the top's (same B).  None unless every lane falls in exactly one group."""
+    if L < 4 or L % 4 or la.strides[-1] != 1 or lb.strides[-1] != 1:
+        return None
+    ao, bo = la.lane.values(L).astype(np.int64), lb.lane.values(L).astype(np.int64)
+    dn, dm = N * 1, M * int(la.strides[-2])
+    where = {}
+    for i in range(L):
+        where.setdefault((int(ao[i]), int(bo[i])), []).append(i)
+    used = np.zeros(L, bool)
+    out = []
+    for i in np.lexsort((bo, ao)):
+        if used[i]:
+            continue
+        a, b = int(ao[i]), int(bo[i])
+        grp = [i]
+        for key in ((a, b + dn), (a + dm, b), (a + dm, b + dn)):
+            cand = [j for j in where.get(key, []) if not used[j] and j not in grp]
+            if not cand:
+                return None
+            grp.append(cand[0])
+        for j in grp:
+            used[j] = True
+        out.extend(grp)
+    return np.asarray(out, dtype=np.int32)
+
+
 def take_value(v, idx: np.ndarray):
     if isinstance(v, np.ndarray):
         return v[idx]
@@ -1561,6 +1591,11 @@ class Executor:
             _fill_leaf(d.c0, lc.with_strides(tuple(lc.strides[-2:])), L, 2, keep)
             d.accumulate = 1
         d.round_dt = rt.DTYPE_CODE[_store_dt(res_dt)]
+        quads = _mm_quads(la, lb, L, M, N) if (M, N) == (128, 128) and K % 64 == 0 else None
+        if quads is not None:
+            qb = self.pool.upload(quads)
+            keep.append(qb)
+            d.quads, d.n_quads = qb.ptr, len(quads) // 4
         self.launch("mm", d, keep + [buf])
         return Tile(Expr("ld", cspec.dtype, (M, N), attr=cspec))
 

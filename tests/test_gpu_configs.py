@@ -80,7 +80,9 @@ def test_row_reduce_f16_bit_exact(cols):
 
 @pytest.mark.parametrize("shape", [(256, 256, 256, 64, 64, 32, 2, 2),      # generic tile path
                                    (256, 256, 512, 128, 128, 64, 2, 2),    # MFMA path, one tile per core
-                                   (512, 256, 256, 128, 128, 64, 2, 1)])   # MFMA path, 2x2 tiles per core
+                                   (512, 256, 256, 128, 128, 64, 2, 1),    # MFMA path, 2x2 tiles per core
+                                   (256, 256, 192, 128, 128, 64, 2, 2),    # odd number of K steps
+                                   (384, 256, 256, 128, 128, 64, 3, 2)])   # 6 tiles: no 2 x 2 grouping
 def test_gemm(shape):
     ref, out, g = _run(_cases.gemm(*shape))
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
