@@ -359,25 +359,23 @@ __device__ __forceinline__ void q256_frags(const uint16_t* as, const uint16_t* b
   }
 }
 
-template <bool BF16>
-__device__ __forceinline__ void q256_step(f32x16 (&acc)[4][4], const uint16_t* as, const uint16_t* bs, int r32, int h,
-                                          const int (&b_off)[2][4]) {
-  uint4 a0[4], b0[4], a1[4], b1[4];
-  q256_frags(as, bs, 0, r32, h, b_off, a0, b0);
 #define Q_MFMA16(A, B)                                                                         \
   _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<BF16>(A[i], B[j], acc[i][j]);
+
+// slices 0..2 of one 64-deep k step (slice 0's fragments already in a0/b0):
+// each slice's 16 MFMAs run with the next slice's 12 fragment reads between
+// them; slice 3's fragments are left in a1/b1
+template <bool BF16>
+__device__ __forceinline__ void q256_slices012(f32x16 (&acc)[4][4], const uint16_t* as, const uint16_t* bs, int r32,
+                                               int h, const int (&b_off)[2][4], uint4 (&a0)[4], uint4 (&b0)[4],
+                                               uint4 (&a1)[4], uint4 (&b1)[4]) {
   q256_frags(as, bs, 1, r32, h, b_off, a1, b1);
   Q_MFMA16(a0, b0)
   q256_frags(as, bs, 2, r32, h, b_off, a0, b0);
   Q_MFMA16(a1, b1)
   q256_frags(as, bs, 3, r32, h, b_off, a1, b1);
   Q_MFMA16(a0, b0)
-  Q_MFMA16(a1, b1)
-#undef Q_MFMA16
-  // schedule: the first slice's 12 reads, then each later slice's 12 reads
-  // one per MFMA of the slice before it
-  __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
 #pragma unroll
   for (int s = 0; s < 3; ++s) {
 #pragma unroll
@@ -387,7 +385,6 @@ __device__ __forceinline__ void q256_step(f32x16 (&acc)[4][4], const uint16_t* a
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 }
 
 template <bool BF16>
@@ -434,37 +431,67 @@ __global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = z16;
-  int64_t s_ = 0, kk0 = 0;
-  // stage the next k step's sub-tile w into P (16 blocks of 1 KB)
+  int64_t s_ = 0, kk0 = 0, di = 0;
+  // element offset of k step (s_, kk0) in this wavefront's operand
+  const int64_t kst = uni(is_a ? d.a_kstep : d.b_kstep), kmul = is_a ? 1 : b_row;
+  // stage sub-tile w of k step di into P (16 blocks of 1 KB); di stops at
+  // the last step, which later calls load again
 #define Q_ISSUE(P)                                                                                     \
   do {                                                                                                 \
-    const int64_t koff = is_a ? s_ * d.a_kstep + kk0 : s_ * d.b_kstep + kk0 * b_row;                   \
+    const int64_t koff = s_ * kst + kk0 * kmul;                                                        \
     uint16_t* dst = (P) + QT * w;                                                                      \
     _Pragma("unroll") for (int b = 0; b < 16; ++b)                                                     \
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 512 * b), 16, \
                                                lo[b & 3], (int)((b * blk_stride + koff) * 2), 0, 0);   \
-    kk0 += BK;                                                                                         \
-    if (kk0 == kt_per_step * BK) { kk0 = 0; ++s_; }                                                    \
+    const int64_t adv = di < nk - 1;                                                                   \
+    di += adv;                                                                                         \
+    kk0 += adv * BK;                                                                                   \
+    const int64_t wrap = kk0 == kt_per_step * BK;                                                      \
+    kk0 = wrap ? 0 : kk0;                                                                              \
+    s_ += wrap;                                                                                        \
   } while (0)
-  // one k step from stage P: A sub-tile wr, B sub-tile 2 + wc.  The
-  // fragments of the next 16-deep slice are read while the 16 MFMAs of this
-  // one run (one LDS read between MFMAs), so the matrix pipe does not wait
-  // for LDS latency.
-#define Q_COMPUTE(P) q256_step<BF16>(acc, (P) + QT * wr, (P) + QT * (2 + wc), r32, h, b_off)
+  // The barrier of k step t sits between its slices 2 and 3: by then every
+  // wavefront has read all of step t's fragments (so the DMA of step t + 2
+  // may overwrite its stage) and waited for its own DMA of step t + 1 (so
+  // that stage is whole).  Slice 3's MFMAs then cover the DMA issue and the
+  // reads of step t + 1's first slice.
+#define Q_STEP(PC, PN)                                                                       \
+  do {                                                                                       \
+    q256_slices012<BF16>(acc, (PC) + QT * wr, (PC) + QT * (2 + wc), r32, h, b_off, a0, b0, a1, b1); \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
+    __builtin_amdgcn_s_waitcnt(0);                                                           \
+    __syncthreads();                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
+    Q_ISSUE(PC);                                                                             \
+    q256_frags((PN) + QT * wr, (PN) + QT * (2 + wc), 0, r32, h, b_off, a0, b0);              \
+    Q_MFMA16(a1, b1)                                                                         \
+    _Pragma("unroll") for (int x = 0; x < 12; ++x) {                                         \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                     \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+    }                                                                                        \
+    _Pragma("unroll") for (int x = 0; x < 4; ++x) {                                          \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                     \
+    }                                                                                        \
+  } while (0)
+  uint4 a0[4], b0[4], a1[4], b1[4];
   Q_ISSUE(P0);
-  // nk is even (checked at launch): whole pairs of steps, one exit
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  Q_ISSUE(P1);
+  q256_frags(P0 + QT * wr, P0 + QT * (2 + wc), 0, r32, h, b_off, a0, b0);
+  // nk is even (checked at launch): whole pairs of steps, one exit.  The DMA
+  // issued in the last two steps reloads step nk - 1 into stages no longer
+  // read, and the reads after the last barrier are not used.
   for (int64_t t = 0; t < nk; t += 2) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (t + 1 < nk) Q_ISSUE(P1);
-    Q_COMPUTE(P0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (t + 2 < nk) Q_ISSUE(P0);
-    Q_COMPUTE(P1);
+    Q_STEP(P0, P1);
+    Q_STEP(P1, P0);
   }
+  __builtin_amdgcn_s_waitcnt(0);
+#undef Q_STEP
 #undef Q_ISSUE
-#undef Q_COMPUTE
+#undef Q_MFMA16
   // epilogue: this wavefront's lane tile (4 x 4 MFMA tiles; lane l holds
   // column 32 j + l % 32, rows 32 i + 8 (e / 4) + 4 h + e % 4)
   const int64_t ln = w == 0 ? q0 : (w == 1 ? q1 : (w == 2 ? q2 : q3));
