@@ -38,6 +38,33 @@ __device__ __forceinline__ f32x16 mfma32(const uint4& a, const uint4& b, f32x16 
   }
 }
 
+// one result element of dtype DT (f32, f16 or bf16, round to nearest even)
+template <int DT>
+__device__ __forceinline__ void mm_put(uint64_t ptr, int64_t off, float v) {
+  if constexpr (DT == KTIR_F32)
+    ((KTIR_G(float)*)ptr)[off] = v;
+  else if constexpr (DT == KTIR_F16)
+    ((KTIR_G(_Float16)*)ptr)[off] = (_Float16)v;
+  else
+    ((KTIR_G(uint16_t)*)ptr)[off] = (uint16_t)(__float_as_uint(round_bf16(v)) >> 16);
+}
+
+// a wavefront's 64 x 64 quadrant as 2 x 2 MFMA tiles, starting at element
+// offset o (lane l: column l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4 of
+// each tile, the lane's part of the row already in o), each element acc + z
+template <int DT>
+__device__ __forceinline__ void mm_quadrant_out(uint64_t ptr, int64_t o, int64_t cs, const f32x16& a00,
+                                                const f32x16& a01, const f32x16& a10, const f32x16& a11, float z) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int64_t r = (8 * (e >> 2) + (e & 3)) * cs;
+    mm_put<DT>(ptr, o + r, __fadd_rn(a00[e], z));
+    mm_put<DT>(ptr, o + r + 32, __fadd_rn(a01[e], z));
+    mm_put<DT>(ptr, o + r + 32 * cs, __fadd_rn(a10[e], z));
+    mm_put<DT>(ptr, o + r + 32 * cs + 32, __fadd_rn(a11[e], z));
+  }
+}
+
 // Epilogue of a 128 x 128 tile (wavefront (wr, wc) holds the 64 x 64
 // quadrant as 2 x 2 MFMA tiles): round the product to the operand dtype of
 // the KTIR matmul, then accumulate into the outs tile (the reference's two
@@ -46,21 +73,18 @@ __device__ __forceinline__ void mm_epilogue(const ktir_mm_t& d, int64_t ln, int6
                                             int lane, const f32x16& acc00, const f32x16& acc01, const f32x16& acc10,
                                             const f32x16& acc11) {
   const int64_t cbase = lane_offset(d.c, ln);
-  if (d.c.dtype == KTIR_F32 && d.round_dt == KTIR_F32 && d.accumulate != 1 && d.c.strides[1] == 1) {
-    // f32 result, outs absent or a zero splat (accumulate == 2: x + 0.0)
-    float* C = (float*)d.c.ptr + cbase;
+  if ((d.c.dtype == KTIR_F32 || d.c.dtype == KTIR_F16 || d.c.dtype == KTIR_BF16) && d.round_dt == KTIR_F32 &&
+      d.accumulate != 1 && d.c.strides[1] == 1) {
+    // outs absent or a zero splat (accumulate == 2: x + 0.0), rounded to the result dtype
     const int64_t cs = d.c.strides[0];
     const float z = d.accumulate == 2 ? 0.f : -0.f;
-#define EPI(a, i, j)                                                                               \
-  do {                                                                                             \
-    float* c = C + (m0 + wr * 64 + (i) * 32 + 4 * (lane >> 5)) * cs + n0 + wc * 64 + (j) * 32 + (lane & 31); \
-    _Pragma("unroll") for (int e = 0; e < 16; ++e) c[(8 * (e >> 2) + (e & 3)) * cs] = __fadd_rn(a[e], z); \
-  } while (0)
-    EPI(acc00, 0, 0);
-    EPI(acc01, 0, 1);
-    EPI(acc10, 1, 0);
-    EPI(acc11, 1, 1);
-#undef EPI
+    const int64_t r0 = m0 + wr * 64 + 4 * (lane >> 5), c0 = n0 + wc * 64 + (lane & 31);
+    if (d.c.dtype == KTIR_F32)
+      mm_quadrant_out<KTIR_F32>(d.c.ptr, cbase + r0 * cs + c0, cs, acc00, acc01, acc10, acc11, z);
+    else if (d.c.dtype == KTIR_F16)
+      mm_quadrant_out<KTIR_F16>(d.c.ptr, cbase + r0 * cs + c0, cs, acc00, acc01, acc10, acc11, z);
+    else
+      mm_quadrant_out<KTIR_BF16>(d.c.ptr, cbase + r0 * cs + c0, cs, acc00, acc01, acc10, acc11, z);
     return;
   }
   const int64_t c0base = d.accumulate == 1 ? lane_offset(d.c0, ln) : 0;
@@ -387,6 +411,20 @@ __device__ __forceinline__ void q256_slices012(f32x16 (&acc)[4][4], const uint16
   }
 }
 
+// a wavefront's 128 x 128 result (4 x 4 MFMA tiles; lane l holds column
+// 32 j + l % 32, rows 32 i + 8 (e / 4) + 4 h + e % 4), each element acc + z
+template <int DT>
+__device__ __forceinline__ void q256_out(uint64_t ptr, int64_t cb, int64_t cs, int h, int r32,
+                                         const f32x16 (&acc)[4][4], float z) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        mm_put<DT>(ptr, cb + (32 * i + 8 * (e >> 2) + 4 * h + (e & 3)) * cs + 32 * j + r32, __fadd_rn(acc[i][j][e], z));
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
   __shared__ __align__(16) uint16_t P0[4 * QT];
@@ -495,17 +533,16 @@ __global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
   // epilogue: this wavefront's lane tile (4 x 4 MFMA tiles; lane l holds
   // column 32 j + l % 32, rows 32 i + 8 (e / 4) + 4 h + e % 4)
   const int64_t ln = w == 0 ? q0 : (w == 1 ? q1 : (w == 2 ? q2 : q3));
-  // f32 result, outs absent or a zero splat (the only form launched here)
-  float* C = (float*)d.c.ptr + lane_offset(d.c, ln);
-  const int64_t cs = d.c.strides[0];
+  // outs absent or a zero splat (accumulate == 2: x + 0.0), rounded to the
+  // result dtype (the only forms launched here)
+  const int64_t cb = lane_offset(d.c, ln), cs = d.c.strides[0];
   const float z = d.accumulate == 2 ? 0.f : -0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        C[(32 * i + 8 * (e >> 2) + 4 * h + (e & 3)) * cs + 32 * j + r32] = __fadd_rn(acc[i][j][e], z);
+  if (d.c.dtype == KTIR_F32)
+    q256_out<KTIR_F32>(d.c.ptr, cb, cs, h, r32, acc, z);
+  else if (d.c.dtype == KTIR_F16)
+    q256_out<KTIR_F16>(d.c.ptr, cb, cs, h, r32, acc, z);
+  else
+    q256_out<KTIR_BF16>(d.c.ptr, cb, cs, h, r32, acc, z);
 }
 
 }  // namespace ktir
@@ -556,7 +593,9 @@ int ktir_launch_matmul_mfma(const ktir_mm_t* d, bool* handled) {
                    d->a_kstep >= 0 && d->b_kstep >= 0;
   const bool q256 = dma && d->quads && d->n_quads * 4 == L && d->M == MT && d->N == NT &&
                     (d->ksteps * kt_steps(d)) % 2 == 0 && d->n_quads < (int64_t)0x7fffffff &&
-                    d->c.dtype == KTIR_F32 && d->round_dt == KTIR_F32 && d->accumulate != 1 && d->c.strides[1] == 1;
+                    (d->c.dtype == KTIR_F32 || d->c.dtype == KTIR_F16 || d->c.dtype == KTIR_BF16) &&
+                    d->round_dt == KTIR_F32 && d->accumulate != 1 && d->c.strides[1] == 1 &&
+                    (127 * d->a.strides[0] + (d->ksteps - 1) * d->a_kstep + d->K) * 2 < (int64_t)0x7fffffff;
   if (q256) {
     if (f16)
       hipLaunchKernelGGL((mm_mfma_256<false>), dim3((unsigned)d->n_quads), dim3(256), 0, stream(), *d);

@@ -145,7 +145,8 @@ def _kloop_matmul(ex, op, lb, st, trips, init: Tile):
     from .program import Expr
     a_t = Tile(Expr("ld", dt, (M, K), attr=leaves[0][0]))
     b_t = Tile(Expr("ld", dt, (K, N), attr=leaves[1][0]))
-    res = ex._matmul(a_t, b_t, init, ksteps=T, a_k=deltas[0], b_k=deltas[1], a_leaf=leaves[0], b_leaf=leaves[1])
+    res = ex._matmul(a_t, b_t, init, ksteps=T, a_k=deltas[0], b_k=deltas[1], a_leaf=leaves[0], b_leaf=leaves[1],
+                     name=op.results[0])
     return [res]
 
 
@@ -891,3 +892,102 @@ def attention_epilogue(ex, e, dest) -> bool:
 def _walk_ld(e):
     from .program import walk
     return [n for n in walk(e) if n.kind == "ld"]
+
+
+# ---------------------------------------------------------------------------
+# matmul result stored straight from the MFMA kernel
+# ---------------------------------------------------------------------------
+
+def _ssa_index(ex):
+    """Static facts of the running function's SSA values: how many operands
+    name each value anywhere in the function, the block (op list) each value
+    is defined in, and the blocks of its uses."""
+    idx = getattr(ex, "_ssa", None)
+    if idx is not None:
+        return idx
+    uses, use_blk, def_blk = {}, {}, {}
+
+    def walk(ops):
+        b = id(ops)
+        for o in ops:
+            for n in o.results:
+                def_blk[n] = b
+            for n in o.operands:
+                uses[n] = uses.get(n, 0) + 1
+                use_blk.setdefault(n, []).append((o, b))
+            for r in o.regions:
+                walk(r.ops)
+
+    walk(ex.fn.operations)
+    ex._ssa = (uses, use_blk, def_blk)
+    return ex._ssa
+
+
+def _sole_use(ssa, name, op_type):
+    """The one op (of type `op_type`) that uses `name`, when that use is in
+    the block defining `name` (so it runs once per definition)."""
+    uses, use_blk, def_blk = ssa
+    if uses.get(name, 0) != 1 or name not in def_blk:
+        return None
+    o, b = use_blk[name][0]
+    return o if o.op_type == op_type and b == def_blk[name] else None
+
+
+def mm_epilogue(ex, store_op, val, dest, alloc, shape) -> bool:
+    """Fold ``store(truncf(C))`` (or ``store(C)``) of the last matmul launch's
+    result C into that launch: its kernel then rounds the f32 sums to the
+    store's dtype and writes the destination directly.  Taken only when the
+    store (through at most one truncf) is the one use of C, both in C's own
+    block, the matmul is the last launch recorded, and nothing live reads the
+    destination.  Same roundings as the store's own program: the f32 result,
+    then one rounding to the destination dtype."""
+    from . import runtime as rt
+    from .program import _fill_leaf
+    from .walker import _reads
+    pend = ex.mm_pending
+    if pend is None or ex.eager or ex.L != pend["lanes"] or len(ex.levels) != pend["level"] \
+            or len(ex.plan.launches) != pend["n"]:
+        return False
+    ssa = _ssa_index(ex)
+    sname = store_op.operands[0]
+    if _sole_use(ssa, sname, "ktdp.store") is not store_op:
+        return False
+    e = val.e
+    cname = sname
+    if e.kind == "cast":
+        if e.attr != "f32" or e.dtype != dest.dtype:
+            return False
+        tr = _sole_use(ssa, pend["name"], "arith.truncf")
+        if tr is None or tr.results[0] != sname:
+            return False
+        cname = pend["name"]
+        e = e.args[0]
+    elif e.dtype != dest.dtype:
+        return False
+    if cname != pend["name"]:
+        return False
+    M, N, L = pend["M"], pend["N"], ex.L
+    buf = pend["buf"]
+    if e.kind != "ld" or e.dtype != "f32" or e.attr.ptr != buf.ptr or e.attr.offsets is not None \
+            or e.attr.winner is not None or tuple(e.shape) != (M, N) or tuple(e.attr.strides) != (N, 1) \
+            or e.attr.lane.arr is not None or e.attr.lane.base != 0 or e.attr.lane.stride != M * N:
+        return False
+    d = pend["desc"]
+    if d.accumulate == 1 or d.round_dt != rt.DTYPE_CODE["f32"]:
+        return False
+    if dest.dtype not in ("f32", "f16", "bf16") or dest.offsets is not None or dest.winner is not None:
+        return False
+    if tuple(val.shape) != (M, N) or tuple(shape) != (M, N) or len(dest.strides) != 2 or dest.strides[1] != 1:
+        return False
+    row = int(dest.strides[0])
+    offs = dest.lane.values(L)
+    if row < N or np.any(offs < dest.lo) or np.any(offs + (M - 1) * row + N - 1 >= dest.hi):
+        return False
+    for fr in ex.frames:
+        for v in fr.vals.values():
+            if isinstance(v, Tile) and v is not val and _reads(v.e, alloc):
+                return False
+    _fill_leaf(d.c, dest, L, 2, pend["keep"])
+    pend["keep"].append(dest)
+    ex.mm_pending = None
+    return True

@@ -270,6 +270,7 @@ class Executor:
         self.sequential = sequential
         self.eager = sequential
         self.attn_pending = None     # last fused attention launch whose epilogue may still fold in
+        self.mm_pending = None       # last matmul launch whose result store may still fold in
         self.allow_expand = allow_expand and not sequential
         self.plan = Plan(pool)
         self.plan.mode = "sequential" if sequential else "lockstep"
@@ -718,7 +719,9 @@ class Executor:
             lo_off = sum(int(l) * int(s) for l, s in zip(cs.lo, v.strides))
             shape = cs.extent
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
-            self._store_expr(val, spec, alloc, shape)
+            from .fusion import mm_epilogue
+            if not mm_epilogue(self, op, val, spec, alloc, shape):
+                self._store_expr(val, spec, alloc, shape)
             self.log(alloc, True, rel, shape, v.strides)
             self._lat_box(rel, shape, v.strides, rt.ELEM_BYTES[v.dtype])
             return None
@@ -1549,7 +1552,8 @@ class Executor:
         m = self.materialize(t)
         return m.e.attr, m.dtype
 
-    def _matmul(self, a: Tile, b: Tile, acc: Optional[Tile], ksteps=1, a_k=0, b_k=0, a_leaf=None, b_leaf=None):
+    def _matmul(self, a: Tile, b: Tile, acc: Optional[Tile], ksteps=1, a_k=0, b_k=0, a_leaf=None, b_leaf=None,
+                name=None):
         if len(a.shape) != 2 or len(b.shape) != 2:
             raise NotImplementedError("linalg.matmul on tiles of rank != 2")
         M, K = a.shape
@@ -1596,13 +1600,19 @@ class Executor:
             qb = self.pool.upload(quads)
             keep.append(qb)
             d.quads, d.n_quads = qb.ptr, len(quads) // 4
-        self.launch("mm", d, keep + [buf])
+        keep.append(buf)
+        self.launch("mm", d, keep)
+        # the SSA value `name` holds this launch's result; a store of it may
+        # still become the launch's own epilogue (fusion.mm_epilogue)
+        self.mm_pending = None if self.eager or name is None else dict(
+            desc=d, keep=keep, buf=buf, lanes=L, level=len(self.levels), n=len(self.plan.launches), M=M, N=N,
+            name=name)
         return Tile(Expr("ld", cspec.dtype, (M, N), attr=cspec))
 
     def h_linalg_matmul(self, op):
         a, b = self.get_value(op.operands[0]), self.get_value(op.operands[1])
         acc = self.get_value(op.operands[2]) if len(op.operands) > 2 else None
-        return self._matmul(a, b, acc if isinstance(acc, Tile) else None)
+        return self._matmul(a, b, acc if isinstance(acc, Tile) else None, name=op.results[0])
 
     def h_linalg_batch_matmul(self, op):
         a, b = self.get_value(op.operands[0]), self.get_value(op.operands[1])

@@ -85,6 +85,8 @@ def test_row_reduce_f16_bit_exact(cols):
                                    (384, 256, 256, 128, 128, 64, 3, 2)])   # 6 tiles: no 2 x 2 grouping
 def test_gemm(shape):
     ref, out, g = _run(_cases.gemm(*shape))
+    # truncf + store of the K loop's result run in the matmul kernel's epilogue
+    assert set(g.last_plan.counts()) == {"mm"}
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
