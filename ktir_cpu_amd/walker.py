@@ -221,7 +221,34 @@ def _mm_quads(la, lb, L: int, M: int, N: int) -> Optional[np.ndarray]:
         for j in grp:
             used[j] = True
         out.extend(grp)
-    return np.asarray(out, dtype=np.int32)
+    return _xcd_blocks(np.asarray(out, dtype=np.int32).reshape(-1, 4), ao, bo).ravel()
+
+
+# workgroups one XCD runs at once (MI355X: 256 CUs in 8 XCDs, one 256 x 256
+# matmul workgroup per CU)
+_XCD_SLOTS, _N_XCD = 32, 8
+
+
+def _xcd_blocks(q: np.ndarray, ao: np.ndarray, bo: np.ndarray) -> np.ndarray:
+    """Order the 2 x 2 groups `q` (rows {tl, tr, bl, br}) so that the 32
+    workgroups an XCD runs together cover a 4 x 8 block of the result grid:
+    the kernel gives XCD x the x-th eighth of the list, so each XCD streams
+    4 rows of A blocks and 8 columns of B blocks per round instead of 1 x 32.
+    Unchanged unless the groups form a full grid that such blocks tile."""
+    n = len(q)
+    if n % (_XCD_SLOTS * _N_XCD):
+        return q
+    ra = np.unique(ao[q[:, 0]], return_inverse=True)[1]
+    cb = np.unique(bo[q[:, 0]], return_inverse=True)[1]
+    nm, nn = int(ra.max()) + 1, int(cb.max()) + 1
+    if nm * nn != n or nm % 4 or nn % 8:
+        return q
+    grid = np.full((nm, nn), -1, np.int64)
+    grid[ra, cb] = np.arange(n)
+    if np.any(grid < 0):
+        return q
+    order = grid.reshape(nm // 4, 4, nn // 8, 8).transpose(0, 2, 1, 3).ravel()
+    return q[order]
 
 
 def take_value(v, idx: np.ndarray):

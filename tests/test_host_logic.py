@@ -115,3 +115,46 @@ def test_oracle_tree_fold_order(n):
     out = o.execute_function("f", x_ptr=x, o_ptr=np.zeros(1, np.float16))
     expect = np.float16(_tree_fold_reference([np.float16(v) for v in x]) + np.float16(0))
     assert out["o_ptr"][0] == expect
+
+
+def _gemm_leaves(tm, tn, K=256, T=128):
+    """A and B leaves of a tm x tn grid of T x T matmul tiles over row-major
+    A [tm*T, K] and B [K, tn*T], lanes in a shuffled order."""
+    from ktir_cpu_amd.program import LeafSpec
+    rng = np.random.default_rng(1)
+    mi, ni = np.divmod(rng.permutation(tm * tn), tn)
+    N = tn * T
+    la = LeafSpec(0, "f16", LaneOff.from_array(mi * T * K), (K, 1), 0, tm * T * K)
+    lb = LeafSpec(0, "f16", LaneOff.from_array(ni * T), (N, 1), 0, K * N)
+    return la, lb, mi, ni
+
+
+def test_mm_quads_groups_2x2():
+    """Every group is {tl, tr, bl, br}: the right lane T columns right of the
+    left one with the same A, the bottom lane T rows below with the same B."""
+    from ktir_cpu_amd.walker import _mm_quads
+    tm, tn = 6, 4
+    la, lb, mi, ni = _gemm_leaves(tm, tn)
+    q = _mm_quads(la, lb, tm * tn, 128, 128).reshape(-1, 4)
+    assert sorted(q.ravel().tolist()) == list(range(tm * tn))
+    for tl, tr, bl, br in q:
+        assert (mi[tr], ni[tr]) == (mi[tl], ni[tl] + 1)
+        assert (mi[bl], ni[bl]) == (mi[tl] + 1, ni[tl])
+        assert (mi[br], ni[br]) == (mi[tl] + 1, ni[tl] + 1)
+    la, lb, _, _ = _gemm_leaves(3, 4)           # odd tile rows: no grouping
+    assert _mm_quads(la, lb, 12, 128, 128) is None
+
+
+def test_mm_quads_xcd_blocks():
+    """64 x 64 tiles = 32 x 32 groups: the kernel gives XCD x groups
+    [128 x, 128 x + 128); round r of that XCD runs 32 of them, which must
+    cover 4 group rows x 8 group columns."""
+    from ktir_cpu_amd.walker import _mm_quads
+    tm = tn = 64
+    la, lb, mi, ni = _gemm_leaves(tm, tn)
+    q = _mm_quads(la, lb, tm * tn, 128, 128).reshape(-1, 4)
+    assert sorted(q.ravel().tolist()) == list(range(tm * tn))
+    for x in range(8):
+        for r in range(4):
+            tl = q[128 * x + 32 * r:128 * x + 32 * r + 32, 0]
+            assert len(set((mi[tl] // 2).tolist())) == 4 and len(set((ni[tl] // 2).tolist())) == 8
