@@ -345,6 +345,17 @@ typedef struct ktir_attn {
   uint64_t o_ptr, o_base;              /* 0: no epilogue; o_base: const int64_t* [lanes] */
   int64_t o_row;
   int32_t o_dtype, pad2;
+  /* optional f16 copy of V for bf16 operands (0: not used): the launch first
+   * converts elements [v16_lo, v16_lo + v16_n) of V into v16_ptr (f16, same
+   * order; v16_lo and v16_n multiples of 8) and sets the device int32 at
+   * v16_flag if any value is not finite or has |v| >= 65536.  If none is,
+   * P @ V runs in f16 with P rounded once to f16 (11 significant bits; V
+   * values below 2^-14 become f16 subnormals, off by at most 2^-25);
+   * otherwise it runs in bf16 with P as hi + lo as without the copy.  Used
+   * only when O = acc / l is the launch's one result (o_ptr set, acc_out 0);
+   * f16 operands take the single-rounding f16 product under the same rule. */
+  uint64_t v16_ptr, v16_flag;
+  int64_t v16_lo, v16_n;
 } ktir_attn_t;
 int ktir_launch_attention(const ktir_attn_t* d);
 

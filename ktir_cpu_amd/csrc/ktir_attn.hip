@@ -36,6 +36,7 @@ typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int AT = 128;            // M = N = D
 constexpr float LOG2E = 1.44269504088896341f;
@@ -136,8 +137,14 @@ __device__ __forceinline__ void tile_to_lds(const uint16_t* src, int64_t row_str
     _Pragma("unroll") for (int i = 0; i < 16; ++i) { BODY; } }
 
 // The position mask keeps score (row, key) iff ((lo <= kpos - qpos <= hi) != inv).
-template <bool BF16>
+// PV16: the P @ V product in f16 (V f16: the f16 operands, or the f16 copy of
+// bf16 V), P rounded once to f16; else in the operand type with P as hi + lo.
+template <bool BF16, bool PV16>
 __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
+  if (BF16 && d.v16_ptr && d.o_ptr && !d.acc_out) {
+    // the conversion before this launch decided which of the two kernels runs
+    if ((*(const int*)d.v16_flag != 0) == PV16) return;
+  }
   __shared__ __align__(16) uint16_t Ks[AT * AT];    // K tile, [key][d] (chunk-swizzled rows)
   __shared__ __align__(16) uint16_t Vs[AT * AT];    // V tile, [key][d] (chunk-swizzled rows)
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, r32 = l & 31;
@@ -145,7 +152,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   const int T = uni(((const int32_t*)d.trips)[lane]);
   const uint16_t* Q = (const uint16_t*)d.q_ptr;
   const uint16_t* K = (const uint16_t*)d.k_ptr;
-  const uint16_t* V = (const uint16_t*)d.v_ptr;
+  const uint16_t* V = BF16 && PV16 ? (const uint16_t*)d.v16_ptr - d.v16_lo : (const uint16_t*)d.v_ptr;
   const int row = w * 32 + r32;                      // this lane's query row
   const int64_t kb0 = uni(((const int64_t*)d.k_base)[lane]), vb0 = uni(((const int64_t*)d.v_base)[lane]);
   uint4 qf[8];                                       // Q^T fragments: Q[row][16 s + 8 h .. + 8]
@@ -184,6 +191,10 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     asm volatile("" : "+v"(kx), "+v"(vfb), "+v"(vx0), "+v"(vx1));
     // S^T = K Q^T: 4 key tiles x 8 d-steps
     f32x16_t s0 = z16, s1 = z16, s2 = z16, s3 = z16;
+    // MFMA blocks run at raised wave priority: of the two waves sharing a
+    // SIMD, the one with matrix work issues first, which moves the other's
+    // softmax under its MFMAs instead of in step with them
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const uint16_t* kp = &Ks[k_off + 8 * ((2 * s + h) ^ kx)];
@@ -192,6 +203,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
       s2 = mfma_at<BF16>(*(const uint4*)(kp + 2 * 32 * AT), qf[s], s2);
       s3 = mfma_at<BF16>(*(const uint4*)(kp + 3 * 32 * AT), qf[s], s3);
     }
+    __builtin_amdgcn_s_setprio(0);
     // lane value (kt, i) is key kt*32 + 8(i/4) + 4h + i%4 of row `row`
     float sv[4][16];
 #pragma unroll
@@ -265,19 +277,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     __syncthreads();                                  // every wave: done with Ks, V_j in LDS
     if (more) tile_to_lds(K + kb0 + (int64_t)(j + 1) * d.k_step, d.k_row, Ks, wu, l);
     // O^T += V^T P^T over 8 key-steps of 16 keys
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       // lane half h holds key groups g0 (a*) and g0 + 1 (b*) of key tile ks / 2;
       // after the swaps both halves hold keys 16 ks + 8 h + [0..8) in order
       const int kt = ks >> 1, g0 = 2 * (ks & 1);
-      uint32_t ah0, ah1, al0, al1, bh0, bh1, bl0, bl1;
-      split4<BF16>(&sv[kt][4 * g0], ah0, ah1, al0, al1);
-      split4<BF16>(&sv[kt][4 * g0 + 4], bh0, bh1, bl0, bl1);
-      swap32(ah0, bh0);
-      swap32(ah1, bh1);
-      swap32(al0, bl0);
-      swap32(al1, bl1);
-      const uint4 ph = make_uint4(ah0, ah1, bh0, bh1), pl = make_uint4(al0, al1, bl0, bl1);
       const uint16_t* vt = &Vs[16 * ks * AT];
       uint4 a[4];
 #pragma unroll
@@ -285,15 +290,38 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
         const uint2 lo = ds_tr16(vt + vfb + 8 * ((4 * dt) ^ vx0)), hi = ds_tr16(vt + vfb + 4 * AT + 8 * ((4 * dt) ^ vx1));
         a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
-      o0 = mfma_at<BF16>(a[0], ph, o0);
-      o1 = mfma_at<BF16>(a[1], ph, o1);
-      o2 = mfma_at<BF16>(a[2], ph, o2);
-      o3 = mfma_at<BF16>(a[3], ph, o3);
-      o0 = mfma_at<BF16>(a[0], pl, o0);
-      o1 = mfma_at<BF16>(a[1], pl, o1);
-      o2 = mfma_at<BF16>(a[2], pl, o2);
-      o3 = mfma_at<BF16>(a[3], pl, o3);
+      if constexpr (PV16) {
+        uint32_t ah0 = cvt2<false>(sv[kt][4 * g0], sv[kt][4 * g0 + 1]);
+        uint32_t ah1 = cvt2<false>(sv[kt][4 * g0 + 2], sv[kt][4 * g0 + 3]);
+        uint32_t bh0 = cvt2<false>(sv[kt][4 * g0 + 4], sv[kt][4 * g0 + 5]);
+        uint32_t bh1 = cvt2<false>(sv[kt][4 * g0 + 6], sv[kt][4 * g0 + 7]);
+        swap32(ah0, bh0);
+        swap32(ah1, bh1);
+        const uint4 ph = make_uint4(ah0, ah1, bh0, bh1);
+        o0 = mfma_at<false>(a[0], ph, o0);
+        o1 = mfma_at<false>(a[1], ph, o1);
+        o2 = mfma_at<false>(a[2], ph, o2);
+        o3 = mfma_at<false>(a[3], ph, o3);
+      } else {
+        uint32_t ah0, ah1, al0, al1, bh0, bh1, bl0, bl1;
+        split4<BF16>(&sv[kt][4 * g0], ah0, ah1, al0, al1);
+        split4<BF16>(&sv[kt][4 * g0 + 4], bh0, bh1, bl0, bl1);
+        swap32(ah0, bh0);
+        swap32(ah1, bh1);
+        swap32(al0, bl0);
+        swap32(al1, bl1);
+        const uint4 ph = make_uint4(ah0, ah1, bh0, bh1), pl = make_uint4(al0, al1, bl0, bl1);
+        o0 = mfma_at<BF16>(a[0], ph, o0);
+        o1 = mfma_at<BF16>(a[1], ph, o1);
+        o2 = mfma_at<BF16>(a[2], ph, o2);
+        o3 = mfma_at<BF16>(a[3], ph, o3);
+        o0 = mfma_at<BF16>(a[0], pl, o0);
+        o1 = mfma_at<BF16>(a[1], pl, o1);
+        o2 = mfma_at<BF16>(a[2], pl, o2);
+        o3 = mfma_at<BF16>(a[3], pl, o3);
+      }
     }
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of K_{j+1} has landed
     __syncthreads();                                  // every wave: done with Vs, K_{j+1} in LDS
     if (more) tile_to_lds(V + vb0 + (int64_t)(j + 1) * d.v_step, d.v_row, Vs, wu, l);
@@ -336,6 +364,29 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   }
 }
 
+// f16 copy of bf16 V: 8 elements per thread and step; *bad |= any value that
+// is not finite or has |v| >= 65536 (bf16 magnitude bits >= 0x4780)
+__global__ __launch_bounds__(256) void attn_v16(const uint16_t* src, uint16_t* dst, int64_t n8, int* bad) {
+  int out = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const u32x4_t x = ((const KTIR_G(u32x4_t)*)src)[i];
+    const uint32_t w[4] = {x[0], x[1], x[2], x[3]};
+    uint32_t y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t m = w[k] & 0x7fff7fffu;
+      out |= (int)(((m + 0x38803880u) & 0x80008000u) != 0);
+      const f16x2_t h = __builtin_convertvector((f32x2_t{__uint_as_float(w[k] << 16), __uint_as_float(w[k] & 0xffff0000u)}),
+                                                f16x2_t);
+      y[k] = __builtin_bit_cast(uint32_t, h);
+    }
+    ((KTIR_G(u32x4_t)*)dst)[i] = u32x4_t{y[0], y[1], y[2], y[3]};
+  }
+  if (__any(out) && (threadIdx.x & 63) == 0) atomicOr(bad, 1);
+}
+
+__global__ void attn_v16_clear(int* bad) { *bad = 0; }
+
 }  // namespace ktir
 
 using namespace ktir;
@@ -362,10 +413,29 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
     default:
       if (d->causal) return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_attention: mask predicate %d", d->pred);
   }
-  if (d->dtype == KTIR_BF16)
-    hipLaunchKernelGGL((attn_kernel<true>), dim3((unsigned)d->lanes), dim3(256), 0, stream(), *d, lo, hi, inv);
-  else
-    hipLaunchKernelGGL((attn_kernel<false>), dim3((unsigned)d->lanes), dim3(256), 0, stream(), *d, lo, hi, inv);
+  const dim3 grid((unsigned)d->lanes);
+  // P rounded once to f16 only when the launch's one result is O = acc / l:
+  // its error there is at most 2^-12 max|V| per element, while an
+  // unnormalised acc would carry it l times over
+  const bool norm = d->o_ptr && !d->acc_out;
+  if (d->dtype == KTIR_BF16 && d->v16_ptr && norm) {
+    if (!d->v16_flag || (d->v16_lo | d->v16_n) & 7 || d->v16_lo < 0 || d->v16_n <= 0 || (d->v16_ptr & 15))
+      return set_error(KTIR_E_ARG, "ktir_launch_attention: bad f16 V copy (range %lld + %lld)",
+                       (long long)d->v16_lo, (long long)d->v16_n);
+    const int64_t n8 = d->v16_n / 8;
+    const int64_t blocks = n8 / 256 + 1 < 16384 ? n8 / 256 + 1 : 16384;
+    hipLaunchKernelGGL(attn_v16_clear, dim3(1), dim3(1), 0, stream(), (int*)d->v16_flag);
+    hipLaunchKernelGGL(attn_v16, dim3((unsigned)blocks), dim3(256), 0, stream(),
+                       (const uint16_t*)d->v_ptr + d->v16_lo, (uint16_t*)d->v16_ptr, n8, (int*)d->v16_flag);
+    hipLaunchKernelGGL((attn_kernel<true, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+    hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+  } else if (d->dtype == KTIR_BF16) {
+    hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+  } else if (norm) {
+    hipLaunchKernelGGL((attn_kernel<false, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+  } else {
+    hipLaunchKernelGGL((attn_kernel<false, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+  }
   KTIR_HIP_CHECK(hipGetLastError());
   return KTIR_OK;
 }

@@ -798,6 +798,21 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     d.q_row, d.k_row, d.v_row = q_row, tiles["k"][2], tiles["v"][2]
     d.k_step, d.v_step = tiles["k"][3], tiles["v"][3]
     d.trips = up(trips.astype(np.int32))
+    if dtype == "bf16":
+        # f16 copy of the V elements the loop reads (the kernel runs P @ V in
+        # f16 when every one converts exactly), when that range is no larger
+        # than the reads themselves
+        _, vrel, vrow, vstep = tiles["v"]
+        run = trips > 0
+        vlo = vrel + np.minimum(0, tm1 * vstep)
+        vhi = vrel + np.maximum(0, tm1 * vstep) + (AT - 1) * vrow + AT
+        if np.any(run):
+            lo_, hi_ = int(vlo[run].min()), int(vhi[run].max())
+            if 0 < hi_ - lo_ <= int(trips[run].sum()) * AT * AT:
+                v16 = ex.pool.temp((hi_ - lo_) * 2)
+                flag = ex.pool.temp(4)
+                keep += [v16, flag]
+                d.v16_ptr, d.v16_flag, d.v16_lo, d.v16_n = v16.ptr, flag.ptr, lo_, hi_ - lo_
     d.order = up(_xcd_order(trips, tiles["k"][1], tiles["v"][1]))
     d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
     d.kpos_step = kpos_step

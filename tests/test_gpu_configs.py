@@ -111,6 +111,20 @@ def test_flash_attention_fused(args):
         np.testing.assert_array_equal(out[k], ref[k])
 
 
+@pytest.mark.parametrize("big", [3.0e5, -7.0e4])
+def test_flash_attention_fused_v_beyond_f16(big):
+    """A V value f16 cannot hold sends P @ V of the launch to the bf16 hi + lo
+    kernel (the f16 copy of V is not used); results still match."""
+    from oracle.interp import bf16_bits
+    src, fn, kw = _cases.flash_attention(S=512, D=128, blk=128)
+    v = bf16_from_bits(kw["v_ptr"])
+    v[0, 1, 300, 5] = big
+    kw["v_ptr"] = bf16_bits(v)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts().get("attn") == 1
+    np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+
+
 def test_flash_attention_unfused_epilogue():
     """An epilogue other than acc / l stays a separate program after the fused loop."""
     src, fn, kw = _cases.flash_attention(S=256, D=128, blk=128)
