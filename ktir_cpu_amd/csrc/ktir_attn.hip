@@ -22,7 +22,10 @@
 // Semantics follow the KTIR loop body (see ktir_hip.h):
 // m' = max(m, rowmax S) (NaN-propagating like arith.maximumf),
 // P = exp(S - m'), alpha = exp(m - m'), acc' = acc*alpha + P@V,
-// l' = l*alpha + rowsum P, all in f32.
+// l' = l*alpha + rowsum P, all in f32.  The kernel keeps P, acc and l
+// relative to a base mr <= m that is moved up to m only when m passes it by
+// more than 8 (and once at the end): the same values up to rounding, with
+// the per-tile rescale of acc mostly gone.
 #include <climits>
 
 #include "ktir_common.h"
@@ -172,7 +175,26 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   const float c1 = __fmul_rn(d.scale, LOG2E);
   const f32x16_t z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   f32x16_t o0 = z16, o1 = z16, o2 = z16, o3 = z16;   // O^T tiles: d = 32 dt + 8g + 4h + t, row r32
-  float m = -__builtin_inff(), lsum = 0.f;
+  // m: running row max (the reference's m).  P, lsum and O are kept relative
+  // to mr <= m, moved up to m only when m passes mr by more than AT_REBASE
+  // (P <= e^8 meanwhile), and brought to m once after the loop: the same
+  // quantities as rescaling every tile, with far fewer rescales.
+  float m = -__builtin_inff(), mr = -__builtin_inff(), lsum = 0.f;
+#define AT_REBASE(MN)                                                    \
+  do {                                                                   \
+    const bool up = (MN) > __fadd_rn(mr, 8.0f);                          \
+    if (__any(up)) {                                                     \
+      const float al = up ? exp_f(__fsub_rn(mr, (MN))) : 1.f;            \
+      _Pragma("unroll") for (int i = 0; i < 16; ++i) {                   \
+        o0[i] = __fmul_rn(o0[i], al);                                    \
+        o1[i] = __fmul_rn(o1[i], al);                                    \
+        o2[i] = __fmul_rn(o2[i], al);                                    \
+        o3[i] = __fmul_rn(o3[i], al);                                    \
+      }                                                                  \
+      lsum = __fmul_rn(lsum, al);                                        \
+      mr = up ? (MN) : mr;                                               \
+    }                                                                    \
+  } while (0)
   // K A-fragments: row 32 kt + r32, chunk 2 s + h at slot (2 s + h) ^ swz16(r32 % 16)
   const int k_off = r32 * AT;
   const int k_x = swz16(r32 & 15);
@@ -218,9 +240,10 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     const bool all_keep = !d.causal ||
         (minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi));
     float mn, ls;
-    if (pos_scale && __all(all_keep)) {
-      // no masked score in the wave: rowmax S = scale * rowmax(QK) (rounding is
-      // monotonic for scale > 0) and P = 2^(QK * scale log2e - m' log2e)
+    // no masked score in the wave and scale > 0: rowmax S = scale * rowmax(QK)
+    // (rounding is monotonic for scale > 0) and P = 2^(QK * scale log2e - mr log2e)
+    const bool fast = pos_scale && __all(all_keep);
+    if (fast) {
       float x0 = fmax_nan(sv[0][0], sv[0][1]), x1 = fmax_nan(sv[1][0], sv[1][1]);
       float x2 = fmax_nan(sv[2][0], sv[2][1]), x3 = fmax_nan(sv[3][0], sv[3][1]);
 #pragma unroll
@@ -233,8 +256,6 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
       float xm = fmax_nan(fmax_nan(x0, x1), fmax_nan(x2, x3));
       xm = fmax_nan(xm, other_half(xm));
       mn = fmax_nan(m, __fmul_rn(d.scale, xm));
-      const float c0 = -__fmul_rn(mn, LOG2E);
-      AT_S_LOOP(sv[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kt][i], c1, c0)))
     } else {
       AT_S_LOOP(sv[kt][i] = __fmul_rn(d.scale, sv[kt][i]))
       if (d.causal) {
@@ -247,7 +268,13 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
       AT_S_LOOP(xm = fmax_nan(xm, sv[kt][i]))
       xm = fmax_nan(xm, other_half(xm));
       mn = fmax_nan(m, xm);
-      AT_S_LOOP(sv[kt][i] = exp_f(__fsub_rn(sv[kt][i], mn)))
+    }
+    AT_REBASE(mn);
+    if (fast) {
+      const float c0 = -__fmul_rn(mr, LOG2E);
+      AT_S_LOOP(sv[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kt][i], c1, c0)))
+    } else {
+      AT_S_LOOP(sv[kt][i] = exp_f(__fsub_rn(sv[kt][i], mr)))
     }
     {
       float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -261,17 +288,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
       ls = __fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3));
       ls = __fadd_rn(ls, other_half(ls));
     }
-    const float alpha = exp_f(__fsub_rn(m, mn));
-    if (!__all(alpha == 1.f)) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        o0[i] = __fmul_rn(o0[i], alpha);
-        o1[i] = __fmul_rn(o1[i], alpha);
-        o2[i] = __fmul_rn(o2[i], alpha);
-        o3[i] = __fmul_rn(o3[i], alpha);
-      }
-    }
-    lsum = __fadd_rn(__fmul_rn(lsum, alpha), ls);
+    lsum = __fadd_rn(lsum, ls);
     m = mn;
     __builtin_amdgcn_s_waitcnt(0);                    // this wave's part of V_j has landed
     __syncthreads();                                  // every wave: done with Ks, V_j in LDS
@@ -326,7 +343,21 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     __syncthreads();                                  // every wave: done with Vs, K_{j+1} in LDS
     if (more) tile_to_lds(V + vb0 + (int64_t)(j + 1) * d.v_step, d.v_row, Vs, wu, l);
   }
-  // final state
+  // final state, relative to m
+  if (T > 0) {
+    const float fin = exp_f(__fsub_rn(mr, m));
+    if (!__all(fin == 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] = __fmul_rn(o0[i], fin);
+        o1[i] = __fmul_rn(o1[i], fin);
+        o2[i] = __fmul_rn(o2[i], fin);
+        o3[i] = __fmul_rn(o3[i], fin);
+      }
+      lsum = __fmul_rn(lsum, fin);
+    }
+  }
+#undef AT_REBASE
   if (h == 0) {
     ((float*)d.m_out)[lane * AT + row] = m;
     ((float*)d.l_out)[lane * AT + row] = lsum;
