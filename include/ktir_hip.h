@@ -356,6 +356,13 @@ typedef struct ktir_attn {
    * f16 operands take the single-rounding f16 product under the same rule. */
   uint64_t v16_ptr, v16_flag;
   int64_t v16_lo, v16_n;
+  /* optional (0 / 0: not used): const int32_t* [2 * n_pairs] lanes run two
+   * per workgroup ({lane, lane or -1}; paired lanes have equal k_base, v_base
+   * and kpos0; every lane appears once).  Used in the cases that run P @ V
+   * in f16: one group of four wavefronts per lane, the two groups taking
+   * turns between MFMA work and softmax. */
+  uint64_t pairs;
+  int64_t n_pairs;
 } ktir_attn_t;
 int ktir_launch_attention(const ktir_attn_t* d);
 

@@ -395,6 +395,305 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
   }
 }
 
+// ---- two query blocks per workgroup, alternating matrix and vector work ----
+//
+// Workgroup of 8 wavefronts: group g = w / 4 runs query block pairs[2 b + g]
+// exactly as attn_kernel runs one (wave w % 4 owns 32 rows), and both groups
+// read the same K/V tile stream (the host pairs lanes with equal K/V bases
+// and key positions).  Per KV tile j a group has a matrix phase M_j
+// (O += P_{j-1} V_{j-1}, then S_j = K_j Q^T: 64 MFMAs) and a vector phase
+// V_j (softmax of S_j into P_j: max, exp, row sum, about 300 VALU
+// instructions).  Group 1 runs one phase behind group 0 and every phase ends
+// at a workgroup barrier, so on each SIMD one wavefront's MFMAs always run
+// beside the other's softmax.  P @ V in f16 (P rounded once), as the PV16
+// form of attn_kernel.  K and V tiles are double-buffered: at even phase 2i
+// every wave streams its 16 rows of K_{i+1} and V_i into the buffers tiles
+// i - 1 and i - 2 have left; they are waited for at the end of phase 2i + 1.
+
+// Wave w8 (uniform, 0..7) copies rows 16 w8 .. 16 w8 + 15 of a 128 x 128 tile
+// into LDS: 4 blocks of 4 rows, as tile_to_lds.
+__device__ __forceinline__ void tile16_to_lds(const uint16_t* src, int64_t row_stride, uint16_t* lds, int w8, int l) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(src + (int64_t)(16 * w8) * row_stride), (short)0, (int)((15 * row_stride + AT) * 2), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds + 512 * (4 * w8 + i)),
+                                             16, tile_lane_off(l, row_stride, i), (int)(i * 8 * row_stride), 0, 0);
+}
+
+// row sum of P: this lane's 64 values plus the other half-wave's
+__device__ __forceinline__ float pp_rowsum(const f32x16_t (&p)[4]) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    a0 = __fadd_rn(a0, p[0][i]);
+    a1 = __fadd_rn(a1, p[1][i]);
+    a2 = __fadd_rn(a2, p[2][i]);
+    a3 = __fadd_rn(a3, p[3][i]);
+  }
+  const float ls = __fadd_rn(__fadd_rn(a0, a1), __fadd_rn(a2, a3));
+  return __fadd_rn(ls, other_half(ls));
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, int mhi, int minv) {
+  if (BF16 && *(const int*)d.v16_flag != 0) return;   // V not exact in f16: attn_kernel<true, false> runs
+  __shared__ __align__(16) uint16_t K0s[AT * AT];     // K tiles of even / odd j
+  __shared__ __align__(16) uint16_t K1s[AT * AT];
+  __shared__ __align__(16) uint16_t V0s[AT * AT];     // V tiles of even / odd j
+  __shared__ __align__(16) uint16_t V1s[AT * AT];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, r32 = l & 31;
+  const int g = __builtin_amdgcn_readfirstlane(w >> 2), w8 = __builtin_amdgcn_readfirstlane(w);
+  const int32_t* pairs = (const int32_t*)d.pairs;
+  const int la = uni(pairs[2 * blockIdx.x]), lb = uni(pairs[2 * blockIdx.x + 1]);
+  const int32_t* trips = (const int32_t*)d.trips;
+  const int ta = la >= 0 ? uni(trips[la]) : 0, tb = lb >= 0 ? uni(trips[lb]) : 0;
+  const int lane = g ? lb : la, T = g ? tb : ta, Tmax = ta > tb ? ta : tb;
+  const int lk = la >= 0 ? la : lb;                   // whose K/V stream (both share it)
+  const uint16_t* K = (const uint16_t*)d.k_ptr;
+  const uint16_t* V = BF16 ? (const uint16_t*)d.v16_ptr - d.v16_lo : (const uint16_t*)d.v_ptr;
+  const int64_t kbase = lk >= 0 ? uni(((const int64_t*)d.k_base)[lk]) : 0;
+  const int64_t vbase = lk >= 0 ? uni(((const int64_t*)d.v_base)[lk]) : 0;
+  const int row = (w & 3) * 32 + r32;
+  uint4 qf[8];
+  int64_t qpos = 0;
+  if (T > 0) {
+    const uint16_t* qr = (const uint16_t*)d.q_ptr + uni(((const int64_t*)d.q_base)[lane]) + (int64_t)row * d.q_row + 8 * h;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) qf[st] = *(const uint4*)(qr + 16 * st);
+    qpos = uni(((const int64_t*)d.qpos0)[lane]) + row;
+  }
+  const int64_t kpos00 = lk >= 0 ? uni(((const int64_t*)d.kpos0)[lk]) : 0;
+  if (Tmax > 0) tile16_to_lds(K + kbase, d.k_row, K0s, w8, l);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const bool pos_scale = d.scale > 0.f;
+  const float c1 = __fmul_rn(d.scale, LOG2E);
+  const f32x16_t z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  f32x16_t o0 = z16, o1 = z16, o2 = z16, o3 = z16;
+  f32x16_t sc[4] = {z16, z16, z16, z16};             // S_j between M_j and V_j
+  uint4 ph[8];                                        // P_j (f16, in MFMA operand order) between V_j and M_{j+1}
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) ph[ks] = make_uint4(0, 0, 0, 0);
+  float m = -__builtin_inff(), mr = -__builtin_inff(), lsum = 0.f;
+  const int k_off = r32 * AT, k_x = swz16(r32 & 15);
+  const int tg = l >> 4, tj = l & 15;
+  const int v_row0 = 8 * (tg >> 1) + (tj >> 2);
+  const int v_c = 2 * (tg & 1) + ((tj >> 1) & 1), v_in = 4 * (tj & 1);
+  const int v_b0 = v_row0 * AT + v_in, v_x0 = v_c ^ swz16(v_row0), v_x1 = v_c ^ swz16(v_row0 + 4);
+
+  // matrix phase M_j: O += P_{j-1} V_{j-1} (V tile in VB), then S_j = K_j Q^T (K tile in KB)
+#define PP_M(J, KB, VB)                                                                              \
+  do {                                                                                               \
+    int kx = k_x, vfb = v_b0, vx0 = v_x0, vx1 = v_x1;                                                \
+    asm volatile("" : "+v"(kx), "+v"(vfb), "+v"(vx0), "+v"(vx1));                                    \
+    __builtin_amdgcn_s_setprio(1);                                                                   \
+    if ((J) >= 1 && (J) <= T) {                                                                      \
+      _Pragma("unroll") for (int ks = 0; ks < 8; ++ks) {                                             \
+        const uint16_t* vt = &(VB)[16 * ks * AT];                                                    \
+        uint4 a[4];                                                                                  \
+        _Pragma("unroll") for (int dt = 0; dt < 4; ++dt) {                                           \
+          const uint2 lo = ds_tr16(vt + vfb + 8 * ((4 * dt) ^ vx0));                                 \
+          const uint2 hi = ds_tr16(vt + vfb + 4 * AT + 8 * ((4 * dt) ^ vx1));                        \
+          a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);                                                \
+        }                                                                                            \
+        o0 = mfma_at<false>(a[0], ph[ks], o0);                                                       \
+        o1 = mfma_at<false>(a[1], ph[ks], o1);                                                       \
+        o2 = mfma_at<false>(a[2], ph[ks], o2);                                                       \
+        o3 = mfma_at<false>(a[3], ph[ks], o3);                                                       \
+      }                                                                                              \
+      /* the 8 fragment reads of key step ks + 1 between the 4 MFMAs of ks */                       \
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);                                             \
+      _Pragma("unroll") for (int x = 0; x < 28; ++x) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                           \
+      }                                                                                              \
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                             \
+    }                                                                                                \
+    if ((J) < T) {                                                                                   \
+      _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) sc[kt] = z16;                                 \
+      _Pragma("unroll") for (int st = 0; st < 8; ++st) {                                             \
+        const uint16_t* kp = &(KB)[k_off + 8 * ((2 * st + h) ^ kx)];                                 \
+        _Pragma("unroll") for (int kt = 0; kt < 4; ++kt)                                             \
+          sc[kt] = mfma_at<BF16>(*(const uint4*)(kp + kt * 32 * AT), qf[st], sc[kt]);                \
+      }                                                                                              \
+      /* the 4 K-fragment reads of d-step st + 1 between the 4 MFMAs of st */                      \
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                                             \
+      _Pragma("unroll") for (int x = 0; x < 28; ++x) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                           \
+      }                                                                                              \
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                             \
+    }                                                                                                \
+    __builtin_amdgcn_s_setprio(0);                                                                   \
+  } while (0)
+
+  // vector phase V_j: softmax of S_j (online, base mr as in attn_kernel) into ph
+#define PP_V(J)                                                                                      \
+  do {                                                                                               \
+    if ((J) >= 0 && (J) < T) {                                                                       \
+      const int dbase = (int)(kpos00 + (int64_t)(J) * d.kpos_step - qpos);                           \
+      const bool all_keep = !d.causal ||                                                             \
+          (minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi));        \
+      const bool fast = pos_scale && __all(all_keep);                                                \
+      float mn;                                                                                      \
+      if (fast) {                                                                                    \
+        float x0 = fmax_nan(sc[0][0], sc[0][1]), x1 = fmax_nan(sc[1][0], sc[1][1]);                  \
+        float x2 = fmax_nan(sc[2][0], sc[2][1]), x3 = fmax_nan(sc[3][0], sc[3][1]);                  \
+        _Pragma("unroll") for (int i = 2; i < 16; i += 2) {                                          \
+          x0 = fmax_nan(x0, fmax_nan(sc[0][i], sc[0][i + 1]));                                       \
+          x1 = fmax_nan(x1, fmax_nan(sc[1][i], sc[1][i + 1]));                                       \
+          x2 = fmax_nan(x2, fmax_nan(sc[2][i], sc[2][i + 1]));                                       \
+          x3 = fmax_nan(x3, fmax_nan(sc[3][i], sc[3][i + 1]));                                       \
+        }                                                                                            \
+        float xm = fmax_nan(fmax_nan(x0, x1), fmax_nan(x2, x3));                                     \
+        xm = fmax_nan(xm, other_half(xm));                                                           \
+        mn = fmax_nan(m, __fmul_rn(d.scale, xm));                                                    \
+      } else {                                                                                       \
+        AT_S_LOOP(sc[kt][i] = __fmul_rn(d.scale, sc[kt][i]))                                         \
+        if (d.causal) {                                                                              \
+          AT_S_LOOP({                                                                                \
+            const int df = dbase + kt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);                         \
+            if ((df >= mlo && df <= mhi) == (bool)minv) sc[kt][i] = d.neg;                           \
+          })                                                                                         \
+        }                                                                                            \
+        float xm = -__builtin_inff();                                                                \
+        AT_S_LOOP(xm = fmax_nan(xm, sc[kt][i]))                                                      \
+        xm = fmax_nan(xm, other_half(xm));                                                           \
+        mn = fmax_nan(m, xm);                                                                        \
+      }                                                                                              \
+      const bool up = mn > __fadd_rn(mr, 8.0f);                                                      \
+      if (__any(up)) {                                                                               \
+        const float al = up ? exp_f(__fsub_rn(mr, mn)) : 1.f;                                        \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                             \
+          o0[i] = __fmul_rn(o0[i], al);                                                              \
+          o1[i] = __fmul_rn(o1[i], al);                                                              \
+          o2[i] = __fmul_rn(o2[i], al);                                                              \
+          o3[i] = __fmul_rn(o3[i], al);                                                              \
+        }                                                                                            \
+        lsum = __fmul_rn(lsum, al);                                                                  \
+        mr = up ? mn : mr;                                                                           \
+      }                                                                                              \
+      if (fast) {                                                                                    \
+        const float c0 = -__fmul_rn(mr, LOG2E);                                                      \
+        AT_S_LOOP(sc[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][i], c1, c0)))             \
+      } else {                                                                                       \
+        AT_S_LOOP(sc[kt][i] = exp_f(__fsub_rn(sc[kt][i], mr)))                                       \
+      }                                                                                              \
+      lsum = __fadd_rn(lsum, pp_rowsum(sc));                                                         \
+      m = mn;                                                                                        \
+      _Pragma("unroll") for (int ks = 0; ks < 8; ++ks) {                                             \
+        const int kt = ks >> 1, g0 = 2 * (ks & 1);                                                   \
+        uint32_t ah0 = cvt2<false>(sc[kt][4 * g0], sc[kt][4 * g0 + 1]);                              \
+        uint32_t ah1 = cvt2<false>(sc[kt][4 * g0 + 2], sc[kt][4 * g0 + 3]);                          \
+        uint32_t bh0 = cvt2<false>(sc[kt][4 * g0 + 4], sc[kt][4 * g0 + 5]);                          \
+        uint32_t bh1 = cvt2<false>(sc[kt][4 * g0 + 6], sc[kt][4 * g0 + 7]);                          \
+        swap32(ah0, bh0);                                                                            \
+        swap32(ah1, bh1);                                                                            \
+        ph[ks] = make_uint4(ah0, ah1, bh0, bh1);                                                     \
+      }                                                                                              \
+    }                                                                                                \
+  } while (0)
+
+  // at even phase 2i: K_{i+1} and V_i start streaming (into the buffers of
+  // tiles i - 1 and i - 2, which the last phase finished with)
+#define PP_DMA(I, KN, VN)                                                                            \
+  do {                                                                                               \
+    if ((I) + 1 < Tmax) tile16_to_lds(K + kbase + (int64_t)((I) + 1) * d.k_step, d.k_row, KN, w8, l); \
+    if ((I) < Tmax) tile16_to_lds(V + vbase + (int64_t)(I) * d.v_step, d.v_row, VN, w8, l);          \
+  } while (0)
+  // group 0 finishes at phase 2 ta, group 1 at 2 tb + 1; four phases per trip
+  const int nph = 2 * Tmax + 2;
+  // phase ends: a plain barrier after an even phase (nothing in LDS changes
+  // hands there), a full one after an odd phase, when the tiles streamed at
+  // the even phase must have landed
+#define PP_SYNC_EVEN()                   \
+  do {                                   \
+    __builtin_amdgcn_sched_barrier(0);   \
+    __builtin_amdgcn_s_barrier();        \
+    __builtin_amdgcn_sched_barrier(0);   \
+  } while (0)
+#define PP_SYNC_ODD()                    \
+  do {                                   \
+    __builtin_amdgcn_sched_barrier(0);   \
+    __builtin_amdgcn_s_waitcnt(0);       \
+    __syncthreads();                     \
+    __builtin_amdgcn_sched_barrier(0);   \
+  } while (0)
+  // each group's own phase sequence (a static M, V order, so S and P live in
+  // registers only between their two phases); both run the same barriers
+  if (g == 0) {
+    for (int p = 0; p < nph; p += 4) {
+      const int i = p >> 1;                           // tiles i (even) and i + 1
+      PP_DMA(i, K1s, V0s);
+      PP_M(i, K0s, V1s);
+      PP_SYNC_EVEN();
+      PP_V(i);
+      PP_SYNC_ODD();
+      PP_DMA(i + 1, K0s, V1s);
+      PP_M(i + 1, K1s, V0s);
+      PP_SYNC_EVEN();
+      PP_V(i + 1);
+      PP_SYNC_ODD();
+    }
+  } else {
+    for (int p = 0; p < nph; p += 4) {
+      const int i = p >> 1;
+      PP_DMA(i, K1s, V0s);
+      PP_V(i - 1);
+      PP_SYNC_EVEN();
+      PP_M(i, K0s, V1s);
+      PP_SYNC_ODD();
+      PP_DMA(i + 1, K0s, V1s);
+      PP_V(i);
+      PP_SYNC_EVEN();
+      PP_M(i + 1, K1s, V0s);
+      PP_SYNC_ODD();
+    }
+  }
+#undef PP_SYNC_EVEN
+#undef PP_SYNC_ODD
+#undef PP_DMA
+#undef PP_V
+#undef PP_M
+  if (lane < 0) return;
+  if (T > 0) {
+    const float fin = exp_f(__fsub_rn(mr, m));
+    if (!__all(fin == 1.f)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] = __fmul_rn(o0[i], fin);
+        o1[i] = __fmul_rn(o1[i], fin);
+        o2[i] = __fmul_rn(o2[i], fin);
+        o3[i] = __fmul_rn(o3[i], fin);
+      }
+      lsum = __fmul_rn(lsum, fin);
+    }
+  }
+  if (h == 0) {
+    ((float*)d.m_out)[lane * AT + row] = m;
+    ((float*)d.l_out)[lane * AT + row] = lsum;
+  }
+  const int64_t ob = uni(((const int64_t*)d.o_base)[lane]) + (int64_t)row * d.o_row + 4 * h;
+#define PP_EPI(o, dt)                                                                            \
+  _Pragma("unroll") for (int gg = 0; gg < 4; ++gg) {                                             \
+    const float q0 = __fdiv_rn(o[4 * gg], lsum), q1 = __fdiv_rn(o[4 * gg + 1], lsum);            \
+    const float q2 = __fdiv_rn(o[4 * gg + 2], lsum), q3 = __fdiv_rn(o[4 * gg + 3], lsum);        \
+    const int64_t e = ob + 32 * dt + 8 * gg;                                                     \
+    if (d.o_dtype == KTIR_F32)                                                                   \
+      *(float4*)((float*)d.o_ptr + e) = make_float4(q0, q1, q2, q3);                             \
+    else if (d.o_dtype == KTIR_BF16)                                                             \
+      *(uint2*)((uint16_t*)d.o_ptr + e) = make_uint2(cvt2<true>(q0, q1), cvt2<true>(q2, q3));     \
+    else                                                                                         \
+      *(uint2*)((uint16_t*)d.o_ptr + e) = make_uint2(cvt2<false>(q0, q1), cvt2<false>(q2, q3));   \
+  }
+  PP_EPI(o0, 0)
+  PP_EPI(o1, 1)
+  PP_EPI(o2, 2)
+  PP_EPI(o3, 3)
+#undef PP_EPI
+}
+
 // f16 copy of bf16 V: 8 elements per thread and step; *bad |= any value that
 // is not finite or has |v| >= 65536 (bf16 magnitude bits >= 0x4780)
 __global__ __launch_bounds__(256) void attn_v16(const uint16_t* src, uint16_t* dst, int64_t n8, int* bad) {
@@ -449,6 +748,8 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
   // its error there is at most 2^-12 max|V| per element, while an
   // unnormalised acc would carry it l times over
   const bool norm = d->o_ptr && !d->acc_out;
+  const bool pp = norm && d->pairs && d->n_pairs > 0 && d->n_pairs < (int64_t)0x7fffffff;
+  const dim3 pgrid((unsigned)(pp ? d->n_pairs : 1));
   if (d->dtype == KTIR_BF16 && d->v16_ptr && norm) {
     if (!d->v16_flag || (d->v16_lo | d->v16_n) & 7 || d->v16_lo < 0 || d->v16_n <= 0 || (d->v16_ptr & 15))
       return set_error(KTIR_E_ARG, "ktir_launch_attention: bad f16 V copy (range %lld + %lld)",
@@ -458,10 +759,15 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
     hipLaunchKernelGGL(attn_v16_clear, dim3(1), dim3(1), 0, stream(), (int*)d->v16_flag);
     hipLaunchKernelGGL(attn_v16, dim3((unsigned)blocks), dim3(256), 0, stream(),
                        (const uint16_t*)d->v_ptr + d->v16_lo, (uint16_t*)d->v16_ptr, n8, (int*)d->v16_flag);
-    hipLaunchKernelGGL((attn_kernel<true, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+    if (pp)
+      hipLaunchKernelGGL((attn_pp<true>), pgrid, dim3(512), 0, stream(), *d, lo, hi, inv);
+    else
+      hipLaunchKernelGGL((attn_kernel<true, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
     hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
   } else if (d->dtype == KTIR_BF16) {
     hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+  } else if (norm && pp) {
+    hipLaunchKernelGGL((attn_pp<false>), pgrid, dim3(512), 0, stream(), *d, lo, hi, inv);
   } else if (norm) {
     hipLaunchKernelGGL((attn_kernel<false, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
   } else {

@@ -592,6 +592,39 @@ def _xcd_order(trips, k_base, v_base, n_xcd=N_XCD):
     return np.asarray(out, np.int32)
 
 
+def _pp_pairs(trips, k_base, v_base, kpos0, n_xcd=N_XCD):
+    """Lane pairs for the two-group attention kernel (flat int32, -1 for a
+    lane without a partner): lanes of one K/V stream (equal K/V bases and key
+    positions) two by two in trip-count order, longest first, the streams
+    spread over the XCDs by work as in _xcd_order."""
+    L = len(trips)
+    if L == 0:
+        return np.zeros(0, np.int32)
+    _, grp = np.unique(np.stack([k_base, v_base, kpos0], 1), axis=0, return_inverse=True)
+    grp = grp.reshape(-1)
+    by_grp = {}
+    for lane in np.lexsort((-trips, grp)):
+        by_grp.setdefault(int(grp[lane]), []).append(int(lane))
+    prs = {g: [(ls[i], ls[i + 1] if i + 1 < len(ls) else -1) for i in range(0, len(ls), 2)]
+           for g, ls in by_grp.items()}
+    work = {g: sum(int(trips[a]) + 1 for a, _ in ps) for g, ps in prs.items()}
+    bins = [[] for _ in range(n_xcd)]
+    load = np.zeros(n_xcd)
+    for g in sorted(work, key=lambda g: -work[g]):
+        x = int(np.argmin(load))
+        bins[x].append(g)
+        load[x] += work[g]
+    seqs = [[p for g in b for p in prs[g]] for b in bins]
+    out, pos = [], [0] * n_xcd
+    n = sum(len(q) for q in seqs)
+    while len(out) < n:
+        for x in range(n_xcd):
+            if pos[x] < len(seqs[x]):
+                out.append(seqs[x][pos[x]])
+                pos[x] += 1
+    return np.asarray(out, np.int32).reshape(-1)
+
+
 def _attention_loop(ex, op, lb, st, trips, inits):
     """Fuse the online-softmax KV loop of flash attention into one launch
     (``ktir_launch_attention``).  The reference executes it op by op
@@ -814,6 +847,8 @@ def _attention_loop(ex, op, lb, st, trips, inits):
                 keep += [v16, flag]
                 d.v16_ptr, d.v16_flag, d.v16_lo, d.v16_n = v16.ptr, flag.ptr, lo_, hi_ - lo_
     d.order = up(_xcd_order(trips, tiles["k"][1], tiles["v"][1]))
+    pairs = _pp_pairs(trips, tiles["k"][1], tiles["v"][1], ck0.astype(np.int64))
+    d.pairs, d.n_pairs = up(pairs), len(pairs) // 2
     d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
     d.kpos_step = kpos_step
     d.scale, d.neg = p0["scale"], neg

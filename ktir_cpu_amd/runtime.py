@@ -114,7 +114,7 @@ class ATTN(C.Structure):
                 ("m_out", C.c_uint64), ("l_out", C.c_uint64), ("acc_out", C.c_uint64),
                 ("o_ptr", C.c_uint64), ("o_base", C.c_uint64), ("o_row", C.c_int64), ("o_dtype", C.c_int32),
                 ("pad2", C.c_int32), ("v16_ptr", C.c_uint64), ("v16_flag", C.c_uint64), ("v16_lo", C.c_int64),
-                ("v16_n", C.c_int64)]
+                ("v16_n", C.c_int64), ("pairs", C.c_uint64), ("n_pairs", C.c_int64)]
 
 
 class KTIRDeviceError(RuntimeError):
