@@ -116,7 +116,7 @@ CONFIGS = {"vector_add": _vector_add, "copy": _copy, "gather": _gather, "softmax
 
 
 # kernels that make up each kind of launch (the HIP kernel names)
-_LAUNCH_KERNELS = {"mm": ("mm_mfma", "mm_generic"), "attn": ("attn_kernel",), "rmw": ("rmw_",),
+_LAUNCH_KERNELS = {"mm": ("mm_mfma", "mm_generic"), "attn": ("attn_kernel", "attn_pp", "attn_v16"), "rmw": ("rmw_",),
                    "prog": ("prog_",)}
 
 
