@@ -49,6 +49,16 @@ def gemm(M=256, N=256, K=256, bm=64, bn=64, bk=32, gm=2, gn=2, seed=42):
             dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16)))
 
 
+def gemm_bf16(M=256, N=256, K=512, bm=128, bn=128, bk=64, gm=2, gn=2, seed=7):
+    """The tiled GEMM with bf16 operands and a bf16 result (the f32 K-loop
+    sums rounded once by the store's truncf)."""
+    rng = np.random.default_rng(seed)
+    a = bf16_bits((rng.standard_normal((M, K)) * K ** -0.5).astype(np.float32))
+    b = bf16_bits((rng.standard_normal((K, N)) * K ** -0.5).astype(np.float32))
+    src = configs.gemm(M, N, K, bm, bn, bk, gm, gn).replace("f16", "bf16")
+    return src, "gemm_kernel", dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.uint16))
+
+
 def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42, dt="bf16", causal=True):
     rng = np.random.default_rng(seed)
     if dt == "bf16":

@@ -90,6 +90,16 @@ def test_gemm(shape):
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("shape", [(256, 256, 512, 128, 128, 64, 2, 2),    # 256 x 256 blocks
+                                   (256, 256, 192, 128, 128, 64, 2, 2)])   # 128 x 128 tiles (odd K steps)
+def test_gemm_bf16(shape):
+    """bf16 operands (the bf16 MFMA) and a bf16 result written by the
+    matmul kernel's epilogue."""
+    ref, out, g = _run(_cases.gemm_bf16(*shape))
+    assert set(g.last_plan.counts()) == {"mm"}
+    np.testing.assert_allclose(bf16_from_bits(out["c_ptr"]), bf16_from_bits(ref["c_ptr"]), rtol=1e-2, atol=1e-3)
+
+
 def test_flash_attention_generic_path():
     """D = 32, 64-row blocks: not the fused kernel's shape, op-by-op launches."""
     ref, out, g = _run(_cases.flash_attention())
