@@ -11,7 +11,8 @@ whose reads past an allocation's end give zeros and whose writes past it are
 dropped.  Pointer arguments are element indices ``stick*128 // bytes``
 (``dtypes.py:79-85``).
 
-How each part is pinned (see ``tests/test_oracle_*.py``):
+How each part is pinned (``tests/test_golden.py``, ``tests/test_oracle_pins.py``,
+``tests/test_host_logic.py``):
 - memory read/write/pad/truncate: reference golden vectors
   (``tests/test_ktir_cpu.py:51-115`` values) + brute-force index checks;
 - load/store/gather/scatter, collisions: reference golden vectors
@@ -19,12 +20,19 @@ How each part is pinned (see ``tests/test_oracle_*.py``):
 - f16 elementwise: closed form (IEEE RNE of the f64 result);
 - ``_tree_fold``: brute-force pairwise-halving model on small inputs and the
   reference's exact small values (reduce → 10, outs init → 110);
-- matmul: closed form (f32 sequential-k sum of exact products for f16);
-- transcendentals on f32 tiles and the f32 BLAS matmul order:
-  tolerance-only ("parity unpinned" beyond rtol/atol, as in the reference's
-  own tests);
-- LX-overflow accounting (``grid.py:255-350``): parity unpinned — restated
-  from source text, no reference fixture exercises its exact boundary.
+- matmul: the tiled K loop on small-integer f16 data, where every product
+  and sum is exact, equals the int64 product (a non-square case, so swapped
+  operands fail); the order of f32 rounding in larger sums is NumPy's BLAS
+  order, pinned only to tolerance (as in the reference's own tests);
+- exp on f32 tiles: within 4 ulps of float64 exp (NumPy's float32 exp, the
+  reference's own call);
+- attention (matmul, mask, max, exp, sum, divide as composed by the KTIR
+  loop): the closed form for Q = 0, where softmax is uniform and O[i] is the
+  mean of the V rows row i may see (causal and full);
+- LX-overflow accounting (``grid.py:255-350``): the reference's golden peak
+  of 622592 bytes for its K-loop matmul kernel
+  (``tests/test_lx_scoping.py:1095-1185``): capacity equal to it runs, one
+  byte less raises the reference's overflow error.
 
 bf16 is an extension (the reference has none, ``dtypes.py:24-39``): bf16
 tiles hold float32 data that is always rounded to the nearest bf16 (RNE);

@@ -54,3 +54,39 @@ def test_gpu_negative_index_raises(scatter):
     g.load(src)
     with pytest.raises(IndexError):
         g.execute_function(fn, **kw)
+
+
+@pytest.mark.parametrize("slack", [0, -1])
+def test_oracle_lx_peak(slack):
+    """The reference's LX peak for its K-loop matmul kernel is 622592 bytes:
+    a capacity of exactly that runs, one byte less overflows."""
+    from fractions import Fraction
+    src, fn, kw, peak = gk.lx_matmul_loop()
+    o = OracleInterpreter(lx_size_mb=Fraction(peak + slack, 1 << 20))
+    o.load(src)
+    if slack < 0:
+        with pytest.raises(MemoryError, match="LX scratchpad overflow"):
+            o.execute_function(fn, **_copy(kw))
+    else:
+        o.execute_function(fn, **_copy(kw))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slack", [0, -1])
+def test_gpu_lx_peak(slack):
+    """The same boundary through the HIP backend's LX accounting, with
+    results equal to the oracle's where it runs."""
+    from fractions import Fraction
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    src, fn, kw, peak = gk.lx_matmul_loop()
+    g = KTIRInterpreter(lx_size_mb=Fraction(peak + slack, 1 << 20))
+    g.load(src)
+    if slack < 0:
+        with pytest.raises(MemoryError, match="LX scratchpad overflow"):
+            g.execute_function(fn, **_copy(kw))
+        return
+    out = g.execute_function(fn, **_copy(kw))
+    o = OracleInterpreter(lx_size_mb=Fraction(peak, 1 << 20))
+    o.load(src)
+    ref = o.execute_function(fn, **_copy(kw))
+    np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
