@@ -866,7 +866,8 @@ def _attention_loop(ex, op, lb, st, trips, inits):
         ex.log(alloc, False, rel, (tmax, AT, AT), (step, row, 1))
     ex.launch("attn", d, keep)
     ex.attn_pending = dict(desc=d, keep=keep, acc=a_buf, l=l_buf, lanes=L, level=len(ex.levels),
-                           body_names=set(names))
+                           body_names=set(names),
+                           reads={id(x) for x in (q_leaf.alloc, tiles["k"][0], tiles["v"][0]) if x is not None})
     vec = lambda b: Tile(Expr("ld", "f32", (AT,), attr=LeafSpec(b.ptr, "f32", LaneOff(0, AT), (1,), 0, L * AT,
                                                                   keep=(b,))))
     res = [None, None, None]
@@ -908,6 +909,9 @@ def attention_epilogue(ex, e, dest) -> bool:
             and _plain_ld(b, l_buf.ptr, (1, 0)) and b.attr.lane.stride == 128):
         return False
     if dest.dtype not in ("f32", "bf16", "f16") or dest.offsets is not None or dest.winner is not None:
+        return False
+    # O is written while other workgroups still read Q, K and V
+    if dest.alloc is not None and id(dest.alloc) in pend["reads"]:
         return False
     dsh = tuple(e.shape)
     dst = tuple(dest.strides)
@@ -1024,6 +1028,10 @@ def mm_epilogue(ex, store_op, val, dest, alloc, shape) -> bool:
         return False
     d = pend["desc"]
     if d.accumulate == 1 or d.round_dt != rt.DTYPE_CODE["f32"]:
+        return False
+    # the kernel writes the destination while its workgroups still read the
+    # operands: never into a tensor the product reads
+    if id(alloc) in pend["reads"]:
         return False
     if dest.dtype not in ("f32", "f16", "bf16") or dest.offsets is not None or dest.winner is not None:
         return False

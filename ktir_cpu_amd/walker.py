@@ -1631,9 +1631,12 @@ class Executor:
         self.launch("mm", d, keep)
         # the SSA value `name` holds this launch's result; a store of it may
         # still become the launch's own epilogue (fusion.mm_epilogue)
+        reads = {id(x.alloc) for x in (la, lb) if x.alloc is not None}
+        if d.accumulate == 1 and lc.alloc is not None:
+            reads.add(id(lc.alloc))
         self.mm_pending = None if self.eager or name is None else dict(
             desc=d, keep=keep, buf=buf, lanes=L, level=len(self.levels), n=len(self.plan.launches), M=M, N=N,
-            name=name)
+            name=name, reads=reads)
         return Tile(Expr("ld", cspec.dtype, (M, N), attr=cspec))
 
     def h_linalg_matmul(self, op):
