@@ -271,13 +271,17 @@ def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8
 # ---------------------------------------------------------------------------
 
 def gemm(M: int = 8192, N: int = 8192, K: int = 8192, bm: int = 128, bn: int = 128, bk: int = 64,
-         gm: int = 8, gn: int = 8) -> str:
+         gm: int = 8, gn: int = 8, out_dt: str = "f16") -> str:
     """C = A @ B on a gm x gn grid; each core loops over its (M/gm)x(N/gn)
-    block in bm x bn tiles, accumulating f32 over K in bk steps."""
+    block in bm x bn tiles, accumulating f32 over K in bk steps; C is f16
+    (the f32 sums rounded by arith.truncf) or, with out_dt="f32", the sums."""
     tm, tn = M // gm // bm, N // gn // bn
     assert tm * gm * bm == M and tn * gn * bn == N and K % bk == 0
     A16, B16 = _t([bm, bk], "f16"), _t([bk, bn], "f16")
     A32, B32, C32, C16 = _t([bm, bk], "f32"), _t([bk, bn], "f32"), _t([bm, bn], "f32"), _t([bm, bn], "f16")
+    assert out_dt in ("f16", "f32")
+    trunc = f"        %c16 = arith.truncf %acc : {C32} to {C16}" if out_dt == "f16" else ""
+    cval, CO = ("%c16", C16) if out_dt == "f16" else ("%acc", C32)
     return f"""module {{
   func.func @gemm_kernel(%a_ptr: index, %b_ptr: index, %c_ptr: index)
       attributes {{grid = [{gm}, {gn}]}} {{
@@ -293,7 +297,7 @@ def gemm(M: int = 8192, N: int = 8192, K: int = 8192, bm: int = 128, bn: int = 1
     %zero = arith.constant 0.0 : f32
 {_view("a_view", "a_ptr", [M, K], [K, 1], "f16")}
 {_view("b_view", "b_ptr", [K, N], [N, 1], "f16")}
-{_view("c_view", "c_ptr", [M, N], [N, 1], "f16")}
+{_view("c_view", "c_ptr", [M, N], [N, 1], out_dt)}
     %m_blk = arith.muli %pid_m, %TM : index
     %n_blk = arith.muli %pid_n, %TN : index
     scf.for %i = %c0 to %TM step %c1 : index {{
@@ -313,9 +317,9 @@ def gemm(M: int = 8192, N: int = 8192, K: int = 8192, bm: int = 128, bn: int = 1
           %acc_n = linalg.matmul ins(%a32, %b32 : {A32}, {B32}) outs(%acc_i : {C32}) -> {C32}
           scf.yield %acc_n : {C32}
         }}
-        %c16 = arith.truncf %acc : {C32} to {C16}
-{_tile("c_acc", "c_view", ["%m0", "%n0"], [bm, bn], [M, N], "f16", "        ")}
-        ktdp.store %c16, %c_acc : {C16}, !ktdp.access_tile<{bm}x{bn}xindex>
+{trunc}
+{_tile("c_acc", "c_view", ["%m0", "%n0"], [bm, bn], [M, N], out_dt, "        ")}
+        ktdp.store {cval}, %c_acc : {CO}, !ktdp.access_tile<{bm}x{bn}xindex>
         scf.yield
       }}
       scf.yield

@@ -41,12 +41,12 @@ def rmsnorm(rows=64, cols=256, cores=8, rblk=4, seed=42):
             dict(x_ptr=x, w_ptr=w, y_ptr=np.zeros_like(x), eps=1e-6))
 
 
-def gemm(M=256, N=256, K=256, bm=64, bn=64, bk=32, gm=2, gn=2, seed=42):
+def gemm(M=256, N=256, K=256, bm=64, bn=64, bk=32, gm=2, gn=2, seed=42, out_dt="f16"):
     rng = np.random.default_rng(seed)
     a = (rng.standard_normal((M, K)) * K ** -0.5).astype(np.float16)
     b = (rng.standard_normal((K, N)) * K ** -0.5).astype(np.float16)
-    return (configs.gemm(M, N, K, bm, bn, bk, gm, gn), "gemm_kernel",
-            dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16)))
+    return (configs.gemm(M, N, K, bm, bn, bk, gm, gn, out_dt), "gemm_kernel",
+            dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16 if out_dt == "f16" else np.float32)))
 
 
 def gemm_bf16(M=256, N=256, K=512, bm=128, bn=128, bk=64, gm=2, gn=2, seed=7):

@@ -90,8 +90,20 @@ def test_gemm(shape):
     np.testing.assert_allclose(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 512, 128, 128, 64, 2, 2),    # 256 x 256 blocks
-                                   (256, 256, 192, 128, 128, 64, 2, 2)])   # 128 x 128 tiles (odd K steps)
+_MFMA_SHAPES = [(256, 256, 512, 128, 128, 64, 2, 2),    # 256 x 256 blocks
+                (256, 256, 192, 128, 128, 64, 2, 2)]    # 128 x 128 tiles (odd K steps)
+
+
+@pytest.mark.parametrize("shape", _MFMA_SHAPES)
+def test_gemm_f32_result(shape):
+    """The f32 K-loop sums stored as they are (no truncf) by the matmul
+    kernel's epilogue."""
+    ref, out, g = _run(_cases.gemm(*shape, out_dt="f32"))
+    assert set(g.last_plan.counts()) == {"mm"}
+    np.testing.assert_allclose(out["c_ptr"], ref["c_ptr"], rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("shape", _MFMA_SHAPES)
 def test_gemm_bf16(shape):
     """bf16 operands (the bf16 MFMA) and a bf16 result written by the
     matmul kernel's epilogue."""
