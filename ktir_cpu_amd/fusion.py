@@ -848,7 +848,8 @@ def _attention_loop(ex, op, lb, st, trips, inits):
                 d.v16_ptr, d.v16_flag, d.v16_lo, d.v16_n = v16.ptr, flag.ptr, lo_, hi_ - lo_
     d.order = up(_xcd_order(trips, tiles["k"][1], tiles["v"][1]))
     pairs = _pp_pairs(trips, tiles["k"][1], tiles["v"][1], ck0.astype(np.int64))
-    d.pairs, d.n_pairs = up(pairs), len(pairs) // 2
+    if len(pairs):
+        d.pairs, d.n_pairs = up(pairs), len(pairs) // 2
     d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
     d.kpos_step = kpos_step
     d.scale, d.neg = p0["scale"], neg

@@ -133,6 +133,18 @@ def test_flash_attention_fused(args):
         np.testing.assert_array_equal(out[k], ref[k])
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_flash_attention_fused_without_pairs(dt, monkeypatch):
+    """A launch that names no lane pairs (as a C-ABI caller may) runs one
+    query block per workgroup, with the same f16 P @ V rule."""
+    from ktir_cpu_amd import fusion
+    monkeypatch.setattr(fusion, "_pp_pairs", lambda *a, **k: np.zeros(0, np.int32))
+    ref, out, g = _run(_cases.flash_attention(S=512, D=128, blk=128, dt=dt))
+    assert g.last_plan.counts().get("attn") == 1
+    f = bf16_from_bits if dt == "bf16" else (lambda x: x.astype(np.float32))
+    np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+
+
 @pytest.mark.parametrize("big", [3.0e5, -7.0e4])
 def test_flash_attention_fused_v_beyond_f16(big):
     """A V value f16 cannot hold sends P @ V of the launch to the bf16 hi + lo
