@@ -54,6 +54,9 @@ __device__ __forceinline__ void load8(const ktir_leaf_t& L, int64_t e0, float* o
 }
 
 template <int DT>
+// 16-bit results go out with non-temporal (streaming) stores, which measured
+// 6.1 against 5.0 TB/s for a 64 Mi-element f16 add; f32 results keep plain
+// stores, which measured faster for an f32 copy (5.5 against 5.0 TB/s)
 __device__ __forceinline__ void store8(const ktir_leaf_t& L, int64_t e0, const float* v) {
   if (e0 >= L.lo && e0 + 8 <= L.hi) {
     if (DT == KTIR_F16) {
@@ -62,13 +65,13 @@ __device__ __forceinline__ void store8(const ktir_leaf_t& L, int64_t e0, const f
       for (int i = 0; i < 4; ++i)
         u[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i]) |
                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1]) << 16);
-      *(KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0) = mu4{u[0], u[1], u[2], u[3]};
+      __builtin_nontemporal_store(mu4{u[0], u[1], u[2], u[3]}, (KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0));
     } else if (DT == KTIR_BF16) {
       uint32_t u[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         u[i] = (__float_as_uint(round_bf16(v[2 * i])) >> 16) | (__float_as_uint(round_bf16(v[2 * i + 1])) & 0xffff0000u);
-      *(KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0) = mu4{u[0], u[1], u[2], u[3]};
+      __builtin_nontemporal_store(mu4{u[0], u[1], u[2], u[3]}, (KTIR_G(mu4)*)((KTIR_G(uint16_t)*)L.ptr + e0));
     } else {
       *(KTIR_G(mf4)*)((KTIR_G(float)*)L.ptr + e0) = mf4{v[0], v[1], v[2], v[3]};
       *(KTIR_G(mf4)*)((KTIR_G(float)*)L.ptr + e0 + 4) = mf4{v[4], v[5], v[6], v[7]};
