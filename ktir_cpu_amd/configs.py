@@ -180,21 +180,21 @@ def _row_header(fn, args, rows, cols, cores, rows_per_core):
             f"    %row_base = arith.muli %core_id, %rpc : index\n")
 
 
-def softmax(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8) -> str:
-    """y = softmax(x) per row: f32 max, exp, f32 sum, divide, round to f16."""
+def softmax(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8, dt: str = "f16") -> str:
+    """y = softmax(x) per row: f32 max, exp, f32 sum, divide, round to `dt` (f16 or bf16)."""
     rpc = rows // cores
     assert rpc * cores == rows and rpc % rblk == 0
-    T16, T32, V32 = _t([rblk, cols], "f16"), _t([rblk, cols], "f32"), _t([rblk], "f32")
+    T16, T32, V32 = _t([rblk, cols], dt), _t([rblk, cols], "f32"), _t([rblk], "f32")
     return f"""module {{
 {_row_header("softmax_kernel", "%x_ptr: index, %y_ptr: index", rows, cols, cores, rpc)}
     %step = arith.constant {rblk} : index
-{_view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16")}
-{_view("y_view", "y_ptr", [rows, cols], [cols, 1], "f16")}
+{_view("x_view", "x_ptr", [rows, cols], [cols, 1], dt)}
+{_view("y_view", "y_ptr", [rows, cols], [cols, 1], dt)}
     %neg_inf = arith.constant 0xFF800000 : f32
     %zero = arith.constant 0.0 : f32
     scf.for %r = %c0 to %rpc step %step : index {{
       %row = arith.addi %row_base, %r : index
-{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], dt, "      ")}
       %x = ktdp.load %x_acc : !ktdp.access_tile<{rblk}x{cols}xindex> -> {T16}
       %xf = arith.extf %x : {T16} to {T32}
       %max_init = tensor.splat %neg_inf : {V32}
@@ -209,7 +209,7 @@ def softmax(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8
       %sb = linalg.broadcast ins(%s : {V32}) outs(%sb_init : {T32}) dimensions = [1]
       %p = arith.divf %e, %sb : {T32}
       %y = arith.truncf %p : {T32} to {T16}
-{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], dt, "      ")}
       ktdp.store %y, %y_acc : {T16}, !ktdp.access_tile<{rblk}x{cols}xindex>
       scf.yield
     }}
@@ -219,26 +219,26 @@ def softmax(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8
 """
 
 
-def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8) -> str:
-    """y = x * rsqrt(mean(x^2) + eps) * w, with f32 math and a f16 result."""
+def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8, dt: str = "f16") -> str:
+    """y = x * rsqrt(mean(x^2) + eps) * w, with f32 math and a `dt` (f16 or bf16) result."""
     rpc = rows // cores
     assert rpc * cores == rows and rpc % rblk == 0
-    T16, T32, V32 = _t([rblk, cols], "f16"), _t([rblk, cols], "f32"), _t([rblk], "f32")
-    W16, W32 = _t([cols], "f16"), _t([cols], "f32")
+    T16, T32, V32 = _t([rblk, cols], dt), _t([rblk, cols], "f32"), _t([rblk], "f32")
+    W16, W32 = _t([cols], dt), _t([cols], "f32")
     return f"""module {{
 {_row_header("rmsnorm_kernel", "%x_ptr: index, %w_ptr: index, %y_ptr: index, %eps: f32", rows, cols, cores, rpc)}
     %step = arith.constant {rblk} : index
-{_view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16")}
-{_view("w_view", "w_ptr", [cols], [1], "f16")}
-{_view("y_view", "y_ptr", [rows, cols], [cols, 1], "f16")}
+{_view("x_view", "x_ptr", [rows, cols], [cols, 1], dt)}
+{_view("w_view", "w_ptr", [cols], [1], dt)}
+{_view("y_view", "y_ptr", [rows, cols], [cols, 1], dt)}
     %zero = arith.constant 0.0 : f32
     %ncols = arith.constant {float(cols)} : f32
-{_tile("w_acc", "w_view", ["%c0"], [cols], [cols], "f16")}
+{_tile("w_acc", "w_view", ["%c0"], [cols], [cols], dt)}
     %w = ktdp.load %w_acc : !ktdp.access_tile<{cols}xindex> -> {W16}
     %wf = arith.extf %w : {W16} to {W32}
     scf.for %r = %c0 to %rpc step %step : index {{
       %row = arith.addi %row_base, %r : index
-{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+{_tile("x_acc", "x_view", ["%row", "%c0"], [rblk, cols], [rows, cols], dt, "      ")}
       %x = ktdp.load %x_acc : !ktdp.access_tile<{rblk}x{cols}xindex> -> {T16}
       %xf = arith.extf %x : {T16} to {T32}
       %sq = arith.mulf %xf, %xf : {T32}
@@ -256,7 +256,7 @@ def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8
       %wb = linalg.broadcast ins(%wf : {W32}) outs(%wb_init : {T32}) dimensions = [0]
       %yf = arith.mulf %xn, %wb : {T32}
       %y = arith.truncf %yf : {T32} to {T16}
-{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], "f16", "      ")}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [rblk, cols], [rows, cols], dt, "      ")}
       ktdp.store %y, %y_acc : {T16}, !ktdp.access_tile<{rblk}x{cols}xindex>
       scf.yield
     }}

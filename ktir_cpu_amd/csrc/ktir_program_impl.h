@@ -150,9 +150,9 @@ __device__ __forceinline__ float unop(int op, int dt, float x) {
     case KTIR_OP_LOG: r = logf(x); break;
     case KTIR_OP_LOG2: r = log2f(x); break;
     case KTIR_OP_LOG1P: r = log1pf(x); break;
-    case KTIR_OP_SQRT: r = __fsqrt_rn(x); break;
-    case KTIR_OP_RSQRT: r = (dt == KTIR_F32) ? __fdiv_rn(1.f, __fsqrt_rn(x))
-                                              : __fdiv_rn(1.f, round_to(__fsqrt_rn(x), dt)); break;
+    case KTIR_OP_SQRT: r = __builtin_sqrtf(x); break;
+    case KTIR_OP_RSQRT: r = (dt == KTIR_F32) ? __fdiv_rn(1.f, __builtin_sqrtf(x))
+                                              : __fdiv_rn(1.f, round_to(__builtin_sqrtf(x), dt)); break;
     case KTIR_OP_TANH: r = tanhf(x); break;
     case KTIR_OP_SIN: r = sinf(x); break;
     case KTIR_OP_COS: r = cosf(x); break;
@@ -345,9 +345,9 @@ __device__ __forceinline__ float unop_simple(int op, int dt, float x) {
     case KTIR_OP_NEGF: return -x;
     case KTIR_OP_ABSF: return fabsf(x);
     case KTIR_OP_EXP: r = expf(x); break;
-    case KTIR_OP_SQRT: r = __fsqrt_rn(x); break;
-    case KTIR_OP_RSQRT: r = (dt == KTIR_F32) ? __fdiv_rn(1.f, __fsqrt_rn(x))
-                                              : __fdiv_rn(1.f, round_to(__fsqrt_rn(x), dt)); break;
+    case KTIR_OP_SQRT: r = __builtin_sqrtf(x); break;
+    case KTIR_OP_RSQRT: r = (dt == KTIR_F32) ? __fdiv_rn(1.f, __builtin_sqrtf(x))
+                                              : __fdiv_rn(1.f, round_to(__builtin_sqrtf(x), dt)); break;
     case KTIR_OP_CEIL: r = ceilf(x); break;
     case KTIR_OP_FLOOR: r = floorf(x); break;
     case KTIR_OP_NOTI: return __int_as_float(__float_as_int(x) ? 0 : 1);

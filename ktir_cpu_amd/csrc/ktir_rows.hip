@@ -318,6 +318,8 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
     } else if (S.n_ops >= 1 && o[0].op == KTIR_OP_MULF && o[0].kind == 3) {
       S.head = 2;
     }
+    // so does a fold into the subtracted register
+    if (S.end == 0 && last_subexp >= 0 && S.dst == R.steps[last_subexp].ops[0].idx) last_subexp = -1;
   }
   return R.n_steps > 0;
 }
@@ -439,8 +441,8 @@ __device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, c
       case KTIR_OP_NEGF: RC_UN(-x)
       case KTIR_OP_ABSF: RC_UN(fabsf(x))
       case KTIR_OP_EXP: RC_UN(exp_hw(x))
-      case KTIR_OP_SQRT: RC_UN(__fsqrt_rn(x))
-      case KTIR_OP_RSQRT: RC_UN(__fdiv_rn(1.f, __fsqrt_rn(x)))
+      case KTIR_OP_SQRT: RC_UN(__builtin_sqrtf(x))
+      case KTIR_OP_RSQRT: RC_UN(__fdiv_rn(1.f, __builtin_sqrtf(x)))
       case KTIR_OP_CAST:
         if (o.dt == KTIR_F16) RC_UN(round_f16(x))
         if (o.dt == KTIR_BF16) RC_UN(round_bf16(x))
@@ -952,7 +954,8 @@ struct RwPos {
   int32_t idx[KTIR_MAX_DIMS - 1];
 };
 
-__device__ __forceinline__ RwPos rw_pos(const RwPlan& SP, int64_t r, int32_t rows_per_lane) {
+template <typename PL>
+__device__ __forceinline__ RwPos rw_pos(const PL& SP, int64_t r, int32_t rows_per_lane) {
   RwPos p;
   const uint32_t ru = (uint32_t)r, rpl = (uint32_t)rows_per_lane;
   const uint32_t lane = ru / rpl;
@@ -1036,7 +1039,8 @@ __device__ __forceinline__ void rw_stage_slow(const RwPlan& SP, int s, const RwP
   }
 }
 
-__device__ __forceinline__ void rw_row_exec(const RwPlan& SP, const ktir_instr_t in, RowRegs& rr, int64_t lane) {
+template <typename PL>
+__device__ __forceinline__ void rw_row_exec(const PL& SP, const ktir_instr_t in, RowRegs& rr, int64_t lane) {
   const int op = in.op;
   const float a = rr.get(in.a), b = rr.get(in.b);
   float v;
@@ -1265,6 +1269,403 @@ static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t ro
   return false;
 }
 
+// ---- fixed-form row kernels -----------------------------------------------------
+//
+// Two row programs get kernels whose passes are straight-line code; the pass
+// plan only supplies their registers, rows and the row instructions between
+// the folds:
+//   softmax:    m <- max fold of x; [row instructions]; s <- add fold of
+//               exp(x - m'); [row instructions]; y <- exp(x - m') / s'
+//               (exp(x - m') computed once and kept);
+//   norm-scale: a <- add fold of x * x; [row instructions];
+//               y <- (x * r) * w, (x * w) * r or x * r   (RMSNorm).
+// A wavefront owns a row of n = 512 NQ 16-bit elements.  Lane l holds chunk i
+// (i < NQ) as the elements 512 i + 8 l + j, j < 8, read and written as 16
+// bytes; the next row's chunks are in flight while the current row is
+// computed.  No LDS: the row's values, exp(x - m') and the weights stay in
+// registers.  The add fold follows the reference's halving tree over this
+// layout: the chunk bits in registers, the lane bits by shuffles (lanes
+// l ^ 32 .. l ^ 1), the bits of j in registers.  The max fold's result does
+// not depend on the order: the largest element, or NaN if any element is NaN.
+constexpr int RF_MAX_ROW = 8;
+enum { RF_SOFTMAX = 1, RF_NORM = 2 };
+
+struct RfPlan {
+  int32_t nd, has_w, w_first, n_row0, n_row1, pad0;
+  int64_t shape[KTIR_MAX_DIMS];
+  uint64_t lane_scalars;
+  int64_t n_lane_scalars;
+  RwLeaf x, w, y;
+  int8_t fold0, fold1;        // registers the folds write
+  int8_t m, s;                // softmax: the subtracted register and the divisor; norm-scale: s the multiplier
+  int32_t pad1;
+  ktir_instr_t row0[RF_MAX_ROW], row1[RF_MAX_ROW];   // after the first and the second fold
+};
+
+template <int DT>
+__device__ __forceinline__ void rf_unpack(const gu4 c, float (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t u = c[k];
+    if (DT == KTIR_BF16) {
+      v[2 * k] = __uint_as_float(u << 16);
+      v[2 * k + 1] = __uint_as_float(u & 0xffff0000u);
+    } else {
+      v[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+      v[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+    }
+  }
+}
+
+// eight values rounded to nearest-even in DT, packed
+template <int DT>
+__device__ __forceinline__ gu4 rf_pack(const float (&v)[8]) {
+  gu4 c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (DT == KTIR_BF16)
+      c[k] = (__float_as_uint(round_bf16(v[2 * k])) >> 16) | (__float_as_uint(round_bf16(v[2 * k + 1])) & 0xffff0000u);
+    else
+      c[k] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * k]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * k + 1]) << 16);
+  }
+  return c;
+}
+
+// the chunks of the 16-bit row at element e0 of L: 16-byte loads when the row
+// lies inside [lo, hi), else element by element (out-of-range elements read 0)
+template <int NQ>
+__device__ __forceinline__ void rf_load(const RwLeaf& L, int64_t e0, int l, gu4 (&c)[NQ]) {
+  if (e0 >= L.lo && e0 + 512 * NQ <= L.hi) {
+    const KTIR_G(uint8_t)* p = (const KTIR_G(uint8_t)*)L.ptr + 2 * e0 + 16 * l;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) c[i] = *(const KTIR_G(gu4)*)(p + 1024 * i);
+    return;
+  }
+  const KTIR_G(uint16_t)* p = (const KTIR_G(uint16_t)*)L.ptr;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t e = e0 + 512 * i + 8 * l + 2 * k;
+      const uint32_t a = (e >= L.lo && e < L.hi) ? p[e] : 0u;
+      const uint32_t b = (e + 1 >= L.lo && e + 1 < L.hi) ? p[e + 1] : 0u;
+      c[i][k] = a | (b << 16);
+    }
+  }
+}
+
+// chunk i of the row at element e0 of L: a streaming 16-byte store when the
+// row lies inside [lo, hi) (`in`), else the in-range elements only
+__device__ __forceinline__ void rf_store(const RwLeaf& L, int64_t e0, bool in, int i, int l, const gu4 c) {
+  const int64_t e = e0 + 512 * i + 8 * l;
+  if (in) {
+    __builtin_nontemporal_store(c, (KTIR_G(gu4)*)((KTIR_G(uint16_t)*)L.ptr + e));
+    return;
+  }
+  KTIR_G(uint16_t)* p = (KTIR_G(uint16_t)*)L.ptr;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (e + k >= L.lo && e + k < L.hi) p[e + k] = (uint16_t)(c[k >> 1] >> (16 * (k & 1)));
+}
+
+// add fold of the row (x * x when SQ) in the reference's halving order
+template <int NQ, bool SQ>
+__device__ __forceinline__ float rf_sum(const float (&v)[NQ][8]) {
+  auto at = [&](int i, int j) { return SQ ? __fmul_rn(v[i][j], v[i][j]) : v[i][j]; };
+  constexpr int H = NQ > 1 ? NQ / 2 : 1;
+  float t[H][8];
+#pragma unroll
+  for (int i = 0; i < H; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[i][j] = NQ > 1 ? __fadd_rn(at(i, j), at(i + H, j)) : at(i, j);
+#pragma unroll
+  for (int h = H / 2; h >= 1; h >>= 1)
+#pragma unroll
+    for (int i = 0; i < h; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[i][j] = __fadd_rn(t[i][j], t[i + h][j]);
+  float a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = t[0][j];
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = __fadd_rn(a[j], __shfl_xor(a[j], s));
+#pragma unroll
+  for (int h = 4; h >= 1; h >>= 1)
+#pragma unroll
+    for (int j = 0; j < h; ++j) a[j] = __fadd_rn(a[j], a[j + h]);
+  return a[0];
+}
+
+__device__ __forceinline__ void rf_set(RowRegs& rr, int r, float v) {
+  rr.set(r, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))));
+}
+
+template <int NQ, int DT>
+__device__ __forceinline__ void rf_softmax(const RfPlan& F, const gu4 (&c)[NQ], const RwPos& p, RowRegs& rr, int l) {
+  float v[NQ][8];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], v[i]);
+  float mx = -__builtin_inff();
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      mx = fmaxf(mx, v[i][j]);
+      nan = nan || v[i][j] != v[i][j];
+    }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
+  rf_set(rr, F.fold0, __any(nan) ? __int_as_float(0x7fc00000) : mx);
+  for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
+  const float m = rr.get(F.m);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i][j] = exp_hw(__fsub_rn(v[i][j], m));
+  rf_set(rr, F.fold1, rf_sum<NQ, false>(v));
+  for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
+  const float s = rr.get(F.s);
+  // x / s as the corrected product with the correctly rounded 1 / s; the
+  // plain quotient for huge or non-finite operands
+  const float r = __fdiv_rn(1.f, s);
+  const float as = fabsf(s);
+  float big = 0.f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) big = fmaxf(big, fabsf(v[i][j]));
+  const bool fast = as > 1e-30f && as < 1e30f && r == r && __all(big < 1e30f);
+  const int64_t e0 = rw_row_base(F.y, p);
+  const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = fast ? div_by(v[i][j], s, r) : __fdiv_rn(v[i][j], s);
+    rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
+  }
+}
+
+template <int NQ, int DT>
+__device__ __forceinline__ void rf_norm(const RfPlan& F, const gu4 (&c)[NQ], const gu4 (&wc)[NQ], const RwPos& p,
+                                        RowRegs& rr, int l) {
+  {
+    float v[NQ][8];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], v[i]);
+    rf_set(rr, F.fold0, rf_sum<NQ, true>(v));
+  }
+  for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
+  const float s = rr.get(F.s);
+  const int64_t e0 = rw_row_base(F.y, p);
+  const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
+  // the row is unpacked again from its 16-bit chunks (half the registers of
+  // keeping the f32 values)
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    float y[8], v[1][8];
+    rf_unpack<DT>(c[i], v[0]);
+    if (F.has_w) {
+      float w[8];
+      rf_unpack<DT>(wc[i], w);
+      if (F.w_first) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(v[0][j], w[j]), s);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(v[0][j], s), w[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(v[0][j], s);
+    }
+    rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
+  }
+}
+
+template <int NQ, int RECIPE, int DT>
+__device__ __forceinline__ void rf_row(const RfPlan& F, const gu4 (&c)[NQ], const gu4 (&wc)[NQ], const RwPos& p,
+                                       RowRegs& rr, int l) {
+  if (RECIPE == RF_SOFTMAX) rf_softmax<NQ, DT>(F, c, p, rr, l);
+  else rf_norm<NQ, DT>(F, c, wc, p, rr, l);
+}
+
+// Rows r = blockIdx.x + k gridDim.x, two row buffers in turn (no copy between
+// them, so the next row's loads stay in flight across the current row).
+template <int NQ, int RECIPE, int DT>
+__global__ __launch_bounds__(64) void prog_rowfix(const RfPlan F, int64_t total_rows) {
+  const int l = threadIdx.x;
+  int64_t rows_per_lane = 1;
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
+    if (d < F.nd - 1) rows_per_lane *= F.shape[d];
+  const int32_t rpl = (int32_t)rows_per_lane;
+  RowRegs rr{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t r = blockIdx.x;
+  if (r >= total_rows) return;
+  gu4 ca[NQ], cb[NQ], wc[NQ];
+  RwPos pa = rw_pos(F, r, rpl);
+  if (RECIPE == RF_NORM && F.has_w) rf_load<NQ>(F.w, rw_row_base(F.w, pa), l, wc);   // the same row for every row
+  rf_load<NQ>(F.x, rw_row_base(F.x, pa), l, ca);
+  for (;;) {
+    const int64_t rb = r + gridDim.x;
+    const RwPos pb = rw_pos(F, rb < total_rows ? rb : r, rpl);
+    if (rb < total_rows) rf_load<NQ>(F.x, rw_row_base(F.x, pb), l, cb);
+    rf_row<NQ, RECIPE, DT>(F, ca, wc, pa, rr, l);
+    if (rb >= total_rows) break;
+    r = rb + gridDim.x;
+    pa = rw_pos(F, r < total_rows ? r : rb, rpl);
+    if (r < total_rows) rf_load<NQ>(F.x, rw_row_base(F.x, pa), l, ca);
+    rf_row<NQ, RECIPE, DT>(F, cb, wc, pb, rr, l);
+    if (r >= total_rows) break;
+  }
+}
+
+template <int NQ, int RECIPE, int DT>
+static void launch_rowfix(const RfPlan& F, int64_t rows) {
+  static int resident = 0;
+  if (!resident) {
+    int per_cu = 0, cus = 0, dev = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prog_rowfix<NQ, RECIPE, DT>, 64, 0) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 || cus < 1) {
+      per_cu = 1;
+      cus = 256;
+    }
+    resident = per_cu * cus;
+  }
+  const int64_t per_block = (rows + resident - 1) / resident;
+  const int64_t blocks = (rows + per_block - 1) / per_block;
+  hipLaunchKernelGGL((prog_rowfix<NQ, RECIPE, DT>), dim3((unsigned)blocks), dim3(64), 0, stream(), F, rows);
+}
+
+template <int NQ>
+static void rowfix_dt(const RfPlan& F, int recipe, int dt, int64_t rows) {
+  if (recipe == RF_SOFTMAX) {
+    if (dt == KTIR_F16) launch_rowfix<NQ, RF_SOFTMAX, KTIR_F16>(F, rows);
+    else launch_rowfix<NQ, RF_SOFTMAX, KTIR_BF16>(F, rows);
+  } else {
+    if (dt == KTIR_F16) launch_rowfix<NQ, RF_NORM, KTIR_F16>(F, rows);
+    else launch_rowfix<NQ, RF_NORM, KTIR_BF16>(F, rows);
+  }
+}
+
+static bool rf_leaf_ok(const ktir_leaf_t& L, int nd, int dt) {
+  return rows_leaf_ok(L, nd) && L.dtype == dt && (L.flags & KTIR_LEAF_VEC8);
+}
+
+static bool rf_invariant(const ktir_prog_t& P, const ktir_leaf_t& L) {
+  bool inv = L.lane_base == 0 && L.lane_stride == 0;
+  for (int d = 0; d < P.ndim - 1; ++d) inv = inv && (L.strides[d] == 0 || P.shape[d] == 1);
+  return inv;
+}
+
+static bool rf_op(const RcOp& o, int op, int kind) { return o.op == op && o.dt == KTIR_F32 && o.kind == kind; }
+
+// Match the pass plan against the two fixed forms and launch; false leaves
+// the program to the general row kernels.
+static bool try_launch_rowfix(const ktir_prog_t& P, const RcPlan& R, int64_t rows, int64_t inner) {
+  if (inner != 512 && inner != 1024 && inner != 2048 && inner != 4096) return false;
+  if (rows > INT32_MAX) return false;
+  for (int d = 0; d < P.ndim; ++d)
+    if (P.shape[d] > INT32_MAX) return false;
+  int pass[3], n_pass = 0, gap[3] = {0, 0, 0};
+  for (int i = 0; i < R.n_steps; ++i) {
+    const RcStep& S = R.steps[i];
+    if (S.kind == 1) {
+      if (n_pass == 3) return false;
+      pass[n_pass++] = i;
+    } else if (S.kind == 0) {
+      if (n_pass == 0 || gap[n_pass - 1] == RF_MAX_ROW) return false;
+      ++gap[n_pass - 1];
+    } else {
+      return false;
+    }
+  }
+  RfPlan F{};
+  F.nd = P.ndim;
+  for (int d = 0; d < KTIR_MAX_DIMS; ++d) F.shape[d] = d < P.ndim ? P.shape[d] : 1;
+  F.lane_scalars = P.lane_scalars;
+  F.n_lane_scalars = P.n_lane_scalars;
+  auto rows_of = [&](int g, ktir_instr_t* dst) {
+    int k = 0;
+    for (int i = pass[g] + 1; i < R.n_steps && R.steps[i].kind == 0; ++i) dst[k++] = P.instr[R.steps[i].pc];
+    return k;
+  };
+  const RcStep& A = R.steps[pass[0]];
+  if (A.end != 0 || A.fold_dt != KTIR_F32) return false;
+  const int sx = A.src;
+  const ktir_leaf_t& X = P.leaves[R.slot_leaf[sx]];
+  const int dt = X.dtype;
+  if ((dt != KTIR_F16 && dt != KTIR_BF16) || !rf_leaf_ok(X, P.ndim, dt)) return false;
+  F.x = rw_leaf(P, R.slot_leaf[sx]);
+  const RcStep& Z = R.steps[pass[n_pass - 1]];   // the storing pass
+  if (Z.end != 1 || Z.src != sx || !rf_leaf_ok(P.leaves[Z.st_leaf], P.ndim, dt) || gap[n_pass - 1] != 0) return false;
+  F.y = rw_leaf(P, Z.st_leaf);
+  // an optional last rounding to the stored dtype (the store rounds the same way)
+  auto tail = [&](const RcStep& S, int n) {
+    return S.n_ops == n || (S.n_ops == n + 1 && S.ops[n].op == KTIR_OP_CAST && S.ops[n].kind == 0 &&
+                            S.ops[n].aux == KTIR_F32 && S.ops[n].dt == dt);
+  };
+  int recipe;
+  if (n_pass == 3) {
+    const RcStep& B = R.steps[pass[1]];
+    if (R.n_slots != 1 || A.n_ops != 0 || A.fold_op != KTIR_OP_MAXIMUMF) return false;
+    if (B.src != sx || B.end != 0 || B.n_ops != 2 || B.fold_op != KTIR_OP_ADDF || B.fold_dt != KTIR_F32) return false;
+    if (!rf_op(B.ops[0], KTIR_OP_SUBF, 1) || B.ops[0].swap || !rf_op(B.ops[1], KTIR_OP_EXP, 0)) return false;
+    if (!tail(Z, 3) || !rf_op(Z.ops[0], KTIR_OP_SUBF, 1) || Z.ops[0].swap || Z.ops[0].idx != B.ops[0].idx ||
+        !rf_op(Z.ops[1], KTIR_OP_EXP, 0) || !rf_op(Z.ops[2], KTIR_OP_DIVF, 1) || Z.ops[2].swap)
+      return false;
+    // exp(x - m') is computed once: m' must hold the same value in both passes
+    const int m = B.ops[0].idx;
+    if (B.dst == m) return false;
+    F.n_row1 = rows_of(1, F.row1);
+    for (int k = 0; k < F.n_row1; ++k)
+      if (F.row1[k].dst == m) return false;
+    F.fold1 = B.dst;
+    F.m = (int8_t)m;
+    F.s = Z.ops[2].idx;
+    recipe = RF_SOFTMAX;
+  } else if (n_pass == 2) {
+    if (A.n_ops != 1 || !rf_op(A.ops[0], KTIR_OP_MULF, 3) || A.fold_op != KTIR_OP_ADDF) return false;
+    const RcOp* o = Z.ops;
+    if (tail(Z, 1) && rf_op(o[0], KTIR_OP_MULF, 1)) {
+      F.s = o[0].idx;
+    } else if (tail(Z, 2) && rf_op(o[0], KTIR_OP_MULF, 1) && rf_op(o[1], KTIR_OP_MULF, 2) && o[1].idx != sx) {
+      F.s = o[0].idx;
+      F.has_w = 1;
+    } else if (tail(Z, 2) && rf_op(o[0], KTIR_OP_MULF, 2) && rf_op(o[1], KTIR_OP_MULF, 1) && o[0].idx != sx) {
+      F.s = o[1].idx;
+      F.has_w = 1;
+      F.w_first = 1;
+    } else {
+      return false;
+    }
+    if (R.n_slots != 1 + F.has_w) return false;
+    if (F.has_w) {
+      const ktir_leaf_t& W = P.leaves[R.slot_leaf[1 - sx]];
+      if (!rf_leaf_ok(W, P.ndim, dt) || !rf_invariant(P, W)) return false;
+      F.w = rw_leaf(P, R.slot_leaf[1 - sx]);
+    }
+    recipe = RF_NORM;
+  } else {
+    return false;
+  }
+  F.fold0 = A.dst;
+  F.n_row0 = rows_of(0, F.row0);
+  switch (inner / 512) {
+    case 1: rowfix_dt<1>(F, recipe, dt, rows); break;
+    case 2: rowfix_dt<2>(F, recipe, dt, rows); break;
+    case 4: rowfix_dt<4>(F, recipe, dt, rows); break;
+    default: rowfix_dt<8>(F, recipe, dt, rows); break;
+  }
+  return true;
+}
+
 // Launch `P` (mode 1) through the row-chain kernel if it has the supported form.
 bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
   if (P.mode != 1 || inner < 64 || inner > 8192 || (inner & (inner - 1))) return false;
@@ -1274,6 +1675,7 @@ bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
   }
   RcPlan R;
   if (!analyze_rows(P, R)) return false;
+  if (try_launch_rowfix(P, R, rows, inner)) return true;
   if (try_launch_rowwave(P, R, rows, inner)) return true;
   // threads per row and elements per thread: n = tpr * E, E in {2..32}, tpr in {32..256}
   int tpr = (int)(inner / 16);

@@ -27,17 +27,27 @@ def gather_scatter_add(rows=1024, dim=32, n_idx=512, cores=4, chunk=32, seed=42,
             dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((rows, dim), np.float32)))
 
 
-def softmax(rows=64, cols=256, cores=8, rblk=4, seed=42):
-    rng = np.random.default_rng(seed)
-    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float16)
-    return configs.softmax(rows, cols, cores, rblk), "softmax_kernel", dict(x_ptr=x, y_ptr=np.zeros_like(x))
+def _half(x, dt):
+    """f32 values as the element type's storage: f16 values, or bf16 bit patterns."""
+    return x.astype(np.float16) if dt == "f16" else bf16_bits(x.astype(np.float32))
 
 
-def rmsnorm(rows=64, cols=256, cores=8, rblk=4, seed=42):
+def softmax(rows=64, cols=256, cores=8, rblk=4, seed=42, dt="f16"):
     rng = np.random.default_rng(seed)
-    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float16)
-    w = rng.uniform(0.5, 1.5, cols).astype(np.float16)
-    return (configs.rmsnorm(rows, cols, cores, rblk), "rmsnorm_kernel",
+    x = _half(rng.standard_normal((rows, cols)) * 2, dt)
+    return configs.softmax(rows, cols, cores, rblk, dt), "softmax_kernel", dict(x_ptr=x, y_ptr=np.zeros_like(x))
+
+
+def rmsnorm(rows=64, cols=256, cores=8, rblk=4, seed=42, dt="f16", wide=False):
+    """`wide`: magnitudes spread over eight decades, so that the order of the
+    sum of squares shows in the result bits."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)) * 2
+    if wide:
+        x = x * 10.0 ** rng.uniform(-4, 3.5, (rows, cols))
+    x = _half(x, dt)
+    w = _half(rng.uniform(0.5, 1.5, cols), dt)
+    return (configs.rmsnorm(rows, cols, cores, rblk, dt), "rmsnorm_kernel",
             dict(x_ptr=x, w_ptr=w, y_ptr=np.zeros_like(x), eps=1e-6))
 
 
@@ -99,3 +109,37 @@ def row_reduce(rows=32, cols=4096, rblk=4, combiner="arith.addf", dt="f32", seed
 }}
 """
     return src, "row_reduce", dict(x_ptr=x, y_ptr=np.zeros(rows, x.dtype))
+
+
+def unary_f32(op="math.sqrt", n=1 << 14, block=512, cores=32, seed=11):
+    """out = op(x) on f32 values spread over many decades (x > 0)."""
+    rng = np.random.default_rng(seed)
+    x = (10.0 ** rng.uniform(-30, 30, n)).astype(np.float32)
+    bpc = n // (cores * block)
+    assert bpc * cores * block == n
+    T = configs._t([block], "f32")
+    src = f"""module {{
+  func.func @unary_kernel(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %bpc = arith.constant {bpc} : index
+    %B = arith.constant {block} : index
+{configs._view("x_view", "x_ptr", [n], [1], "f32")}
+{configs._view("y_view", "y_ptr", [n], [1], "f32")}
+    %first = arith.muli %core_id, %bpc : index
+    scf.for %b = %c0 to %bpc step %c1 : index {{
+      %blk = arith.addi %first, %b : index
+      %off = arith.muli %blk, %B : index
+{configs._tile("x_tile", "x_view", ["%off"], [block], [n], "f32", "      ")}
+      %x = ktdp.load %x_tile : !ktdp.access_tile<{block}xindex> -> {T}
+      %y = {op} %x : {T}
+{configs._tile("y_tile", "y_view", ["%off"], [block], [n], "f32", "      ")}
+      ktdp.store %y, %y_tile : {T}, !ktdp.access_tile<{block}xindex>
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+    return src, "unary_kernel", dict(x_ptr=x, y_ptr=np.zeros_like(x))

@@ -62,6 +62,38 @@ def test_rmsnorm(cols):
     np.testing.assert_allclose(out["y_ptr"].astype(np.float32), ref["y_ptr"].astype(np.float32), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("op", ["math.sqrt", "math.rsqrt"])
+def test_sqrt_rsqrt_bit_exact(op):
+    """f32 sqrt is correctly rounded (as NumPy's) and rsqrt is 1 / sqrt(x) with
+    two correct roundings, over thirty decades either side of 1."""
+    ref, out, _ = _run(_cases.unary_f32(op))
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
+def _half_f32(x, dt):
+    return bf16_from_bits(x) if dt == "bf16" else x.astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096])
+def test_softmax_fixed_form(cols, dt):
+    """Softmax rows of 512 .. 4096 elements (the fixed-form row kernel), f16 and bf16."""
+    ref, out, g = _run(_cases.softmax(rows=48, cols=cols, cores=4, dt=dt))
+    assert g.last_plan.counts() == {"prog": 1}
+    np.testing.assert_allclose(_half_f32(out["y_ptr"], dt), _half_f32(ref["y_ptr"], dt), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096])
+def test_rmsnorm_bit_exact(cols, dt):
+    """RMSNorm with magnitudes over eight decades: every step is a correctly
+    rounded f32 operation and the sum of squares follows the reference's
+    halving order, so the results match bit for bit."""
+    ref, out, g = _run(_cases.rmsnorm(rows=48, cols=cols, cores=4, dt=dt, wide=True))
+    assert g.last_plan.counts() == {"prog": 1}
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
 @pytest.mark.parametrize("cols", [64, 256, 1024, 4096, 8192, 96, 3000])
 @pytest.mark.parametrize("combiner", ["arith.addf", "arith.maximumf"])
 def test_row_reduce_bit_exact(cols, combiner):
