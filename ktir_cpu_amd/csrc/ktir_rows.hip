@@ -1039,8 +1039,8 @@ __device__ __forceinline__ void rw_stage_slow(const RwPlan& SP, int s, const RwP
   }
 }
 
-template <typename PL>
-__device__ __forceinline__ void rw_row_exec(const PL& SP, const ktir_instr_t in, RowRegs& rr, int64_t lane) {
+template <typename PL, typename RR>
+__device__ __forceinline__ void rw_row_exec(const PL& SP, const ktir_instr_t in, RR& rr, int64_t lane) {
   const int op = in.op;
   const float a = rr.get(in.a), b = rr.get(in.b);
   float v;
@@ -1369,16 +1369,29 @@ __device__ __forceinline__ void rf_store(const RwLeaf& L, int64_t e0, bool in, i
     if (e + k >= L.lo && e + k < L.hi) p[e + k] = (uint16_t)(c[k >> 1] >> (16 * (k & 1)));
 }
 
-// add fold of the row (x * x when SQ) in the reference's halving order
-template <int NQ, bool SQ>
-__device__ __forceinline__ float rf_sum(const float (&v)[NQ][8]) {
-  auto at = [&](int i, int j) { return SQ ? __fmul_rn(v[i][j], v[i][j]) : v[i][j]; };
+// add fold in the reference's halving order of the row's values, which
+// get(i, v) produces for chunk i
+template <int NQ, typename G>
+__device__ __forceinline__ float rf_sum(G get) {
   constexpr int H = NQ > 1 ? NQ / 2 : 1;
   float t[H][8];
 #pragma unroll
-  for (int i = 0; i < H; ++i)
+  for (int i = 0; i < H; ++i) {
+    float a[8];
+    get(i, a);
+    if (NQ > 1) {
+      float b[8];
+      get(i + H, b);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[i][j] = NQ > 1 ? __fadd_rn(at(i, j), at(i + H, j)) : at(i, j);
+      for (int j = 0; j < 8; ++j) t[i][j] = __fadd_rn(a[j], b[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[i][j] = a[j];
+    }
+    // one chunk pair at a time: the values of all chunks at once would
+    // take more registers than the row itself
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int h = H / 2; h >= 1; h >>= 1)
 #pragma unroll
@@ -1399,128 +1412,167 @@ __device__ __forceinline__ float rf_sum(const float (&v)[NQ][8]) {
   return a[0];
 }
 
-__device__ __forceinline__ void rf_set(RowRegs& rr, int r, float v) {
-  rr.set(r, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))));
+// Row registers in lanes 0..7 of one vector register: a read is one lane
+// access and a write one lane select, with no selection over the register
+// number.
+struct RowLanes {
+  int v, lane;
+  __device__ __forceinline__ float get(int i) const { return __int_as_float(__builtin_amdgcn_readlane(v, i)); }
+  __device__ __forceinline__ void set(int i, float x) {
+    const int u = __builtin_amdgcn_readfirstlane(__float_as_int(x));
+    v = lane == i ? u : v;
+  }
+};
+
+// An empty statement that the compiler must assume rewrites the chunks: the
+// row is unpacked again in each pass from its 16-bit chunks instead of being
+// kept as f32 values (twice the registers) between the passes.
+template <int NQ>
+__device__ __forceinline__ void rf_fence(gu4 (&c)[NQ]) {
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t u = c[i][k];
+      asm volatile("" : "+v"(u));
+      c[i][k] = u;
+    }
 }
 
 template <int NQ, int DT>
-__device__ __forceinline__ void rf_softmax(const RfPlan& F, const gu4 (&c)[NQ], const RwPos& p, RowRegs& rr, int l) {
-  float v[NQ][8];
-#pragma unroll
-  for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], v[i]);
+__device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const RwPos& p, RowLanes& rr, int l) {
   float mx = -__builtin_inff();
   bool nan = false;
 #pragma unroll
-  for (int i = 0; i < NQ; ++i)
+  for (int i = 0; i < NQ; ++i) {
+    float v[8];
+    rf_unpack<DT>(c[i], v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      mx = fmaxf(mx, v[i][j]);
-      nan = nan || v[i][j] != v[i][j];
+      mx = fmaxf(mx, v[j]);
+      nan = nan || v[j] != v[j];
     }
+  }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
-  rf_set(rr, F.fold0, __any(nan) ? __int_as_float(0x7fc00000) : mx);
+  rr.set(F.fold0, __any(nan) ? __int_as_float(0x7fc00000) : mx);
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float m = rr.get(F.m);
+  rf_fence<NQ>(c);
+  // exp(x - m') is computed the same way in both passes
+  float big = 0.f;
+  const float sum = rf_sum<NQ>([&](int i, float (&e)[8]) {
+    rf_unpack<DT>(c[i], e);
 #pragma unroll
-  for (int i = 0; i < NQ; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = exp_hw(__fsub_rn(v[i][j], m));
-  rf_set(rr, F.fold1, rf_sum<NQ, false>(v));
+    for (int j = 0; j < 8; ++j) {
+      e[j] = exp_hw(__fsub_rn(e[j], m));
+      big = fmaxf(big, fabsf(e[j]));
+    }
+  });
+  rr.set(F.fold1, sum);
   for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
   const float s = rr.get(F.s);
   // x / s as the corrected product with the correctly rounded 1 / s; the
   // plain quotient for huge or non-finite operands
   const float r = __fdiv_rn(1.f, s);
   const float as = fabsf(s);
-  float big = 0.f;
-#pragma unroll
-  for (int i = 0; i < NQ; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) big = fmaxf(big, fabsf(v[i][j]));
   const bool fast = as > 1e-30f && as < 1e30f && r == r && __all(big < 1e30f);
   const int64_t e0 = rw_row_base(F.y, p);
   const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
+  rf_fence<NQ>(c);
+  // the two divisions on separate (uniform) branches: one per launch of code
+  auto out = [&](auto div) {
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    float y[8];
+    for (int i = 0; i < NQ; ++i) {
+      float y[8];
+      rf_unpack<DT>(c[i], y);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = fast ? div_by(v[i][j], s, r) : __fdiv_rn(v[i][j], s);
-    rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
-  }
+      for (int j = 0; j < 8; ++j) y[j] = div(exp_hw(__fsub_rn(y[j], m)));
+      rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (fast) out([&](float e) { return div_by(e, s, r); });
+  else out([&](float e) { return __fdiv_rn(e, s); });
 }
 
+// w: the weight row in LDS (lane l's own 16-byte pieces, at 1024 i + 16 l)
 template <int NQ, int DT>
-__device__ __forceinline__ void rf_norm(const RfPlan& F, const gu4 (&c)[NQ], const gu4 (&wc)[NQ], const RwPos& p,
-                                        RowRegs& rr, int l) {
-  {
-    float v[NQ][8];
+__device__ __forceinline__ void rf_norm(const RfPlan& F, gu4 (&c)[NQ], const gu4* w, const RwPos& p, RowLanes& rr,
+                                        int l) {
+  rr.set(F.fold0, rf_sum<NQ>([&](int i, float (&v)[8]) {
+    rf_unpack<DT>(c[i], v);
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], v[i]);
-    rf_set(rr, F.fold0, rf_sum<NQ, true>(v));
-  }
+    for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(v[j], v[j]);
+  }));
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float s = rr.get(F.s);
   const int64_t e0 = rw_row_base(F.y, p);
   const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
-  // the row is unpacked again from its 16-bit chunks (half the registers of
-  // keeping the f32 values)
+  rf_fence<NQ>(c);
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
-    float y[8], v[1][8];
-    rf_unpack<DT>(c[i], v[0]);
+    float y[8];
+    rf_unpack<DT>(c[i], y);
     if (F.has_w) {
-      float w[8];
-      rf_unpack<DT>(wc[i], w);
+      float wv[8];
+      rf_unpack<DT>(w[64 * i + l], wv);
       if (F.w_first) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(v[0][j], w[j]), s);
+        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(y[j], wv[j]), s);
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(v[0][j], s), w[j]);
+        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(y[j], s), wv[j]);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(v[0][j], s);
+      for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(y[j], s);
     }
     rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
 template <int NQ, int RECIPE, int DT>
-__device__ __forceinline__ void rf_row(const RfPlan& F, const gu4 (&c)[NQ], const gu4 (&wc)[NQ], const RwPos& p,
-                                       RowRegs& rr, int l) {
+__device__ __forceinline__ void rf_row(const RfPlan& F, gu4 (&c)[NQ], const gu4* w, const RwPos& p, RowLanes& rr,
+                                       int l) {
   if (RECIPE == RF_SOFTMAX) rf_softmax<NQ, DT>(F, c, p, rr, l);
-  else rf_norm<NQ, DT>(F, c, wc, p, rr, l);
+  else rf_norm<NQ, DT>(F, c, w, p, rr, l);
 }
 
 // Rows r = blockIdx.x + k gridDim.x, two row buffers in turn (no copy between
 // them, so the next row's loads stay in flight across the current row).
 template <int NQ, int RECIPE, int DT>
 __global__ __launch_bounds__(64) void prog_rowfix(const RfPlan F, int64_t total_rows) {
+  __shared__ gu4 w[RECIPE == RF_NORM ? 64 * NQ : 1];
   const int l = threadIdx.x;
   int64_t rows_per_lane = 1;
 #pragma unroll
   for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
     if (d < F.nd - 1) rows_per_lane *= F.shape[d];
   const int32_t rpl = (int32_t)rows_per_lane;
-  RowRegs rr{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  RowLanes rr{0, l};
   int64_t r = blockIdx.x;
   if (r >= total_rows) return;
-  gu4 ca[NQ], cb[NQ], wc[NQ];
+  gu4 ca[NQ], cb[NQ];
   RwPos pa = rw_pos(F, r, rpl);
-  if (RECIPE == RF_NORM && F.has_w) rf_load<NQ>(F.w, rw_row_base(F.w, pa), l, wc);   // the same row for every row
+  if (RECIPE == RF_NORM && F.has_w) {
+    // the same row for every row; each lane reads back only what it wrote
+    rf_load<NQ>(F.w, rw_row_base(F.w, pa), l, ca);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) w[64 * i + l] = ca[i];
+  }
   rf_load<NQ>(F.x, rw_row_base(F.x, pa), l, ca);
   for (;;) {
     const int64_t rb = r + gridDim.x;
     const RwPos pb = rw_pos(F, rb < total_rows ? rb : r, rpl);
     if (rb < total_rows) rf_load<NQ>(F.x, rw_row_base(F.x, pb), l, cb);
-    rf_row<NQ, RECIPE, DT>(F, ca, wc, pa, rr, l);
+    rf_row<NQ, RECIPE, DT>(F, ca, w, pa, rr, l);
     if (rb >= total_rows) break;
     r = rb + gridDim.x;
     pa = rw_pos(F, r < total_rows ? r : rb, rpl);
     if (r < total_rows) rf_load<NQ>(F.x, rw_row_base(F.x, pa), l, ca);
-    rf_row<NQ, RECIPE, DT>(F, cb, wc, pb, rr, l);
+    rf_row<NQ, RECIPE, DT>(F, cb, w, pb, rr, l);
     if (r >= total_rows) break;
   }
 }
