@@ -1452,6 +1452,7 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
       mx = fmaxf(mx, v[j]);
       nan = nan || v[j] != v[j];
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
@@ -1492,8 +1493,17 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  if (fast) out([&](float e) { return div_by(e, s, r); });
-  else out([&](float e) { return __fdiv_rn(e, s); });
+  if (fast) {
+    out([&](float e) { return div_by(e, s, r); });
+  } else {
+    // rare (huge or non-finite operands): one quotient at a time, so that
+    // this branch does not set the kernel's register count
+    out([&](float e) {
+      const float q = __fdiv_rn(e, s);
+      __builtin_amdgcn_sched_barrier(0);
+      return q;
+    });
+  }
 }
 
 // w: the weight row in LDS (lane l's own 16-byte pieces, at 1024 i + 16 l)
