@@ -1460,15 +1460,21 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float m = rr.get(F.m);
   rf_fence<NQ>(c);
-  // exp(x - m') is computed the same way in both passes
+  // exp(x - m'), kept for the store pass
+  float ev[NQ][8];
   float big = 0.f;
-  const float sum = rf_sum<NQ>([&](int i, float (&e)[8]) {
-    rf_unpack<DT>(c[i], e);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    rf_unpack<DT>(c[i], ev[i]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      e[j] = exp_hw(__fsub_rn(e[j], m));
-      big = fmaxf(big, fabsf(e[j]));
+      ev[i][j] = exp_hw(__fsub_rn(ev[i][j], m));
+      big = fmaxf(big, fabsf(ev[i][j]));
     }
+  }
+  const float sum = rf_sum<NQ>([&](int i, float (&e)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = ev[i][j];
   });
   rr.set(F.fold1, sum);
   for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
@@ -1480,15 +1486,13 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   const bool fast = as > 1e-30f && as < 1e30f && r == r && __all(big < 1e30f);
   const int64_t e0 = rw_row_base(F.y, p);
   const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
-  rf_fence<NQ>(c);
-  // the two divisions on separate (uniform) branches: one per launch of code
+  // the two divisions on separate (uniform) branches
   auto out = [&](auto div) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       float y[8];
-      rf_unpack<DT>(c[i], y);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = div(exp_hw(__fsub_rn(y[j], m)));
+      for (int j = 0; j < 8; ++j) y[j] = div(ev[i][j]);
       rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
       __builtin_amdgcn_sched_barrier(0);
     }
