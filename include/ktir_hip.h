@@ -202,6 +202,11 @@ typedef struct ktir_prog {
 /* ---- runtime (reference: interpreter.py:95-120 builds the simulated HBM) ---- */
 const char* ktir_last_error(void);
 int ktir_init(int device);
+/* Waits for the library stream, then releases what ktir_init and later calls
+ * created (stream, device error flag); device buffers from ktir_malloc stay
+ * the caller's.  A later ktir_init starts over.  The reference has no teardown
+ * (its HBM is garbage collected); this is the C side's end of a session. */
+int ktir_shutdown(void);
 int ktir_device_info(int* cu_count, int* clock_khz, int64_t* hbm_bytes, char* name, int name_len);
 int ktir_malloc(uint64_t bytes, uint64_t* dptr);
 int ktir_free(uint64_t dptr);
@@ -226,6 +231,12 @@ int ktir_event_destroy(uint64_t ev);
  * The descriptor travels by value in the kernel arguments (no host-device
  * copy per launch), so launches stay asynchronous on the library stream. */
 int ktir_launch_program(const ktir_prog_t* prog);
+/* Upper bound on the workgroups of one row-program launch (0, the default:
+ * as many as the device holds at once, or one per row).  The row kernels
+ * stride their workgroups over the rows, so results do not depend on it; a
+ * small bound makes every workgroup run many rows (used by tests to cover
+ * that path at small sizes).  No reference counterpart: a launch-shape knob. */
+int ktir_set_row_grid_limit(int64_t max_workgroups);
 
 /* ---- last-writer-wins scatter support ----
  * Reference memory.py:281-291 writes duplicates in enumeration order, so the
@@ -309,6 +320,13 @@ typedef struct ktir_rmw {
   uint64_t srcs;           /* int32_t [n_inst * K] scratch: source row of each entry */
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
+/* Which apply kernel ktir_launch_row_rmw takes for `d` (host-only, launches
+ * nothing): KTIR_RMW_ROWS, the destination-row-order kernel (f32 rows, f16 or
+ * f32 sources, unit column stride, 16-byte aligned rows of a multiple of 128
+ * columns), or KTIR_RMW_GENERIC; a negative KTIR_E_* code for a bad descriptor. */
+#define KTIR_RMW_GENERIC 0
+#define KTIR_RMW_ROWS 1
+int ktir_rmw_variant(const ktir_rmw_t* d);
 
 /* ---- fused online-softmax attention loop ----
  * Replaces a whole KV `scf.for` of the flash-attention form (the reference's

@@ -243,6 +243,7 @@ using namespace ktir;
 namespace ktir {
 bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner);
 bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner);
+int64_t row_grid_limit(int64_t blocks);
 }
 
 extern "C" int ktir_launch_program(const ktir_prog_t* P) {
@@ -325,7 +326,7 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
       KTIR_HIP_CHECK(hipGetLastError());
       return KTIR_OK;
     }
-    int64_t blocks = rows < 65536 ? rows : 65536;
+    int64_t blocks = row_grid_limit(rows < 65536 ? rows : 65536);
     int64_t per = v4 ? inner / 4 : inner;
     int threads = per >= 256 ? 256 : (int)((per + 63) / 64 * 64);
     if (v4)

@@ -239,10 +239,29 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d) {
   for (int i = half; i < n; i += 2) {
     const int4 it = items[wv][i];
     const int64_t de = d.dst_base + (int64_t)it.x * d.dst_row;
+    const int64_t se = d.src_base + (int64_t)it.w * d.src_row;
+    // a source row outside its allocation (index past the table, or a
+    // negative index that the host reports after the launch) reads zeros and
+    // a destination row that ends past its allocation drops the columns
+    // there (memory.py:243-305): such rows take the per-element path
+    if (!(de >= 0 && de + d.D <= d.dst_hi && se >= 0 && se + d.D <= d.src_hi)) {
+      for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
+        float x[4], g[4];
+        load4(d, true, de + c, c, true, x);
+        if (it.z == -1) {
+          load4(d, false, se + c, c, true, g);
+          for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[q]);
+        } else {
+          apply_chain(d, it.y, de, c, true, x);
+        }
+        store4(d, de + c, c, true, x);
+      }
+      continue;
+    }
     for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
       const gf4 v = *(const KTIR_G(gf4)*)(dst + de + c);
       float g[4];
-      rmw_src4<SDT>(d, d.src_base + (int64_t)it.w * d.src_row + c, g);
+      rmw_src4<SDT>(d, se + c, g);
       float x[4] = {v[0], v[1], v[2], v[3]};
       if (it.z == -1) {   // the head entry was also the chain's first: one entry
         for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[q]);
@@ -258,20 +277,38 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d) {
 
 using namespace ktir;
 
-extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
+static int rmw_check(const ktir_rmw_t* d, const char* who) {
   if (!d || d->K < 1 || d->K > RMW_MAXK || d->D < 1 || d->n_inst < 0)
-    return set_error(KTIR_E_ARG, "ktir_launch_row_rmw: bad descriptor");
+    return set_error(KTIR_E_ARG, "%s: bad descriptor", who);
   if (d->n_inst * d->K >= (int64_t)0x7fffffff || d->n_rows >= (int64_t)0x7fffffff)
-    return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_row_rmw: too many entries");
+    return set_error(KTIR_E_UNSUPPORTED, "%s: too many entries", who);
+  return KTIR_OK;
+}
+
+// The row-order apply kernel takes f32 destination rows, f16 / f32 source
+// rows with unit column stride, positive row strides and 16-byte aligned
+// rows of a multiple of 128 columns; everything else takes rmw_apply.
+static bool rmw_rows_form(const ktir_rmw_t* d) {
+  return d->dst_col == 1 && d->src_col == 1 && d->dst_dtype == KTIR_F32 && d->dt == KTIR_F32 &&
+         (d->src_dtype == KTIR_F16 || d->src_dtype == KTIR_F32) && d->D % 128 == 0 && d->dst_row > 0 &&
+         d->src_row >= 0 && d->dst_base % 4 == 0 && d->dst_row % 4 == 0 && d->src_base % 4 == 0 &&
+         d->src_row % 4 == 0 && d->dst_ptr % 16 == 0 && d->src_ptr % 16 == 0;
+}
+
+extern "C" int ktir_rmw_variant(const ktir_rmw_t* d) {
+  const int rc = rmw_check(d, "ktir_rmw_variant");
+  if (rc != KTIR_OK) return rc;
+  return rmw_rows_form(d) ? KTIR_RMW_ROWS : KTIR_RMW_GENERIC;
+}
+
+extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
+  const int rc = rmw_check(d, "ktir_launch_row_rmw");
+  if (rc != KTIR_OK) return rc;
   if (d->n_inst == 0) return KTIR_OK;
   int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());
   const int64_t total = d->n_inst * d->K;
-  const bool vec = d->dst_col == 1 && d->src_col == 1 && d->dst_dtype == KTIR_F32 && d->dt == KTIR_F32 &&
-                   (d->src_dtype == KTIR_F16 || d->src_dtype == KTIR_F32) && d->D % 128 == 0 &&
-                   d->dst_base % 4 == 0 && d->dst_row % 4 == 0 && d->src_base % 4 == 0 && d->src_row % 4 == 0 &&
-                   d->dst_ptr % 16 == 0 && d->src_ptr % 16 == 0;
-  if (vec) {
+  if (rmw_rows_form(d)) {
     const int64_t blocks = (d->n_rows + 255) / 256;
     if (d->src_dtype == KTIR_F16)
       hipLaunchKernelGGL(rmw_apply_rows<KTIR_F16>, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);

@@ -1158,6 +1158,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(rw_waves<K, 
   }
 }
 
+// Upper bound on the workgroups of a row-kernel launch (0: none).  Every row
+// kernel strides its workgroups over the rows, so any bound gives the same
+// results; a small one makes each workgroup run many rows.
+static int64_t g_row_grid_limit = 0;
+
+int64_t row_grid_limit(int64_t blocks) {
+  return g_row_grid_limit > 0 && blocks > g_row_grid_limit ? g_row_grid_limit : blocks;
+}
+
 // One resident wavefront per row stream: as many workgroups as the device
 // holds at once (so no second, partial round of workgroups), each taking an
 // equal share of the rows.
@@ -1176,7 +1185,7 @@ static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows) {
     cached_lds = lds_bytes;
   }
   const int64_t per_block = (rows + cached_resident - 1) / cached_resident;
-  const int64_t blocks = (rows + per_block - 1) / per_block;
+  const int64_t blocks = row_grid_limit((rows + per_block - 1) / per_block);
   hipLaunchKernelGGL((prog_rowwave<K, NQ>), dim3((unsigned)blocks), dim3(64), lds_bytes, stream(), W, rows);
 }
 
@@ -1605,7 +1614,7 @@ static void launch_rowfix(const RfPlan& F, int64_t rows) {
     resident = per_cu * cus;
   }
   const int64_t per_block = (rows + resident - 1) / resident;
-  const int64_t blocks = (rows + per_block - 1) / per_block;
+  const int64_t blocks = row_grid_limit((rows + per_block - 1) / per_block);
   hipLaunchKernelGGL((prog_rowfix<NQ, RECIPE, DT>), dim3((unsigned)blocks), dim3(64), 0, stream(), F, rows);
 }
 
@@ -1754,6 +1763,7 @@ bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
   const int rpw = 256 / tpr;
   int64_t blocks = (rows + rpw - 1) / rpw;
   if (blocks > 65536) blocks = 65536;
+  blocks = row_grid_limit(blocks);
   switch (E) {
     case 2: hipLaunchKernelGGL(prog_rowchain<2>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
     case 4: hipLaunchKernelGGL(prog_rowchain<4>, dim3((unsigned)blocks), dim3(256), 0, stream(), P, R, tpr_log2, rows); break;
@@ -1766,3 +1776,9 @@ bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
 }
 
 }  // namespace ktir
+
+extern "C" int ktir_set_row_grid_limit(int64_t max_workgroups) {
+  if (max_workgroups < 0) return ktir::set_error(KTIR_E_ARG, "ktir_set_row_grid_limit: negative limit");
+  ktir::g_row_grid_limit = max_workgroups;
+  return KTIR_OK;
+}

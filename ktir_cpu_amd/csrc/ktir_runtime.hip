@@ -46,6 +46,17 @@ extern "C" int ktir_init(int device) {
   return KTIR_OK;
 }
 
+extern "C" int ktir_shutdown(void) {
+  if (!g_stream) return KTIR_OK;
+  KTIR_HIP_CHECK(hipStreamSynchronize(g_stream));
+  KTIR_HIP_CHECK(hipFree(g_err_flag));
+  KTIR_HIP_CHECK(hipStreamDestroy(g_stream));
+  g_err_flag = nullptr;
+  g_stream = nullptr;
+  g_device = -1;
+  return KTIR_OK;
+}
+
 extern "C" int ktir_device_info(int* cu_count, int* clock_khz, int64_t* hbm_bytes, char* name, int name_len) {
   hipDeviceProp_t p;
   int dev = g_device < 0 ? 0 : g_device;

@@ -435,6 +435,19 @@ class Plan:
             out[kind] = out.get(kind, 0) + 1
         return out
 
+    def rmw_variants(self) -> List[str]:
+        """The apply kernel of each ordered row RMW launch ("rows" or "generic")."""
+        import ctypes as C
+        names = {rt.K["KTIR_RMW_ROWS"]: "rows", rt.K["KTIR_RMW_GENERIC"]: "generic"}
+        out = []
+        for kind, desc, _ in self.launches:
+            if kind == "rmw":
+                v = rt.lib().ktir_rmw_variant(C.byref(desc))
+                if v < 0:
+                    rt.check(v, "ktir_rmw_variant")
+                out.append(names[v])
+        return out
+
 
 def _launch(L, kind, desc):
     import ctypes as C

@@ -327,6 +327,8 @@ def _row_rmw(ex, op, lb, st, trips):
     ex.log(ad, True, z, (1,), (1,), whole=True, group=grp)
     ex.log(as_, False, z, (1,), (1,), whole=True, group=grp)
     ex.log(ia_d, False, z, (1,), (1,), whole=True, group=grp)
+    if ia_s is not ia_d:
+        ex.log(ia_s, False, z, (1,), (1,), whole=True, group=grp)
     ex.launch("rmw", d, keep)
     return []
 

@@ -141,7 +141,7 @@ def lib():
                      "ktir_launch_program", "ktir_scatter_winners", "ktir_iat_offsets",
                      "ktir_launch_matmul", "ktir_event_create", "ktir_event_record",
                      "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info",
-                     "ktir_launch_row_rmw", "ktir_launch_attention"):
+                     "ktir_launch_row_rmw", "ktir_launch_attention", "ktir_rmw_variant", "ktir_shutdown", "ktir_set_row_grid_limit"):
             getattr(L, name).restype = C.c_int
         L.ktir_malloc.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.ktir_free.argtypes = [C.c_uint64]
@@ -154,6 +154,8 @@ def lib():
         L.ktir_iat_offsets.argtypes = [C.POINTER(IAT)]
         L.ktir_launch_matmul.argtypes = [C.POINTER(MM)]
         L.ktir_launch_row_rmw.argtypes = [C.POINTER(RMW)]
+        L.ktir_rmw_variant.argtypes = [C.POINTER(RMW)]
+        L.ktir_set_row_grid_limit.argtypes = [C.c_int64]
         L.ktir_launch_attention.argtypes = [C.POINTER(ATTN)]
         L.ktir_event_create.argtypes = [C.POINTER(C.c_uint64)]
         L.ktir_event_record.argtypes = [C.c_uint64]
@@ -182,6 +184,11 @@ def check(rc: int, what: str = ""):
     if rc == K["KTIR_E_UNSUPPORTED"]:
         raise NotImplementedError(msg)
     raise KTIRDeviceError(msg)
+
+
+def set_row_grid_limit(max_workgroups: int):
+    """Bound the workgroups of row-program launches (0: no bound)."""
+    check(lib().ktir_set_row_grid_limit(int(max_workgroups)), "ktir_set_row_grid_limit")
 
 
 def device_info() -> dict:

@@ -32,22 +32,59 @@ def test_vector_add_bit_exact(n, block, cores):
     np.testing.assert_array_equal(out["x_ptr"], ref["x_ptr"])
 
 
-def test_gather_scatter_add_bit_exact():
-    ref, out, g = _run(_cases.gather_scatter_add())
+def _rmw_kernel(dim):
+    """The apply kernel the ordered row RMW takes for f32 rows of `dim` columns."""
+    return "rows" if dim % 128 == 0 else "generic"
+
+
+@pytest.mark.parametrize("dim", [32, 128, 256])
+def test_gather_scatter_add_bit_exact(dim):
+    ref, out, g = _run(_cases.gather_scatter_add(dim=dim))
     np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
     assert g.last_plan.counts() == {"rmw": 1}
+    assert g.last_plan.rmw_variants() == [_rmw_kernel(dim)]
 
 
+@pytest.mark.parametrize("dim", [32, 128])
 @pytest.mark.parametrize("rows", [16, 3])
-def test_gather_scatter_add_heavy_duplicates(rows):
+def test_gather_scatter_add_heavy_duplicates(rows, dim):
     """Many repeats inside one chunk (last writer wins) and long per-row chains
     across chunks and cores (sequential accumulation order)."""
-    src, fn, kw = _cases.gather_scatter_add(rows=1024, dim=32, n_idx=512, cores=4, chunk=32)
+    src, fn, kw = _cases.gather_scatter_add(rows=1024, dim=dim, n_idx=512, cores=4, chunk=32)
     rng = np.random.default_rng(7)
     kw["idx_ptr"] = rng.integers(0, rows, 512).astype(np.int32)
-    kw["out_ptr"] = rng.standard_normal((1024, 32)).astype(np.float32)
-    ref, out, _ = _run((src, fn, kw))
+    kw["out_ptr"] = rng.standard_normal((1024, dim)).astype(np.float32)
+    ref, out, g = _run((src, fn, kw))
     np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    assert g.last_plan.rmw_variants() == [_rmw_kernel(dim)]
+
+
+@pytest.mark.parametrize("dim", [32, 128])
+def test_gather_scatter_add_rows_past_allocation(dim):
+    """Indices past the end of the table read zero rows, and a destination
+    allocation that ends inside its last row drops the columns past its end
+    (reference memory.py:243-305), in both apply kernels."""
+    src, fn, kw = _cases.gather_scatter_add(rows=1024, dim=dim, n_idx=512, cores=4, chunk=32)
+    rng = np.random.default_rng(11)
+    kw["table_ptr"] = kw["table_ptr"][:700].copy()          # rows 700.. of the table view are past its end
+    kw["idx_ptr"] = np.concatenate([rng.integers(600, 1024, 500), [1023] * 12]).astype(np.int32)
+    kw["out_ptr"] = rng.standard_normal(1024 * dim - 24).astype(np.float32)   # last row ends 24 columns short
+    ref, out, g = _run((src, fn, kw))
+    np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    np.testing.assert_array_equal(out["table_ptr"], ref["table_ptr"])
+    assert g.last_plan.rmw_variants() == [_rmw_kernel(dim)]
+
+
+@pytest.mark.parametrize("dim", [32, 128])
+def test_gather_scatter_add_negative_index_raises(dim):
+    """A negative index raises IndexError (reference ops/memory_ops.py:378-382)."""
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    src, fn, kw = _cases.gather_scatter_add(rows=1024, dim=dim, n_idx=512, cores=4, chunk=32)
+    kw["idx_ptr"][77] = -5
+    g = KTIRInterpreter()
+    g.load(src)
+    with pytest.raises(IndexError):
+        g.execute_function(fn, **kw)
 
 
 @pytest.mark.parametrize("cols", [256, 4096])
@@ -94,12 +131,42 @@ def test_rmsnorm_bit_exact(cols, dt):
     np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
 
 
+@pytest.fixture
+def row_grid_limit():
+    """Bound the row kernels' workgroups for one test (reset afterwards)."""
+    from ktir_cpu_amd import runtime as rt
+    yield rt.set_row_grid_limit
+    rt.set_row_grid_limit(0)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 4096])
+def test_softmax_fixed_form_many_rows_per_workgroup(cols, dt, row_grid_limit):
+    """48 rows on 5 workgroups: every workgroup runs 9 or 10 rows through the
+    kernel's two alternating row buffers (odd and even row counts)."""
+    row_grid_limit(5)
+    ref, out, g = _run(_cases.softmax(rows=48, cols=cols, cores=4, dt=dt))
+    assert g.last_plan.counts() == {"prog": 1}
+    np.testing.assert_allclose(_half_f32(out["y_ptr"], dt), _half_f32(ref["y_ptr"], dt), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 4096])
+def test_rmsnorm_bit_exact_many_rows_per_workgroup(cols, dt, row_grid_limit):
+    row_grid_limit(5)
+    ref, out, g = _run(_cases.rmsnorm(rows=48, cols=cols, cores=4, dt=dt, wide=True))
+    assert g.last_plan.counts() == {"prog": 1}
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
+@pytest.mark.parametrize("limit", [0, 3])
 @pytest.mark.parametrize("cols", [64, 256, 1024, 4096, 8192, 96, 3000])
 @pytest.mark.parametrize("combiner", ["arith.addf", "arith.maximumf"])
-def test_row_reduce_bit_exact(cols, combiner):
+def test_row_reduce_bit_exact(cols, combiner, limit, row_grid_limit):
     """Row folds reproduce the reference's pairwise-halving order bit for bit
     (power-of-two rows take the register-resident row kernel, the others the
-    general row program)."""
+    general row program); with limit 3, 32 rows run on 3 workgroups."""
+    row_grid_limit(limit)
     ref, out, _ = _run(_cases.row_reduce(rows=32, cols=cols, combiner=combiner))
     np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
 

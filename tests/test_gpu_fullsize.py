@@ -1,0 +1,121 @@
+"""GPU parity at the benchmark's full sizes (bench.py's own input generators).
+
+* gather + scatter-add, 1 Mi x 128 table, 262 144 indices, 64 cores: bit-exact
+  against the whole oracle run, through the row-order apply kernel.
+* softmax and RMSNorm, 32 768 x 4096: the oracle runs eight of the 512
+  simulated cores (cores own disjoint 64-row blocks and share nothing), and
+  those cores' rows are compared: RMSNorm bit-exact, softmax at rtol 1e-2 /
+  atol 1e-3.  Every row kernel workgroup runs many rows at this size.
+* vector_add, 64 Mi f16: bit-exact against NumPy's f16 addition, which is
+  what the reference's ``_float_binop`` computes (``dialects/_helpers.py:39-54``).
+* GEMM 8192^3 and causal attention 4 x 32 x 8192 x 128: sampled output rows
+  against float64 NumPy from the same inputs, rtol 1e-2 / atol 1e-3.  The
+  oracle would take hours here; float64 is the exact answer the f32
+  accumulations approximate.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import bench
+from oracle.interp import OracleInterpreter, bf16_from_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu(cfg):
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    g = KTIRInterpreter()
+    g.load(cfg["src"])
+    out = g.execute_function(cfg["fn"], **cfg["kw"])
+    print(cfg["workload"], g.last_plan.mode, g.last_plan.counts(), flush=True)
+    return out, g
+
+
+def test_gather_scatter_add_full_config():
+    cfg = bench.CONFIGS["gather"]()
+    out, g = _gpu(cfg)
+    assert g.last_plan.counts() == {"rmw": 1}
+    assert g.last_plan.rmw_variants() == ["rows"]
+    o = OracleInterpreter()
+    o.load(cfg["src"])
+    ref = o.execute_function(cfg["fn"], **cfg["kw"])
+    np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    assert np.count_nonzero(out["out_ptr"].any(axis=1)) > 200000
+
+
+_SAMPLE_CORES = [0, 1, 100, 255, 256, 383, 510, 511]
+
+
+def _sampled_oracle(cfg, key):
+    o = OracleInterpreter()
+    o.load(cfg["src"])
+    o.cores_to_run = _SAMPLE_CORES
+    ref = o.execute_function(cfg["fn"], **cfg["kw"])
+    rpc = cfg["kw"][key].shape[0] // cfg["cores"]
+    rows = np.concatenate([np.arange(c * rpc, (c + 1) * rpc) for c in _SAMPLE_CORES])
+    return ref[key][rows], rows
+
+
+def test_softmax_full_size_sampled_cores():
+    cfg = bench.CONFIGS["softmax"]()
+    out, g = _gpu(cfg)
+    assert g.last_plan.counts() == {"prog": 1}
+    ref, rows = _sampled_oracle(cfg, "y_ptr")
+    np.testing.assert_allclose(out["y_ptr"][rows].astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+    # every row of the output is a distribution
+    s = out["y_ptr"].astype(np.float32).sum(axis=1)
+    assert np.all(np.abs(s - 1) < 0.02), (s.min(), s.max())
+
+
+def test_rmsnorm_full_size_sampled_cores_bit_exact():
+    cfg = bench.CONFIGS["rmsnorm"]()
+    out, g = _gpu(cfg)
+    assert g.last_plan.counts() == {"prog": 1}
+    ref, rows = _sampled_oracle(cfg, "y_ptr")
+    np.testing.assert_array_equal(out["y_ptr"][rows], ref)
+
+
+def test_vector_add_64mi_bit_exact():
+    cfg = bench.CONFIGS["vector_add"]()
+    out, _ = _gpu(cfg)
+    x, y = cfg["kw"]["x_ptr"], cfg["kw"]["y_ptr"]
+    np.testing.assert_array_equal(out["output_ptr"], x + y)
+
+
+def test_gemm_8192_sampled_rows():
+    cfg = bench.CONFIGS["gemm"]()
+    out, g = _gpu(cfg)
+    assert set(g.last_plan.counts()) == {"mm"}
+    a, b = cfg["kw"]["a_ptr"], cfg["kw"]["b_ptr"]
+    rows = np.random.default_rng(3).choice(a.shape[0], 64, replace=False)
+    ref = a[rows].astype(np.float64) @ b.astype(np.float64)
+    got = out["c_ptr"][rows].astype(np.float64)
+    err = np.abs(got - ref)
+    print(f"gemm 8192^3: max |err| {err.max():.3e}, max |C| {np.abs(ref).max():.3e}", flush=True)
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_attention_full_size_sampled_rows():
+    """Causal attention at B=4, H=32, S=8192, D=128 (bf16): 32 random query
+    rows against float64 softmax(q K^T / sqrt(D)) V over their causal prefix.
+    Records the largest error of the f16 P @ V form at this size."""
+    cfg = bench.CONFIGS["attention"]()
+    out, g = _gpu(cfg)
+    assert g.last_plan.counts().get("attn") == 1
+    q, k, v = (bf16_from_bits(cfg["kw"][n]).astype(np.float64) for n in ("q_ptr", "k_ptr", "v_ptr"))
+    o = bf16_from_bits(out["o_ptr"]).astype(np.float64)
+    B, H, S, D = q.shape
+    rng = np.random.default_rng(5)
+    picks = [(rng.integers(B), rng.integers(H), rng.integers(S)) for _ in range(29)]
+    picks += [(0, 0, 0), (B - 1, H - 1, S - 1), (1, 2, 127)]
+    worst = 0.0
+    for b, h, i in picks:
+        s = k[b, h, :i + 1] @ q[b, h, i] / math.sqrt(D)
+        p = np.exp(s - s.max())
+        ref = (p @ v[b, h, :i + 1]) / p.sum()
+        got = o[b, h, i]
+        worst = max(worst, float(np.max(np.abs(got - ref) / (1e-3 + 1e-2 * np.abs(ref)))))
+        np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3, err_msg=f"(b, h, q) = {(b, h, i)}")
+    print(f"attention full size: worst |err| / (atol + rtol |ref|) = {worst:.3f}", flush=True)
