@@ -143,3 +143,43 @@ def unary_f32(op="math.sqrt", n=1 << 14, block=512, cores=32, seed=11):
 }}
 """
     return src, "unary_kernel", dict(x_ptr=x, y_ptr=np.zeros_like(x))
+
+
+def elementwise(body, ins, out_dt, n=4096, cores=4, name="ew_kernel"):
+    """One tile per core: load each input (`ins`: list of dtypes, SSA names
+    %a, %b, %c, ...), run `body` (KTIR lines over those names and the tile
+    type `T<dt>` written as {T_dt}), store %r (dtype `out_dt`) to the output.
+    Returns (src, fn, arg-name list)."""
+    blk = n // cores
+    assert blk * cores == n
+    names = "abcdefg"[:len(ins)]
+    args = ", ".join([f"%{x}_ptr: index" for x in names] + ["%r_ptr: index"])
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             f"    %B = arith.constant {blk} : index",
+             "    %off = arith.muli %core_id, %B : index"]
+    at = f"!ktdp.access_tile<{blk}xindex>"
+    for x, dt in zip(names, ins):
+        lines.append(configs._view(f"{x}_view", f"{x}_ptr", [n], [1], dt))
+        lines.append(configs._tile(f"{x}_t", f"{x}_view", ["%off"], [blk], [n], dt))
+        lines.append(f"    %{x} = ktdp.load %{x}_t : {at} -> {configs._t([blk], dt)}")
+    types = {f"T_{dt}": configs._t([blk], dt) for dt in ("f16", "bf16", "f32", "i1", "i32")}
+    lines += ["    " + ln.format(**types) for ln in body]
+    lines.append(configs._view("r_view", "r_ptr", [n], [1], out_dt))
+    lines.append(configs._tile("r_t", "r_view", ["%off"], [blk], [n], out_dt))
+    lines.append(f"    ktdp.store %r, %r_t : {configs._t([blk], out_dt)}, {at}")
+    src = (f"module {{\n  func.func @{name}({args}) attributes {{grid = [{cores}, 1]}} {{\n"
+           + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, name, [f"{x}_ptr" for x in names] + ["r_ptr"]
+
+
+def f16_patterns(n, seed=0, specials=True):
+    """`n` f16 values: random bit patterns (all exponents, subnormals
+    included), plus zeros, infinities and NaN when `specials`."""
+    rng = np.random.default_rng(seed)
+    bits = rng.integers(0, 1 << 16, n, dtype=np.uint32).astype(np.uint16)
+    v = bits.view(np.float16).copy()
+    if specials:
+        v[:8] = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0, 65504.0], np.float16)
+    else:
+        v[~np.isfinite(v)] = np.float16(1.5)
+    return v
