@@ -327,6 +327,16 @@ int ktir_launch_row_rmw(const ktir_rmw_t* d);
 #define KTIR_RMW_GENERIC 0
 #define KTIR_RMW_ROWS 1
 int ktir_rmw_variant(const ktir_rmw_t* d);
+/* ktir_launch_row_rmw without caller scratch: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  head, link,
+ * rows and srcs of `d` are ignored; the library's own 20 MiB device array
+ * (one per device, set up by ktir_init, kept until the process ends) holds
+ * them.  Limits: n_rows <= 2^21 and n_inst * K <= 2^20, else
+ * KTIR_E_UNSUPPORTED.  Allocates nothing.  All calls on one device share the
+ * array: calls that overlap on one device (other streams, other threads)
+ * race and must not be issued. */
+int ktir_launch_row_rmw_noalloc(const ktir_rmw_t* d);
 
 /* ---- fused online-softmax attention loop ----
  * Replaces a whole KV `scf.for` of the flash-attention form (the reference's

@@ -10,6 +10,7 @@ namespace ktir {
 int set_error(int code, const char* fmt, ...);
 hipStream_t stream();
 int* device_error_flag();   // device int: 1 = negative indirect index seen
+int rmw_scratch_setup(int device);   // ktir_init: per-device scratch of the allocation-free RMW
 
 #define KTIR_HIP_CHECK(expr)                                                        \
   do {                                                                              \

@@ -301,9 +301,72 @@ extern "C" int ktir_rmw_variant(const ktir_rmw_t* d) {
   return rmw_rows_form(d) ? KTIR_RMW_ROWS : KTIR_RMW_GENERIC;
 }
 
+// The allocation-free form keeps the head, link, rows and srcs arrays in one
+// file-scope device array: heads in a fixed region of RMW_NA_ROWS slots (all
+// -1 between calls), then link, rows and srcs in fixed regions of
+// RMW_NA_ENTRIES slots each, so no call's entries ever land in another call's
+// heads.  In host code `scratch` names a host-side stand-in; its device
+// address (one per device) comes from hipGetSymbolAddress, taken once per
+// device by rmw_scratch_setup with that device current.
+constexpr int64_t RMW_NA_ROWS = (int64_t)2 << 20;      // destination rows
+constexpr int64_t RMW_NA_ENTRIES = (int64_t)1 << 20;   // n_inst * K
+constexpr int64_t RMW_SCRATCH_WORDS = RMW_NA_ROWS + 3 * RMW_NA_ENTRIES;   // 20 MiB of int32
+constexpr int RMW_MAX_DEVICES = 64;
+__device__ __align__(256) int32_t scratch[RMW_SCRATCH_WORDS];
+static int32_t* g_scratch[RMW_MAX_DEVICES];
+
+__global__ __launch_bounds__(256) void rmw_fill(int32_t* p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// Called by ktir_init with `device` current: the device address of this
+// device's copy of `scratch`, and every head slot set to -1 (the head table is
+// all -1 between calls: each launch resets the heads it uses).
+int ktir::rmw_scratch_setup(int device) {
+  if (device < 0 || device >= RMW_MAX_DEVICES)
+    return set_error(KTIR_E_UNSUPPORTED, "ktir_init: device %d beyond the %d the RMW scratch table covers", device,
+                     RMW_MAX_DEVICES);
+  if (g_scratch[device]) return KTIR_OK;
+  int32_t* ptr = nullptr;
+  KTIR_HIP_CHECK(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
+  hipLaunchKernelGGL(rmw_fill, dim3(1024), dim3(256), 0, stream(), ptr, RMW_NA_ROWS, (int32_t)-1);
+  KTIR_HIP_CHECK(hipGetLastError());
+  KTIR_HIP_CHECK(hipStreamSynchronize(stream()));
+  g_scratch[device] = ptr;
+  return KTIR_OK;
+}
+
+static int rmw_launch(const ktir_rmw_t* d);
+
+extern "C" int ktir_launch_row_rmw_noalloc(const ktir_rmw_t* d) {
+  const int rc = rmw_check(d, "ktir_launch_row_rmw_noalloc");
+  if (rc != KTIR_OK) return rc;
+  int dev = -1;
+  KTIR_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= RMW_MAX_DEVICES || !g_scratch[dev])
+    return set_error(KTIR_E_ARG, "ktir_launch_row_rmw_noalloc: ktir_init was not called for device %d", dev);
+  const int64_t entries = d->n_inst * d->K;
+  if (d->n_rows > RMW_NA_ROWS || entries > RMW_NA_ENTRIES)
+    return set_error(KTIR_E_UNSUPPORTED,
+                     "ktir_launch_row_rmw_noalloc: %lld destination rows and %lld entries (n_inst * K) exceed "
+                     "the scratch array's %lld rows and %lld entries (use ktir_launch_row_rmw with caller buffers)",
+                     (long long)d->n_rows, (long long)entries, (long long)RMW_NA_ROWS, (long long)RMW_NA_ENTRIES);
+  ktir_rmw_t w = *d;
+  int32_t* base = g_scratch[dev];
+  w.head = (uint64_t)base;
+  w.link = (uint64_t)(base + RMW_NA_ROWS);
+  w.rows = (uint64_t)(base + RMW_NA_ROWS + RMW_NA_ENTRIES);
+  w.srcs = (uint64_t)(base + RMW_NA_ROWS + 2 * RMW_NA_ENTRIES);
+  return rmw_launch(&w);
+}
+
 extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
   const int rc = rmw_check(d, "ktir_launch_row_rmw");
   if (rc != KTIR_OK) return rc;
+  return rmw_launch(d);
+}
+
+static int rmw_launch(const ktir_rmw_t* d) {
   if (d->n_inst == 0) return KTIR_OK;
   int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());

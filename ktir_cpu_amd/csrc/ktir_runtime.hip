@@ -43,7 +43,7 @@ extern "C" int ktir_init(int device) {
   KTIR_HIP_CHECK(hipMemsetAsync(g_err_flag, 0, sizeof(int), g_stream));
   KTIR_HIP_CHECK(hipStreamSynchronize(g_stream));
   g_device = device;
-  return KTIR_OK;
+  return rmw_scratch_setup(device);
 }
 
 extern "C" int ktir_shutdown(void) {

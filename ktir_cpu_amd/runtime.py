@@ -141,7 +141,8 @@ def lib():
                      "ktir_launch_program", "ktir_scatter_winners", "ktir_iat_offsets",
                      "ktir_launch_matmul", "ktir_event_create", "ktir_event_record",
                      "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info",
-                     "ktir_launch_row_rmw", "ktir_launch_attention", "ktir_rmw_variant", "ktir_shutdown", "ktir_set_row_grid_limit"):
+                     "ktir_launch_row_rmw", "ktir_launch_attention", "ktir_rmw_variant", "ktir_shutdown", "ktir_set_row_grid_limit",
+                     "ktir_launch_row_rmw_noalloc"):
             getattr(L, name).restype = C.c_int
         L.ktir_malloc.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.ktir_free.argtypes = [C.c_uint64]
@@ -155,6 +156,7 @@ def lib():
         L.ktir_launch_matmul.argtypes = [C.POINTER(MM)]
         L.ktir_launch_row_rmw.argtypes = [C.POINTER(RMW)]
         L.ktir_rmw_variant.argtypes = [C.POINTER(RMW)]
+        L.ktir_launch_row_rmw_noalloc.argtypes = [C.POINTER(RMW)]
         L.ktir_set_row_grid_limit.argtypes = [C.c_int64]
         L.ktir_launch_attention.argtypes = [C.POINTER(ATTN)]
         L.ktir_event_create.argtypes = [C.POINTER(C.c_uint64)]
