@@ -1,12 +1,17 @@
 """Benchmark of the KTIR gfx950 backend on BASELINE.json's configurations.
 
-`python bench.py [--config NAME] [--steps K] [--warmup W]` prints ONE JSON
-line.  A step is one replay of the recorded launch plan of the config's KTIR
-kernel over inputs already resident in HBM (the host IR walk and the
-host<->device copies are outside the timed region).  Timing uses HIP events
-on the library's stream.  The CPU baseline times the NumPy oracle (a
-restatement of the reference interpreter) on the host on a bounded sample of
-the same workload and extrapolates by core count.
+`python bench.py [--config NAME|all] [--steps K] [--warmup W] [--no-cpu]`
+prints ONE JSON line.  A step is one replay of the recorded launch plan of a
+config's KTIR kernel over inputs already resident in HBM (the host IR walk
+and the host<->device copies are outside the timed region).  Timing uses HIP
+events on the library's stream, with an event after every launch, so the
+dominant launch's own time gives `roofline.achieved`.  By default the line's
+top-level fields are the gather + scatter-add config
+and `per_config` holds the same measurement for every config; each entry also
+reports the host side of a real call (copies in and out, one end-to-end
+execute_function).  The CPU baseline times the NumPy oracle (a restatement of
+the reference interpreter, one core) on a bounded sample of the same
+workload, median of 3, and extrapolates by simulated-core count.
 """
 
 import argparse
@@ -35,6 +40,18 @@ def _vector_add():
     return dict(src=configs.vector_add(n, block, cores), fn="add_kernel", kw=kw, cores=cores,
                 bytes=6 * n, flops=n, bound="hbm", dtype="f16",
                 workload=f"vector_add n={n} f16 grid={cores} BLOCK={block}")
+
+
+def _vector_add_4096():
+    from ktir_cpu_amd import configs
+    n, block, cores = 4096, 128, 32
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal(n).astype(np.float16)
+    y = rng.standard_normal(n).astype(np.float16)
+    kw = dict(x_ptr=x, y_ptr=y, output_ptr=np.zeros(n, np.float16), BLOCK_SIZE=block)
+    return dict(src=configs.vector_add(n, block, cores), fn="add_kernel", kw=kw, cores=cores,
+                bytes=6 * n, flops=n, bound="hbm", dtype="f16",
+                workload=f"vector_add n={n} f16 grid={cores} BLOCK={block} (launch-bound: reported only)")
 
 
 def _copy():
@@ -99,19 +116,27 @@ def _gemm():
                 workload=f"gemm {M}x{N}x{K} f16 tiles 128x128x64 grid=8x8")
 
 
+def _bf16_bits(x):
+    """bf16 bit patterns of finite float32 values, rounded to nearest even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = u + np.uint32(0x7FFF)
+    r += (u >> np.uint32(16)) & np.uint32(1)
+    return (r >> np.uint32(16)).astype(np.uint16)
+
+
 def _attention():
     from ktir_cpu_amd import configs
-    from oracle.interp import bf16_bits
     B, H, S, D = 4, 32, 8192, 128
     rng = np.random.default_rng(42)
-    q, k, v = (bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)) for _ in range(3))
+    q, k, v = (_bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)) for _ in range(3))
     kw = dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D))
     return dict(src=configs.flash_attention(B, H, S, D, 128), fn="flash_attention", kw=kw, cores=B * H * S // 128,
                 bytes=4 * B * H * S * D * 2, flops=4 * B * H * S * S * D // 2, bound="mfma", dtype="bf16 (f32 acc)",
+                f32_blas=True,
                 workload=f"flash_attention causal B={B} H={H} S={S} D={D} kv_tile=128")
 
 
-CONFIGS = {"vector_add": _vector_add, "copy": _copy, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
+CONFIGS = {"vector_add": _vector_add, "vector_add_4096": _vector_add_4096, "copy": _copy, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
            "gemm": _gemm, "attention": _attention}
 
 
@@ -137,75 +162,62 @@ def _traffic(config, kind):
     return round(sum(b)) if b else None
 
 
-def cpu_baseline(cfg, budget_s=15.0):
-    """Time the oracle on k evenly spaced cores for growing k (1, 2, 4, ...)
-    until about `budget_s` of CPU work, then extrapolate the per-core slope
-    to all cores.  Even spacing keeps the sample representative where the
-    work per core differs (causal attention: core qb visits qb + 1 KV tiles)."""
+def _cpu_env():
+    """Host cores and BLAS thread settings the CPU baseline ran under."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
+    blas = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
+    return {"os_cpu_count": os.cpu_count(), "sched_affinity": aff, "blas_threads": blas}
+
+
+def cpu_baseline(cfg, budget_s=2.5, repeats=3):
+    """The oracle (a NumPy restatement of the reference interpreter, one core)
+    timed on the host: the fixed part of a run (placing and reading back the
+    arrays, no simulated core) and a run of k evenly spaced simulated cores,
+    k doubling until the cores' part takes about `budget_s`; each the median
+    of `repeats` runs.  The time per simulated core is extrapolated to all
+    cores.  Even spacing keeps the sample representative where the work per
+    core differs (causal attention: core qb visits qb + 1 KV tiles)."""
     from oracle.interp import OracleInterpreter
     o = OracleInterpreter(lx_size_mb=64)
     o.load(cfg["src"])
     cores = cfg["cores"]
     kw = cfg["kw"]
-    samples = []
-    k = 1
-    t_all = time.perf_counter()
-    while True:
-        kk = min(k, cores)
-        o.cores_to_run = sorted(set(int(c) for c in np.linspace(0, cores - 1, kk + 2)[1:-1].round()))
-        kk = len(o.cores_to_run)
+
+    def sample(k):
+        o.cores_to_run = sorted(set(int(c) for c in np.linspace(0, cores - 1, k + 2)[1:-1].round())) if k else []
         t0 = time.perf_counter()
         o.execute_function(cfg["fn"], **kw)
-        samples.append((kk, time.perf_counter() - t0))
-        if k >= cores or time.perf_counter() - t_all > budget_s:
+        return len(o.cores_to_run), time.perf_counter() - t0
+
+    t_fixed = float(np.median([sample(0)[1] for _ in range(repeats)]))
+    k = 1
+    while True:
+        kk, t = sample(min(k, cores))
+        if k >= cores or t - t_fixed > budget_s:
             break
         k *= 2
-    if len(samples) >= 2:
-        (k1, t1), (k2, t2) = samples[-2], samples[-1]
-        per_core = max((t2 - t1) / max(k2 - k1, 1), 1e-9)
-        setup = max(t1 - per_core * k1, 0.0)
-    else:
-        k2, t2 = samples[-1]
-        per_core, setup = t2 / k2, 0.0
-    t_full = setup + per_core * cores
-    return t_full, samples
+    t_k = float(np.median([t] + [sample(kk)[1] for _ in range(repeats - 1)]))
+    per_core = max(t_k - t_fixed, 1e-9) / kk
+    t_full = t_fixed + per_core * cores
+    return t_full, {"k": kk, "t_k": t_k, "t_fixed": t_fixed}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="gather", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU runs are not part of this build",
-                          "n_gpus": args.gpus}))
-        sys.exit(2)
+def _instrumented_steps(prep, steps):
+    """K replays of the plan with a HIP event after every launch (library
+    stream): returns (ms per step, mean ms of each launch)."""
     from ktir_cpu_amd import runtime as rt
-    from ktir_cpu_amd.interpreter import KTIRInterpreter
-    cfg = CONFIGS[args.config]()
-    interp = KTIRInterpreter()
-    interp.load(cfg["src"])
-    t0 = time.perf_counter()
-    prep = interp.prepare(cfg["fn"], **cfg["kw"])          # host walk + first launch
-    walk_s = time.perf_counter() - t0
-    plan = prep.plan
-    for _ in range(args.warmup):
-        prep.run()
-    rt.sync()
-    # Timed region: K replays of the plan on the library's stream, with a HIP
-    # event after every launch so each launch's duration comes from the same
-    # run that gives ms_per_step.
     from ktir_cpu_amd.executor import _launch
+    plan = prep.plan
     L = rt.lib()
     n = len(plan.launches)
     instrument = 0 < n <= 64
-    evs = [[rt.Event() for _ in range(n)] for _ in range(args.steps)] if instrument else None
+    evs = [[rt.Event() for _ in range(n)] for _ in range(steps)] if instrument else None
     e0, e1 = rt.Event(), rt.Event()
     e0.record()
-    for s_ in range(args.steps):
+    for s_ in range(steps):
         if instrument:
             for i, (kind, desc, _) in enumerate(plan.launches):
                 _launch(L, kind, desc)
@@ -214,48 +226,166 @@ def main():
             prep.run()
     e1.record()
     rt.sync()
-    ms = e0.elapsed_ms(e1) / args.steps
+    ms = e0.elapsed_ms(e1) / steps
     durs = np.zeros(n)
     if instrument:
-        for s_ in range(args.steps):
+        for s_ in range(steps):
             prev = e0 if s_ == 0 else evs[s_ - 1][-1]
             for i in range(n):
                 durs[i] += prev.elapsed_ms(evs[s_][i])
                 prev = evs[s_][i]
-        durs /= args.steps
+        durs /= steps
+    return ms, durs
+
+
+def measure(name, steps, warmup, with_cpu):
+    """One config: whole-step throughput on resident inputs, the dominant
+    launch against its roofline, host<->device copy times, one end-to-end
+    execute_function, and (optionally) the CPU baseline."""
+    from ktir_cpu_amd import runtime as rt
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    cfg = CONFIGS[name]()
+    interp = KTIRInterpreter()
+    interp.load(cfg["src"])
+    t0 = time.perf_counter()
+    prep = interp.prepare(cfg["fn"], **cfg["kw"])          # copies in, host walk, first launch
+    prepare_s = time.perf_counter() - t0
+    plan = prep.plan
+    for _ in range(warmup):
+        prep.run()
+    rt.sync()
+    ms, durs = _instrumented_steps(prep, steps)
+    n = len(plan.launches)
     dom = int(np.argmax(durs)) if n else 0
-    dom_ms = float(durs[dom]) if instrument else ms
-    # every bench workload's dominant launch processes all of the workload's
-    # algorithmic units (all bytes moved / all flops), so per-launch units are
-    # the workload's
+    dom_ms = float(durs[dom]) if n and durs.any() else ms
+    kind = plan.launches[dom][0] if n else None
+    # every workload's dominant launch processes all of the workload's
+    # algorithmic units (all bytes moved / all flops)
     if cfg["bound"] == "hbm":
-        value = cfg["bytes"] / (ms * 1e-3) / 1e9
-        unit, peak = "GB/s", HBM_PEAK_GBS
-        achieved = cfg["bytes"] / (dom_ms * 1e-3) / 1e9
+        units, unit, peak, scale = cfg["bytes"], "GB/s", HBM_PEAK_GBS, 1e9
     else:
-        value = cfg["flops"] / (ms * 1e-3) / 1e12
-        unit, peak = "TFLOP/s", MFMA_F16_TFLOPS
-        achieved = cfg["flops"] / (dom_ms * 1e-3) / 1e12
+        units, unit, peak, scale = cfg["flops"], "TFLOP/s", MFMA_F16_TFLOPS, 1e12
+    value = units / (ms * 1e-3) / scale
+    achieved = units / (dom_ms * 1e-3) / scale
+    # host <-> device copies of all array arguments, and one whole call
+    t0 = time.perf_counter()
+    prep.reset_inputs()
+    rt.sync()
+    h2d_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    prep.outputs()
+    d2h_s = time.perf_counter() - t0
+    del prep
+    t0 = time.perf_counter()
+    interp.execute_function(cfg["fn"], **cfg["kw"])
+    e2e_s = time.perf_counter() - t0
+    out = {"config": name, "workload": cfg["workload"], "value": round(value, 3), "unit": unit,
+           "ms_per_step": round(ms, 6), "dtype": cfg["dtype"], "launches_per_step": n, "plan_mode": plan.mode,
+           "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                        "frac": round(achieved / peak, 4), "traffic": _traffic(name, kind),
+                        "dominant_launch": kind, "dominant_ms": round(dom_ms, 6)},
+           "host": {"prepare_s": round(prepare_s, 3), "h2d_s": round(h2d_s, 4), "d2h_s": round(d2h_s, 4),
+                    "execute_function_s": round(e2e_s, 3),
+                    "execute_function_rate": round(units / e2e_s / scale, 4)}}
+    if with_cpu:
+        t_full, smp = cpu_baseline(cfg)
+        env = _cpu_env()
+        # the oracle is single-threaded NumPy except f32 matmuls, which go
+        # through BLAS (attention's S = Q K^T and P V are f32 products)
+        blas_n = int(env["blas_threads"].get("OPENBLAS_NUM_THREADS") or env["blas_threads"].get("OMP_NUM_THREADS")
+                     or env["sched_affinity"] or 1)
+        cores = blas_n if cfg.get("f32_blas") else 1
+        out["cpu_baseline"] = {"value": units / t_full / scale, "unit": unit, "cores": cores, "kind": "port",
+                               "sample": f"oracle on {smp['k']} evenly spaced of {cfg['cores']} simulated cores "
+                                         f"({smp['t_k']:.2f} s, of which {smp['t_fixed']:.2f} s is the run's "
+                                         f"fixed part, timed without cores; medians of 3), extrapolated by "
+                                         f"core count to {t_full:.1f} s for the full run"
+                                         + ("; f32 matmuls on BLAS threads, the rest on one core"
+                                            if cfg.get("f32_blas") else "; one core"),
+                               **env}
+    print(f"[bench] {name}: {out['value']} {unit}, frac {out['roofline']['frac']}", file=sys.stderr, flush=True)
+    return out
+
+
+HEADLINE = "gather"
+PER_CONFIG = ["vector_add", "gather", "softmax", "rmsnorm", "gemm", "attention", "vector_add_4096"]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="all", choices=["all"] + sorted(CONFIGS),
+                    help="one config, or all (the gather headline plus every config in per_config)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--collect-traffic", metavar="DIR",
+                    help="build profiles/traffic.json from rocprofv3 FETCH_SIZE/WRITE_SIZE runs under DIR")
+    args = ap.parse_args()
+    if args.collect_traffic:
+        collect_traffic(args.collect_traffic)
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU runs are not part of this build",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    names = PER_CONFIG if args.config == "all" else [args.config]
+    head = HEADLINE if args.config == "all" else args.config
+    results = [measure(n, args.steps, args.warmup, not args.no_cpu) for n in names]
+    h = next(r for r in results if r["config"] == head)
     out = {
         "metric": "achieved HBM GB/s & MFMA TFLOP/s per KTIR kernel (% of roofline) vs NumPy",
-        "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": cfg["dtype"], "data": "synthetic (seed 42)",
-        "config": {"workload": cfg["workload"], "launches_per_step": len(plan.launches),
-                   "plan_mode": plan.mode, "host_walk_s": round(walk_s, 3)},
-        "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": _traffic(args.config, plan.launches[dom][0] if plan.launches else None),
-                     "dominant_launch": plan.launches[dom][0] if plan.launches else None,
-                     "dominant_ms": round(dom_ms, 6)},
+        "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": h["dtype"], "data": "synthetic (seed 42)",
+        "config": {"workload": h["workload"], "launches_per_step": h["launches_per_step"],
+                   "plan_mode": h["plan_mode"]},
+        "roofline": h["roofline"],
     }
-    if not args.no_cpu:
-        t_full, samples = cpu_baseline(cfg)
-        cpu_val = (cfg["bytes"] / t_full / 1e9) if cfg["bound"] == "hbm" else (cfg["flops"] / t_full / 1e12)
-        out["cpu_baseline"] = {"value": cpu_val, "unit": unit, "cores": 1, "kind": "port",
-                               "sample": f"oracle on {samples[-1][0]} evenly spaced of {cfg['cores']} simulated cores "
-                                         f"({samples[-1][1]:.1f} s), extrapolated linearly by core count to "
-                                         f"{t_full:.1f} s for the full run"}
+    if "cpu_baseline" in h:
+        out["cpu_baseline"] = h["cpu_baseline"]
+    out["host"] = h["host"]
+    if args.config == "all":
+        out["per_config"] = results
     print(json.dumps(out))
+
+
+def collect_traffic(root):
+    """profiles/traffic.json from two rocprofv3 --pmc runs per config
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) under ROOT/traffic_<config>_<counter>/,
+    each scaled by what the counter reads for the `copy` config (256 MiB in,
+    256 MiB out per dispatch)."""
+    import csv
+    import glob
+
+    def per_kernel(config, counter):
+        files = glob.glob(os.path.join(root, f"traffic_{config}_{counter}", "**", "*counter_collection.csv"),
+                          recursive=True)
+        vals = {}
+        for fn in files:
+            with open(fn) as f:
+                for row in csv.DictReader(f):
+                    if row.get("Counter_Name") == counter:
+                        vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return {k: float(np.median(v)) for k, v in vals.items()}
+
+    cf, cw = per_kernel("copy", "FETCH_SIZE"), per_kernel("copy", "WRITE_SIZE")
+    ck = max(cf, key=cf.get)
+    each = 256 * 1024 * 1024
+    fscale, wscale = each / (cf[ck] * 1024), each / (cw[ck] * 1024)
+    out = {"calibration": {"kernel": ck, "bytes_each_way": each, "fetch_kib": cf[ck], "write_kib": cw[ck],
+                           "fetch_scale": fscale, "write_scale": wscale}, "configs": {}}
+    for config in sorted(CONFIGS):
+        f, w = per_kernel(config, "FETCH_SIZE"), per_kernel(config, "WRITE_SIZE")
+        if not f:
+            continue
+        ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0),
+                  "bytes": f[k] * 1024 * fscale + w.get(k, 0.0) * 1024 * wscale} for k in f}
+        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values()), "kernels": ks}
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(path)
 
 
 if __name__ == "__main__":

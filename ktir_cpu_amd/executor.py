@@ -58,23 +58,35 @@ class Alloc:
         return self.nbytes // rt.ELEM_BYTES[self.dtype]
 
 
+# an arena spanning more bytes than this is refused (sparse seeded addresses)
+MAX_ARENA_SPAN = 1 << 37
+
+
 class Arena:
-    """Argument tensors laid out as the reference lays them out in HBM, in one
-    device buffer; the byte address of every element matches the reference."""
+    """Allocations at the byte addresses the reference's HBM simulator gives
+    them, in one device buffer that spans them: the byte address of every
+    element matches the reference."""
 
     def __init__(self):
         self.allocs: List[Alloc] = []
         self.buf: Optional[rt.DeviceBuffer] = None
         self._starts: List[int] = []
+        self.base = HBM_BASE
 
-    def layout(self, specs: List[Tuple[str, str, int, Tuple[int, ...]]]):
-        nxt = HBM_BASE
-        self.allocs = []
-        for name, dt, nbytes, shape in specs:
-            a = Alloc(name, dt, nxt, nbytes, shape, nxt - HBM_BASE)
-            self.allocs.append(a)
-            nxt = (nxt + nbytes + STICK_BYTES - 1) & ~(STICK_BYTES - 1)
-        total = max(nxt - HBM_BASE, STICK_BYTES)
+    def layout(self, specs: List[Tuple[str, str, int, int, Tuple[int, ...]]]):
+        """`specs`: (name, dtype, byte address, nbytes, shape) per allocation;
+        allocations must not overlap."""
+        order = sorted(specs, key=lambda t: t[2])
+        for (n0, _, a0, b0, _), (n1, _, a1, _, _) in zip(order, order[1:]):
+            if a0 + b0 > a1:
+                raise NotImplementedError(f"HBM allocations {n0!r} and {n1!r} overlap "
+                                          f"(0x{a0:x}+{b0} > 0x{a1:x})")
+        self.base = min([HBM_BASE] + [t[2] & ~(STICK_BYTES - 1) for t in order])
+        end = max([HBM_BASE + STICK_BYTES] + [t[2] + max(t[3], 1) for t in order])
+        if end - self.base > MAX_ARENA_SPAN:
+            raise NotImplementedError(f"HBM allocations span {end - self.base} bytes")
+        self.allocs = [Alloc(name, dt, addr, nbytes, shape, addr - self.base) for name, dt, addr, nbytes, shape in order]
+        total = (end - self.base + STICK_BYTES - 1) & ~(STICK_BYTES - 1)
         if self.buf is None or self.buf.nbytes < total:
             if self.buf is not None:
                 self.buf.free()

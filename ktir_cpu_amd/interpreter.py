@@ -22,6 +22,7 @@ from . import runtime as rt
 from .executor import Arena, NeedEager, Plan, Pool, STICK_BYTES
 from .ir import IRModule
 from .latency import LatencyReport, LatencyTracker
+from .memory import DeviceMemory
 from .parser import KTIRParser
 from .walker import Executor
 
@@ -38,34 +39,47 @@ def ktir_dtype_of(arr: np.ndarray) -> str:
         raise ValueError(f"Unsupported array dtype {arr.dtype} (reference dtypes.py:24-39 plus bf16 as uint16)")
 
 
+def _storage_dtype(arr: np.ndarray) -> str:
+    """KTIR dtype of a staged HBM seed (any host dtype: one of the same size)."""
+    try:
+        return ktir_dtype_of(arr)
+    except ValueError:
+        return {1: "i8", 2: "i16", 4: "i32", 8: "i64"}[arr.dtype.itemsize]
+
+
 class Prepared:
     """Arguments resident on the device plus the launch plan of one function:
     `run()` replays the device work only (no host walk, no copies)."""
 
     def __init__(self, interp: "KTIRInterpreter", fn_name: str, names: List[str], plan: Plan, arena: Arena,
-                 arrays: Dict[str, np.ndarray]):
+                 arrays: Dict[str, np.ndarray], initial: Optional[Dict[str, np.ndarray]] = None):
         self.interp = interp
         self.fn_name = fn_name
         self.names = names
         self.plan = plan
         self.arena = arena
         self.arrays = arrays
+        self.initial = initial if initial is not None else arrays
 
     def run(self):
         self.plan.run()
 
     def reset_inputs(self):
         for a in self.arena.allocs:
-            arr = self.arrays[a.name]
+            arr = self.initial[a.name]
             self.arena.buf.upload(np.ascontiguousarray(arr).reshape(-1).view(np.uint8), a.off)
 
     def outputs(self) -> Dict[str, np.ndarray]:
+        """Every array argument read back (staged HBM seeds are not arguments)."""
         rt.sync()
         out = {}
         for a in self.arena.allocs:
+            if a.name not in self.arrays:
+                continue
             src = self.arrays[a.name]
-            raw = self.arena.buf.download(a.nbytes, a.off)
-            out[a.name] = np.frombuffer(raw.tobytes(), dtype=src.dtype).reshape(src.shape).copy()
+            dst = np.empty(src.shape, dtype=src.dtype)
+            self.arena.buf.download_into(dst, a.off)
+            out[a.name] = dst
         return out
 
 
@@ -83,6 +97,7 @@ class KTIRInterpreter:
         self.last_plan: Optional[Plan] = None
         self._arena = Arena()
         self._pool = None
+        self.memory: Optional[DeviceMemory] = None
         # latency model (reference interpreter.py:76-78): charged op by op during the run
         self._latency_tracker = LatencyTracker(latency_config, trace=trace_latency) if latency_config is not None \
             else None
@@ -116,6 +131,12 @@ class KTIRInterpreter:
         prep = self.prepare(fn_name, **kwargs)
         return prep.outputs()
 
+    def _prepare_execution(self, grid_shape):
+        """A fresh memory for one run (reference interpreter.py:95-120).
+        Callers may wrap this to seed ``self.memory.hbm`` at literal sticks."""
+        nx, ny, nz = grid_shape
+        self.memory = DeviceMemory(nx * ny * nz, self.lx_size_mb)
+
     # -- GPU-specific ---------------------------------------------------------
     def prepare(self, fn_name: str, **kwargs) -> Prepared:
         """Place the arguments on the device, walk the function once, launch
@@ -123,13 +144,22 @@ class KTIRInterpreter:
         if not self.module:
             raise RuntimeError("No module loaded. Call load() first.")
         fn = self.module.get_function(fn_name)
+        self._prepare_execution(fn.grid)
+        hbm = self.memory.hbm
         declared = fn.arg_names
         if kwargs and declared and not any(k in declared for k in kwargs):
             if len(kwargs) == len(declared):
                 kwargs = dict(zip(declared, kwargs.values()))
         rt.lib()
         arrays = {k: v for k, v in kwargs.items() if isinstance(v, np.ndarray)}
-        specs = [(k, ktir_dtype_of(v), int(v.nbytes), tuple(v.shape)) for k, v in arrays.items()]
+        initial: Dict[str, np.ndarray] = dict(arrays)
+        specs = []
+        for k, v in arrays.items():
+            specs.append((k, ktir_dtype_of(v), hbm.allocate(v.nbytes) * STICK_BYTES, int(v.nbytes), tuple(v.shape)))
+        for addr, v in hbm.staged():
+            name = f"__hbm_0x{addr:x}"
+            initial[name] = v
+            specs.append((name, _storage_dtype(v), addr, int(v.nbytes), tuple(v.shape)))
         if self._pool is not None:
             self._pool.free_all()
         self._pool = Pool()
@@ -138,9 +168,11 @@ class KTIRInterpreter:
         self._arena = arena
         args: Dict[str, Any] = {}
         for a in arena.allocs:
-            v = arrays[a.name]
+            v = initial[a.name]
             arena.buf.upload(np.ascontiguousarray(v).reshape(-1).view(np.uint8), a.off)
-            args[a.name] = np.int64(a.addr // rt.ELEM_BYTES[a.dtype])
+            if a.name in arrays:
+                args[a.name] = np.int64(a.addr // rt.ELEM_BYTES[a.dtype])
+        hbm.attach(arena, {k: v.dtype for k, v in initial.items()})
         for k, v in kwargs.items():
             if not isinstance(v, np.ndarray):
                 args[k] = np.asarray(v)
@@ -166,4 +198,4 @@ class KTIRInterpreter:
                 plan.fallback_reason = str(why)
         rt.sync()
         self.last_plan = plan
-        return Prepared(self, fn_name, list(arrays), plan, arena, arrays)
+        return Prepared(self, fn_name, list(arrays), plan, arena, arrays, initial)

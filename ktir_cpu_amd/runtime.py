@@ -223,6 +223,12 @@ class DeviceBuffer:
         assert offset + a.nbytes <= self.nbytes
         check(lib().ktir_memcpy_h2d(self.ptr + offset, a.ctypes.data, a.nbytes), "ktir_memcpy_h2d")
 
+    def download_into(self, dst: np.ndarray, offset: int = 0):
+        """Copy dst.nbytes bytes from the buffer (at `offset`) into the
+        C-contiguous host array `dst`."""
+        assert dst.flags.c_contiguous and offset + dst.nbytes <= self.nbytes
+        check(lib().ktir_memcpy_d2h(dst.ctypes.data, self.ptr + offset, dst.nbytes), "ktir_memcpy_d2h")
+
     def download(self, nbytes: int, offset: int = 0) -> bytes:
         out = np.empty(nbytes, dtype=np.uint8)
         check(lib().ktir_memcpy_d2h(out.ctypes.data, self.ptr + offset, nbytes), "ktir_memcpy_d2h")

@@ -92,12 +92,19 @@ def to_ktir_dtype(npd) -> str:
 
 
 def bf16_round(x) -> np.ndarray:
-    """Round float32 values to the nearest bf16 (ties to even), as float32."""
-    a = np.asarray(x, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    out = r.astype(np.uint32).view(np.float32)
-    return np.where(np.isnan(a), a, out).astype(np.float32)
+    """Round float32 values to the nearest bf16 (ties to even), as float32.
+    A NaN stays a NaN, quieted as IEEE conversions deliver it (a signaling NaN
+    whose payload lies in the low half would otherwise truncate to inf).
+    Finite values never carry out of 32 bits: 0xFF7FFFFF + 0x8000 < 2^32."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    u = a.view(np.uint32)
+    r = u + np.uint32(0x7FFF)
+    r += (u >> np.uint32(16)) & np.uint32(1)
+    r &= np.uint32(0xFFFF0000)
+    nan = np.isnan(a)
+    if nan.any():
+        r[nan] = (u[nan] | np.uint32(0x400000)) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
 
 
 def bf16_bits(x) -> np.ndarray:

@@ -149,6 +149,9 @@ def test_oracle_bf16_round_against_exact_rounding():
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(got), nan)
     np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # a signaling NaN whose payload is only in the low half stays a NaN
+    snan = np.array([0x7F800001, 0xFF800100], np.uint32).view(np.float32)
+    assert np.isnan(bf16_from_bits(bf16_bits(snan))).all()
 
 
 def test_oracle_erf_within_abramowitz_stegun_bound():
