@@ -315,9 +315,10 @@ typedef struct ktir_rmw {
   int32_t op, order, dt, pad;
   int64_t n_rows;          /* destination rows covered by the head table */
   uint64_t head;           /* int32_t [n_rows] scratch: -1 in every entry on entry, and so left on return */
-  uint64_t link;           /* int32_t [n_inst * K] scratch */
-  uint64_t rows;           /* int32_t [n_inst * K] scratch: destination row of each entry */
-  uint64_t srcs;           /* int32_t [n_inst * K] scratch: source row of each entry */
+  uint64_t link;           /* int32_t [2 * n_inst * K] scratch (a successor slot per entry):
+                              -1 in every word on entry, and so left on return */
+  uint64_t rows;           /* int32_t [2 * n_inst * K] scratch: the record of each entry */
+  uint64_t srcs;           /* unused (0) */
 } ktir_rmw_t;
 int ktir_launch_row_rmw(const ktir_rmw_t* d);
 /* Which apply kernel ktir_launch_row_rmw takes for `d` (host-only, launches
@@ -330,7 +331,7 @@ int ktir_rmw_variant(const ktir_rmw_t* d);
 /* ktir_launch_row_rmw without caller scratch: no counterpart in the
  * reference; for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc).  head, link,
- * rows and srcs of `d` are ignored; the library's own 20 MiB device array
+ * rows and srcs of `d` are ignored; the library's own 24 MiB device array
  * (one per device, set up by ktir_init, kept until the process ends) holds
  * them.  Limits: n_rows <= 2^21 and n_inst * K <= 2^20, else
  * KTIR_E_UNSUPPORTED.  Allocates nothing.  All calls on one device share the

@@ -7,26 +7,29 @@
 // back, where a destination repeated inside one instance keeps the value of
 // its last position (computed from the row as it was before the instance).
 //
-//   pass 1 (one workgroup per instance): read the instance's K destination and
-//     source indices, find the surviving (last) position of every destination
-//     row inside the instance, and push survivors on the row's chain:
-//     link[e] = atomicExch(&head[row], e).  The entry that finds the chain
-//     empty (link[e] == -1) is the row's owner; entries that do not survive
-//     get link[e] = -2.
-//   pass 2: every row with a chain is applied once.  A row with one entry is
-//     a single load-combine-store; a longer chain is applied entry by entry
+//   pass 1 (rmw_link, one workgroup per instance): the instance's last
+//     position of every destination row survives (an LDS table keyed by a
+//     hash of the row keeps the largest position; a slot won by another row
+//     falls back to a scan).  A survivor e of row r exchanges itself into
+//     head[r]; the entry that finds head[r] empty is the row's owner, and
+//     every later arrival writes (its entry, its source row) into its
+//     predecessor's successor slot.  The record of entry e is the pair
+//     (r for an owner, -2 - r for a later arrival, -1 for an entry that does
+//     not survive; the source row).
+//   pass 2 (rmw_apply_rows / rmw_apply): the owner of each row reads its
+//     record and its successor slot together, so a row with one or two
+//     entries issues all its loads in one round trip; the entries are applied
 //     in ascending e, which is the reference's instance order, so the
-//     floating point accumulation order is exactly the reference's.  The
-//     common form (f32 rows, f16 / f32 sources) walks the head table in row
-//     order; other forms give each owner entry half a wavefront.  Pass 2
-//     resets every head it reads to -1, so the head table is all -1 between
-//     calls (the caller fills it once).
+//     floating point accumulation order is exactly the reference's.  Longer
+//     chains (rare) are walked.  Pass 2 leaves head[] and the successor slots
+//     at -1 again, so they are -1 between calls (the caller fills them once).
 #include "ktir_common.h"
 
 namespace ktir {
 
 typedef float gf4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gu2 __attribute__((ext_vector_type(2)));
+typedef int32_t gi2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int64_t read_index(uint64_t ptr, int dt, int64_t e, int64_t hi, bool* bad) {
   if (e < 0 || e >= hi) return 0;   // over-read of the index tensor reads zeros
@@ -58,31 +61,57 @@ __device__ __forceinline__ float combine(int op, int order, int dt, float dst, f
 }
 
 constexpr int RMW_MAXK = 1024;
+constexpr int RMW_TBL = 4096;   // LDS hash slots for the last-position test (>= 4 * RMW_MAXK)
 
 __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
   __shared__ int32_t rows[RMW_MAXK];
+  __shared__ int32_t tbl[RMW_TBL];
   const int64_t inst = blockIdx.x;
   const int64_t p0 = ((const int64_t*)d.dst_pos)[inst];
   const int64_t q0 = ((const int64_t*)d.src_pos)[inst];
+  const int K = (int)d.K;
+  // table size: a power of two, at least 4 slots per position
+  int tb = 64;
+  while (tb < 4 * K) tb <<= 1;
+  const int tshift = 32 - __builtin_ctz(tb);
   bool bad = false;
-  for (int k = threadIdx.x; k < d.K; k += blockDim.x) {
+  for (int i = threadIdx.x; i < tb; i += blockDim.x) tbl[i] = -1;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
     int64_t r = read_index(d.dst_idx_ptr, d.dst_idx_dtype, p0 + k, d.dst_idx_hi, &bad);
     rows[k] = (r >= 0 && r < d.n_rows) ? (int32_t)r : -1;
   }
   __syncthreads();
-  for (int k = threadIdx.x; k < d.K; k += blockDim.x) {
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    const int32_t r = rows[k];
+    if (r >= 0) atomicMax(&tbl[((uint32_t)r * 2654435761u) >> tshift], k);
+  }
+  __syncthreads();
+  int2* rec = (int2*)d.rows;
+  int2* nxt = (int2*)d.link;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
     const int64_t e = inst * d.K + k;
     const int32_t r = rows[k];
-    bool last = r >= 0;
-    for (int j = k + 1; j < d.K && last; ++j) last = rows[j] != r;
-    int32_t prev = -2;
-    if (last) {
-      int64_t s = read_index(d.src_idx_ptr, d.src_idx_dtype, q0 + k, d.src_idx_hi, &bad);
-      ((int32_t*)d.rows)[e] = r;
-      ((int32_t*)d.srcs)[e] = (int32_t)(s < 0x7fffffff ? s : 0x7fffffff);
-      prev = atomicExch(&((int32_t*)d.head)[r], (int32_t)e);
+    bool last = false;
+    if (r >= 0) {
+      const int w = tbl[((uint32_t)r * 2654435761u) >> tshift];
+      if (w == k) {
+        last = true;
+      } else if (rows[w] != r) {     // the slot's winner is another row: look for a later position of r
+        last = true;
+        for (int j = k + 1; j < K && last; ++j) last = rows[j] != r;
+      }
     }
-    ((int32_t*)d.link)[e] = prev;
+    int32_t code = -1, s32 = 0;
+    if (last) {
+      const int64_t s = read_index(d.src_idx_ptr, d.src_idx_dtype, q0 + k, d.src_idx_hi, &bad);
+      s32 = (int32_t)(s < 0x7fffffff ? s : 0x7fffffff);
+      const int32_t prev = atomicExch(&((int32_t*)d.head)[r], (int32_t)e);
+      // heads hold entries of this call only (-1 between calls); the bound
+      // keeps a corrupted head from turning into a stray write
+      if (prev >= 0 && prev < d.n_inst * d.K) nxt[prev] = make_int2((int32_t)e, s32);
+      code = prev >= 0 ? -2 - r : r;
+    }
+    rec[e] = make_int2(code, s32);
   }
   if (bad) *err = 1;
 }
@@ -122,87 +151,48 @@ __device__ __forceinline__ void store4(const ktir_rmw_t& d, int64_t e0, int64_t 
   }
 }
 
-__device__ __forceinline__ void apply_chain(const ktir_rmw_t& d, int32_t head, int64_t drow, int64_t c, bool vec,
-                                         float* v) {
-  const int32_t* link = (const int32_t*)d.link;
-  const int32_t* srcs = (const int32_t*)d.srcs;
-  int32_t prev = -1;
-  while (true) {
-    int32_t ent = 0x7fffffff;
-    for (int32_t x = head; x >= 0; x = link[x])
-      if (x > prev && x < ent) ent = x;
-    if (ent == 0x7fffffff) break;
-    prev = ent;
+// A chain of three or more entries (rare): starting from the owner (entry e,
+// source s), the successor slots list the others in arrival order; apply
+// them in ascending entry order by repeated selection (bounded walks).
+// Each arrival links only to an earlier one, so chains are acyclic and at most
+// n_entries long: that bound never cuts a chain short.
+template <typename SRC4>
+__device__ __forceinline__ void apply_long_chain(const ktir_rmw_t& d, int32_t e, int32_t s, int2 nx, int dt,
+                                                 float* x, SRC4 src4) {
+  const int2* nxt = (const int2*)d.link;
+  const int64_t bound = d.n_inst * d.K + 1;
+  int32_t prevm = -1;
+  for (int64_t it = 0; it < bound; ++it) {
+    int32_t m = 0x7fffffff, sm = 0;
+    if (e > prevm) { m = e; sm = s; }
+    int64_t steps = 0;
+    for (int2 t = nx; t.x >= 0 && t.x < bound - 1 && steps < bound; t = nxt[t.x], ++steps)
+      if (t.x > prevm && t.x < m) { m = t.x; sm = t.y; }
+    if (m == 0x7fffffff) break;
+    prevm = m;
     float g[4];
-    load4(d, false, d.src_base + (int64_t)srcs[ent] * d.src_row + c * d.src_col, c, vec, g);
-    for (int i = 0; i < 4; ++i) v[i] = combine(d.op, d.order, d.dt, v[i], g[i]);
+    src4(sm, g);
+    for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, dt, x[q], g[q]);
   }
 }
 
-// RMW_NE entries per half-wavefront (32 lanes x 4 columns cover a 128-wide
-// row per step): the entries' chain records are read together, then, for
-// owners, the chain heads and all rows, before anything is combined.
-constexpr int RMW_NE = 4;
-
-__global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d, int64_t n_entries) {
-  const int half = threadIdx.x / 32, hl = threadIdx.x % 32;
-  const bool vec = d.dst_col == 1 && d.src_col == 1 && d.dst_dtype == KTIR_F32 &&
-                   (d.src_dtype == KTIR_F16 || d.src_dtype == KTIR_F32) &&
-                   (d.dst_base % 4 == 0) && (d.dst_row % 4 == 0) && (d.src_base % 4 == 0) && (d.src_row % 4 == 0);
-  const int32_t* link = (const int32_t*)d.link;
-  const int32_t* rows = (const int32_t*)d.rows;
-  const int32_t* srcs = (const int32_t*)d.srcs;
-  const int32_t* head = (const int32_t*)d.head;
-  const int64_t step = (int64_t)gridDim.x * 8 * RMW_NE;
-  for (int64_t e0 = ((int64_t)blockIdx.x * 8 + half) * RMW_NE; e0 < n_entries; e0 += step) {
-    bool own[RMW_NE];
-    int32_t r[RMW_NE], sr[RMW_NE], h[RMW_NE];
-    // records of entries that do not survive are never read (their rows and
-    // sources were not written): read all, use the owners'
-#pragma unroll
-    for (int j = 0; j < RMW_NE; ++j) {
-      const int64_t e = e0 + j < n_entries ? e0 + j : e0;
-      own[j] = e0 + j < n_entries && link[e] == -1;
-      r[j] = rows[e];
-      sr[j] = srcs[e];
-    }
-#pragma unroll
-    for (int j = 0; j < RMW_NE; ++j) h[j] = own[j] ? head[r[j]] : 0;
-    // the row's owner leaves its head empty again for the next call
-#pragma unroll
-    for (int j = 0; j < RMW_NE; ++j)
-      if (own[j]) ((int32_t*)d.head)[r[j]] = -1;
-    for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
-      float v[RMW_NE][4], g[RMW_NE][4];
-#pragma unroll
-      for (int j = 0; j < RMW_NE; ++j) {
-        if (!own[j]) continue;
-        load4(d, true, d.dst_base + (int64_t)r[j] * d.dst_row + c * d.dst_col, c, vec, v[j]);
-        load4(d, false, d.src_base + (int64_t)sr[j] * d.src_row + c * d.src_col, c, vec, g[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < RMW_NE; ++j) {
-        if (!own[j]) continue;
-        const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
-        if (h[j] == (int32_t)(e0 + j)) {   // the row's only entry
-          for (int i = 0; i < 4; ++i) v[j][i] = combine(d.op, d.order, d.dt, v[j][i], g[j][i]);
-        } else {
-          apply_chain(d, h[j], de, c, vec, v[j]);
-        }
-        store4(d, de + c * d.dst_col, c, vec, v[j]);
-      }
-    }
+// Lane 0 of the owner's half-wave leaves the row's head and successor slots
+// empty again (after every lane has read them).
+__device__ __forceinline__ void rmw_reset(const ktir_rmw_t& d, int32_t r, int32_t e, int2 nx, int hl) {
+  __builtin_amdgcn_wave_barrier();
+  if (hl != 0) return;
+  ((int32_t*)d.head)[r] = -1;
+  int2* nxt = (int2*)d.link;
+  if (nx.x < 0) return;
+  int32_t y = e;
+  const int64_t bound = d.n_inst * d.K + 1;
+  for (int64_t steps = 0; y >= 0 && y < bound - 1 && steps < bound; ++steps) {
+    const int32_t y2 = nxt[y].x;
+    nxt[y] = make_int2(-1, -1);
+    y = y2;
   }
 }
 
-// The common form: f32 destination rows and f16 / f32 source rows, unit
-// column stride, 16-byte aligned rows, D a multiple of 128, f32 result.
-// Destination-row order: wave w covers rows 64 w .. 64 w + 63 (one head
-// entry per lane, read coalesced); the rows with a chain are compacted in
-// LDS with their head entry's link and source, then applied by half
-// wavefronts in ascending row order, so the row reads and writes of
-// neighbouring wavefronts fall on neighbouring addresses.  Each head is reset
-// to -1 once read.
 template <int SDT>
 __device__ __forceinline__ void rmw_src4(const ktir_rmw_t& d, int64_t se, float* g) {
   if (SDT == KTIR_F16) {
@@ -217,59 +207,133 @@ __device__ __forceinline__ void rmw_src4(const ktir_rmw_t& d, int64_t se, float*
   }
 }
 
-template <int SDT>
-__global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d) {
-  __shared__ int4 items[4][64];
-  const int wv = threadIdx.x / 64, l = threadIdx.x % 64, half = l / 32, hl = l % 32;
-  const int64_t r = ((int64_t)blockIdx.x * 4 + wv) * 64 + l;
-  const int32_t h = r < d.n_rows ? ((const KTIR_G(int32_t)*)d.head)[r] : -1;
-  const uint64_t mask = __ballot(h >= 0);
-  const int n = __popcll(mask);
-  if (h >= 0) {
-    const int rank = __popcll(mask & ((1ull << l) - 1));
-    const int32_t lk = ((const KTIR_G(int32_t)*)d.link)[h];
-    const int32_t sr = ((const KTIR_G(int32_t)*)d.srcs)[h];
-    items[wv][rank] = make_int4((int32_t)r, h, lk, sr);
-    ((KTIR_G(int32_t)*)d.head)[r] = -1;
+// The common form: f32 destination rows and f16 / f32 source rows, unit
+// column stride, 16-byte aligned rows, D a multiple of 128, f32 result.  A
+// half-wave takes RMW_NE consecutive entries; lane l covers columns
+// 4l .. 4l + 3 of each 128-column group.  An owner's record, its successor
+// slot, its destination row and every source row of a one- or two-entry
+// chain are loaded before anything is combined.
+constexpr int RMW_NE = 2;
+
+template <int SDT, bool D128>
+__global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_t n_entries) {
+  const int64_t hw = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 32;
+  const int hl = threadIdx.x % 32;
+  const int64_t e0 = hw * RMW_NE;
+  if (e0 >= n_entries) return;
+  const int64_t D = D128 ? 128 : d.D;
+  const KTIR_G(gi2)* rec = (const KTIR_G(gi2)*)d.rows;
+  KTIR_G(gi2)* nxt = (KTIR_G(gi2)*)d.link;
+  KTIR_G(int32_t)* head = (KTIR_G(int32_t)*)d.head;
+  int32_t r[RMW_NE], s[RMW_NE];
+  int2 nx[RMW_NE], n2[RMW_NE];
+  bool fast[RMW_NE];
+#pragma unroll
+  for (int j = 0; j < RMW_NE; ++j) {
+    const int64_t e = e0 + j < n_entries ? e0 + j : e0;
+    const gi2 t = rec[e], u = nxt[e];
+    r[j] = e0 + j < n_entries ? t.x : -1;
+    s[j] = t.y;
+    // a successor outside this call's entries cannot occur when the slots
+    // hold -1 on entry; such a value is never dereferenced
+    nx[j] = u.x >= 0 && u.x < n_entries ? make_int2(u.x, u.y) : make_int2(-1, -1);
   }
-  // the records are written and read by this wavefront only (its LDS
-  // operations complete in order)
-  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < RMW_NE; ++j) {
+    const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
+    const int64_t se = d.src_base + (int64_t)s[j] * d.src_row;
+    const int64_t se2 = d.src_base + (int64_t)nx[j].y * d.src_row;
+    // every row the owner touches lies inside its allocation (else the
+    // per-element path below: zeros past the end, dropped writes; memory.py:243-305)
+    fast[j] = r[j] >= 0 && de >= 0 && de + D <= d.dst_hi && se >= 0 && se + D <= d.src_hi &&
+              (nx[j].x < 0 || (se2 >= 0 && se2 + D <= d.src_hi));
+  }
   const KTIR_G(float)* dst = (const KTIR_G(float)*)d.dst_ptr;
-  for (int i = half; i < n; i += 2) {
-    const int4 it = items[wv][i];
-    const int64_t de = d.dst_base + (int64_t)it.x * d.dst_row;
-    const int64_t se = d.src_base + (int64_t)it.w * d.src_row;
-    // a source row outside its allocation (index past the table, or a
-    // negative index that the host reports after the launch) reads zeros and
-    // a destination row that ends past its allocation drops the columns
-    // there (memory.py:243-305): such rows take the per-element path
-    if (!(de >= 0 && de + d.D <= d.dst_hi && se >= 0 && se + d.D <= d.src_hi)) {
-      for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
-        float x[4], g[4];
-        load4(d, true, de + c, c, true, x);
-        if (it.z == -1) {
-          load4(d, false, se + c, c, true, g);
-          for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[q]);
-        } else {
-          apply_chain(d, it.y, de, c, true, x);
-        }
-        store4(d, de + c, c, true, x);
+  for (int64_t c = (int64_t)hl * 4; c < D; c += 128) {
+    gf4 v[RMW_NE];
+    float g[RMW_NE][4], g2[RMW_NE][4];
+    // the owner's rows, its successor's source row and the successor's own
+    // successor slot (a third entry) are all read in this one round trip
+#pragma unroll
+    for (int j = 0; j < RMW_NE; ++j) {
+      n2[j] = make_int2(-1, -1);
+      if (!fast[j]) continue;
+      v[j] = *(const KTIR_G(gf4)*)(dst + d.dst_base + (int64_t)r[j] * d.dst_row + c);
+      rmw_src4<SDT>(d, d.src_base + (int64_t)s[j] * d.src_row + c, g[j]);
+      if (nx[j].x >= 0) {
+        rmw_src4<SDT>(d, d.src_base + (int64_t)nx[j].y * d.src_row + c, g2[j]);
+        const gi2 t = nxt[nx[j].x];
+        n2[j] = make_int2(t.x, t.y);
       }
-      continue;
     }
+#pragma unroll
+    for (int j = 0; j < RMW_NE; ++j) {
+      if (!fast[j] || n2[j].x >= 0) continue;
+      float x[4] = {v[j][0], v[j][1], v[j][2], v[j][3]};
+      const bool second_first = nx[j].x >= 0 && nx[j].x < e0 + j;
+      if (second_first)
+        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g2[j][q]);
+      for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[j][q]);
+      if (nx[j].x >= 0 && !second_first)
+        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g2[j][q]);
+      if (hl == 0 && c + 128 >= D) {    // the row's last column group: leave its head and slot empty
+        head[r[j]] = -1;
+        if (nx[j].x >= 0) nxt[e0 + j] = gi2{-1, -1};
+      }
+      *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + d.dst_base + (int64_t)r[j] * d.dst_row + c) =
+          gf4{x[0], x[1], x[2], x[3]};
+    }
+  }
+  // chains of three or more entries and rows reaching past their allocation
+  // (rare): element by element, then the same resets
+#pragma unroll
+  for (int j = 0; j < RMW_NE; ++j) {
+    if (r[j] < 0 || (fast[j] && n2[j].x < 0)) continue;
+    const int32_t e = (int32_t)(e0 + j);
+    const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
+    for (int64_t c = (int64_t)hl * 4; c < D; c += 128) {
+      float x[4];
+      load4(d, true, de + c, c, true, x);
+      apply_long_chain(d, e, s[j], nx[j], KTIR_F32, x, [&](int32_t sm, float* gg) {
+        load4(d, false, d.src_base + (int64_t)sm * d.src_row + c, c, true, gg);
+      });
+      store4(d, de + c, c, true, x);
+    }
+    rmw_reset(d, r[j], e, nx[j], hl);
+  }
+}
+
+// Every other form (other dtypes, strided columns, any D): the same records,
+// element by element (16-byte accesses where the layout allows).
+__global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d, int64_t n_entries) {
+  const int64_t hw = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 32;
+  const int hl = threadIdx.x % 32;
+  const int64_t e0 = hw * RMW_NE;
+  if (e0 >= n_entries) return;
+  const bool vec = d.dst_col == 1 && d.src_col == 1 && d.dst_dtype == KTIR_F32 &&
+                   (d.src_dtype == KTIR_F16 || d.src_dtype == KTIR_F32) &&
+                   (d.dst_base % 4 == 0) && (d.dst_row % 4 == 0) && (d.src_base % 4 == 0) && (d.src_row % 4 == 0);
+  const int2* rec = (const int2*)d.rows;
+  const int2* nxt = (const int2*)d.link;
+#pragma unroll
+  for (int j = 0; j < RMW_NE; ++j) {
+    if (e0 + j >= n_entries) break;
+    const int32_t e = (int32_t)(e0 + j);
+    const int2 re = rec[e];
+    const int32_t r = re.x;
+    if (r < 0) continue;
+    const int32_t s = re.y;
+    const int2 nx = nxt[e].x < n_entries ? nxt[e] : make_int2(-1, -1);
+    const int64_t de = d.dst_base + (int64_t)r * d.dst_row;
     for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
-      const gf4 v = *(const KTIR_G(gf4)*)(dst + de + c);
-      float g[4];
-      rmw_src4<SDT>(d, se + c, g);
-      float x[4] = {v[0], v[1], v[2], v[3]};
-      if (it.z == -1) {   // the head entry was also the chain's first: one entry
-        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[q]);
-      } else {
-        apply_chain(d, it.y, de, c, true, x);
-      }
-      *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + de + c) = gf4{x[0], x[1], x[2], x[3]};
+      float x[4];
+      load4(d, true, de + c * d.dst_col, c, vec, x);
+      apply_long_chain(d, e, s, nx, d.dt, x, [&](int32_t sm, float* gg) {
+        load4(d, false, d.src_base + (int64_t)sm * d.src_row + c * d.src_col, c, vec, gg);
+      });
+      store4(d, de + c * d.dst_col, c, vec, x);
     }
+    rmw_reset(d, r, e, nx, hl);
   }
 }
 
@@ -302,15 +366,15 @@ extern "C" int ktir_rmw_variant(const ktir_rmw_t* d) {
 }
 
 // The allocation-free form keeps the head, link, rows and srcs arrays in one
-// file-scope device array: heads in a fixed region of RMW_NA_ROWS slots (all
-// -1 between calls), then link, rows and srcs in fixed regions of
-// RMW_NA_ENTRIES slots each, so no call's entries ever land in another call's
-// heads.  In host code `scratch` names a host-side stand-in; its device
+// file-scope device array: heads in a fixed region of RMW_NA_ROWS slots and
+// successor slots (link, two words per entry) in a fixed region, both -1
+// between calls, then the entry records (two words per entry) in a fixed
+// region, so no call's records ever land in another call's heads or links.  In host code `scratch` names a host-side stand-in; its device
 // address (one per device) comes from hipGetSymbolAddress, taken once per
 // device by rmw_scratch_setup with that device current.
 constexpr int64_t RMW_NA_ROWS = (int64_t)2 << 20;      // destination rows
 constexpr int64_t RMW_NA_ENTRIES = (int64_t)1 << 20;   // n_inst * K
-constexpr int64_t RMW_SCRATCH_WORDS = RMW_NA_ROWS + 3 * RMW_NA_ENTRIES;   // 20 MiB of int32
+constexpr int64_t RMW_SCRATCH_WORDS = RMW_NA_ROWS + 4 * RMW_NA_ENTRIES;   // 24 MiB of int32: heads, links, records
 constexpr int RMW_MAX_DEVICES = 64;
 __device__ __align__(256) int32_t scratch[RMW_SCRATCH_WORDS];
 static int32_t* g_scratch[RMW_MAX_DEVICES];
@@ -320,8 +384,8 @@ __global__ __launch_bounds__(256) void rmw_fill(int32_t* p, int64_t n, int32_t v
 }
 
 // Called by ktir_init with `device` current: the device address of this
-// device's copy of `scratch`, and every head slot set to -1 (the head table is
-// all -1 between calls: each launch resets the heads it uses).
+// device's copy of `scratch`, and every head and link slot set to -1 (they
+// are all -1 between calls: each launch resets the ones it uses).
 int ktir::rmw_scratch_setup(int device) {
   if (device < 0 || device >= RMW_MAX_DEVICES)
     return set_error(KTIR_E_UNSUPPORTED, "ktir_init: device %d beyond the %d the RMW scratch table covers", device,
@@ -329,7 +393,8 @@ int ktir::rmw_scratch_setup(int device) {
   if (g_scratch[device]) return KTIR_OK;
   int32_t* ptr = nullptr;
   KTIR_HIP_CHECK(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
-  hipLaunchKernelGGL(rmw_fill, dim3(1024), dim3(256), 0, stream(), ptr, RMW_NA_ROWS, (int32_t)-1);
+  hipLaunchKernelGGL(rmw_fill, dim3(1024), dim3(256), 0, stream(), ptr, RMW_NA_ROWS + 2 * RMW_NA_ENTRIES,
+                     (int32_t)-1);
   KTIR_HIP_CHECK(hipGetLastError());
   KTIR_HIP_CHECK(hipStreamSynchronize(stream()));
   g_scratch[device] = ptr;
@@ -355,8 +420,8 @@ extern "C" int ktir_launch_row_rmw_noalloc(const ktir_rmw_t* d) {
   int32_t* base = g_scratch[dev];
   w.head = (uint64_t)base;
   w.link = (uint64_t)(base + RMW_NA_ROWS);
-  w.rows = (uint64_t)(base + RMW_NA_ROWS + RMW_NA_ENTRIES);
-  w.srcs = (uint64_t)(base + RMW_NA_ROWS + 2 * RMW_NA_ENTRIES);
+  w.rows = (uint64_t)(base + RMW_NA_ROWS + 2 * RMW_NA_ENTRIES);
+  w.srcs = 0;
   return rmw_launch(&w);
 }
 
@@ -368,18 +433,20 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
 
 static int rmw_launch(const ktir_rmw_t* d) {
   if (d->n_inst == 0) return KTIR_OK;
-  int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
+  const int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());
   const int64_t total = d->n_inst * d->K;
+  const int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
   if (rmw_rows_form(d)) {
-    const int64_t blocks = (d->n_rows + 255) / 256;
-    if (d->src_dtype == KTIR_F16)
-      hipLaunchKernelGGL(rmw_apply_rows<KTIR_F16>, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
-    else
-      hipLaunchKernelGGL(rmw_apply_rows<KTIR_F32>, dim3((unsigned)blocks), dim3(256), 0, stream(), *d);
+    const bool d128 = d->D == 128;
+    if (d->src_dtype == KTIR_F16) {
+      if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+      else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+    } else {
+      if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+      else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+    }
   } else {
-    int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
-    if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(rmw_apply, dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
   }
   KTIR_HIP_CHECK(hipGetLastError());

@@ -316,12 +316,16 @@ def _row_rmw(ex, op, lb, st, trips):
     d.op, d.order, d.dt = rt.op(_RMW_OPS[val.op_type]), order, rt.DTYPE_CODE[res_dt]
     n_rows = max(1, -(-(ad.n_elems - int(bd[0])) // max(int(vd.strides[0]), 1)))
     d.n_rows = n_rows
-    # the chain heads: all -1 between calls (the launch resets what it uses)
+    # the chain heads and the successor slots: all -1 between calls (the
+    # launch resets what it uses), so they are filled once here
+    n_ent = max(1, n_inst * K)
     head = rt.DeviceBuffer(n_rows * 4)
     head.upload(np.full(n_rows, -1, np.int32))
-    scratch = [ex.pool.temp(max(1, n_inst * K) * 4) for _ in range(3)]
-    d.head, d.link, d.rows, d.srcs = head.ptr, scratch[0].ptr, scratch[1].ptr, scratch[2].ptr
-    keep += [head] + scratch
+    link = rt.DeviceBuffer(n_ent * 8)
+    link.upload(np.full(2 * n_ent, -1, np.int32))
+    records = ex.pool.temp(n_ent * 8)
+    d.head, d.link, d.rows, d.srcs = head.ptr, link.ptr, records.ptr, 0
+    keep += [head, link, records]
     grp = id(d)
     z = np.zeros(L, np.int64)
     ex.log(ad, True, z, (1,), (1,), whole=True, group=grp)
