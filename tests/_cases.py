@@ -183,3 +183,45 @@ def f16_patterns(n, seed=0, specials=True):
     else:
         v[~np.isfinite(v)] = np.float16(1.5)
     return v
+
+
+def gather_rows(rows=2048, dim=128, n_idx=1024, cores=8, chunk=64, seed=3):
+    """Plain blocked-indirect row gather: out[i, :] = table[idx[i], :] (f16),
+    chunk by chunk, no read-modify-write (the unfused indirect load path)."""
+    rng = np.random.default_rng(seed)
+    table = rng.standard_normal((rows, dim)).astype(np.float16)
+    idx = rng.integers(0, rows, n_idx).astype(np.int32)
+    per_core = n_idx // cores
+    nch = per_core // chunk
+    vss = f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {chunk - 1} >= 0, d1 >= 0, -d1 + {dim - 1} >= 0)>"
+    T = configs._t([chunk, dim], "f16")
+    src = f"""module {{
+  func.func @gather_rows(%table_ptr: index, %idx_ptr: index, %out_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %nch = arith.constant {nch} : index
+    %per_core = arith.constant {per_core} : index
+    %chunk = arith.constant {chunk} : index
+{configs._view("table_view", "table_ptr", [rows, dim], [dim, 1], "f16")}
+{configs._view("idx_view", "idx_ptr", [n_idx], [1], "i32")}
+{configs._view("out_view", "out_ptr", [n_idx, dim], [dim, 1], "f16")}
+    %core_base = arith.muli %core_id, %per_core : index
+    scf.for %ch = %c0 to %nch step %c1 : index {{
+      %ch_off = arith.muli %ch, %chunk : index
+      %row0 = arith.addi %core_base, %ch_off : index
+      %g_tile = ktdp.construct_indirect_access_tile intermediate_variables(%r, %c)
+          %table_view[ind(%idx_view[%row0 + %r]), (%c)] {{
+        variables_space_set = {vss},
+        variables_space_order = affine_map<(d0, d1) -> (d0, d1)>
+      }} : memref<{rows}x{dim}xf16>, memref<{n_idx}xi32> -> !ktdp.access_tile<{chunk}x{dim}xindex>
+      %g = ktdp.load %g_tile : !ktdp.access_tile<{chunk}x{dim}xindex> -> {T}
+{configs._tile("o_tile", "out_view", ["%row0", "%c0"], [chunk, dim], [n_idx, dim], "f16", "      ")}
+      ktdp.store %g, %o_tile : {T}, !ktdp.access_tile<{chunk}x{dim}xindex>
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+    return src, "gather_rows", dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((n_idx, dim), np.float16))

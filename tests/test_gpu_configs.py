@@ -76,6 +76,18 @@ def test_gather_scatter_add_rows_past_allocation(dim):
 
 
 @pytest.mark.parametrize("dim", [32, 128])
+def test_blocked_indirect_gather_bit_exact(dim):
+    """The unfused blocked-indirect row gather (indirect load, then a plain
+    store): bit-exact, and equal to table[idx] (reference
+    ops/memory_ops.py:224-486)."""
+    src, fn, kw = _cases.gather_rows(dim=dim)
+    ref, out, g = _run((src, fn, kw))
+    np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    np.testing.assert_array_equal(out["out_ptr"], kw["table_ptr"][kw["idx_ptr"]])
+    assert "rmw" not in g.last_plan.counts()
+
+
+@pytest.mark.parametrize("dim", [32, 128])
 def test_gather_scatter_add_negative_index_raises(dim):
     """A negative index raises IndexError (reference ops/memory_ops.py:378-382)."""
     from ktir_cpu_amd.interpreter import KTIRInterpreter
