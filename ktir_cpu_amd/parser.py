@@ -690,6 +690,18 @@ def _b_memory_view(op, toks, aliases):
     op.result_types = [mt]
 
 
+def _b_dist_view(op, toks, aliases):
+    """``ktdp.construct_distributed_memory_view (%p0, %p1 : memref, memref) : memref<GxH..>``:
+    the partition views and the global shape (``None`` for ``?``) and dtype
+    of the result type (reference dialects/ktdp_ops.py:109-140)."""
+    _generic(op, toks, aliases)
+    mt = op.result_types[0] if op.result_types else None
+    if not isinstance(mt, ShapedType) or mt.kind != "memref":
+        raise KTIRParseError("construct_distributed_memory_view: missing memref<> result type")
+    op.attributes["shape"] = tuple(mt.shape)
+    op.attributes["dtype"] = mt.elem
+
+
 def _b_access_tile(op, toks, aliases):
     view = next(t.text for t in toks if t.kind == "ssa")
     k = _idx(toks, "[")
@@ -1057,6 +1069,7 @@ def _b_yield(op, toks, aliases):
 _BUILDERS = {
     "ktdp.get_compute_tile_id": _b_tile_id,
     "ktdp.construct_memory_view": _b_memory_view,
+    "ktdp.construct_distributed_memory_view": _b_dist_view,
     "ktdp.construct_access_tile": _b_access_tile,
     "ktdp.construct_indirect_access_tile": _b_indirect_tile,
     "ktdp.load": _b_load,

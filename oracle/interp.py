@@ -163,6 +163,26 @@ class TileRef:
 
 
 @dataclass
+class DistributedMemRef:
+    """construct_distributed_memory_view (reference ir_types.py:267-316):
+    partition views, each with its coordinate set B_i in global coordinates."""
+    partitions: List[MemRef]
+    shape: Tuple
+    dtype: str
+
+
+@dataclass
+class DistributedTileRef:
+    """An access tile routed to partitions (reference memory_ops.py:986-1098):
+    per surviving partition (view, C_i, p_i) with C_i = B_i & (x + A) as a
+    Box or as a list of global points, p_i = min(B_i)."""
+    partitions: List[Tuple[MemRef, Any, Tuple]]
+    shape: Tuple
+    dtype: str
+    global_base: Tuple
+
+
+@dataclass
 class AccessTile:
     parent_ref: TileRef
     shape: Tuple
@@ -522,6 +542,51 @@ def indirect_store(ctx, tile: OracleTile, iat: IndirectAccessTile):
     mem_store(ctx, tile, tref, coords=coords)
 
 
+def _dist_sub(part: MemRef, C: Box, p_i) -> TileRef:
+    """The partition's sub-tile covering box C (global coordinates),
+    reference memory_ops.py:1101-1124."""
+    bpe = bytes_per_elem(part.dtype)
+    lo = [C.lo[d] - p_i[d] for d in range(len(C.lo))]
+    off = sum(l * s for l, s in zip(lo, part.strides)) * bpe
+    return TileRef(part.byte_address + off, tuple(h - l for l, h in zip(C.lo, C.hi)), list(part.strides), part,
+                   part.dtype)
+
+
+def distributed_load(ctx, dref: DistributedTileRef, out_shape) -> OracleTile:
+    """Reference memory_ops.py:1127-1196: each survivor's C_i, read from its
+    partition at C_i - p_i, lands at C_i - x of a zero tile."""
+    x = dref.global_base
+    nd = len(x)
+    out = np.zeros(out_shape, dtype=to_np_dtype(dref.dtype) if dref.dtype != "bf16" else np.float32)
+    for part, C, p_i in dref.partitions:
+        if isinstance(C, Box):
+            t = mem_load(ctx, _dist_sub(part, C, p_i))
+            out[tuple(slice(C.lo[d] - x[d], C.hi[d] - x[d]) for d in range(nd))] = t.data
+            continue
+        local = [tuple(c[d] - p_i[d] for d in range(nd)) for c in C]
+        offs = _flat_offsets(part.shape, part.strides, local)
+        data = _store_for(ctx, part).read(part.byte_address, len(offs), part.dtype, offsets=offs)
+        out[tuple(np.array([c[d] - x[d] for c in C], dtype=np.intp) for d in range(nd))] = data
+    _write_to_lx(ctx, _to_storage(out, dref.dtype))
+    return OracleTile(out, dref.dtype, tuple(out_shape))
+
+
+def distributed_store(ctx, tile: OracleTile, dref: DistributedTileRef):
+    """Reference memory_ops.py:1199-1259: only C_i is written in each partition."""
+    x = dref.global_base
+    nd = len(x)
+    for part, C, p_i in dref.partitions:
+        if isinstance(C, Box):
+            sl = tuple(slice(C.lo[d] - x[d], C.hi[d] - x[d]) for d in range(nd))
+            src = np.ascontiguousarray(tile.data[sl])
+            mem_store(ctx, OracleTile(src, part.dtype, src.shape), _dist_sub(part, C, p_i))
+            continue
+        local = [tuple(c[d] - p_i[d] for d in range(nd)) for c in C]
+        offs = _flat_offsets(part.shape, part.strides, local)
+        src = tile.data[tuple(np.array([c[d] - x[d] for c in C], dtype=np.intp) for d in range(nd))]
+        _store_for(ctx, part).write(part.byte_address, _to_storage(src, part.dtype), offsets=offs)
+
+
 # ---------------------------------------------------------------------------
 # Elementwise helpers (reference dialects/_helpers.py:39-72, ops/_helpers.py)
 # ---------------------------------------------------------------------------
@@ -719,6 +784,7 @@ class OracleInterpreter:
                 ptrs[name] = (stick * STICK_BYTES) // bytes_per_elem(dt)
             else:
                 ptrs[name] = t
+        self.lxs = lxs
         if self.prepare_hook is not None:
             self.prepare_hook(self)
         counts = _use_counts(fn.operations)
@@ -806,6 +872,68 @@ class OracleInterpreter:
         lx = a.get("lx_core_id") if a["memory_space"] == "LX" else None
         return MemRef(ptr, shape, strides, a["memory_space"], a["dtype"], cs, lx)
 
+    def _h_ktdp_construct_distributed_memory_view(self, op, ctx):
+        """Reference dialects/ktdp_ops.py:109-140 with ir_types.py:176-265:
+        dynamic global dims take the partitions' extent max(hi); a declared
+        dim must equal it."""
+        parts = [ctx.get_value(n) for n in op.operands]
+        for i, p in enumerate(parts):
+            if not isinstance(p, MemRef):
+                raise ValueError(f"construct_distributed_memory_view: operand {i} is {type(p).__name__}, "
+                                 f"expected MemRef")
+            if p.coordinate_set is None:
+                raise ValueError(f"DistributedMemRef partition {i} must have a coordinate_set")
+        a = op.attributes
+        if "shape" not in a or "dtype" not in a:
+            raise ValueError("construct_distributed_memory_view: missing required attributes 'shape'/'dtype'")
+        shape = list(a["shape"])
+        for axis in range(len(shape)):
+            his = [p.coordinate_set.hi[axis] for p in parts if isinstance(p.coordinate_set, Box)]
+            ext = max(his) if his else None
+            if shape[axis] is None:
+                if ext is None:
+                    raise ValueError("construct_distributed_memory_view: dynamic axis with no box partition")
+                shape[axis] = ext
+            elif ext is not None and shape[axis] != ext:
+                raise ValueError(f"construct_distributed_memory_view: declared dim {shape[axis]} on axis {axis} "
+                                 f"does not match the partition extent {ext}")
+        for i, p in enumerate(parts):
+            if p.dtype != a["dtype"]:
+                raise ValueError(f"DistributedMemRef partition {i} dtype {p.dtype!r} does not match view dtype "
+                                 f"{a['dtype']!r}")
+        return DistributedMemRef(parts, tuple(shape), a["dtype"])
+
+    def _dist_tile_access(self, dist: DistributedMemRef, access_shape, x, A):
+        """Reference memory_ops.py:986-1098: C_i = B_i & (x + A) per partition."""
+        nd = len(dist.shape)
+        xA = Box(tuple(l + x[d] for d, l in enumerate(A.lo)), tuple(h + x[d] for d, h in enumerate(A.hi))) \
+            if isinstance(A, Box) else None
+        survivors = []
+        for part in dist.partitions:
+            B = part.coordinate_set
+            if isinstance(B, Box) and xA is not None:
+                lo = tuple(max(a, b) for a, b in zip(B.lo, xA.lo))
+                hi = tuple(min(a, b) for a, b in zip(B.hi, xA.hi))
+                if any(h <= l for l, h in zip(lo, hi)):
+                    continue
+                survivors.append((part, Box(lo, hi), tuple(B.lo)))
+                continue
+            pts = B.enumerate() if isinstance(B, Box) else B.enumerate(dist.shape)
+            if not pts:
+                continue
+            p_i = tuple(min(pt[d] for pt in pts) for d in range(nd))
+            if A is None:
+                inside = lambda pt: all(0 <= pt[d] - x[d] < access_shape[d] for d in range(nd))
+            else:
+                inside = lambda pt: A.contains(tuple(pt[d] - x[d] for d in range(nd)))
+            C = [tuple(pt) for pt in pts if inside(pt)]
+            if C:
+                survivors.append((part, C, p_i))
+        if not survivors:
+            raise ValueError(f"distributed_tile_access: no partition covers access region global_base={tuple(x)} "
+                             f"shape={tuple(access_shape)}")
+        return DistributedTileRef(survivors, dist.shape, dist.dtype, tuple(x))
+
     def _h_ktdp_construct_access_tile(self, op, ctx):
         parent = ctx.get_value(op.operands[0])
         idx = [ctx.get_value(o) for o in op.operands[1:]]
@@ -813,6 +941,10 @@ class OracleInterpreter:
         cs = a["coordinate_set"]
         if isinstance(cs, Box) and not cs.is_concrete:
             raise NotImplementedError("construct_access_tile: symbolic access_tile_set is not supported")
+        if isinstance(parent, DistributedMemRef):
+            dref = self._dist_tile_access(parent, tuple(a["shape"]), tuple(int(v) for v in a["base_map"].eval(idx)),
+                                          cs)
+            return AccessTile(dref, tuple(a["shape"]), a["base_map"], cs, a.get("coordinate_order"))
         base = a["base_map"].eval(idx)
         bpe = bytes_per_elem(parent.dtype)
         off = sum(int(c) * int(s) for c, s in zip(base, parent.strides))
@@ -864,6 +996,8 @@ class OracleInterpreter:
         rs = op.attributes.get("_result_shape")
         if isinstance(at, IndirectAccessTile):
             return indirect_load(ctx, at, rs if rs is not None else at.shape)
+        if isinstance(at.parent_ref, DistributedTileRef):
+            return distributed_load(ctx, at.parent_ref, tuple(rs) if rs is not None else tuple(at.shape))
         cs, co = at.coordinate_set, at.coordinate_order
         if isinstance(cs, Box) and co is None:
             return mem_load(ctx, _subtile(at.parent_ref, cs))
@@ -879,6 +1013,9 @@ class OracleInterpreter:
         at = ctx.get_value(op.operands[1])
         if isinstance(at, IndirectAccessTile):
             indirect_store(ctx, val, at)
+            return None
+        if isinstance(at.parent_ref, DistributedTileRef):
+            distributed_store(ctx, val, at.parent_ref)
             return None
         cs, co = at.coordinate_set, at.coordinate_order
         if isinstance(cs, Box) and co is None:

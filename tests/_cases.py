@@ -225,3 +225,148 @@ def gather_rows(rows=2048, dim=128, n_idx=1024, cores=8, chunk=64, seed=3):
 }}
 """
     return src, "gather_rows", dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((n_idx, dim), np.float16))
+
+
+# ---------------------------------------------------------------------------
+# distributed memory views (two partitions of a 4 x 4 f16 tensor)
+# ---------------------------------------------------------------------------
+
+# (id, p0, p1, access shape, access indices); a partition is
+# (rows (first, last), cols (first, last), space, strides, element address).
+# The layouts and expected slices are the reference's test table
+# (tests/test_distributed_view.py:207-470): the tensor is arange(16) and
+# the result is its access-tile slice.
+DIST_CASES = [
+    ("row_hbm_hbm_full", ((0, 1), (0, 3), "HBM", (4, 1), 0), ((2, 3), (0, 3), "HBM", (4, 1), 4096), (4, 4), (0, 0)),
+    ("row_hbm_hbm_partial_p1_pruned", ((0, 1), (0, 3), "HBM", (4, 1), 0), ((2, 3), (0, 3), "HBM", (4, 1), 4096),
+     (2, 4), (0, 0)),
+    ("row_hbm_hbm_subtile_nonzero", ((0, 1), (0, 3), "HBM", (4, 1), 0), ((2, 3), (0, 3), "HBM", (4, 1), 4096),
+     (2, 2), (1, 1)),
+    ("row_hbm_lx_col_packed_full", ((0, 1), (0, 3), "HBM", (4, 1), 0), ((2, 3), (0, 3), "LX", (1, 4), 4096),
+     (4, 4), (0, 0)),
+    ("row_lx_hbm_col_packed_full", ((0, 1), (0, 3), "LX", (1, 4), 0), ((2, 3), (0, 3), "HBM", (4, 1), 4096),
+     (4, 4), (0, 0)),
+    ("row_hbm_lx_subtile_nonzero", ((0, 1), (0, 3), "HBM", (4, 1), 0), ((2, 3), (0, 3), "LX", (1, 4), 4096),
+     (2, 2), (1, 1)),
+    ("row_hbm_hbm_unequal_full", ((0, 0), (0, 3), "HBM", (4, 1), 0), ((1, 3), (0, 3), "HBM", (4, 1), 4096),
+     (4, 4), (0, 0)),
+    ("row_hbm_hbm_unequal_partial_p0_pruned", ((0, 0), (0, 3), "HBM", (4, 1), 0),
+     ((1, 3), (0, 3), "HBM", (4, 1), 4096), (2, 4), (1, 0)),
+    ("col_hbm_hbm_full", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((0, 3), (2, 3), "HBM", (2, 1), 4096), (4, 4), (0, 0)),
+    ("col_hbm_hbm_partial_p1_pruned", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((0, 3), (2, 3), "HBM", (2, 1), 4096),
+     (4, 2), (0, 0)),
+    ("col_hbm_hbm_subtile_nonzero", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((0, 3), (2, 3), "HBM", (2, 1), 4096),
+     (2, 2), (1, 1)),
+    ("col_hbm_lx_col_packed_full", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((0, 3), (2, 3), "LX", (1, 4), 4096),
+     (4, 4), (0, 0)),
+    ("mixed_left_block_only", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((2, 3), (2, 3), "HBM", (2, 1), 4096),
+     (4, 2), (0, 0)),
+    ("mixed_bottom_left_only", ((0, 3), (0, 1), "HBM", (2, 1), 0), ((2, 3), (2, 3), "HBM", (2, 1), 4096),
+     (2, 2), (2, 0)),
+    ("mixed_lx_left_hbm_right_bottom_only", ((0, 3), (0, 1), "LX", (1, 4), 0), ((2, 3), (2, 3), "HBM", (2, 1), 4096),
+     (2, 2), (2, 0)),
+]
+DIST_OUT = 8192      # element address of the output (f16)
+
+
+def _box_set(r0, r1, c0, c1):
+    return f"affine_set<(d0, d1) : (d0 - {r0} >= 0, -d0 + {r1} >= 0, d1 - {c0} >= 0, -d1 + {c1} >= 0)>"
+
+
+def _space(sp, ct=None):
+    if sp == "HBM":
+        return "#ktdp.memory_space<global>"
+    return "#ktdp.memory_space<ct_local>" if ct is None else f"#ktdp.memory_space<ct_local, ct_id = {ct}>"
+
+
+def dist_copy(p0, p1, ashape, idx, gshape=(4, 4)):
+    """Load an access tile of a two-partition distributed view at literal
+    element addresses and store it to a contiguous output at DIST_OUT."""
+    parts = []
+    for k, (rows, cols, sp, st, addr) in enumerate((p0, p1)):
+        nr, nc = rows[1] - rows[0] + 1, cols[1] - cols[0] + 1
+        parts.append(f"""    %a{k} = arith.constant {addr} : index
+    %P{k} = ktdp.construct_memory_view %a{k}, sizes: [{nr}, {nc}], strides: [{st[0]}, {st[1]}] {{
+      coordinate_set = {_box_set(rows[0], rows[1], cols[0], cols[1])}, memory_space = {_space(sp)}
+    }} : memref<{nr}x{nc}xf16>""")
+    m = lambda p: f"memref<{p[0][1] - p[0][0] + 1}x{p[1][1] - p[1][0] + 1}xf16>"
+    acs = _box_set(0, ashape[0] - 1, 0, ashape[1] - 1)
+    G = f"memref<{gshape[0]}x{gshape[1]}xf16>"
+    return f"""module {{
+  func.func @dist_copy() attributes {{grid = [1, 1]}} {{
+    %c0 = arith.constant 0 : index
+    %i0 = arith.constant {idx[0]} : index
+    %i1 = arith.constant {idx[1]} : index
+{parts[0]}
+{parts[1]}
+    %A = ktdp.construct_distributed_memory_view (%P0, %P1 : {m(p0)}, {m(p1)}) : {G}
+    %ob = arith.constant {DIST_OUT} : index
+    %B = ktdp.construct_memory_view %ob, sizes: [{ashape[0]}, {ashape[1]}], strides: [{ashape[1]}, 1] {{
+      coordinate_set = {acs}, memory_space = #ktdp.memory_space<global>
+    }} : memref<{ashape[0]}x{ashape[1]}xf16>
+    %at = ktdp.construct_access_tile %A[%i0, %i1] {{
+      access_tile_set = {acs}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>
+    }} : {G} -> !ktdp.access_tile<{ashape[0]}x{ashape[1]}xindex>
+    %bt = ktdp.construct_access_tile %B[%c0, %c0] {{
+      access_tile_set = {acs}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>
+    }} : memref<{ashape[0]}x{ashape[1]}xf16> -> !ktdp.access_tile<{ashape[0]}x{ashape[1]}xindex>
+    %v = ktdp.load %at : !ktdp.access_tile<{ashape[0]}x{ashape[1]}xindex> -> tensor<{ashape[0]}x{ashape[1]}xf16>
+    ktdp.store %v, %bt : tensor<{ashape[0]}x{ashape[1]}xf16>, !ktdp.access_tile<{ashape[0]}x{ashape[1]}xindex>
+    return
+  }}
+}}
+"""
+
+
+def strided_block(block, strides):
+    """The memory image of a 2-D block laid out with element `strides`
+    (holes zero), as the reference's test seeds partitions."""
+    r, c = np.indices(block.shape)
+    offs = (r * strides[0] + c * strides[1]).reshape(-1)
+    buf = np.zeros(int(offs.max()) + 1, dtype=block.dtype)
+    buf[offs] = block.reshape(-1)
+    return buf
+
+
+def dist_copy_2core():
+    """A 192 x 64 f16 tensor over three partitions: rows 0..95 in HBM
+    (row-major), rows 96..127 in core 0's LX (column-major, ct_id = 0), rows
+    128..191 in core 1's LX (row-major, ct_id = 1).  Core c copies rows
+    96c .. 96c + 95 to the output, so core 1 reads core 0's LX."""
+    sets = [_box_set(0, 95, 0, 63), _box_set(96, 127, 0, 63), _box_set(128, 191, 0, 63)]
+    acs = _box_set(0, 95, 0, 63)
+    return f"""module {{
+  func.func @dist_rows() attributes {{grid = [2, 1]}} {{
+    %core = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %c96 = arith.constant 96 : index
+    %row = arith.muli %core, %c96 : index
+    %ah = arith.constant 0 : index
+    %al0 = arith.constant 12288 : index
+    %al1 = arith.constant 16384 : index
+    %ab = arith.constant 24576 : index
+    %H = ktdp.construct_memory_view %ah, sizes: [96, 64], strides: [64, 1] {{
+      coordinate_set = {sets[0]}, memory_space = {_space("HBM")}
+    }} : memref<96x64xf16>
+    %L0 = ktdp.construct_memory_view %al0, sizes: [32, 64], strides: [1, 32] {{
+      coordinate_set = {sets[1]}, memory_space = {_space("LX", 0)}
+    }} : memref<32x64xf16>
+    %L1 = ktdp.construct_memory_view %al1, sizes: [64, 64], strides: [64, 1] {{
+      coordinate_set = {sets[2]}, memory_space = {_space("LX", 1)}
+    }} : memref<64x64xf16>
+    %A = ktdp.construct_distributed_memory_view (%H, %L0, %L1 : memref<96x64xf16>, memref<32x64xf16>, memref<64x64xf16>) : memref<192x64xf16>
+    %B = ktdp.construct_memory_view %ab, sizes: [192, 64], strides: [64, 1] {{
+      coordinate_set = {_box_set(0, 191, 0, 63)}, memory_space = {_space("HBM")}
+    }} : memref<192x64xf16>
+    %at = ktdp.construct_access_tile %A[%row, %c0] {{
+      access_tile_set = {acs}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>
+    }} : memref<192x64xf16> -> !ktdp.access_tile<96x64xindex>
+    %bt = ktdp.construct_access_tile %B[%row, %c0] {{
+      access_tile_set = {acs}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>
+    }} : memref<192x64xf16> -> !ktdp.access_tile<96x64xindex>
+    %v = ktdp.load %at : !ktdp.access_tile<96x64xindex> -> tensor<96x64xf16>
+    ktdp.store %v, %bt : tensor<96x64xf16>, !ktdp.access_tile<96x64xindex>
+    return
+  }}
+}}
+"""
