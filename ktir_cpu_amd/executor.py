@@ -51,7 +51,8 @@ class Alloc:
     addr: int          # reference byte address (stick-aligned, from 0x10000)
     nbytes: int
     shape: Tuple[int, ...]
-    off: int = 0       # byte offset inside the device arena
+    off: int = 0       # byte offset inside the device arena (or inside `buf`)
+    buf: Any = None    # a device buffer of its own (the LX space), else the arena's
 
     @property
     def n_elems(self) -> int:
@@ -102,7 +103,45 @@ class Arena:
         raise ValueError(f"Read from unmapped address 0x{int(addr):x}")
 
     def ptr_of(self, a: Alloc) -> int:
-        return self.buf.ptr + a.off
+        return (a.buf if a.buf is not None else self.buf).ptr + a.off
+
+
+class LXSpace:
+    """Every core's LX scratchpad (reference ``memory.py:400-446``) in one
+    device buffer: core c's byte b lives at ``c * bytes_per_core + b``.
+
+    Reads and writes address LX as a flat per-core byte array: bytes never
+    written read zero, and an access that leaves ``[0, bytes_per_core)``
+    is refused by the walker.  One allocation record (byte-sized elements)
+    stands for the whole space, so the hazard check sees two lanes that
+    touch the same core's bytes, whatever their dtypes."""
+
+    def __init__(self, n_cores: int, bytes_per_core: int):
+        self.n_cores = int(n_cores)
+        self.bytes_per_core = int(bytes_per_core)
+        total = self.n_cores * self.bytes_per_core
+        self.buf = rt.DeviceBuffer(total)
+        self.alloc = Alloc("__lx__", "i8", -1, total, (total,), 0, self.buf)
+        self.seeds: List[Tuple[int, int, np.ndarray]] = []
+
+    def seed(self, seeds: List[Tuple[int, int, np.ndarray]]):
+        """(core, byte address, data) written before the run; zero elsewhere."""
+        for core, addr, data in seeds:
+            raw = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
+            if not (0 <= core < self.n_cores) or addr < 0 or addr + raw.size > self.bytes_per_core:
+                raise NotImplementedError(f"LX seed of {raw.size} bytes at 0x{addr:x} on core {core} lies outside "
+                                          f"the {self.bytes_per_core}-byte scratchpad")
+        self.seeds = list(seeds)
+        self.reset()
+
+    def reset(self):
+        self.buf.memset(0)
+        for core, addr, data in self.seeds:
+            raw = np.ascontiguousarray(data).reshape(-1).view(np.uint8)
+            self.buf.upload(raw, core * self.bytes_per_core + addr)
+
+    def free(self):
+        self.buf.free()
 
 
 # ---------------------------------------------------------------------------
@@ -195,9 +234,36 @@ class View:
     dtype: str
     space: str
     cs: Any = None
+    core: Optional[np.ndarray] = None   # LX views: per-lane core whose scratchpad is addressed
 
     def take(self, idx):
-        return View(self.base[idx], self.shape, self.strides, self.dtype, self.space, self.cs)
+        return View(self.base[idx], self.shape, self.strides, self.dtype, self.space, self.cs,
+                    None if self.core is None else self.core[idx])
+
+
+@dataclass
+class DistView:
+    """ktdp.construct_distributed_memory_view (reference ir_types.py:126-316):
+    partition views, each with a box coordinate set in global coordinates."""
+    parts: List[View]
+    shape: Tuple[int, ...]
+    dtype: str
+
+    def take(self, idx):
+        return DistView([p.take(idx) for p in self.parts], self.shape, self.dtype)
+
+
+@dataclass
+class DistATile:
+    """An access tile over a distributed view: per-lane global origin `x`
+    (one array per dimension) and the access tile set."""
+    dist: DistView
+    x: Tuple[np.ndarray, ...]
+    shape: Tuple[int, ...]
+    cs: Any
+
+    def take(self, idx):
+        return DistATile(self.dist.take(idx), tuple(v[idx] for v in self.x), self.shape, self.cs)
 
 
 @dataclass

@@ -128,6 +128,8 @@ def _kloop_matmul(ex, op, lb, st, trips, init: Tile):
         if not np.array_equal(al.origin, a0.origin + (T - 1) * dk):
             return None
         v = a0.view
+        if v.space != "HBM":
+            return None
         lo_off = sum(int(l) * int(s) for l, s in zip(a0.cs.lo, v.strides))
         shape = a0.cs.extent
         spec, alloc, rel = ex._hbm_leaf(v, a0.origin + lo_off, shape, v.strides)
@@ -799,7 +801,7 @@ def _attention_loop(ex, op, lb, st, trips, inits):
         if np.any(d != d.flat[0]) or not np.array_equal(al.origin, a0.origin + tm1 * d.flat[0]):
             return None
         v = a0.view
-        if v.dtype != dtype:
+        if v.dtype != dtype or v.space != "HBM":
             return None
         ext = tuple(a0.cs.extent)
         big = [i for i, e in enumerate(ext) if e != 1]

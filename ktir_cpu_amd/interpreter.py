@@ -19,7 +19,7 @@ from typing import Any, Dict, List, Optional
 import numpy as np
 
 from . import runtime as rt
-from .executor import Arena, NeedEager, Plan, Pool, STICK_BYTES
+from .executor import Arena, LXSpace, NeedEager, Plan, Pool, STICK_BYTES
 from .ir import IRModule
 from .latency import LatencyReport, LatencyTracker
 from .memory import DeviceMemory
@@ -39,6 +39,20 @@ def ktir_dtype_of(arr: np.ndarray) -> str:
         raise ValueError(f"Unsupported array dtype {arr.dtype} (reference dtypes.py:24-39 plus bf16 as uint16)")
 
 
+def _uses_lx(ops) -> bool:
+    """Whether any memory view of the function lies in LX (ct_local)."""
+    for op in ops:
+        if op.attributes.get("memory_space") == "LX":
+            return True
+        if any(_uses_lx(r.ops) for r in op.regions):
+            return True
+    return False
+
+
+# the LX space of one run (cores x LX bytes) is refused above this size
+MAX_LX_SPACE = 32 << 30
+
+
 def _storage_dtype(arr: np.ndarray) -> str:
     """KTIR dtype of a staged HBM seed (any host dtype: one of the same size)."""
     try:
@@ -52,8 +66,9 @@ class Prepared:
     `run()` replays the device work only (no host walk, no copies)."""
 
     def __init__(self, interp: "KTIRInterpreter", fn_name: str, names: List[str], plan: Plan, arena: Arena,
-                 arrays: Dict[str, np.ndarray], initial: Optional[Dict[str, np.ndarray]] = None):
+                 arrays: Dict[str, np.ndarray], initial: Optional[Dict[str, np.ndarray]] = None, lx=None):
         self.interp = interp
+        self.lx = lx
         self.fn_name = fn_name
         self.names = names
         self.plan = plan
@@ -68,6 +83,8 @@ class Prepared:
         for a in self.arena.allocs:
             arr = self.initial[a.name]
             self.arena.buf.upload(np.ascontiguousarray(arr).reshape(-1).view(np.uint8), a.off)
+        if self.lx is not None:
+            self.lx.reset()
 
     def outputs(self) -> Dict[str, np.ndarray]:
         """Every array argument read back (staged HBM seeds are not arguments)."""
@@ -97,6 +114,7 @@ class KTIRInterpreter:
         self.last_plan: Optional[Plan] = None
         self._arena = Arena()
         self._pool = None
+        self._lx: Optional[LXSpace] = None
         self.memory: Optional[DeviceMemory] = None
         # latency model (reference interpreter.py:76-78): charged op by op during the run
         self._latency_tracker = LatencyTracker(latency_config, trace=trace_latency) if latency_config is not None \
@@ -163,6 +181,19 @@ class KTIRInterpreter:
         if self._pool is not None:
             self._pool.free_all()
         self._pool = Pool()
+        if self._lx is not None:
+            self._lx.free()
+            self._lx = None
+        seeds = self.memory.lx_seeds()
+        if seeds or _uses_lx(fn.operations):
+            nx, ny, nz = fn.grid
+            per = self.memory.lx_size_mb * 1024 * 1024
+            if nx * ny * nz * per > MAX_LX_SPACE:
+                raise NotImplementedError(f"LX space of {nx * ny * nz} cores x {per} bytes exceeds "
+                                          f"{MAX_LX_SPACE} bytes")
+            self._lx = LXSpace(nx * ny * nz, per)
+            self._lx.seed(seeds)
+        self.memory.attach_lx(self._lx)
         arena = Arena()
         arena.layout(specs)
         self._arena = arena
@@ -184,18 +215,21 @@ class KTIRInterpreter:
             nx, ny, nz = fn.grid
             lat.reset()
             lat.set_cores_active(nx * ny * nz)
-            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb, latency=lat)
+            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb, latency=lat,
+                          lx=self._lx)
             plan = ex.run()
             plan.fallback_reason = "latency model"
         else:
             try:
-                ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb)
+                ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb,
+                              lx=self._lx)
                 plan = ex.run()
                 plan.run()
             except NeedEager as why:
-                ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb)
+                ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb,
+                              lx=self._lx)
                 plan = ex.run()
                 plan.fallback_reason = str(why)
         rt.sync()
         self.last_plan = plan
-        return Prepared(self, fn_name, list(arrays), plan, arena, arrays, initial)
+        return Prepared(self, fn_name, list(arrays), plan, arena, arrays, initial, self._lx)

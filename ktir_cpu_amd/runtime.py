@@ -229,6 +229,11 @@ class DeviceBuffer:
         assert dst.flags.c_contiguous and offset + dst.nbytes <= self.nbytes
         check(lib().ktir_memcpy_d2h(dst.ctypes.data, self.ptr + offset, dst.nbytes), "ktir_memcpy_d2h")
 
+    def memset(self, value: int = 0, offset: int = 0, nbytes: Optional[int] = None):
+        n = self.nbytes - offset if nbytes is None else int(nbytes)
+        assert offset + n <= self.nbytes
+        check(lib().ktir_memset(self.ptr + offset, int(value), n), "ktir_memset")
+
     def download(self, nbytes: int, offset: int = 0) -> bytes:
         out = np.empty(nbytes, dtype=np.uint8)
         check(lib().ktir_memcpy_d2h(out.ctypes.data, self.ptr + offset, nbytes), "ktir_memcpy_d2h")

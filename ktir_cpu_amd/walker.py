@@ -16,7 +16,7 @@ import numpy as np
 
 from . import runtime as rt
 from .affine import AffineMap, AffineSet, Box, evaluate
-from .executor import (Access, Alloc, Arena, ATile, IATile, Instances, Lanes, NeedEager, Plan, Pool, Tile,
+from .executor import (Access, Alloc, Arena, ATile, DistATile, DistView, IATile, Instances, Lanes, NeedEager, Plan, Pool, Tile,
                        View, _launch, verify)
 from .ir import IRFunction, Operation, Region
 from .program import CompileError, Expr, LaneOff, LeafSpec, compile_program, is_float, round_host, topo
@@ -256,7 +256,7 @@ def take_value(v, idx: np.ndarray):
         return v[idx]
     if isinstance(v, Tile):
         return Tile(remap_lanes(v.e, idx))
-    if isinstance(v, (View, ATile, IATile)):
+    if isinstance(v, (View, ATile, IATile, DistView, DistATile)):
         return v.take(idx)
     if isinstance(v, tuple):
         return tuple(take_value(x, idx) for x in v)
@@ -286,8 +286,11 @@ class _Level:
 
 class Executor:
     def __init__(self, fn: IRFunction, arena: Arena, args: Dict[str, Any], pool: Pool, *, sequential: bool,
-                 lx_size_mb: int = 2, allow_expand: bool = True, latency=None):
+                 lx_size_mb: int = 2, allow_expand: bool = True, latency=None, lx=None):
         self.fn = fn
+        # every core's LX scratchpad on the device (executor.LXSpace), or None
+        # when the function addresses no LX memory
+        self.lx = lx
         # latency model (ktir_cpu_amd.latency.LatencyTracker) charged op by op, or None
         self.lat = latency
         self._lat_mem: Optional[np.ndarray] = None
@@ -537,10 +540,11 @@ class Executor:
                         raise NotImplementedError("access tile spans several argument tensors across lanes")
         return a0
 
-    def _hbm_leaf(self, view: View, origin: np.ndarray, shape, strides) -> Tuple[LeafSpec, Alloc, np.ndarray]:
+    def _hbm_leaf(self, view: View, origin: np.ndarray, shape, strides,
+                  offs: Optional[np.ndarray] = None) -> Tuple[LeafSpec, Alloc, np.ndarray]:
         bpe = rt.ELEM_BYTES[view.dtype]
         if view.space != "HBM":
-            raise NotImplementedError("LX (ct_local) memory views are not supported by the GPU backend")
+            return self._lx_leaf(view, origin, shape, strides, offs)
         elem = view.base.astype(np.int64) + origin.astype(np.int64)
         a = self._alloc_of(elem * bpe)
         if rt.ELEM_BYTES[a.dtype] != bpe:
@@ -549,10 +553,55 @@ class Executor:
         spec = LeafSpec(self.arena.ptr_of(a), view.dtype, LaneOff.from_array(rel), strides, 0, a.n_elems, alloc=a)
         return spec, a, rel
 
-    def log(self, alloc, store, base, shape, strides, whole=False, group=None):
+    def _lx_leaf(self, view: View, origin: np.ndarray, shape, strides, offs: Optional[np.ndarray] = None,
+                 span: Optional[Tuple[np.ndarray, np.ndarray]] = None):
+        """A leaf over the addressed core's LX: element `core * (bytes per
+        core / bpe) + pointer + origin` of the LX space.  Refuses an access
+        that leaves the core's scratchpad (`offs`: the element offsets of an
+        offset-list access shared by all lanes; `span`: per-lane [lo, hi)
+        element offsets, lanes with an empty span access nothing)."""
+        lx = self.lx
+        bpe = rt.ELEM_BYTES[view.dtype]
+        if lx is None or view.core is None:
+            raise NotImplementedError("LX memory view without an LX space")
+        if lx.bytes_per_core % bpe:
+            raise NotImplementedError("LX size is not a multiple of the element size")
+        start = view.base.astype(np.int64) + origin.astype(np.int64)
+        if span is not None:
+            live = span[1] > span[0]
+            lo_e, hi_e = (start + span[0])[live], (start + span[1])[live]
+        elif offs is not None and len(offs):
+            lo_e, hi_e = start + int(np.min(offs)), start + int(np.max(offs)) + 1
+        else:
+            ext = sum((int(n) - 1) * abs(int(st)) for n, st in zip(shape, strides) if int(n) > 0)
+            neg = sum((int(n) - 1) * int(st) for n, st in zip(shape, strides) if int(st) < 0 and int(n) > 0)
+            lo_e, hi_e = start + neg, start + neg + ext + 1
+        if np.any(lo_e < 0) or np.any(hi_e * bpe > lx.bytes_per_core):
+            raise NotImplementedError(f"LX access outside the {lx.bytes_per_core}-byte scratchpad")
+        core = np.broadcast_to(np.asarray(view.core, dtype=np.int64), start.shape)
+        rel = core * (lx.bytes_per_core // bpe) + start
+        spec = LeafSpec(lx.buf.ptr, view.dtype, LaneOff.from_array(rel), strides, 0, lx.alloc.nbytes // bpe,
+                        alloc=lx.alloc)
+        return spec, lx.alloc, rel
+
+    def _log_mem(self, alloc, store, rel, shape, strides, dtype, mask=None):
+        """Log an access in the allocation's units: elements for a tensor,
+        bytes for the LX space (whose views may differ in dtype)."""
+        if self.lx is not None and alloc is self.lx.alloc:
+            bpe = rt.ELEM_BYTES[dtype]
+            rel = np.asarray(rel, dtype=np.int64) * bpe
+            shape = tuple(shape) + (bpe,)
+            strides = tuple(int(s) * bpe for s in strides) + (1,)
+        self.log(alloc, store, rel, shape, strides, mask=mask)
+
+    def log(self, alloc, store, base, shape, strides, whole=False, group=None, mask=None):
         if self.sequential:
             return
-        self.accesses.append(Access(alloc, store, self.lanes.inst.copy(), np.asarray(base, dtype=np.int64),
+        inst = self.lanes.inst.copy()
+        base = np.broadcast_to(np.asarray(base, dtype=np.int64), inst.shape)
+        if mask is not None:
+            inst, base = inst[mask], base[mask]
+        self.accesses.append(Access(alloc, store, inst, np.ascontiguousarray(base),
                                     tuple(shape), tuple(strides), whole, group))
 
     def materialize(self, t: Tile, dest: Optional[LeafSpec] = None) -> Tile:
@@ -647,7 +696,47 @@ class Executor:
         if isinstance(cs, Box) and not cs.is_concrete:
             cs = cs.specialize(tuple(int(_uniform(self.get_value(s), "view size"))
                                      for s in a["shape"] if isinstance(s, str)))
-        return View(np.asarray(ptr, dtype=np.int64), shape, strides, _canon(a["dtype"]), a["memory_space"], cs)
+        core = None
+        if a["memory_space"] == "LX":
+            ct = a.get("lx_core_id")
+            if ct is not None and not 0 <= int(ct) < self.n_cores:
+                raise IndexError(f"ct_id {ct} names no core of the {self.n_cores}-core grid")
+            core = self.lanes.cores.astype(np.int64) if ct is None else np.full(self.L, int(ct), np.int64)
+        return View(np.asarray(ptr, dtype=np.int64), shape, strides, _canon(a["dtype"]), a["memory_space"], cs,
+                    core)
+
+    def h_ktdp_construct_distributed_memory_view(self, op):
+        """Reference dialects/ktdp_ops.py:109-140 with ir_types.py:176-265:
+        a dynamic global dim takes the partitions' extent max(hi); a
+        declared dim must equal it; every partition has a coordinate set and
+        the view's dtype."""
+        parts = [self.get_value(n) for n in op.operands]
+        for i, p in enumerate(parts):
+            if not isinstance(p, View):
+                raise ValueError(f"construct_distributed_memory_view: operand {i} is {type(p).__name__}, "
+                                 f"expected a memory view")
+            if p.cs is None:
+                raise ValueError(f"DistributedMemRef partition {i} must have a coordinate_set")
+        a = op.attributes
+        if "shape" not in a or "dtype" not in a:
+            raise ValueError("construct_distributed_memory_view: missing required attributes 'shape'/'dtype'")
+        shape = list(a["shape"])
+        dtype = _canon(a["dtype"])
+        for axis in range(len(shape)):
+            his = [p.cs.hi[axis] for p in parts if isinstance(p.cs, Box)]
+            ext = max(his) if his else None
+            if shape[axis] is None:
+                if ext is None:
+                    raise ValueError("construct_distributed_memory_view: dynamic axis with no box partition")
+                shape[axis] = ext
+            elif ext is not None and shape[axis] != ext:
+                raise ValueError(f"construct_distributed_memory_view: declared dim {shape[axis]} on axis {axis} "
+                                 f"does not match the partition extent {ext}")
+        for i, p in enumerate(parts):
+            if p.dtype != dtype:
+                raise ValueError(f"DistributedMemRef partition {i} dtype {p.dtype!r} does not match view dtype "
+                                 f"{dtype!r}")
+        return DistView(parts, tuple(shape), dtype)
 
     def h_ktdp_construct_access_tile(self, op):
         parent = self.get_value(op.operands[0])
@@ -657,6 +746,11 @@ class Executor:
         if isinstance(cs, Box) and not cs.is_concrete:
             raise NotImplementedError("construct_access_tile: symbolic access_tile_set is not supported")
         base = a["base_map"].eval(idx)
+        if isinstance(parent, DistView):
+            x = tuple(np.broadcast_to(np.asarray(c, dtype=np.int64), (self.L,)).copy() for c in base)
+            if len(x) != len(parent.shape):
+                raise ValueError("construct_access_tile: index rank does not match the distributed view")
+            return DistATile(parent, x, tuple(a["shape"]), cs)
         off = np.zeros(self.L, dtype=np.int64)
         for c, s in zip(base, parent.strides):
             off = off + np.asarray(c, dtype=np.int64) * int(s)
@@ -702,13 +796,15 @@ class Executor:
         rs = op.attributes.get("_result_shape")
         if isinstance(at, IATile):
             return self.indirect_load(at, rs if rs is not None else at.shape)
+        if isinstance(at, DistATile):
+            return self.distributed_load(at, tuple(rs) if rs is not None else tuple(at.shape))
         v = at.view
         cs, co = at.cs, at.co
         if isinstance(cs, Box) and co is None:
             lo_off = sum(int(l) * int(s) for l, s in zip(cs.lo, v.strides))
             shape = cs.extent
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
-            self.log(alloc, False, rel, shape, v.strides)
+            self._log_mem(alloc, False, rel, shape, v.strides, v.dtype)
             self._lat_box(rel, shape, v.strides, rt.ELEM_BYTES[v.dtype])
             return Tile(Expr("ld", v.dtype, shape, attr=spec))
         coords = cs.enumerate(at.shape)
@@ -723,13 +819,13 @@ class Executor:
             np.zeros(0, np.int64)
         if len(offs) != _prod(out_shape):
             raise ValueError(f"cannot reshape {len(offs)} loaded elements into {out_shape}")
-        spec, alloc, rel = self._hbm_leaf(v, origin, out_shape, _cstrides(out_shape))
+        spec, alloc, rel = self._hbm_leaf(v, origin, out_shape, _cstrides(out_shape), offs=offs)
         self._lat_elems(rel, offs, rt.ELEM_BYTES[v.dtype])
         buf = self.pool.upload(offs)
         spec.offsets, spec.offsets_ls = buf, 0
         spec.strides = _cstrides(out_shape) if out_shape else (1,)
-        self.log(alloc, False, rel + (offs.min() if len(offs) else 0), (int(np.ptp(offs)) + 1 if len(offs) else 1,),
-                 (1,))
+        self._log_mem(alloc, False, rel + (offs.min() if len(offs) else 0),
+                      (int(np.ptp(offs)) + 1 if len(offs) else 1,), (1,), v.dtype)
         return Tile(Expr("ld", v.dtype, out_shape, attr=spec))
 
     def h_ktdp_store(self, op):
@@ -740,6 +836,9 @@ class Executor:
         if isinstance(at, IATile):
             self.indirect_store(val, at)
             return None
+        if isinstance(at, DistATile):
+            self.distributed_store(val, at)
+            return None
         v = at.view
         cs, co = at.cs, at.co
         if isinstance(cs, Box) and co is None:
@@ -749,7 +848,7 @@ class Executor:
             from .fusion import mm_epilogue
             if not mm_epilogue(self, op, val, spec, alloc, shape):
                 self._store_expr(val, spec, alloc, shape)
-            self.log(alloc, True, rel, shape, v.strides)
+            self._log_mem(alloc, True, rel, shape, v.strides, v.dtype)
             self._lat_box(rel, shape, v.strides, rt.ELEM_BYTES[v.dtype])
             return None
         coords = cs.enumerate(at.shape)
@@ -760,14 +859,14 @@ class Executor:
         n = _prod(val.shape)
         if len(offs) != n:
             raise ValueError("ktdp.store: tile size does not match the access tile's points")
-        spec, alloc, rel = self._hbm_leaf(v, at.origin, val.shape, _cstrides(val.shape))
+        spec, alloc, rel = self._hbm_leaf(v, at.origin, val.shape, _cstrides(val.shape), offs=offs)
         self._lat_elems(rel, offs, rt.ELEM_BYTES[v.dtype])
         spec.offsets, spec.offsets_ls = self.pool.upload(offs), 0
         if len(np.unique(offs)) != len(offs):
             self._winners(spec, n)
         self._store_expr(val, spec, alloc, val.shape)
-        self.log(alloc, True, rel + (offs.min() if len(offs) else 0), (int(np.ptp(offs)) + 1 if len(offs) else 1,),
-                 (1,))
+        self._log_mem(alloc, True, rel + (offs.min() if len(offs) else 0),
+                      (int(np.ptp(offs)) + 1 if len(offs) else 1,), (1,), v.dtype)
         return None
 
     def _store_expr(self, val: Tile, dest: LeafSpec, alloc: Alloc, shape):
@@ -799,9 +898,198 @@ class Executor:
         spec.winner_base = 0
 
     # -- indirect access (reference ops/memory_ops.py:224-576, 868-964) --------
+    # -- distributed views (reference ops/memory_ops.py:986-1259) ------------
+    _ABSENT = 1 << 60      # offset-list entry that lies past every window: read 0, write dropped
+
+    def _dist_routes(self, at: DistATile):
+        """Per partition i, for every lane: C_i = B_i & (x + A) and the
+        partition origin p_i = min(B_i) (reference memory_ops.py:986-1098).
+        Returns [(view, kind, lane mask, data, p_i)] with kind "box" (data =
+        per-lane lo/hi arrays) or "pts" (data = the partition's points)."""
+        dist, x, A, L = at.dist, at.x, at.cs, self.L
+        nd = len(dist.shape)
+        if isinstance(A, Box) and not A.is_concrete:
+            raise NotImplementedError("construct_access_tile: symbolic access_tile_set is not supported")
+        routes, any_hit = [], np.zeros(L, dtype=bool)
+        for part in dist.parts:
+            B = part.cs
+            if isinstance(B, Box) and isinstance(A, Box):
+                lo = [np.maximum(B.lo[d], x[d] + A.lo[d]) for d in range(nd)]
+                hi = [np.minimum(B.hi[d], x[d] + A.hi[d]) for d in range(nd)]
+                m = np.ones(L, dtype=bool)
+                for l, h in zip(lo, hi):
+                    m &= h > l
+                routes.append((part, "box", m, (lo, hi), tuple(B.lo)))
+            else:
+                pts = np.asarray(B.enumerate() if isinstance(B, Box) else B.enumerate(dist.shape),
+                                 dtype=np.int64).reshape(-1, nd)
+                if not len(pts):
+                    continue
+                rel = pts[None, :, :] - np.stack(x, axis=1)[:, None, :]            # lane x point x dim
+                if A is None:
+                    inside = np.all((rel >= 0) & (rel < np.asarray(at.shape, dtype=np.int64)), axis=2)
+                else:
+                    inside = A.mask([rel[:, :, d] for d in range(nd)])
+                m = inside.any(axis=1)
+                routes.append((part, "pts", m, (pts, inside), tuple(int(v) for v in pts.min(axis=0))))
+            any_hit |= routes[-1][2]
+        if not np.all(any_hit):
+            c = int(self.lanes.cores[int(np.flatnonzero(~any_hit)[0])])
+            xs = tuple(int(v[int(np.flatnonzero(~any_hit)[0])]) for v in x)
+            raise ValueError(f"distributed_tile_access: no partition covers access region global_base={xs} "
+                             f"shape={tuple(at.shape)} (core {c})")
+        return routes
+
+    def _dist_single(self, at: DistATile, routes, shape):
+        """The common case as one strided leaf: every lane's access lies
+        whole inside one partition, the tile starts at the access origin,
+        and the partitions reached share strides and memory space.  Returns
+        (leaf, alloc, rel, strides) or None."""
+        A = at.cs
+        if not isinstance(A, Box) or any(l != 0 for l in A.lo) or tuple(A.hi) != tuple(shape):
+            return None
+        L, nd = self.L, len(shape)
+        pick = np.full(L, -1, dtype=np.int64)
+        for k, (part, kind, m, data, p_i) in enumerate(routes):
+            if not m.any():
+                continue
+            if kind != "box":
+                return None
+            lo, hi = data
+            full = m.copy()
+            for d in range(nd):
+                full &= (lo[d] == at.x[d]) & (hi[d] == at.x[d] + A.hi[d])
+            if np.any(m != full) or np.any(pick[m] >= 0):
+                return None
+            pick[m] = k
+        used = [routes[k][0] for k in np.unique(pick)]
+        v0 = used[0]
+        if any(v.strides != v0.strides or v.space != v0.space for v in used):
+            return None
+        base = np.zeros(L, dtype=np.int64)
+        core = None if v0.core is None else np.zeros(L, dtype=np.int64)
+        for k in np.unique(pick):
+            part, _, _, _, p_i = routes[k]
+            sel = pick == k
+            off = np.zeros(int(sel.sum()), dtype=np.int64)
+            for d in range(nd):
+                off += (at.x[d][sel] - p_i[d]) * part.strides[d]
+            base[sel] = part.base[sel] + off
+            if core is not None:
+                core[sel] = part.core[sel]
+        view = View(base, tuple(shape), v0.strides, v0.dtype, v0.space, None, core)
+        try:
+            spec, alloc, rel = self._hbm_leaf(view, np.zeros(L, dtype=np.int64), shape, v0.strides)
+        except NotImplementedError:
+            return None
+        return spec, alloc, rel, v0.strides
+
+    def _dist_offsets(self, at: DistATile, route, shape):
+        """Offset lists of one partition: for every lane and every position
+        n of the tile, the element offset inside the partition (from its
+        pointer) of global point x + n when that point lies in C_i, else
+        absent; plus the per-lane lowest/highest offset used."""
+        part, kind, m, data, p_i = route
+        L, nd, N = self.L, len(shape), _prod(shape)
+        cst = np.asarray(_cstrides(shape), dtype=np.int64)
+        pst = np.asarray(part.strides, dtype=np.int64)
+        pos = np.full((L, N), self._ABSENT, dtype=np.int64)
+        src = np.full((L, N), self._ABSENT, dtype=np.int64)
+        lo_o = np.zeros(L, dtype=np.int64)
+        hi_o = np.zeros(L, dtype=np.int64)
+        for l in np.flatnonzero(m):
+            xl = np.array([int(v[l]) for v in at.x], dtype=np.int64)
+            if kind == "box":
+                lo, hi = data
+                g = np.indices(tuple(int(hi[d][l] - lo[d][l]) for d in range(nd))).reshape(nd, -1).T
+                g = g + np.array([int(lo[d][l]) for d in range(nd)], dtype=np.int64)
+            else:
+                pts, inside = data
+                g = pts[inside[l]]
+            rel = g - xl
+            if np.any(rel < 0) or np.any(rel >= np.asarray(shape, dtype=np.int64)):
+                raise ValueError("distributed access: a covered point falls outside the result tile")
+            n = rel @ cst
+            o = (g - np.asarray(p_i, dtype=np.int64)) @ pst
+            pos[l, n] = n
+            src[l, n] = o
+            if len(np.unique(o)) != len(o):
+                raise NotImplementedError("distributed partition whose strides alias elements")
+            lo_o[l], hi_o[l] = int(o.min()), int(o.max()) + 1
+        return pos, src, lo_o, hi_o
+
+    def _dist_leaf(self, route, src, lo_o, hi_o, shape):
+        part, _, m, _, _ = route
+        L = self.L
+        if part.space == "HBM":
+            spec, alloc, rel = self._hbm_leaf(part, np.zeros(L, dtype=np.int64), shape, _cstrides(shape))
+        else:
+            spec, alloc, rel = self._lx_leaf(part, np.zeros(L, dtype=np.int64), shape, _cstrides(shape),
+                                             span=(lo_o, hi_o))
+        spec.offsets, spec.offsets_ls = self.pool.upload(src), _prod(shape)
+        spec.strides = _cstrides(shape)
+        return spec, alloc, rel
+
+    def distributed_load(self, at: DistATile, shape):
+        """Reference memory_ops.py:1127-1196: a zero tile; each partition's
+        C_i, read at C_i - p_i, lands at C_i - x."""
+        shape = tuple(int(d) for d in shape)
+        dtype = at.dist.dtype
+        routes = self._dist_routes(at)
+        one = self._dist_single(at, routes, shape)
+        if one is not None:
+            spec, alloc, rel, strides = one
+            self._log_mem(alloc, False, rel, shape, strides, dtype)
+            self._lat_box(rel, shape, strides, rt.ELEM_BYTES[dtype])
+            return Tile(Expr("ld", dtype, shape, attr=spec))
+        L, N = self.L, _prod(shape)
+        out = self.materialize(Tile(E_const(0, _store_dt(dtype), shape)))
+        dst = out.e.attr
+        for route in routes:
+            part, _, m, _, _ = route
+            if not m.any():
+                continue
+            pos, src, lo_o, hi_o = self._dist_offsets(at, route, shape)
+            spec, alloc, rel = self._dist_leaf(route, src, lo_o, hi_o, shape)
+            dest = LeafSpec(dst.ptr, dst.dtype, dst.lane, dst.strides, dst.lo, dst.hi,
+                            offsets=self.pool.upload(pos), offsets_ls=N, keep=dst.keep)
+            self._emit_store(Expr("ld", dtype, shape, attr=spec), dest)
+            self._log_mem(alloc, False, rel + lo_o, (int(np.max(hi_o - lo_o)),), (1,), dtype, mask=m)
+        return Tile(Expr("ld", dst.dtype, shape, attr=dst))
+
+    def distributed_store(self, val: Tile, at: DistATile):
+        """Reference memory_ops.py:1199-1259: only C_i is written in each
+        partition, from the tile's positions C_i - x."""
+        shape = tuple(int(d) for d in at.shape)
+        dtype = at.dist.dtype
+        if tuple(val.shape) != shape:
+            if _prod(val.shape) != _prod(shape):
+                raise ValueError(f"ktdp.store: tile shape {tuple(val.shape)} does not match the access tile "
+                                 f"{shape}")
+            val = self.reshape(val, shape)
+        routes = self._dist_routes(at)
+        one = self._dist_single(at, routes, shape)
+        if one is not None:
+            spec, alloc, rel, strides = one
+            self._store_expr(val, spec, alloc, shape)
+            self._log_mem(alloc, True, rel, shape, strides, dtype)
+            self._lat_box(rel, shape, strides, rt.ELEM_BYTES[dtype])
+            return
+        live = [r for r in routes if r[2].any()]
+        if len(live) > 1:
+            val = self.materialize(val)
+        for route in live:
+            _, _, m, _, _ = route
+            pos, src, lo_o, hi_o = self._dist_offsets(at, route, shape)
+            spec, alloc, rel = self._dist_leaf(route, src, lo_o, hi_o, shape)
+            self._store_expr(val, spec, alloc, shape)
+            self._log_mem(alloc, True, rel + lo_o, (int(np.max(hi_o - lo_o)),), (1,), dtype, mask=m)
+
     def _iat_offsets(self, at: IATile) -> Tuple[rt.DeviceBuffer, int, LeafSpec, Alloc]:
         if at.vso is not None and not at.vso.is_permutation():
             raise ValueError("variables_space_order must permute its input dimensions")
+        if at.parent.space != "HBM" or any(v.space != "HBM" for v in at.views):
+            raise NotImplementedError("indirect access tile over LX memory")
         pts = at.vss.enumerate(at.shape)
         if at.vso is not None:
             pts = sorted(pts, key=lambda p: at.vso.eval(p))

@@ -370,3 +370,59 @@ def dist_copy_2core():
   }}
 }}
 """
+
+
+DIST_IN = 8192       # element address of the stored tile's source (f16)
+
+
+def dist_store(p0, p1, ashape, idx, gshape=(4, 4)):
+    """Load a contiguous tile from DIST_IN and store it through an access
+    tile of a two-partition distributed view (partitions as in dist_copy)."""
+    src = dist_copy(p0, p1, ashape, idx, gshape).replace("@dist_copy", "@dist_store")
+    src = src.replace(f"%ob = arith.constant {DIST_OUT} : index", f"%ob = arith.constant {DIST_IN} : index")
+    t = f"!ktdp.access_tile<{ashape[0]}x{ashape[1]}xindex>"
+    r = f"tensor<{ashape[0]}x{ashape[1]}xf16>"
+    src = src.replace(f"    %v = ktdp.load %at : {t} -> {r}\n    ktdp.store %v, %bt : {r}, {t}\n",
+                      f"    %v = ktdp.load %bt : {t} -> {r}\n    ktdp.store %v, %at : {r}, {t}\n")
+    assert "ktdp.store %v, %at" in src
+    return src
+
+
+def lx_exchange(n=256, out=4096):
+    """Two cores: each loads n f16 from its own LX (byte 0) and stores them
+    into core 1's LX (ct_id = 1) and to HBM at element out + n * core.  Core
+    0 runs first in the reference, so core 1 loads what core 0 stored."""
+    box = f"affine_set<(d0) : (d0 >= 0, -d0 + {n - 1} >= 0)>"
+    tile = f"!ktdp.access_tile<{n}xindex>"
+    return f"""module {{
+  func.func @lx_exchange() attributes {{grid = [2, 1]}} {{
+    %core = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %cn = arith.constant {n} : index
+    %ob = arith.constant {out} : index
+    %off = arith.muli %core, %cn : index
+    %own = ktdp.construct_memory_view %c0, sizes: [{n}], strides: [1] {{
+      coordinate_set = {box}, memory_space = {_space("LX")}
+    }} : memref<{n}xf16>
+    %to1 = ktdp.construct_memory_view %c0, sizes: [{n}], strides: [1] {{
+      coordinate_set = {box}, memory_space = {_space("LX", 1)}
+    }} : memref<{n}xf16>
+    %hv = ktdp.construct_memory_view %ob, sizes: [{2 * n}], strides: [1] {{
+      coordinate_set = affine_set<(d0) : (d0 >= 0, -d0 + {2 * n - 1} >= 0)>, memory_space = {_space("HBM")}
+    }} : memref<{2 * n}xf16>
+    %ta = ktdp.construct_access_tile %own[%c0] {{
+      access_tile_set = {box}, access_tile_order = affine_map<(d0) -> (d0)>
+    }} : memref<{n}xf16> -> {tile}
+    %tb = ktdp.construct_access_tile %to1[%c0] {{
+      access_tile_set = {box}, access_tile_order = affine_map<(d0) -> (d0)>
+    }} : memref<{n}xf16> -> {tile}
+    %tc = ktdp.construct_access_tile %hv[%off] {{
+      access_tile_set = {box}, access_tile_order = affine_map<(d0) -> (d0)>
+    }} : memref<{2 * n}xf16> -> {tile}
+    %v = ktdp.load %ta : {tile} -> tensor<{n}xf16>
+    ktdp.store %v, %tb : tensor<{n}xf16>, {tile}
+    ktdp.store %v, %tc : tensor<{n}xf16>, {tile}
+    return
+  }}
+}}
+"""

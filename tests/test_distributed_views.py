@@ -80,3 +80,70 @@ def test_oracle_distributed_view_rejects_wrong_extent():
     o.load(src)
     with pytest.raises(ValueError):
         o.execute_function("dist_copy")
+
+
+BG = -(np.arange(16, dtype=np.float16) + 1).reshape(4, 4)
+
+
+def store_input(ashape):
+    return (100 + np.arange(ashape[0] * ashape[1])).astype(np.float16).reshape(ashape)
+
+
+def expected_store_images(p0, p1, ashape, idx):
+    """Each partition's memory image after the store: the background tensor
+    with the access tile's region replaced by the input, laid out with the
+    partition's strides (holes stay zero)."""
+    g = BG.copy()
+    g[idx[0]:idx[0] + ashape[0], idx[1]:idx[1] + ashape[1]] = store_input(ashape)
+    return [_cases.strided_block(g[r[0]:r[1] + 1, c[0]:c[1] + 1], st) for r, c, _, st, _ in (p0, p1)]
+
+
+def store_seeds(p0, p1):
+    return [(sp, addr, _cases.strided_block(BG[r[0]:r[1] + 1, c[0]:c[1] + 1], st)) for r, c, sp, st, addr in (p0, p1)]
+
+
+def oracle_dist_store(p0, p1, ashape, idx):
+    o = OracleInterpreter()
+    o.load(_cases.dist_store(p0, p1, ashape, idx))
+    seeds = store_seeds(p0, p1)
+
+    def seed(o):
+        for sp, addr, buf in seeds:
+            (o.hbm.memory if sp == "HBM" else o.lxs[0].memory).write(addr * 2, buf)
+        o.hbm.memory.write(_cases.DIST_IN * 2, store_input(ashape).reshape(-1))
+        o.lxs[0].next_ptr = 1 << 20
+    o.prepare_hook = seed
+    o.execute_function("dist_store")
+    return [(o.hbm.memory if sp == "HBM" else o.lxs[0].memory).read(addr * 2, buf.size, "f16")
+            for sp, addr, buf in seeds]
+
+
+@pytest.mark.parametrize("case", _cases.DIST_CASES, ids=[c[0] for c in _cases.DIST_CASES])
+def test_oracle_distributed_store(case):
+    _, p0, p1, ashape, idx = case
+    for got, want in zip(oracle_dist_store(p0, p1, ashape, idx), expected_store_images(p0, p1, ashape, idx)):
+        np.testing.assert_array_equal(got, want)
+
+
+def oracle_lx_exchange(n=256):
+    s0 = np.arange(n, dtype=np.float16)
+    s1 = -np.arange(n, dtype=np.float16) - 1
+    o = OracleInterpreter()
+    o.load(_cases.lx_exchange(n))
+
+    def seed(o):
+        o.lxs[0].memory.write(0, s0)
+        o.lxs[1].memory.write(0, s1)
+        o.hbm.memory.write(4096 * 2, np.zeros(2 * n, np.float16))
+        o.lxs[0].next_ptr = o.lxs[1].next_ptr = 1 << 20
+    o.prepare_hook = seed
+    o.execute_function("lx_exchange")
+    return o.hbm.memory.read(4096 * 2, 2 * n, "f16"), o.lxs[1].memory.read(0, n, "f16"), s0, s1
+
+
+def test_oracle_lx_exchange_in_core_order():
+    """Core 1 runs after core 0, so it loads the values core 0 stored into
+    its LX: both HBM halves and core 1's LX end up holding core 0's data."""
+    out, lx1, s0, _ = oracle_lx_exchange()
+    np.testing.assert_array_equal(out, np.concatenate([s0, s0]))
+    np.testing.assert_array_equal(lx1, s0)
