@@ -494,6 +494,7 @@ class Plan:
         self.pool = pool
         self.launches: List[Tuple] = []
         self.replayable = True
+        self.ran_during_walk = False     # launches already ran as they were walked
         self.mode = "lockstep"
         self.fallback_reason = None
 

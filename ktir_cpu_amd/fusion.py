@@ -28,6 +28,11 @@ _SKIP = {"ktdp.load", "arith.extf", "linalg.matmul", "scf.yield"}
 
 def try_fuse_loop(ex, op, lb, st, trips, inits) -> Optional[List]:
     names = op.attributes.get("iter_args", [])
+    if ex.collective:
+        from .walker import _has_op
+        if _has_op(op.regions[0].ops, "ktdp.inter_tile_reduce") or \
+                _has_op(op.regions[0].ops, "ktdp.inter_tile_produce"):
+            return None      # a ring reduce in the body needs the op-by-op walk
     if not _lx_fits(ex, op.regions[0].ops):
         return None          # let the op-by-op path raise the reference's LX overflow
     if len(names) == 1 and isinstance(inits[0], Tile):

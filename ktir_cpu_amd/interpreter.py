@@ -224,7 +224,8 @@ class KTIRInterpreter:
                 ex = Executor(fn, arena, args, self._pool, sequential=False, lx_size_mb=self.lx_size_mb,
                               lx=self._lx)
                 plan = ex.run()
-                plan.run()
+                if not plan.ran_during_walk:
+                    plan.run()
             except NeedEager as why:
                 ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb,
                               lx=self._lx)

@@ -702,6 +702,91 @@ def _b_dist_view(op, toks, aliases):
     op.attributes["dtype"] = mt.elem
 
 
+def _named_set(toks: List[Tok], key: str, aliases, what: str, required: bool = True):
+    """`key = #alias` or `key = affine_set<...>` among the op's own tokens."""
+    k = _idx(toks, key, kind="ident")
+    if k < 0 or k + 2 >= len(toks) or toks[k + 1].text != "=":
+        if required:
+            raise KTIRParseError(f"{what}: missing {key}")
+        return None
+    v = toks[k + 2]
+    text = aliases.get(v.text) if v.kind == "alias" else v.text
+    if not isinstance(text, str) or not text.startswith("affine_set"):
+        raise KTIRParseError(f"{what}: {key} is not an affine_set ({v.text!r})")
+    return parse_affine_set(text)
+
+
+def _future_groups(toks: List[Tok], aliases, what: str):
+    """The `groups = <set>` inside the tile_future type, in either spelling:
+    `!ktdp.tile_future<T, groups = S>` or the shortened `<(T), groups = S>`
+    (reference dialects/ktdp_ops.py:1034-1080)."""
+    for t in toks:
+        if t.kind == "blob" and t.text.startswith("!ktdp.tile_future<"):
+            m = re.search(r"groups\s*=\s*(affine_set<.*>|#[\w$.-]+)\s*>\s*$", t.text, re.S)
+            if m is None:
+                raise KTIRParseError(f"{what}: missing groups inside !ktdp.tile_future<...> type")
+            text = aliases.get(m.group(1), m.group(1)) if m.group(1).startswith("#") else m.group(1)
+            return parse_affine_set(text)
+    return _named_set(toks, "groups", aliases, what + " (groups inside the tile_future type)")
+
+
+def _b_inter_tile_produce(op, toks, aliases):
+    """``%f = ktdp.inter_tile_produce producer_tiles_per_group = S -> <(T), groups = G> { ^bb0(%gid): ... }``
+    (reference dialects/ktdp_ops.py:1083-1130)."""
+    op.regions = _regions(toks)
+    top = [t for t in toks if t.kind != "region"]
+    op.attributes["producer_tiles_per_group"] = _named_set(top, "producer_tiles_per_group", aliases,
+                                                           "ktdp.inter_tile_produce")
+    op.attributes["groups"] = _future_groups(top, aliases, "ktdp.inter_tile_produce")
+    op.operands = []
+
+
+def _b_inter_tile_reduce(op, toks, aliases):
+    """``%r = ktdp.inter_tile_reduce(%f) consumer_tiles_per_group = S, identity(%id : T) : <future> -> T_r {...}``:
+    operands [future, identity...], the consumer set, the future's groups,
+    the optional dependency set and the result shape (reference
+    dialects/ktdp_ops.py:1234-1307)."""
+    op.regions = _regions(toks)
+    top = [t for t in toks if t.kind != "region"]
+    what = "ktdp.inter_tile_reduce"
+    if len(top) < 3 or top[0].text != "(" or top[1].kind != "ssa" or top[2].text != ")":
+        raise KTIRParseError(f"{what}: expected ( %future ) after the op name")
+    operands = [top[1].text]
+    k = _idx(top, "identity", kind="ident")
+    if k >= 0 and k + 1 < len(top) and top[k + 1].text == "(":
+        j = k + 2
+        depth = 1
+        while j < len(top) and depth:
+            t = top[j]
+            if t.kind == "punct" and t.text == "(":
+                depth += 1
+            elif t.kind == "punct" and t.text == ")":
+                depth -= 1
+            elif t.kind == "ssa" and depth == 1:
+                operands.append(t.text)
+            j += 1
+    op.operands = operands
+    op.attributes["consumer_tiles_per_group"] = _named_set(top, "consumer_tiles_per_group", aliases, what)
+    op.attributes["groups"] = _future_groups(top, aliases, what)
+    dep = _named_set(top, "producer_dependency_per_consumer", aliases, what, required=False)
+    if dep is not None:
+        op.attributes["producer_dependency_per_consumer"] = dep
+    arrows = [i for i, t in enumerate(top) if t.kind == "punct" and t.text == "->"]
+    if arrows and arrows[-1] + 1 < len(top):
+        rt_ = parse_type(top[arrows[-1] + 1].text)
+        if isinstance(rt_, ShapedType):
+            op.result_types = [rt_]
+            op.attributes["_result_shape"] = tuple(rt_.shape)
+
+
+def _b_yield_values(op, toks, aliases):
+    """``ktdp.yield_partial`` / ``ktdp.yield_reduced``: the yielded SSA values."""
+    op.operands = _ssa([t for t in toks if t.kind != "region"])
+    k = _idx(toks, ":")
+    if k >= 0:
+        op.operands = _ssa(toks[:k])
+
+
 def _b_access_tile(op, toks, aliases):
     view = next(t.text for t in toks if t.kind == "ssa")
     k = _idx(toks, "[")
@@ -1071,6 +1156,10 @@ _BUILDERS = {
     "ktdp.construct_memory_view": _b_memory_view,
     "ktdp.construct_distributed_memory_view": _b_dist_view,
     "ktdp.construct_access_tile": _b_access_tile,
+    "ktdp.inter_tile_produce": _b_inter_tile_produce,
+    "ktdp.inter_tile_reduce": _b_inter_tile_reduce,
+    "ktdp.yield_partial": _b_yield_values,
+    "ktdp.yield_reduced": _b_yield_values,
     "ktdp.construct_indirect_access_tile": _b_indirect_tile,
     "ktdp.load": _b_load,
     "ktdp.store": _b_load,

@@ -251,12 +251,27 @@ def _xcd_blocks(q: np.ndarray, ao: np.ndarray, bo: np.ndarray) -> np.ndarray:
     return q[order]
 
 
+class _Future:
+    """ktdp.inter_tile_produce result (reference ir_types.py:481-530): every
+    lane's yielded partial(s), its group index and the sets."""
+
+    __slots__ = ("partials", "gid", "producer_set", "groups_set")
+
+    def __init__(self, partials, gid, producer_set, groups_set):
+        self.partials, self.gid = partials, gid
+        self.producer_set, self.groups_set = producer_set, groups_set
+
+    def take(self, idx):
+        return _Future(None if self.partials is None else tuple(take_value(p, idx) for p in self.partials),
+                       self.gid[idx], self.producer_set, self.groups_set)
+
+
 def take_value(v, idx: np.ndarray):
     if isinstance(v, np.ndarray):
         return v[idx]
     if isinstance(v, Tile):
         return Tile(remap_lanes(v.e, idx))
-    if isinstance(v, (View, ATile, IATile, DistView, DistATile)):
+    if isinstance(v, (View, ATile, IATile, DistView, DistATile, _Future)):
         return v.take(idx)
     if isinstance(v, tuple):
         return tuple(take_value(x, idx) for x in v)
@@ -291,6 +306,9 @@ class Executor:
         # every core's LX scratchpad on the device (executor.LXSpace), or None
         # when the function addresses no LX memory
         self.lx = lx
+        # cores meet at ktdp.inter_tile_reduce: every core must run in lockstep
+        self.collective = _has_op(fn.operations, "ktdp.inter_tile_reduce")
+        self.had_reduce = False
         # latency model (ktir_cpu_amd.latency.LatencyTracker) charged op by op, or None
         self.lat = latency
         self._lat_mem: Optional[np.ndarray] = None
@@ -324,6 +342,9 @@ class Executor:
             self._run_body(lanes)
             why = verify(self.accesses, self.insts)
             if why is not None:
+                if self.had_reduce:
+                    raise NotImplementedError(f"cross-core dependence through memory after "
+                                              f"ktdp.inter_tile_reduce: {why}")
                 raise NeedEager(why)
         return self.plan
 
@@ -1489,6 +1510,8 @@ class Executor:
         idx = [self.get_value(o) for o in op.operands[1:]]
         if not isinstance(src, Tile):
             return src
+        if not self.eager and self.collective:
+            self._go_eager()
         if not self.eager:
             raise NeedEager("tensor.extract reads tile data on the host")
         data = self.read_tile(src)
@@ -1502,6 +1525,20 @@ class Executor:
         if src.dtype in ("f32", "bf16"):
             return v.astype(np.float32)
         return v.astype(np.int64) if src.dtype != "i1" else v.astype(bool)
+
+    def _go_eager(self):
+        """Run what the walk has recorded so far and launch the rest as it
+        is walked, all lanes still together: the walk may then read tile
+        data on the host.  Used where the cores cannot run one after another
+        (they meet at a ring reduce)."""
+        L = rt.lib()
+        for kind, desc, _ in self.plan.launches:
+            _launch(L, kind, desc)
+        self.eager = True
+        self.plan.ran_during_walk = True
+        self.plan.replayable = False
+        self.attn_pending = None
+        self.mm_pending = None
 
     def read_tile(self, t: Tile) -> np.ndarray:
         m = self.materialize(t)
@@ -2086,12 +2123,125 @@ class Executor:
     h_tensor_yield = h_linalg_yield
 
     # ======================================================================
+    # inter-tile communication (reference dialects/ktdp_ops.py:951-1230,
+    # ops/comm_ops.py:229-345)
+    # ======================================================================
+    def h_ktdp_inter_tile_produce(self, op):
+        """Each lane's group g (the one group whose producer set holds its
+        core, dialects/ktdp_ops.py:917-944), the producer region run with
+        %gid = g, its yielded partial(s) kept on a future."""
+        P = op.attributes["producer_tiles_per_group"]
+        G = op.attributes["groups"]
+        n = self.n_cores
+        keys = [g for g in range(n) if G.contains([g])]
+        gid = np.empty(self.L, dtype=np.int64)
+        for c in np.unique(self.lanes.cores):
+            hits = [g for g in keys if P.contains([int(c)], [g])]
+            if not hits:
+                raise RuntimeError(f"tile {int(c)} is not contained in any producer group")
+            if len(hits) > 1:
+                raise RuntimeError(f"tile {int(c)} matched multiple groups {hits} — violates the disjointness "
+                                   f"invariant")
+            gid[self.lanes.cores == c] = hits[0]
+        region = op.regions[0] if op.regions else None
+        if region is not None and region.args:
+            self.set_value(region.args[0][0], gid)
+        y = self._run(region.ops) if region is not None else None
+        vals = y.values if isinstance(y, _Yield) else ([y] if y is not None else None)
+        return _Future(tuple(vals) if vals else None, gid, P, G)
+
+    def h_ktdp_yield_partial(self, op):
+        return _Yield([self.get_value(n) for n in op.operands])
+
+    h_ktdp_yield_reduced = h_ktdp_yield_partial
+
+    def h_ktdp_inter_tile_reduce(self, op):
+        """The ring reduce of every core at once: lane c starts from its own
+        partial and, for k = 1 .. n-1, folds in the partial of core
+        (c - k) mod n as combine(acc, partial) when that core produces for
+        c's group -- the fold order of the reference's ring, where round k
+        delivers that core's seed.  Cores outside the consumer set get the
+        value too (the reference leaves it unbound; a valid function does
+        not read it there)."""
+        fut = self.get_value(op.operands[0])
+        if not isinstance(fut, _Future):
+            raise TypeError(f"ktdp.inter_tile_reduce: operand 0 must be a TileFuture, got {type(fut)}")
+        for name in op.operands[1:]:
+            self.get_value(name)
+        if self.sequential:
+            raise NotImplementedError("ktdp.inter_tile_reduce: the cores of this function cannot run in lockstep "
+                                      "(it reads tile data on the host or has a cross-core memory dependence)")
+        n, L = self.n_cores, self.L
+        cores = self.lanes.cores.astype(np.int64)
+        if L != n or not np.array_equal(np.sort(cores), np.arange(n)):
+            raise NotImplementedError("ktdp.inter_tile_reduce reached by other than one lane per core")
+        why = verify(self.accesses, self.insts)
+        if why is not None:
+            raise NotImplementedError(f"cross-core dependence through memory before ktdp.inter_tile_reduce: {why}")
+        self.accesses.clear()
+        self.had_reduce = True
+        region = op.regions[0] if op.regions else None
+        if region is None or len(region.args) < 2:
+            raise ValueError("ktdp.inter_tile_reduce: combiner region needs >=2 block args (lhs, rhs)")
+        lhs, rhs = region.args[0][0], region.args[1][0]
+        if not fut.partials or not isinstance(fut.partials[0], Tile):
+            raise NotImplementedError("ktdp.inter_tile_reduce of a non-tile partial")
+        P = fut.producer_set
+        prod = {int(g): np.array([P.contains([i], [int(g)]) for i in range(n)]) for g in np.unique(fut.gid)}
+        pm = np.stack([prod[int(g)] for g in fut.gid])                     # lane x core
+        lane_of = np.empty(n, dtype=np.int64)
+        lane_of[cores] = np.arange(L)
+        seed = self.materialize(fut.partials[0])
+        acc = seed
+        for k in range(1, n):
+            origin = (cores - k) % n
+            fold = pm[np.arange(L), origin]
+            if not fold.any():
+                continue
+            got = Tile(remap_lanes(seed.e, lane_of[origin]))
+            self.push_scope()
+            try:
+                self.set_value(lhs, acc)
+                self.set_value(rhs, got)
+                r = _unwrap(self._run(region.ops))
+            finally:
+                self.pop_scope()
+            if not isinstance(r, Tile):
+                raise TypeError(f"ktdp.inter_tile_reduce: combiner did not yield a Tile, got {type(r)}")
+            if not fold.all():
+                ea = acc.e if tuple(acc.shape) == tuple(r.shape) else self._operand(acc, r.dtype, r.shape, False)
+                r = Tile(Expr("sel", r.dtype, r.shape, [E_scalar(fold.astype(np.int64), "i32", r.shape), r.e, ea]))
+            acc = self.materialize(r)
+        rs = op.attributes.get("_result_shape")
+        if rs is not None and tuple(rs) != tuple(acc.shape):
+            acc = self.reshape(acc, tuple(rs))
+        return acc
+
+    # ======================================================================
     # scf (reference dialects/scf_ops.py, ops/control_ops.py)
     # ======================================================================
     def h_scf_if(self, op):
-        c = np.asarray(self.get_value(op.operands[0]))
-        cu = bool(_uniform(c.astype(bool), "scf.if condition"))
+        c = self.get_value(op.operands[0])
+        if isinstance(c, Tile):
+            raise NeedEager("scf.if on a tile value")
+        c = np.broadcast_to(np.asarray(c).astype(bool), (self.L,))
         regions = op.regions
+        if c.size and np.any(c != c.flat[0]) and not op.results:
+            # lanes split: each branch runs on the lanes that take it
+            for region, sel in ((regions[0], c), (regions[1] if len(regions) > 1 else None, ~c)):
+                if region is None or not region.ops or not sel.any():
+                    continue
+                active = np.flatnonzero(sel)
+                cur = self.lanes
+                self.levels.append(_Level(Lanes(cur.cores[active], cur.inst[active]), active))
+                self.push_scope()
+                try:
+                    self._run(region.ops)
+                finally:
+                    self.pop_scope()
+                    self.levels.pop()
+            return None
+        cu = bool(_uniform(c, "scf.if condition"))
         region = regions[0] if cu else (regions[1] if len(regions) > 1 else None)
         if region is None or not region.ops:
             return None
@@ -2373,13 +2523,18 @@ def _use_counts(ops) -> Dict[str, int]:
     return counts
 
 
+def _has_op(ops, name: str) -> bool:
+    return any(op.op_type == name or any(_has_op(r.ops, name) for r in op.regions) for op in ops)
+
+
 def _expandable(ops) -> bool:
     """Iterations can run as lanes: no indirect stores, no host reads of tile
     data, no ops whose result depends on another iteration."""
     for op in ops:
         if op.op_type in ("tensor.extract", "arith.index_cast", "arith.index_castui"):
             return False
-        if op.op_type == "ktdp.construct_indirect_access_tile":
+        if op.op_type in ("ktdp.construct_indirect_access_tile", "ktdp.inter_tile_produce",
+                          "ktdp.inter_tile_reduce"):
             return False
         if op.op_type == "linalg.reduce" and op.attributes.get("dimensions") is None:
             return False

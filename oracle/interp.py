@@ -34,6 +34,15 @@ How each part is pinned (``tests/test_golden.py``, ``tests/test_oracle_pins.py``
   (``tests/test_lx_scoping.py:1095-1185``): capacity equal to it runs, one
   byte less raises the reference's overflow error.
 
+Cores that meet at ``ktdp.inter_tile_reduce`` run as threads of which one
+at a time holds the turn, scheduled exactly as the reference's generator
+scheduler (``grid.py:524-623``): each core runs in id order until it waits
+on a ring message, then the lowest-id core whose message has arrived
+resumes.  The ring itself follows ``ops/comm_ops.py:229-345``; pinned by the
+closed form of a ring sum on exactly representable values, by the fold
+order on values where f16 addition order shows, and by the reference's
+deadlock message.
+
 bf16 is an extension (the reference has none, ``dtypes.py:24-39``): bf16
 tiles hold float32 data that is always rounded to the nearest bf16 (RNE);
 HBM stores bf16 as uint16 bit patterns.
@@ -44,6 +53,8 @@ from __future__ import annotations
 import bisect
 import math
 import operator
+import threading
+from collections import deque
 from dataclasses import dataclass, field
 from typing import Any, Dict, List, Optional, Sequence, Tuple
 
@@ -399,6 +410,10 @@ class _Core:
         return self.lx if core_id is None or core_id == self.core_id else self._lxs[core_id]
 
 
+def _has_op(ops: List[Operation], name: str) -> bool:
+    return any(op.op_type == name or any(_has_op(r.ops, name) for r in op.regions) for op in ops)
+
+
 def _use_counts(ops: List[Operation]) -> Dict[str, int]:
     """Textual operand counts over the body and nested regions (parser_utils.py:62-84)."""
     counts: Dict[str, int] = {}
@@ -724,6 +739,114 @@ def _cast(value, target, op_name):
 # Interpreter
 # ---------------------------------------------------------------------------
 
+@dataclass
+class _TileFuture:
+    """Reference ir_types.py:481-530: this core's yielded partial(s), the
+    producer / group sets and the core's group index."""
+    local_partial: Optional[Tuple[Any, ...]]
+    producer_set: Any
+    groups_set: Any
+    group_idx: int
+
+
+def _find_tile_group(core: int, producer_set, groups_set, n_cores: int) -> int:
+    """The one group g in groups_set (searched over [0, n_cores)) whose
+    producer set contains `core` (reference dialects/ktdp_ops.py:917-944)."""
+    hits = [g for g in range(n_cores) if groups_set.contains([g]) and producer_set.contains([core], [g])]
+    if not hits:
+        raise RuntimeError(f"tile {core} is not contained in any producer group")
+    if len(hits) > 1:
+        raise RuntimeError(f"tile {core} matched multiple groups {hits} — violates the disjointness invariant")
+    return hits[0]
+
+
+class _Abort(BaseException):
+    pass
+
+
+class _Scheduler:
+    """One thread per core, one holding the turn at a time; the main thread
+    replays the reference's scheduling loop (grid.py:524-623)."""
+
+    def __init__(self, n: int):
+        self.n = n
+        self.cv = threading.Condition()
+        self.turn: Optional[int] = None
+        self.messages: Dict[Tuple[int, int], deque] = {}
+        self.waiting: Dict[int, int] = {}
+        self.inbox: Dict[int, Any] = {}
+        self.done: set = set()
+        self.error: Optional[BaseException] = None
+        self.abort = False
+
+    # -- core side -------------------------------------------------------------
+    def send(self, src: int, dst: int, tile):
+        self.messages.setdefault((src, dst), deque()).append(tile)
+
+    def recv(self, me: int, src: int):
+        with self.cv:
+            self.waiting[me] = src
+            self.turn = None
+            self.cv.notify_all()
+            self.cv.wait_for(lambda: self.turn == me or self.abort)
+            if self.abort:
+                raise _Abort()
+            return self.inbox.pop(me)
+
+    def _body(self, me: int, fn):
+        with self.cv:
+            self.cv.wait_for(lambda: self.turn == me or self.abort)
+        try:
+            if not self.abort:
+                fn()
+        except _Abort:
+            pass
+        except BaseException as e:     # handed to the main thread
+            with self.cv:
+                self.error = e
+        with self.cv:
+            self.done.add(me)
+            self.turn = None
+            self.cv.notify_all()
+
+    # -- main side ---------------------------------------------------------------
+    def _step(self, c: int, value=None):
+        with self.cv:
+            if value is not None:
+                self.inbox[c] = value
+            self.turn = c
+            self.cv.notify_all()
+            self.cv.wait_for(lambda: self.turn is None)
+            if self.error is not None:
+                raise self.error
+
+    def run(self, bodies):
+        threads = [threading.Thread(target=self._body, args=(c, f), daemon=True) for c, f in enumerate(bodies)]
+        for t in threads:
+            t.start()
+        try:
+            for c in range(self.n):
+                self._step(c)
+            while len(self.done) < self.n:
+                for c in range(self.n):
+                    src = self.waiting.get(c)
+                    q = self.messages.get((src, c)) if src is not None else None
+                    if q:
+                        tile = q.popleft()
+                        del self.waiting[c]
+                        self._step(c, tile)
+                        break
+                else:
+                    desc = "; ".join(f"core {c} waiting on recv from core {s}" for c, s in self.waiting.items())
+                    raise RuntimeError(f"Deadlock detected: {desc}")
+        finally:
+            with self.cv:
+                self.abort = True
+                self.cv.notify_all()
+            for t in threads:
+                t.join(timeout=5)
+
+
 class OracleInterpreter:
     """``load`` / ``tensor_input_output_sizes`` / ``execute_function`` like the reference."""
 
@@ -789,14 +912,24 @@ class OracleInterpreter:
             self.prepare_hook(self)
         counts = _use_counts(fn.operations)
         order = range(ncores) if self.cores_to_run is None else self.cores_to_run
-        for cid in order:
+        self.num_cores = ncores
+
+        def core(cid):
             z = cid // (nx * ny)
             rem = cid % (nx * ny)
             ctx = _Core(cid, (rem % nx, rem // nx, z), lxs[cid], self.hbm, lxs)
             ctx.use_counts = counts
             for name, v in ptrs.items():
                 ctx.set_value("%" + name, v)
-            self._run(fn.operations, ctx)
+            return ctx
+
+        if _has_op(fn.operations, "ktdp.inter_tile_reduce") and self.cores_to_run is None:
+            self._sched = _Scheduler(ncores)
+            self._sched.run([(lambda c=c: self._run(fn.operations, core(c))) for c in range(ncores)])
+        else:
+            self._sched = None
+            for cid in order:
+                self._run(fn.operations, core(cid))
         out = {}
         for name, t in kwargs.items():
             if isinstance(t, np.ndarray):
@@ -1500,6 +1633,70 @@ class OracleInterpreter:
         if isinstance(res, OracleTile):
             return _mk(res.data.astype(to_np_dtype(dt)), dt, shape)
         return _mk(np.full(shape, res, dtype=to_np_dtype(dt)), dt, shape)
+
+    # inter-tile communication (reference dialects/ktdp_ops.py:951-1230) --------
+    def _h_ktdp_inter_tile_produce(self, op, ctx):
+        P = op.attributes["producer_tiles_per_group"]
+        G = op.attributes["groups"]
+        gid = _find_tile_group(ctx.core_id, P, G, self.num_cores)
+        region = op.regions[0] if op.regions else None
+        if region is not None and region.args:
+            ctx.set_value(region.args[0][0], gid)
+        y = self._run(region.ops, ctx) if region is not None else None
+        vals = y.values if isinstance(y, _Yield) else ([y] if y is not None else None)
+        return _TileFuture(tuple(vals) if vals else None, P, G, gid)
+
+    def _h_ktdp_yield_partial(self, op, ctx):
+        return _Yield([ctx.get_value(n) for n in op.operands])
+
+    _h_ktdp_yield_reduced = _h_ktdp_yield_partial
+
+    def _h_ktdp_inter_tile_reduce(self, op, ctx):
+        """Ring reduce over the whole workgroup (ops/comm_ops.py:229-345):
+        seed = own partial (producer) or identity; round k receives the seed
+        of core (me - k) mod n, folded as combine(acc, received) when that
+        core produces for this core's group; non-consumers get nothing."""
+        fut = ctx.get_value(op.operands[0])
+        if not isinstance(fut, _TileFuture):
+            raise TypeError(f"ktdp.inter_tile_reduce: operand 0 must be a TileFuture, got {type(fut)}")
+        identity = ctx.get_value(op.operands[1]) if len(op.operands) > 1 else None
+        n, me, g = self.num_cores, ctx.core_id, fut.group_idx
+        producers = {i for i in range(n) if fut.producer_set.contains([i], [g])}
+        consumers = {i for i in range(n) if op.attributes["consumer_tiles_per_group"].contains([i], [g])}
+        region = op.regions[0] if op.regions else None
+        if region is None or len(region.args) < 2:
+            raise ValueError("ktdp.inter_tile_reduce: combiner region needs >=2 block args (lhs, rhs)")
+        lhs, rhs = region.args[0][0], region.args[1][0]
+
+        def combine(a, b):
+            ctx.push_scope()
+            ctx.set_value(lhs, a)
+            ctx.set_value(rhs, b)
+            r = _unwrap(self._run(region.ops, ctx))
+            ctx.pop_scope()
+            if not isinstance(r, OracleTile):
+                raise TypeError(f"ktdp.inter_tile_reduce: combiner did not yield a Tile, got {type(r)}")
+            return r
+
+        local = fut.local_partial[0] if fut.local_partial else None
+        seed = local if me in producers else identity
+        result, fwd = seed.copy(), seed.copy()
+        sched = self._sched
+        if sched is None:
+            raise RuntimeError("ktdp.inter_tile_reduce outside a scheduled run")
+        for k in range(1, n):
+            origin = (me - k) % n
+            sched.send(me, (me + 1) % n, fwd)
+            got = sched.recv(me, (me - 1) % n)
+            if origin in producers:
+                result = combine(result, got)
+            fwd = got
+        if me not in consumers:
+            return None
+        rs = op.attributes.get("_result_shape")
+        if rs is not None and tuple(rs) != tuple(result.shape):
+            result = OracleTile(result.data.reshape(tuple(rs)), result.dtype, tuple(rs))
+        return result
 
     # scf ----------------------------------------------------------------------
     def _h_scf_for(self, op, ctx):

@@ -426,3 +426,188 @@ def lx_exchange(n=256, out=4096):
   }}
 }}
 """
+
+
+def ring_reduce(n_cores=4, cols=128, group_size=None, strided=False, combiner="add", iters=0, dtype="f16",
+                only_core0=False):
+    """Every core loads its row of a [n_cores, cols] tensor, the rows are
+    combined across each group with ktdp.inter_tile_produce /
+    inter_tile_reduce, and every core stores its group's result to its own
+    output row.  Groups: `group_size` consecutive cores, or with `strided`
+    n_cores / group_size groups g = {g, g + G, g + 2G, ...}.  `combiner`:
+    "add" (linalg.add) or "max" (arith.maximumf).  With `iters` > 0 the
+    reduce sits in an scf.for whose iter_arg accumulates the results.  With
+    `only_core0` just core 0 reaches the reduce (the others skip it), which
+    the reference reports as a deadlock."""
+    gs = n_cores if group_size is None else group_size
+    ng = n_cores // gs
+    if strided:
+        pset = (f"affine_set<(i)[g] : ((i - g) mod {ng} == 0, i - g >= 0, -i + g + {n_cores - ng} >= 0)>")
+    else:
+        pset = f"affine_set<(i)[g] : (i - {gs}*g >= 0, -i + {gs}*g + {gs - 1} >= 0)>"
+    groups = f"affine_set<(g) : (g >= 0, -g + {ng - 1} >= 0)>"
+    T = f"tensor<1x{cols}x{dtype}>"
+    fut = f"!ktdp.tile_future<{T}, groups = {groups}>"
+    row = f"affine_set<(d0, d1) : (d0 >= 0, -d0 >= 0, d1 >= 0, -d1 + {cols - 1} >= 0)>"
+    idm = "affine_map<(d0, d1) -> (d0, d1)>"
+    if combiner == "add":
+        comb = (f"        %init = tensor.empty() : {T}\n"
+                f"        %r = linalg.add ins(%lhs, %rhs : {T}, {T}) outs(%init : {T}) -> {T}\n")
+    else:
+        comb = f"        %r = arith.maximumf %lhs, %rhs : {T}\n"
+    reduce_ops = f"""    %fut = ktdp.inter_tile_produce producer_tiles_per_group = {pset}
+        : {T} -> {fut}
+    {{
+      ^bb0(%gid: index):
+        ktdp.yield_partial %partial : {T}
+    }}
+    %e = tensor.empty() : {T}
+    %id = linalg.fill ins(%z : {dtype}) outs(%e : {T}) -> {T}
+    %red = ktdp.inter_tile_reduce(%fut) consumer_tiles_per_group = {pset}, identity(%id : {T})
+        : {fut} -> {T}
+    {{
+      ^bb0(%lhs: {T}, %rhs: {T}):
+{comb}        ktdp.yield_reduced %r : {T}
+    }}
+"""
+    if iters:
+        body = f"""    %z0 = arith.constant dense<0.0> : {T}
+    %c1 = arith.constant 1 : index
+    %cit = arith.constant {iters} : index
+    %res = scf.for %it = %c0 to %cit step %c1 iter_args(%acc = %z0) -> ({T}) {{
+{reduce_ops}      %nx = arith.addf %acc, %red : {T}
+      scf.yield %nx : {T}
+    }}
+"""
+    else:
+        body = reduce_ops + "    %res = arith.addf %red, %zt : " + T + "\n"
+    if only_core0:
+        body = body.replace("    %fut = ktdp.inter_tile_produce", "    %is0 = arith.cmpi eq, %pid, %c0 : index\n"
+                            "    scf.if %is0 {\n    %fut = ktdp.inter_tile_produce") + "    }\n"
+        body = body.replace("    %res = arith.addf %red, %zt", "    %unused = arith.addf %red, %zt") + \
+            "    %res = arith.addf %partial, %zt : " + T + "\n"
+    return f"""module {{
+  func.func @ring_reduce(%in_ptr: index, %out_ptr: index) attributes {{grid = [{n_cores}]}} {{
+    %c0 = arith.constant 0 : index
+    %cols = arith.constant {cols} : index
+    %z = arith.constant 0.0 : {dtype}
+    %zt = arith.constant dense<0.0> : {T}
+    %pid = ktdp.get_compute_tile_id : index
+    %offs = arith.muli %pid, %cols : index
+    %rp = arith.addi %in_ptr, %offs : index
+    %wp = arith.addi %out_ptr, %offs : index
+    %rv = ktdp.construct_memory_view %rp, sizes: [1, {cols}], strides: [{cols}, 1] {{
+      coordinate_set = {row}, memory_space = #ktdp.memory_space<global>
+    }} : memref<1x{cols}x{dtype}>
+    %ra = ktdp.construct_access_tile %rv[%c0, %c0] {{
+      access_tile_set = {row}, access_tile_order = {idm}
+    }} : memref<1x{cols}x{dtype}> -> !ktdp.access_tile<1x{cols}xindex>
+    %partial = ktdp.load %ra : !ktdp.access_tile<1x{cols}xindex> -> {T}
+{body}    %wv = ktdp.construct_memory_view %wp, sizes: [1, {cols}], strides: [{cols}, 1] {{
+      coordinate_set = {row}, memory_space = #ktdp.memory_space<global>
+    }} : memref<1x{cols}x{dtype}>
+    %wa = ktdp.construct_access_tile %wv[%c0, %c0] {{
+      access_tile_set = {row}, access_tile_order = {idm}
+    }} : memref<1x{cols}x{dtype}> -> !ktdp.access_tile<1x{cols}xindex>
+    ktdp.store %res, %wa : {T}, !ktdp.access_tile<1x{cols}xindex>
+    return
+  }}
+}}
+"""
+
+
+def rmsnorm_2x2(rows=16, H=256):
+    """RMSNorm over a [rows, H] f16 tensor on a 2 x 2 grid: core (c, r)
+    owns columns c*H/2 .. and rows r*rows/2 ..; each row's sum of squares
+    (f32) is folded across the two column partners with inter_tile_reduce.
+
+    X is a distributed view whose left half is the argument X0 (HBM) and
+    whose right half sits in core 1's LX at byte 0 (ct_id = 1, row-major),
+    so cores 1 and 3 read core 1's scratchpad; W is one [1, H] tensor seen
+    through two partitions; Y's halves are the separate arguments Y0, Y1."""
+    h = H // 2
+    rh = rows // 2
+    T16, T32, V32 = f"tensor<1x{h}xf16>", f"tensor<1x{h}xf32>", "tensor<1xf32>"
+    cset = lambda c0, c1, r1: f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {r1} >= 0, d1 - {c0} >= 0, -d1 + {c1} >= 0)>"
+    blk = f"affine_set<(d0, d1) : (d0 >= 0, -d0 >= 0, d1 >= 0, -d1 + {h - 1} >= 0)>"
+    idm = "affine_map<(d0, d1) -> (d0, d1)>"
+    pset = "affine_set<(i)[g] : (i - 2*g >= 0, -i + 2*g + 1 >= 0)>"
+    fut = f"!ktdp.tile_future<{V32}, groups = affine_set<(g) : (g >= 0, -g + 1 >= 0)>>"
+    G, M = f"memref<{rows}x{H}xf16>", f"memref<{rows}x{h}xf16>"
+    WG, WM = f"memref<1x{H}xf16>", f"memref<1x{h}xf16>"
+    at = f"!ktdp.access_tile<1x{h}xindex>"
+
+    def part(name, ptr, shape, cs, space):
+        return (f"    %{name} = ktdp.construct_memory_view {ptr}, sizes: [{shape[0]}, {shape[1]}], "
+                f"strides: [{shape[2]}, 1] {{\n      coordinate_set = {cs}, memory_space = {space}\n    }} : "
+                f"memref<{shape[0]}x{shape[1]}xf16>")
+
+    def tile(name, view, idx, mem):
+        return (f"      %{name} = ktdp.construct_access_tile %{view}[{idx}] {{\n"
+                f"        access_tile_set = {blk}, access_tile_order = {idm}\n      }} : {mem} -> {at}")
+
+    hbm, lx1 = "#ktdp.memory_space<global>", "#ktdp.memory_space<ct_local, ct_id = 1>"
+    return f"""module {{
+  func.func @rmsnorm_2x2(%X0: index, %W: index, %Y0: index, %Y1: index, %eps: f16) attributes {{grid = [2, 2]}} {{
+    %col_id, %row_id = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %ch = arith.constant {h} : index
+    %crh = arith.constant {rh} : index
+    %zero = arith.constant 0.0 : f32
+    %nf = arith.constant {float(H)} : f32
+    %row_start = arith.muli %row_id, %crh : index
+    %row_end = arith.addi %row_start, %crh : index
+    %col = arith.muli %col_id, %ch : index
+    %W1 = arith.addi %W, %ch : index
+{part("X_p0", "%X0", (rows, h, h), cset(0, h - 1, rows - 1), hbm)}
+{part("X_p1", "%c0", (rows, h, h), cset(h, H - 1, rows - 1), lx1)}
+    %X = ktdp.construct_distributed_memory_view (%X_p0, %X_p1 : {M}, {M}) : {G}
+{part("W_p0", "%W", (1, h, H), cset(0, h - 1, 0), hbm)}
+{part("W_p1", "%W1", (1, h, H), cset(h, H - 1, 0), hbm)}
+    %Wv = ktdp.construct_distributed_memory_view (%W_p0, %W_p1 : {WM}, {WM}) : {WG}
+{part("Y_p0", "%Y0", (rows, h, h), cset(0, h - 1, rows - 1), hbm)}
+{part("Y_p1", "%Y1", (rows, h, h), cset(h, H - 1, rows - 1), hbm)}
+    %Y = ktdp.construct_distributed_memory_view (%Y_p0, %Y_p1 : {M}, {M}) : {G}
+{tile("w_t", "Wv", "%c0, %col", WG).replace("      ", "    ", 1)}
+    %w = ktdp.load %w_t : {at} -> {T16}
+    %wf = arith.extf %w : {T16} to {T32}
+    scf.for %row = %row_start to %row_end step %c1 {{
+{tile("x_t", "X", "%row, %col", G)}
+      %x = ktdp.load %x_t : {at} -> {T16}
+      %xf = arith.extf %x : {T16} to {T32}
+      %sq = arith.mulf %xf, %xf : {T32}
+      %ss_init = tensor.splat %zero : {V32}
+      %ss = linalg.reduce {{ arith.addf }} ins(%sq : {T32}) outs(%ss_init : {V32}) dimensions = [1]
+      %fut = ktdp.inter_tile_produce producer_tiles_per_group = {pset}
+          : {V32} -> {fut}
+      {{
+        ^bb0(%gid: index):
+          ktdp.yield_partial %ss : {V32}
+      }}
+      %id_init = tensor.empty() : {V32}
+      %add_id = linalg.fill ins(%zero : f32) outs(%id_init : {V32}) -> {V32}
+      %full = ktdp.inter_tile_reduce(%fut) consumer_tiles_per_group = {pset}, identity(%add_id : {V32})
+          : {fut} -> {V32}
+      {{
+        ^bb0(%lhs: {V32}, %rhs: {V32}):
+          %init = tensor.empty() : {V32}
+          %sum = linalg.add ins(%lhs, %rhs : {V32}, {V32}) outs(%init : {V32}) -> {V32}
+          ktdp.yield_reduced %sum : {V32}
+      }}
+      %s = tensor.extract %full[%c0] : {V32}
+      %ms = arith.divf %s, %nf : f32
+      %mse = arith.addf %ms, %eps : f32
+      %rstd = math.rsqrt %mse : f32
+      %rb = tensor.splat %rstd : {T32}
+      %xn = arith.mulf %xf, %rb : {T32}
+      %yf = arith.mulf %xn, %wf : {T32}
+      %y = arith.truncf %yf : {T32} to {T16}
+{tile("y_t", "Y", "%row, %col", G)}
+      ktdp.store %y, %y_t : {T16}, {at}
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""

@@ -1,0 +1,85 @@
+"""ktdp.inter_tile_produce / inter_tile_reduce on the GPU, bit-exact against
+the oracle (reference ops/comm_ops.py:229-345, dialects/ktdp_ops.py:951-1230):
+group sums and maxima over contiguous, paired and strided groups, the ring's
+fold order where f16 rounding shows it, a reduce inside an scf.for, and a
+2 x 2 RMSNorm whose rows cross a distributed view (one half in core 1's LX)
+and whose mean square is folded across the column partners."""
+import numpy as np
+import pytest
+
+from tests import _cases
+from tests.test_inter_tile import (FOLD_WANT, FOLD_X, VARIANTS, oracle_ring, oracle_rmsnorm_2x2, ring_expected,
+                                   ring_inputs, rms_args, rms_inputs, rms_model, RMS_H, RMS_ROWS)
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_ring(kw, x):
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    interp = KTIRInterpreter()
+    interp.load(_cases.ring_reduce(**kw))
+    out = interp.execute_function("ring_reduce", in_ptr=x, out_ptr=np.zeros_like(x))["out_ptr"]
+    return out, interp.last_plan
+
+
+@pytest.mark.parametrize("name,kw", VARIANTS, ids=[v[0] for v in VARIANTS])
+def test_ring_reduce_groups(name, kw):
+    print(f"[ring] {name}", flush=True)
+    x = ring_inputs(kw, seed=1)
+    got, plan = gpu_ring(kw, x)
+    np.testing.assert_array_equal(got, oracle_ring(kw, x))
+    np.testing.assert_array_equal(got, ring_expected(kw, x))
+    assert plan.mode == "lockstep"
+
+
+@pytest.mark.parametrize("name,kw", VARIANTS[:3], ids=[v[0] for v in VARIANTS[:3]])
+def test_ring_reduce_random_f16_bit_exact(name, kw):
+    """Values where every fold rounds: the GPU must fold in the ring's order."""
+    print(f"[ring] random {name}", flush=True)
+    n = kw.get("n_cores", 4)
+    x = (np.random.default_rng(5).standard_normal((n, 128)) * 100).astype(np.float16)
+    got, _ = gpu_ring(kw, x)
+    np.testing.assert_array_equal(got, oracle_ring(kw, x))
+
+
+def test_ring_fold_order():
+    print("[ring] fold order", flush=True)
+    got, _ = gpu_ring({}, FOLD_X)
+    np.testing.assert_array_equal(got, FOLD_WANT[:, None].repeat(128, 1))
+
+
+def test_ring_reduce_by_one_core_is_refused():
+    """Only core 0 reaches the reduce (the reference deadlocks): refused
+    before the reduce runs, with no GPU work left waiting."""
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    interp = KTIRInterpreter()
+    interp.load(_cases.ring_reduce(only_core0=True))
+    x = ring_inputs({})
+    with pytest.raises(NotImplementedError):
+        interp.execute_function("ring_reduce", in_ptr=x, out_ptr=np.zeros_like(x))
+
+
+def gpu_rmsnorm_2x2(X, W):
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    interp = KTIRInterpreter()
+    interp.load(_cases.rmsnorm_2x2(RMS_ROWS, RMS_H))
+    orig = interp._prepare_execution
+
+    def prepare_and_seed(grid):
+        orig(grid)
+        interp.memory.get_lx(1).write(0, np.ascontiguousarray(X[:, RMS_H // 2:]).reshape(-1))
+
+    interp._prepare_execution = prepare_and_seed
+    out = interp.execute_function("rmsnorm_2x2", **rms_args(X, W))
+    return np.concatenate([out["Y0"], out["Y1"]], 1), interp
+
+
+def test_rmsnorm_2x2_distributed_ring():
+    print("[ring] rmsnorm 2x2", flush=True)
+    X, W = rms_inputs()
+    Y, interp = gpu_rmsnorm_2x2(X, W)
+    np.testing.assert_array_equal(Y, oracle_rmsnorm_2x2(X, W))
+    np.testing.assert_allclose(Y.astype(np.float64), rms_model(X, W), rtol=1e-2, atol=1e-2)
+    # core 1's LX still holds the right half of X
+    got_lx = interp.memory.get_lx(1).read(0, RMS_ROWS * RMS_H // 2, "f16")
+    np.testing.assert_array_equal(got_lx, np.ascontiguousarray(X[:, RMS_H // 2:]).reshape(-1))

@@ -1,0 +1,122 @@
+"""ktdp.inter_tile_produce / inter_tile_reduce in the oracle (no GPU).
+
+The reference's ring (ops/comm_ops.py:229-345) folds, at core c, its own
+partial and then the partials of cores c-1, c-2, ... (mod n) that produce
+for c's group, as combine(acc, received), with cores scheduled as in
+grid.py:524-623.  Pinned by: the exact group sums and maxima of small
+integers (any fold order gives them); f16 values where the order shows, with
+the expected results worked out by hand below; the reference's deadlock
+error when one core alone reaches the reduce; and an RMSNorm whose mean
+square crosses cores, against a float64 model.
+"""
+import numpy as np
+import pytest
+
+from oracle.interp import OracleInterpreter
+from tests import _cases
+
+VARIANTS = [
+    ("one_group", dict()),
+    ("pairs", dict(group_size=2)),
+    ("strided_8x4", dict(n_cores=8, group_size=4, strided=True)),
+    ("max", dict(combiner="max")),
+    ("inner_loop_3", dict(iters=3)),
+]
+
+
+def ring_inputs(kw, seed=0):
+    n = kw.get("n_cores", 4)
+    rng = np.random.default_rng(seed)
+    return rng.integers(-8, 9, size=(n, 128)).astype(np.float16)
+
+
+def ring_expected(kw, x):
+    """Each core's group result from the group membership alone."""
+    n = x.shape[0]
+    gs = kw.get("group_size") or n
+    ng = n // gs
+    out = np.empty_like(x)
+    for c in range(n):
+        members = [i for i in range(n) if (i % ng == c % ng)] if kw.get("strided") else \
+            [i for i in range(n) if i // gs == c // gs]
+        v = x[members].astype(np.float64)
+        out[c] = v.max(0) if kw.get("combiner") == "max" else v.sum(0) * max(1, kw.get("iters", 0))
+    return out
+
+
+def oracle_ring(kw, x):
+    o = OracleInterpreter()
+    o.load(_cases.ring_reduce(**kw))
+    return o.execute_function("ring_reduce", in_ptr=x, out_ptr=np.zeros_like(x))["out_ptr"]
+
+
+@pytest.mark.parametrize("name,kw", VARIANTS, ids=[v[0] for v in VARIANTS])
+def test_oracle_ring_reduce_group_results(name, kw):
+    x = ring_inputs(kw)
+    np.testing.assert_array_equal(oracle_ring(kw, x), ring_expected(kw, x))
+
+
+# partials 2048, 1, 1, 1 (f16 spacing at 2048 is 2, ties round to even):
+#   core 0: 2048 +1 -> 2048, +1 -> 2048, +1 -> 2048            = 2048
+#   core 1: 1 + 2048 -> 2048 (2049 ties to even), +1, +1        = 2048
+#   core 2: 1 + 1 = 2, + 2048 = 2050, + 1 -> 2052 (2051 ties up) = 2052
+#   core 3: 1 + 1 + 1 = 3, + 2048 -> 2052 (2051 ties up)        = 2052
+FOLD_X = np.array([2048, 1, 1, 1], np.float16)[:, None].repeat(128, 1)
+FOLD_WANT = np.array([2048, 2048, 2052, 2052], np.float16)
+
+
+def test_oracle_ring_fold_order():
+    out = oracle_ring({}, FOLD_X)
+    np.testing.assert_array_equal(out, FOLD_WANT[:, None].repeat(128, 1))
+
+
+def test_oracle_ring_deadlock_when_one_core_reduces():
+    o = OracleInterpreter()
+    o.load(_cases.ring_reduce(only_core0=True))
+    x = ring_inputs({})
+    with pytest.raises(RuntimeError, match="Deadlock detected: core 0 waiting on recv from core 3"):
+        o.execute_function("ring_reduce", in_ptr=x, out_ptr=np.zeros_like(x))
+
+
+RMS_ROWS, RMS_H = 16, 256
+
+
+def rms_inputs(seed=3):
+    rng = np.random.default_rng(seed)
+    X = (rng.standard_normal((RMS_ROWS, RMS_H)) * 2).astype(np.float16)
+    W = rng.uniform(0.5, 1.5, (1, RMS_H)).astype(np.float16)
+    return X, W
+
+
+def rms_args(X, W):
+    h = RMS_H // 2
+    z = np.zeros((RMS_ROWS, h), np.float16)
+    return dict(X0=np.ascontiguousarray(X[:, :h]), W=W, Y0=z, Y1=z.copy(), eps=np.float16(1e-5))
+
+
+def oracle_rmsnorm_2x2(X, W):
+    o = OracleInterpreter()
+    o.load(_cases.rmsnorm_2x2(RMS_ROWS, RMS_H))
+
+    def seed(o):
+        o.lxs[1].memory.write(0, np.ascontiguousarray(X[:, RMS_H // 2:]).reshape(-1))
+        o.lxs[1].next_ptr = 1 << 20
+    o.prepare_hook = seed
+    out = o.execute_function("rmsnorm_2x2", **rms_args(X, W))
+    return np.concatenate([out["Y0"], out["Y1"]], 1)
+
+
+def rms_model(X, W):
+    x = X.astype(np.float64)
+    return x / np.sqrt((x * x).mean(1, keepdims=True) + 1e-5) * W.astype(np.float64)
+
+
+def test_oracle_rmsnorm_2x2_distributed():
+    X, W = rms_inputs()
+    Y = oracle_rmsnorm_2x2(X, W)
+    np.testing.assert_allclose(Y.astype(np.float64), rms_model(X, W), rtol=1e-2, atol=1e-2)
+    # a row whose right half is zero: only core (0, r) contributes to the fold
+    X2 = X.copy()
+    X2[3, RMS_H // 2:] = 0
+    Y2 = oracle_rmsnorm_2x2(X2, W)
+    np.testing.assert_allclose(Y2.astype(np.float64), rms_model(X2, W), rtol=1e-2, atol=1e-2)
