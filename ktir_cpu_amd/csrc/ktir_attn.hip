@@ -421,6 +421,13 @@ __device__ __forceinline__ void tile16_to_lds(const uint16_t* src, int64_t row_s
                                              16, tile_lane_off(l, row_stride, i), (int)(i * 8 * row_stride), 0, 0);
 }
 
+// c + the two f16 values of w (v_dot2_f32_f16 against (1, 1): exact
+// products, one f32 sum)
+__device__ __forceinline__ float dot2_one(uint32_t w, float c) {
+  const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, c, false);
+}
+
 // row sum of P: this lane's 64 values plus the other half-wave's
 __device__ __forceinline__ float pp_rowsum(const f32x16_t (&p)[4]) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -478,9 +485,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
   float m = -__builtin_inff(), mr = -__builtin_inff(), lsum = 0.f;
   const int k_off = r32 * AT, k_x = swz16(r32 & 15);
   const int tg = l >> 4, tj = l & 15;
-  const int v_row0 = 8 * (tg >> 1) + (tj >> 2);
+  // P@V runs over the keys in the order that puts every lane's own S values
+  // in its P fragment: MFMA k = 8h + j is key 4h + j (j < 4) or 8 + 4h + j - 4
+  // of the 16-key step, so the V fragment of half h reads rows 4h .. 4h+3
+  // and 8 + 4h .. 8 + 4h + 3 of the step (no exchange between half-waves)
+  const int v_row0 = 4 * (tg >> 1) + (tj >> 2);
   const int v_c = 2 * (tg & 1) + ((tj >> 1) & 1), v_in = 4 * (tj & 1);
-  const int v_b0 = v_row0 * AT + v_in, v_x0 = v_c ^ swz16(v_row0), v_x1 = v_c ^ swz16(v_row0 + 4);
+  const int v_b0 = v_row0 * AT + v_in, v_x0 = v_c ^ swz16(v_row0), v_x1 = v_c ^ swz16(v_row0 + 8);
 
   // matrix phase M_j: O += P_{j-1} V_{j-1} (V tile in VB), then S_j = K_j Q^T (K tile in KB)
 #define PP_M(J, KB, VB)                                                                              \
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
         uint4 a[4];                                                                                  \
         _Pragma("unroll") for (int dt = 0; dt < 4; ++dt) {                                           \
           const uint2 lo = ds_tr16(vt + vfb + 8 * ((4 * dt) ^ vx0));                                 \
-          const uint2 hi = ds_tr16(vt + vfb + 4 * AT + 8 * ((4 * dt) ^ vx1));                        \
+          const uint2 hi = ds_tr16(vt + vfb + 8 * AT + 8 * ((4 * dt) ^ vx1));                        \
           a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);                                                \
         }                                                                                            \
         o0 = mfma_at<false>(a[0], ph[ks], o0);                                                       \
@@ -580,18 +591,23 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
       } else {                                                                                       \
         AT_S_LOOP(sc[kt][i] = exp_f(__fsub_rn(sc[kt][i], mr)))                                       \
       }                                                                                              \
-      lsum = __fadd_rn(lsum, pp_rowsum(sc));                                                         \
       m = mn;                                                                                        \
+      /* the row sum from the f16 P the product uses: two values per dot2 */                        \
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;                                                  \
       _Pragma("unroll") for (int ks = 0; ks < 8; ++ks) {                                             \
         const int kt = ks >> 1, g0 = 2 * (ks & 1);                                                   \
         uint32_t ah0 = cvt2<false>(sc[kt][4 * g0], sc[kt][4 * g0 + 1]);                              \
         uint32_t ah1 = cvt2<false>(sc[kt][4 * g0 + 2], sc[kt][4 * g0 + 3]);                          \
         uint32_t bh0 = cvt2<false>(sc[kt][4 * g0 + 4], sc[kt][4 * g0 + 5]);                          \
         uint32_t bh1 = cvt2<false>(sc[kt][4 * g0 + 6], sc[kt][4 * g0 + 7]);                          \
-        swap32(ah0, bh0);                                                                            \
-        swap32(ah1, bh1);                                                                            \
+        s0 = dot2_one(ah0, s0);                                                                      \
+        s1 = dot2_one(ah1, s1);                                                                      \
+        s2 = dot2_one(bh0, s2);                                                                      \
+        s3 = dot2_one(bh1, s3);                                                                      \
         ph[ks] = make_uint4(ah0, ah1, bh0, bh1);                                                     \
       }                                                                                              \
+      const float ls = __fadd_rn(__fadd_rn(s0, s1), __fadd_rn(s2, s3));                              \
+      lsum = __fadd_rn(lsum, __fadd_rn(ls, other_half(ls)));                                         \
     }                                                                                                \
   } while (0)
 

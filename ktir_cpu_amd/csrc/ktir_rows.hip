@@ -1341,6 +1341,22 @@ __device__ __forceinline__ gu4 rf_pack(const float (&v)[8]) {
   return c;
 }
 
+// as rf_pack, f16 pairs converted by one instruction (v_cvt_pk_f16_f32, round
+// to nearest even); the row kernels whose register count it does not raise
+template <int DT>
+__device__ __forceinline__ gu4 rf_pack2(const float (&v)[8]) {
+  if (DT == KTIR_BF16) return rf_pack<DT>(v);
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  gu4 c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f2 x = {v[2 * k], v[2 * k + 1]};
+    c[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+  }
+  return c;
+}
+
 // the chunks of the 16-bit row at element e0 of L: 16-byte loads when the row
 // lies inside [lo, hi), else element by element (out-of-range elements read 0)
 template <int NQ>
@@ -1450,36 +1466,59 @@ __device__ __forceinline__ void rf_fence(gu4 (&c)[NQ]) {
 
 template <int NQ, int DT>
 __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const RwPos& p, RowLanes& rr, int l) {
-  float mx = -__builtin_inff();
-  bool nan = false;
+  // row max, NaN-propagating as arith.maximumf (exact on the 16-bit values:
+  // f16 rows two at a time with v_pk_maximum3_f16)
+  float mx;
+  if (DT == KTIR_F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 a = {-__builtin_inff16(), -__builtin_inff16()}, b = a;
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    float v[8];
-    rf_unpack<DT>(c[i], v);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      mx = fmaxf(mx, v[j]);
-      nan = nan || v[j] != v[j];
+    for (int i = 0; i < NQ; ++i) {
+      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, c[i][0]));
+      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, c[i][1]));
+      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, c[i][2]));
+      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, c[i][3]));
     }
-    __builtin_amdgcn_sched_barrier(0);
+    a = __builtin_elementwise_maximum(a, b);
+    mx = __builtin_elementwise_maximum((float)a.x, (float)a.y);
+  } else {
+    float a = -__builtin_inff(), b = a;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      float v[8];
+      rf_unpack<DT>(c[i], v);
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        a = __builtin_elementwise_maximum(a, v[j]);
+        b = __builtin_elementwise_maximum(b, v[j + 1]);
+      }
+    }
+    mx = __builtin_elementwise_maximum(a, b);
   }
 #pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
-  rr.set(F.fold0, __any(nan) ? __int_as_float(0x7fc00000) : mx);
+  for (int s = 32; s >= 1; s >>= 1) mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, s));
+  rr.set(F.fold0, mx);
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float m = rr.get(F.m);
   rf_fence<NQ>(c);
-  // exp(x - m'), kept for the store pass
+  // exp(x - m'), kept for the store pass (x <= m', so every value is at most
+  // 1, or NaN when the row holds NaN or +inf)
   float ev[NQ][8];
-  float big = 0.f;
+  const bool near = fabsf(m) < 2048.f;
+  const float c0 = -__fmul_rn(m, 1.44269504088896341f);
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    rf_unpack<DT>(c[i], ev[i]);
+  for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], ev[i]);
+  if (near) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      ev[i][j] = exp_hw(__fsub_rn(ev[i][j], m));
-      big = fmaxf(big, fabsf(ev[i][j]));
-    }
+    for (int i = 0; i < NQ; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        ev[i][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(ev[i][j], 1.44269504088896341f, c0));
+  } else {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ev[i][j] = exp_hw(__fsub_rn(ev[i][j], m));
   }
   const float sum = rf_sum<NQ>([&](int i, float (&e)[8]) {
 #pragma unroll
@@ -1488,11 +1527,12 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   rr.set(F.fold1, sum);
   for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
   const float s = rr.get(F.s);
-  // x / s as the corrected product with the correctly rounded 1 / s; the
-  // plain quotient for huge or non-finite operands
+  // x / s as x times the correctly rounded 1 / s (within 1.5 f32 ulps of the
+  // quotient, before the 16-bit rounding of the store); the plain quotient
+  // for a sum that is tiny, huge or not finite
   const float r = __fdiv_rn(1.f, s);
   const float as = fabsf(s);
-  const bool fast = as > 1e-30f && as < 1e30f && r == r && __all(big < 1e30f);
+  const bool fast = as > 1e-30f && as < 1e30f && r == r;
   const int64_t e0 = rw_row_base(F.y, p);
   const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
   // the two divisions on separate (uniform) branches
@@ -1502,12 +1542,12 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
       float y[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = div(ev[i][j]);
-      rf_store(F.y, e0, in, i, l, rf_pack<DT>(y));
+      rf_store(F.y, e0, in, i, l, rf_pack2<DT>(y));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
   if (fast) {
-    out([&](float e) { return div_by(e, s, r); });
+    out([&](float e) { return __fmul_rn(e, r); });
   } else {
     // rare (huge or non-finite operands): one quotient at a time, so that
     // this branch does not set the kernel's register count

@@ -165,7 +165,8 @@ YTILE
 
 def test_scf_if_lane_varying_condition():
     """scf.if whose condition differs between cores (cores 0-2 store x + x,
-    the others exp(x)): the executor runs the cores one at a time."""
+    the others exp(x)): each branch runs on the lanes that take it, all
+    cores still together."""
     from ktir_cpu_amd import configs
     from ktir_cpu_amd.interpreter import KTIRInterpreter
     src = (_IF_KERNEL.replace("XVIEW", configs._view("x_view", "x_ptr", [2048], [1], "f16"))
@@ -179,7 +180,7 @@ def test_scf_if_lane_varying_condition():
     g = KTIRInterpreter()
     g.load(src)
     got = g.execute_function("if_kernel", x_ptr=x, y_ptr=np.zeros(2048, np.float16))["y_ptr"]
-    assert g.last_plan.mode == "sequential"
+    assert g.last_plan.mode == "lockstep"
     d = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
     assert d[:768].max() == 0 and d.max() <= 1
     np.testing.assert_array_equal(got[:768], x[:768] + x[:768])
