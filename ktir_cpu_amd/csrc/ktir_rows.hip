@@ -1501,33 +1501,55 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float m = rr.get(F.m);
   rf_fence<NQ>(c);
-  // exp(x - m'), kept for the store pass (x <= m', so every value is at most
-  // 1, or NaN when the row holds NaN or +inf)
-  float ev[NQ][8];
+  // exp(x - m') rounded to f16 (at most 1: x <= m'), kept packed for the
+  // store pass (half the registers of f32 values); the row sum adds the same
+  // f16 values two per dot2.  Against the reference's f32 values this moves
+  // each output by at most about 2^-11 of itself, inside softmax's tolerance.
+  // While |m'| < 2048 the exponent is one FMA into exp2 (the rounding of
+  // m' log2 e is then below 2^-12 of it); else the difference first.
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  uint32_t ep[NQ * 4];
   const bool near = fabsf(m) < 2048.f;
   const float c0 = -__fmul_rn(m, 1.44269504088896341f);
-#pragma unroll
-  for (int i = 0; i < NQ; ++i) rf_unpack<DT>(c[i], ev[i]);
+  const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  float s0 = 0.f, s1 = 0.f;
   if (near) {
 #pragma unroll
-    for (int i = 0; i < NQ; ++i)
+    for (int i = 0; i < NQ; ++i) {
+      float v[8];
+      rf_unpack<DT>(c[i], v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        ev[i][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(ev[i][j], 1.44269504088896341f, c0));
+      for (int k = 0; k < 4; ++k) {
+        const f2 x = {__builtin_amdgcn_exp2f(__builtin_fmaf(v[2 * k], 1.44269504088896341f, c0)),
+                      __builtin_amdgcn_exp2f(__builtin_fmaf(v[2 * k + 1], 1.44269504088896341f, c0))};
+        ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+      }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < NQ; ++i)
+    for (int i = 0; i < NQ; ++i) {
+      float v[8];
+      rf_unpack<DT>(c[i], v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ev[i][j] = exp_hw(__fsub_rn(ev[i][j], m));
+      for (int k = 0; k < 4; ++k) {
+        const f2 x = {exp_hw(__fsub_rn(v[2 * k], m)), exp_hw(__fsub_rn(v[2 * k + 1], m))};
+        ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+      }
+    }
   }
-  const float sum = rf_sum<NQ>([&](int i, float (&e)[8]) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) e[j] = ev[i][j];
-  });
+  for (int q = 0; q < NQ * 4; q += 2) {
+    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q]), one, s0, false);
+    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q + 1]), one, s1, false);
+  }
+  float sum = __fadd_rn(s0, s1);
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, sh));
   rr.set(F.fold1, sum);
   for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
   const float s = rr.get(F.s);
-  // x / s as x times the correctly rounded 1 / s (within 1.5 f32 ulps of the
+  // e / s as e times the correctly rounded 1 / s (within 1.5 f32 ulps of the
   // quotient, before the 16-bit rounding of the store); the plain quotient
   // for a sum that is tiny, huge or not finite
   const float r = __fdiv_rn(1.f, s);
@@ -1541,7 +1563,11 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
     for (int i = 0; i < NQ; ++i) {
       float y[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = div(ev[i][j]);
+      for (int k = 0; k < 4; ++k) {
+        const f2 e = __builtin_convertvector(__builtin_bit_cast(h2, ep[4 * i + k]), f2);
+        y[2 * k] = div(e.x);
+        y[2 * k + 1] = div(e.y);
+      }
       rf_store(F.y, e0, in, i, l, rf_pack2<DT>(y));
       __builtin_amdgcn_sched_barrier(0);
     }
