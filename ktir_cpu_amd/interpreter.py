@@ -24,7 +24,7 @@ from .ir import IRModule
 from .latency import LatencyReport, LatencyTracker
 from .memory import DeviceMemory
 from .parser import KTIRParser
-from .walker import Executor
+from .walker import Executor, _has_op
 
 _NP_TO_KTIR = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.int32): "i32",
                np.dtype(np.int64): "i64", np.dtype(np.uint16): "bf16", np.dtype(np.bool_): "i1",
@@ -215,9 +215,14 @@ class KTIRInterpreter:
             nx, ny, nz = fn.grid
             lat.reset()
             lat.set_cores_active(nx * ny * nz)
-            ex = Executor(fn, arena, args, self._pool, sequential=True, lx_size_mb=self.lx_size_mb, latency=lat,
-                          lx=self._lx)
-            plan = ex.run()
+            # cores that meet at a ring reduce run together (op by op, as walked)
+            collective = _has_op(fn.operations, "ktdp.inter_tile_reduce")
+            ex = Executor(fn, arena, args, self._pool, sequential=not collective, lx_size_mb=self.lx_size_mb,
+                          latency=lat, lx=self._lx)
+            try:
+                plan = ex.run()
+            except NeedEager as why:
+                raise NotImplementedError(f"latency model for cores that meet at a ring reduce: {why}") from None
             plan.fallback_reason = "latency model"
         else:
             try:

@@ -309,6 +309,10 @@ class Executor:
         # cores meet at ktdp.inter_tile_reduce: every core must run in lockstep
         self.collective = _has_op(fn.operations, "ktdp.inter_tile_reduce")
         self.had_reduce = False
+        # latency model: lanes charged by the op being recorded (None: all),
+        # and the ring bytes a reduce moved per core
+        self._lat_mask: Optional[np.ndarray] = None
+        self._lat_comm = 0
         # latency model (ktir_cpu_amd.latency.LatencyTracker) charged op by op, or None
         self.lat = latency
         self._lat_mem: Optional[np.ndarray] = None
@@ -338,6 +342,9 @@ class Executor:
                 lanes = Lanes(np.array([c], dtype=np.int64), np.array([c], dtype=np.int64))
                 self._run_body(lanes)
         else:
+            if self.lat is not None:
+                # the latency model reads device data op by op: launch as walked
+                self._go_eager()
             lanes = Lanes(np.arange(self.n_cores, dtype=np.int64), np.arange(self.n_cores, dtype=np.int64))
             self._run_body(lanes)
             why = verify(self.accesses, self.insts)
@@ -495,10 +502,16 @@ class Executor:
         from . import latency
         cat = latency.category_of(t)
         cores = self.lanes.cores
+        sel = np.arange(len(cores)) if self._lat_mask is None else np.flatnonzero(self._lat_mask)
+        cores = cores[sel]
         if cat == latency.LC.MEMORY:
-            sticks = self._lat_mem if self._lat_mem is not None else np.zeros(len(cores), np.int64)
+            sticks = self._lat_mem[sel] if self._lat_mem is not None else np.zeros(len(cores), np.int64)
             for c, k in zip(cores, sticks):
                 self.lat.record_op(int(c), t, nbytes=int(k) * latency.STICK_BYTES)
+            return
+        if cat == latency.LC.COMM:
+            for c in cores:
+                self.lat.record_op(int(c), t, nbytes=int(self._lat_comm))
             return
         if cat == latency.LC.COMPUTE_MATMUL:
             tiles = [v for v in (operands or []) if isinstance(v, Tile)]
@@ -2200,11 +2213,13 @@ class Executor:
                 continue
             got = Tile(remap_lanes(seed.e, lane_of[origin]))
             self.push_scope()
+            self._lat_mask = fold          # the combiner runs on the cores that fold at this round
             try:
                 self.set_value(lhs, acc)
                 self.set_value(rhs, got)
                 r = _unwrap(self._run(region.ops))
             finally:
+                self._lat_mask = None
                 self.pop_scope()
             if not isinstance(r, Tile):
                 raise TypeError(f"ktdp.inter_tile_reduce: combiner did not yield a Tile, got {type(r)}")
@@ -2212,6 +2227,15 @@ class Executor:
                 ea = acc.e if tuple(acc.shape) == tuple(r.shape) else self._operand(acc, r.dtype, r.shape, False)
                 r = Tile(Expr("sel", r.dtype, r.shape, [E_scalar(fold.astype(np.int64), "i32", r.shape), r.e, ea]))
             acc = self.materialize(r)
+        if self.lat is not None:
+            # every core sends its seed n - 1 times (ops/comm_ops.py:229-345);
+            # the reference's latency tracker needs a result on every core
+            # (latency.py:533-558), so a non-consumer is an error there
+            C = op.attributes["consumer_tiles_per_group"]
+            for c, g in zip(cores, fut.gid):
+                if not C.contains([int(c)], [int(g)]):
+                    raise RuntimeError("_comm_size: comm op result must be a Tile, got NoneType")
+            self._lat_comm = (n - 1) * _prod(seed.shape) * rt.ELEM_BYTES[seed.dtype]
         rs = op.attributes.get("_result_shape")
         if rs is not None and tuple(rs) != tuple(acc.shape):
             acc = self.reshape(acc, tuple(rs))

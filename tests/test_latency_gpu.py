@@ -119,3 +119,39 @@ def test_report_text_and_summary():
     assert "Kernel cycles" in s and "Roofline: PER-CORE" in s
     d = rep.summary_dict()
     assert d["grid_cores"] == 32 and math.isclose(d["kernel_cycles"], rep.kernel_cycles)
+
+
+@pytest.mark.parametrize("group_size,folds", [(None, 3), (2, 1)])
+def test_ring_reduce_comm_charge(group_size, folds):
+    """The reference's ring-reduce latency breakdown
+    (tests/test_latency.py:2235-2420) on this repository's 4-core ring
+    kernel: every core's reduce is charged (n - 1) x 256 ring bytes in the
+    comm bucket (the ring spans the whole workgroup, whatever the groups),
+    the combiner's linalg.add runs once per round that folds a producer of
+    the core's group (3 in one group of 4, 1 in pairs), produce is free,
+    and the results match the run without the model."""
+    from tests.test_inter_tile import ring_inputs
+    cfg = HardwareConfig()
+    kw = {} if group_size is None else {"group_size": group_size}
+    x = ring_inputs(kw, seed=4)
+    case = (_cases.ring_reduce(**kw), "ring_reduce", {"in_ptr": x, "out_ptr": np.zeros_like(x)})
+    rep, out = _run(case, cfg, trace=True)
+    g = KTIRInterpreter()
+    g.load(case[0])
+    plain = g.execute_function("ring_reduce", in_ptr=x, out_ptr=np.zeros_like(x))
+    np.testing.assert_array_equal(out["out_ptr"], plain["out_ptr"])
+    ring = 3 * 128 * 2
+    assert set(rep.counters) == {0, 1, 2, 3}
+    for core, cc in rep.counters.items():
+        ops = [t.op_type for t in cc.trace]
+        assert ops.count("ktdp.inter_tile_produce") == 1 and ops.count("ktdp.inter_tile_reduce") == 1
+        assert ops.count("linalg.add") == folds
+        prod = next(t for t in cc.trace if t.op_type == "ktdp.inter_tile_produce")
+        assert prod.cycles == 0 and prod.category == "zero"
+        red = next(t for t in cc.trace if t.op_type == "ktdp.inter_tile_reduce")
+        assert red.category == "comm" and red.cycles == pytest.approx(ring / cfg.ring_bytes_per_cycle)
+        assert cc.comm_bytes == ring
+        assert cc.comm_cycles == pytest.approx(ring / cfg.ring_bytes_per_cycle)
+        # one 1 x 128 f16 load and one store: two sticks each
+        assert cc.dram_bytes == 2 * 2 * STICK_BYTES
+        assert cc.total_bytes == cc.dram_bytes + cc.comm_bytes
