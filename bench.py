@@ -365,8 +365,13 @@ def collect_traffic(root):
         for fn in files:
             with open(fn) as f:
                 for row in csv.DictReader(f):
+                    name = row.get("Kernel_Name", "")
+                    # set-up work outside the timed launch: the runtime's copies and
+                    # fills, and the library's one-time fill of its own scratch array
+                    if name.startswith("__amd_rocclr") or name.startswith("rmw_fill"):
+                        continue
                     if row.get("Counter_Name") == counter:
-                        vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+                        vals.setdefault(name, []).append(float(row["Counter_Value"]))
         return {k: float(np.median(v)) for k, v in vals.items()}
 
     cf, cw = per_kernel("copy", "FETCH_SIZE"), per_kernel("copy", "WRITE_SIZE")

@@ -142,16 +142,13 @@ __device__ __forceinline__ void tile_to_lds(const uint16_t* src, int64_t row_str
 // The position mask keeps score (row, key) iff ((lo <= kpos - qpos <= hi) != inv).
 // PV16: the P @ V product in f16 (V f16: the f16 operands, or the f16 copy of
 // bf16 V), P rounded once to f16; else in the operand type with P as hi + lo.
+// one query block (lane order[blk], or blk) of the launch
 template <bool BF16, bool PV16>
-__global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
-  if (BF16 && d.v16_ptr && d.o_ptr && !d.acc_out) {
-    // the conversion before this launch decided which of the two kernels runs
-    if ((*(const int*)d.v16_flag != 0) == PV16) return;
-  }
+__device__ __forceinline__ void attn_block(const ktir_attn_t& d, int mlo, int mhi, int minv, int64_t blk) {
   __shared__ __align__(16) uint16_t Ks[AT * AT];    // K tile, [key][d] (chunk-swizzled rows)
   __shared__ __align__(16) uint16_t Vs[AT * AT];    // V tile, [key][d] (chunk-swizzled rows)
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, r32 = l & 31;
-  const int64_t lane = uni(d.order ? ((const int32_t*)d.order)[blockIdx.x] : (int)blockIdx.x);
+  const int64_t lane = uni(d.order ? ((const int32_t*)d.order)[blk] : blk);
   const int T = uni(((const int32_t*)d.trips)[lane]);
   const uint16_t* Q = (const uint16_t*)d.q_ptr;
   const uint16_t* K = (const uint16_t*)d.k_ptr;
@@ -392,6 +389,27 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int m
     AT_EPI(o2, 2)
     AT_EPI(o3, 3)
 #undef AT_EPI
+  }
+}
+
+template <bool BF16, bool PV16>
+__global__ __launch_bounds__(256, 2) void attn_kernel(const ktir_attn_t d, int mlo, int mhi, int minv) {
+  if (BF16 && d.v16_ptr && d.o_ptr && !d.acc_out) {
+    // the conversion before this launch decided which of the two kernels runs
+    if ((*(const int*)d.v16_flag != 0) == PV16) return;
+  }
+  attn_block<BF16, PV16>(d, mlo, mhi, minv, blockIdx.x);
+}
+
+// The hi + lo bf16 variant behind the f16 form: it runs only when the V
+// conversion found a value f16 cannot hold, and otherwise every workgroup
+// exits at once, so it takes a small grid whose workgroups loop over the
+// query blocks.
+__global__ __launch_bounds__(256, 2) void attn_kernel_gated(const ktir_attn_t d, int mlo, int mhi, int minv) {
+  if (*(const int*)d.v16_flag == 0) return;
+  for (int64_t blk = blockIdx.x; blk < d.lanes; blk += gridDim.x) {
+    if (blk != (int64_t)blockIdx.x) __syncthreads();   // the previous block's LDS reads are done
+    attn_block<true, false>(d, mlo, mhi, minv, blk);
   }
 }
 
@@ -779,7 +797,8 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
       hipLaunchKernelGGL((attn_pp<true>), pgrid, dim3(512), 0, stream(), *d, lo, hi, inv);
     else
       hipLaunchKernelGGL((attn_kernel<true, true>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
-    hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
+    const dim3 fgrid((unsigned)(d->lanes < 512 ? d->lanes : 512));
+    hipLaunchKernelGGL(attn_kernel_gated, fgrid, dim3(256), 0, stream(), *d, lo, hi, inv);
   } else if (d->dtype == KTIR_BF16) {
     hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, stream(), *d, lo, hi, inv);
   } else if (norm && pp) {
