@@ -611,3 +611,78 @@ def rmsnorm_2x2(rows=16, H=256):
   }}
 }}
 """
+
+
+def splitk_pv(K=1024, N=128, nx=2, ny=4):
+    """Decode P @ V split over a [nx, ny] grid (the reference's
+    examples/sdsc/sdpa_pv_ksplit.mlir shape of problem, written here): core
+    (x, y) multiplies P[0, yK/ny ..] (1 x K/ny, f16) by V[yK/ny .., xN/nx ..]
+    in f32, rounds the 1 x N/nx partial to f16, and the partials of the cores
+    with the same x -- the strided group {x, x + nx, x + 2 nx, ...} of linear
+    ids -- are summed by inter_tile_reduce (an f16 combiner); core (x, 0)
+    stores C[0, xN/nx ..]."""
+    kb, nb = K // ny, N // nx
+    T = lambda s, dt: f"tensor<{s[0]}x{s[1]}x{dt}>"
+    pset = f"affine_set<(i)[g] : ((i - g) mod {nx} == 0, i - g >= 0, -i + g + {nx * ny - nx} >= 0)>"
+    groups = f"affine_set<(g) : (g >= 0, -g + {nx - 1} >= 0)>"
+    fut = f"!ktdp.tile_future<{T((1, nb), 'f16')}, groups = {groups}>"
+    box = lambda r, c: f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {r - 1} >= 0, d1 >= 0, -d1 + {c - 1} >= 0)>"
+    idm = "affine_map<(d0, d1) -> (d0, d1)>"
+    hbm = "#ktdp.memory_space<global>"
+
+    def view(name, ptr, shape, strides):
+        return (f"    %{name} = ktdp.construct_memory_view %{ptr}, sizes: [{shape[0]}, {shape[1]}], strides: "
+                f"[{strides[0]}, {strides[1]}] {{\n      coordinate_set = {box(*shape)}, memory_space = {hbm}\n"
+                f"    }} : memref<{shape[0]}x{shape[1]}xf16>")
+
+    def tile(name, v, idx, shape, vshape):
+        return (f"    %{name} = ktdp.construct_access_tile %{v}[{idx}] {{\n      access_tile_set = {box(*shape)}, "
+                f"access_tile_order = {idm}\n    }} : memref<{vshape[0]}x{vshape[1]}xf16> -> "
+                f"!ktdp.access_tile<{shape[0]}x{shape[1]}xindex>")
+    return f"""module {{
+  func.func @splitk_pv(%p_ptr: index, %v_ptr: index, %c_ptr: index) attributes {{grid = [{nx}, {ny}]}} {{
+    %x, %y = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+    %ckb = arith.constant {kb} : index
+    %cnb = arith.constant {nb} : index
+    %k0 = arith.muli %y, %ckb : index
+    %n0 = arith.muli %x, %cnb : index
+{view("pv", "p_ptr", (1, K), (K, 1))}
+{view("vv", "v_ptr", (K, N), (N, 1))}
+{view("cv", "c_ptr", (1, N), (N, 1))}
+{tile("pt", "pv", "%c0, %k0", (1, kb), (1, K))}
+{tile("vt", "vv", "%k0, %n0", (kb, nb), (K, N))}
+    %p = ktdp.load %pt : !ktdp.access_tile<1x{kb}xindex> -> {T((1, kb), 'f16')}
+    %v = ktdp.load %vt : !ktdp.access_tile<{kb}x{nb}xindex> -> {T((kb, nb), 'f16')}
+    %pf = arith.extf %p : {T((1, kb), 'f16')} to {T((1, kb), 'f32')}
+    %vf = arith.extf %v : {T((kb, nb), 'f16')} to {T((kb, nb), 'f32')}
+    %zf = arith.constant 0.0 : f32
+    %acc0 = tensor.splat %zf : {T((1, nb), 'f32')}
+    %prod = linalg.matmul ins(%pf, %vf : {T((1, kb), 'f32')}, {T((kb, nb), 'f32')}) outs(%acc0 : {T((1, nb), 'f32')}) -> {T((1, nb), 'f32')}
+    %part = arith.truncf %prod : {T((1, nb), 'f32')} to {T((1, nb), 'f16')}
+    %fut = ktdp.inter_tile_produce producer_tiles_per_group = {pset}
+        : {T((1, nb), 'f16')} -> {fut}
+    {{
+      ^bb0(%gid: index):
+        ktdp.yield_partial %part : {T((1, nb), 'f16')}
+    }}
+    %z = arith.constant 0.0 : f16
+    %e = tensor.empty() : {T((1, nb), 'f16')}
+    %id = linalg.fill ins(%z : f16) outs(%e : {T((1, nb), 'f16')}) -> {T((1, nb), 'f16')}
+    %red = ktdp.inter_tile_reduce(%fut) consumer_tiles_per_group = {pset}, identity(%id : {T((1, nb), 'f16')})
+        : {fut} -> {T((1, nb), 'f16')}
+    {{
+      ^bb0(%lhs: {T((1, nb), 'f16')}, %rhs: {T((1, nb), 'f16')}):
+        %init = tensor.empty() : {T((1, nb), 'f16')}
+        %s = linalg.add ins(%lhs, %rhs : {T((1, nb), 'f16')}, {T((1, nb), 'f16')}) outs(%init : {T((1, nb), 'f16')}) -> {T((1, nb), 'f16')}
+        ktdp.yield_reduced %s : {T((1, nb), 'f16')}
+    }}
+    %is0 = arith.cmpi eq, %y, %c0 : index
+    scf.if %is0 {{
+{tile("ct", "cv", "%c0, %n0", (1, nb), (1, N)).replace("    ", "      ", 1)}
+      ktdp.store %red, %ct : {T((1, nb), 'f16')}, !ktdp.access_tile<1x{nb}xindex>
+    }}
+    return
+  }}
+}}
+"""

@@ -83,3 +83,27 @@ def test_rmsnorm_2x2_distributed_ring():
     # core 1's LX still holds the right half of X
     got_lx = interp.memory.get_lx(1).read(0, RMS_ROWS * RMS_H // 2, "f16")
     np.testing.assert_array_equal(got_lx, np.ascontiguousarray(X[:, RMS_H // 2:]).reshape(-1))
+
+
+def test_splitk_pv_strided_groups():
+    """Split-K decode P @ V over a [2, 4] grid with strided reduce groups:
+    integer data (every product, partial and fold exact) must match the
+    integer product; random data the oracle (rtol 1e-2 / atol 1e-3: the f32
+    summation order inside each partial's matmul differs) and P @ V at the
+    reference's split-K tolerance."""
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    from tests.test_inter_tile import oracle_splitk, splitk_inputs
+    print("[ring] split-K P@V", flush=True)
+
+    def run(P, V):
+        g = KTIRInterpreter()
+        g.load(_cases.splitk_pv(P.shape[1], V.shape[1]))
+        return g.execute_function("splitk_pv", p_ptr=P, v_ptr=V, c_ptr=np.zeros((1, V.shape[1]), np.float16))["c_ptr"]
+
+    Pi = np.random.default_rng(1).integers(-2, 3, (1, 1024)).astype(np.float16)
+    Vi = np.random.default_rng(2).integers(-2, 3, (1024, 128)).astype(np.float16)
+    np.testing.assert_array_equal(run(Pi, Vi), (Pi.astype(np.int64) @ Vi.astype(np.int64)).astype(np.float16))
+    P, V = splitk_inputs()
+    C = run(P, V)
+    np.testing.assert_allclose(C.astype(np.float32), oracle_splitk(P, V).astype(np.float32), rtol=1e-2, atol=1e-3)
+    np.testing.assert_allclose(C.astype(np.float32), P.astype(np.float32) @ V.astype(np.float32), rtol=2e-2, atol=2e-1)

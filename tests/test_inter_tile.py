@@ -120,3 +120,28 @@ def test_oracle_rmsnorm_2x2_distributed():
     X2[3, RMS_H // 2:] = 0
     Y2 = oracle_rmsnorm_2x2(X2, W)
     np.testing.assert_allclose(Y2.astype(np.float64), rms_model(X2, W), rtol=1e-2, atol=1e-2)
+
+
+def splitk_inputs(K=1024, N=128, seed=9):
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((1, K)).astype(np.float16), rng.standard_normal((K, N)).astype(np.float16)
+
+
+def oracle_splitk(P, V):
+    o = OracleInterpreter()
+    o.load(_cases.splitk_pv(P.shape[1], V.shape[1]))
+    return o.execute_function("splitk_pv", p_ptr=P, v_ptr=V, c_ptr=np.zeros((1, V.shape[1]), np.float16))["c_ptr"]
+
+
+def test_oracle_splitk_pv_strided_groups():
+    """Split-K decode P @ V with strided reduce groups: C = P @ V within the
+    f16 rounding of the partials and of every fold (the reference's own
+    tolerance for its split-K kernel, tests/test_examples.py:683-723)."""
+    P, V = splitk_inputs()
+    C = oracle_splitk(P, V)
+    want = P.astype(np.float32) @ V.astype(np.float32)
+    np.testing.assert_allclose(C.astype(np.float32), want, rtol=2e-2, atol=2e-1)
+    # the same with integer data, where every product, partial and fold is exact
+    Pi = np.random.default_rng(1).integers(-2, 3, (1, 1024)).astype(np.float16)
+    Vi = np.random.default_rng(2).integers(-2, 3, (1024, 128)).astype(np.float16)
+    np.testing.assert_array_equal(oracle_splitk(Pi, Vi), (Pi.astype(np.int64) @ Vi.astype(np.int64)).astype(np.float16))
