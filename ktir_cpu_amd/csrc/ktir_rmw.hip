@@ -207,6 +207,84 @@ __device__ __forceinline__ void rmw_src4(const ktir_rmw_t& d, int64_t se, float*
   }
 }
 
+// A chain of three to RMW_CH entries whose rows lie inside their
+// allocations: walk it once from the owner's third entry, keeping every
+// (entry, source) pair, order the sources by ascending entry, then combine
+// them in that order (instead of a walk per entry with a load after each).
+// Returns false, having changed nothing, for a longer chain or a source row
+// outside its allocation (the element-by-element path takes those).
+constexpr int RMW_CH = 8;
+
+template <int SDT, bool D128>
+__device__ __forceinline__ bool apply_short_chain(const ktir_rmw_t& d, int32_t r, int32_t e, int32_t s, int2 nx,
+                                                  int2 n2, int64_t n_entries, int hl) {
+  const KTIR_G(gi2)* nxt = (const KTIR_G(gi2)*)d.link;
+  int32_t ce[RMW_CH], cs[RMW_CH];
+  ce[0] = e; cs[0] = s;
+  ce[1] = nx.x; cs[1] = nx.y;
+  ce[2] = n2.x; cs[2] = n2.y;
+  int L = 3;
+  int2 t = n2;
+#pragma unroll
+  for (int q = 3; q <= RMW_CH; ++q) {
+    const gi2 u = nxt[t.x];
+    t = u.x >= 0 && u.x < n_entries ? make_int2(u.x, u.y) : make_int2(-1, -1);
+    if (t.x < 0) break;
+    if (q == RMW_CH) return false;       // longer than RMW_CH entries
+    ce[q] = t.x;
+    cs[q] = t.y;
+    L = q + 1;
+  }
+  const int64_t D = D128 ? 128 : d.D;
+#pragma unroll
+  for (int q = 0; q < RMW_CH; ++q) {
+    if (q >= L) break;
+    const int64_t se = d.src_base + (int64_t)cs[q] * d.src_row;
+    if (se < 0 || se + D > d.src_hi) return false;
+  }
+  const KTIR_G(float)* dst = (const KTIR_G(float)*)d.dst_ptr;
+  const int64_t de = d.dst_base + (int64_t)r * d.dst_row;
+  // the order of application: sources by ascending entry
+  int32_t os[RMW_CH];
+  int32_t prev = -1;
+#pragma unroll
+  for (int it = 0; it < RMW_CH; ++it) {
+    int32_t m = 0x7fffffff, sm = 0;
+#pragma unroll
+    for (int q = 0; q < RMW_CH; ++q) {
+      const bool take = q < L && ce[q] > prev && ce[q] < m;
+      m = take ? ce[q] : m;
+      sm = take ? cs[q] : sm;
+    }
+    prev = m;
+    os[it] = sm;
+  }
+  for (int64_t c = (int64_t)hl * 4; c < D; c += 128) {
+    const gf4 v = *(const KTIR_G(gf4)*)(dst + de + c);
+    float x[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+    for (int it = 0; it < RMW_CH; ++it) {
+      if (it >= L) break;
+      float g[4];
+      rmw_src4<SDT>(d, d.src_base + (int64_t)os[it] * d.src_row + c, g);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = combine(d.op, d.order, KTIR_F32, x[k], g[k]);
+    }
+    *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + de + c) = gf4{x[0], x[1], x[2], x[3]};
+  }
+  // leave the row's head and every slot of the chain empty (after every lane
+  // of the half-wave has read them)
+  __builtin_amdgcn_wave_barrier();
+  if (hl == 0) {
+    ((KTIR_G(int32_t)*)d.head)[r] = -1;
+    KTIR_G(gi2)* slot = (KTIR_G(gi2)*)d.link;
+#pragma unroll
+    for (int q = 0; q < RMW_CH; ++q)
+      if (q < L) slot[ce[q]] = gi2{-1, -1};
+  }
+  return true;
+}
+
 // The common form: f32 destination rows and f16 / f32 source rows, unit
 // column stride, 16-byte aligned rows, D a multiple of 128, f32 result.  A
 // half-wave takes RMW_NE consecutive entries; lane l covers columns
@@ -285,11 +363,13 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
     }
   }
   // chains of three or more entries and rows reaching past their allocation
-  // (rare): element by element, then the same resets
+  // (rare): short chains at once, the rest element by element, then the
+  // same resets
 #pragma unroll
   for (int j = 0; j < RMW_NE; ++j) {
     if (r[j] < 0 || (fast[j] && n2[j].x < 0)) continue;
     const int32_t e = (int32_t)(e0 + j);
+    if (fast[j] && apply_short_chain<SDT, D128>(d, r[j], e, s[j], nx[j], n2[j], n_entries, hl)) continue;
     const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
     for (int64_t c = (int64_t)hl * 4; c < D; c += 128) {
       float x[4];
