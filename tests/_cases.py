@@ -686,3 +686,90 @@ def splitk_pv(K=1024, N=128, nx=2, ny=4):
   }}
 }}
 """
+
+
+def ffn_swiglu_4core(seq=4, d=256, f=1024, cores=4):
+    """SwiGLU feed-forward with the hidden dimension split over `cores`
+    cores (the shape of problem of the reference's ffn_swiglu_4core
+    example, written here): x [seq, d] is read by every core; core c owns
+    columns c*f/cores .. of W_gate and W_up and the matching rows of W_down,
+    computes h = silu(x W_gate_c) * (x W_up_c) and its partial h W_down_c
+    (f16 matmuls, f32 accumulation inside), the partials are summed by
+    inter_tile_reduce, and core 0 adds the residual x and stores."""
+    fc = f // cores
+    T = lambda r, c: f"tensor<{r}x{c}xf16>"
+    box = lambda r, c: f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {r - 1} >= 0, d1 >= 0, -d1 + {c - 1} >= 0)>"
+    idm = "affine_map<(d0, d1) -> (d0, d1)>"
+    hbm = "#ktdp.memory_space<global>"
+    pset = f"affine_set<(i)[g] : (i - {cores}*g >= 0, -i + {cores}*g + {cores - 1} >= 0)>"
+    fut = f"!ktdp.tile_future<{T(seq, d)}, groups = affine_set<(g) : (g == 0)>>"
+
+    def view(name, ptr, shape):
+        return (f"    %{name} = ktdp.construct_memory_view %{ptr}, sizes: [{shape[0]}, {shape[1]}], strides: "
+                f"[{shape[1]}, 1] {{\n      coordinate_set = {box(*shape)}, memory_space = {hbm}\n    }} : "
+                f"memref<{shape[0]}x{shape[1]}xf16>")
+
+    def load(name, v, idx, shape, vshape):
+        return (f"    %{name}_t = ktdp.construct_access_tile %{v}[{idx}] {{\n      access_tile_set = {box(*shape)}, "
+                f"access_tile_order = {idm}\n    }} : memref<{vshape[0]}x{vshape[1]}xf16> -> "
+                f"!ktdp.access_tile<{shape[0]}x{shape[1]}xindex>\n"
+                f"    %{name} = ktdp.load %{name}_t : !ktdp.access_tile<{shape[0]}x{shape[1]}xindex> -> "
+                f"{T(*shape)}")
+    return f"""module {{
+  func.func @ffn_swiglu(%x_ptr: index, %wg_ptr: index, %wu_ptr: index, %wd_ptr: index, %out_ptr: index)
+      attributes {{grid = [{cores}]}} {{
+    %c = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %cfc = arith.constant {fc} : index
+    %col = arith.muli %c, %cfc : index
+    %one = arith.constant 1.0 : f16
+    %zero = arith.constant 0.0 : f16
+{view("xv", "x_ptr", (seq, d))}
+{view("wgv", "wg_ptr", (d, f))}
+{view("wuv", "wu_ptr", (d, f))}
+{view("wdv", "wd_ptr", (f, d))}
+{view("ov", "out_ptr", (seq, d))}
+{load("x", "xv", "%c0, %c0", (seq, d), (seq, d))}
+{load("wg", "wgv", "%c0, %col", (d, fc), (d, f))}
+{load("wu", "wuv", "%c0, %col", (d, fc), (d, f))}
+{load("wd", "wdv", "%col, %c0", (fc, d), (f, d))}
+    %g0 = tensor.splat %zero : {T(seq, fc)}
+    %gate = linalg.matmul ins(%x, %wg : {T(seq, d)}, {T(d, fc)}) outs(%g0 : {T(seq, fc)}) -> {T(seq, fc)}
+    %u0 = tensor.splat %zero : {T(seq, fc)}
+    %up = linalg.matmul ins(%x, %wu : {T(seq, d)}, {T(d, fc)}) outs(%u0 : {T(seq, fc)}) -> {T(seq, fc)}
+    %ng = arith.negf %gate : {T(seq, fc)}
+    %en = math.exp %ng : {T(seq, fc)}
+    %ones = tensor.splat %one : {T(seq, fc)}
+    %den = arith.addf %ones, %en : {T(seq, fc)}
+    %silu = arith.divf %gate, %den : {T(seq, fc)}
+    %h = arith.mulf %silu, %up : {T(seq, fc)}
+    %p0 = tensor.splat %zero : {T(seq, d)}
+    %part = linalg.matmul ins(%h, %wd : {T(seq, fc)}, {T(fc, d)}) outs(%p0 : {T(seq, d)}) -> {T(seq, d)}
+    %fut = ktdp.inter_tile_produce producer_tiles_per_group = {pset}
+        : {T(seq, d)} -> {fut}
+    {{
+      ^bb0(%gid: index):
+        ktdp.yield_partial %part : {T(seq, d)}
+    }}
+    %e = tensor.empty() : {T(seq, d)}
+    %id = linalg.fill ins(%zero : f16) outs(%e : {T(seq, d)}) -> {T(seq, d)}
+    %sum = ktdp.inter_tile_reduce(%fut) consumer_tiles_per_group = {pset}, identity(%id : {T(seq, d)})
+        : {fut} -> {T(seq, d)}
+    {{
+      ^bb0(%lhs: {T(seq, d)}, %rhs: {T(seq, d)}):
+        %init = tensor.empty() : {T(seq, d)}
+        %s = linalg.add ins(%lhs, %rhs : {T(seq, d)}, {T(seq, d)}) outs(%init : {T(seq, d)}) -> {T(seq, d)}
+        ktdp.yield_reduced %s : {T(seq, d)}
+    }}
+    %y = arith.addf %sum, %x : {T(seq, d)}
+    %is0 = arith.cmpi eq, %c, %c0 : index
+    scf.if %is0 {{
+      %o_t = ktdp.construct_access_tile %ov[%c0, %c0] {{
+        access_tile_set = {box(seq, d)}, access_tile_order = {idm}
+      }} : memref<{seq}x{d}xf16> -> !ktdp.access_tile<{seq}x{d}xindex>
+      ktdp.store %y, %o_t : {T(seq, d)}, !ktdp.access_tile<{seq}x{d}xindex>
+    }}
+    return
+  }}
+}}
+"""

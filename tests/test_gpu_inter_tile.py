@@ -107,3 +107,19 @@ def test_splitk_pv_strided_groups():
     C = run(P, V)
     np.testing.assert_allclose(C.astype(np.float32), oracle_splitk(P, V).astype(np.float32), rtol=1e-2, atol=1e-3)
     np.testing.assert_allclose(C.astype(np.float32), P.astype(np.float32) @ V.astype(np.float32), rtol=2e-2, atol=2e-1)
+
+
+def test_ffn_swiglu_4core():
+    """SwiGLU FFN with the hidden dimension split over 4 cores and the
+    partials summed by the ring reduce: against the oracle (f16 matmuls:
+    rtol 1e-2 / atol 1e-3 over the f32 summation order) and a float64 model."""
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    from tests.test_inter_tile import ffn_inputs, ffn_model, oracle_ffn
+    print("[ring] ffn swiglu", flush=True)
+    x, wg, wu, wd = ffn_inputs()
+    g = KTIRInterpreter()
+    g.load(_cases.ffn_swiglu_4core())
+    out = g.execute_function("ffn_swiglu", x_ptr=x, wg_ptr=wg, wu_ptr=wu, wd_ptr=wd, out_ptr=np.zeros_like(x))
+    y = out["out_ptr"].astype(np.float64)
+    np.testing.assert_allclose(y, oracle_ffn(x, wg, wu, wd).astype(np.float64), rtol=1e-2, atol=1e-3)
+    np.testing.assert_allclose(y, ffn_model(x, wg, wu, wd), rtol=2e-2, atol=2e-2)

@@ -145,3 +145,35 @@ def test_oracle_splitk_pv_strided_groups():
     Pi = np.random.default_rng(1).integers(-2, 3, (1, 1024)).astype(np.float16)
     Vi = np.random.default_rng(2).integers(-2, 3, (1024, 128)).astype(np.float16)
     np.testing.assert_array_equal(oracle_splitk(Pi, Vi), (Pi.astype(np.int64) @ Vi.astype(np.int64)).astype(np.float16))
+
+
+def ffn_inputs(seq=4, d=256, f=1024, seed=11):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((seq, d)).astype(np.float16)
+    wg = (rng.standard_normal((d, f)) / 16).astype(np.float16)
+    wu = (rng.standard_normal((d, f)) / 16).astype(np.float16)
+    wd = (rng.standard_normal((f, d)) / 32).astype(np.float16)
+    return x, wg, wu, wd
+
+
+def ffn_model(x, wg, wu, wd):
+    x64 = x.astype(np.float64)
+    g, u = x64 @ wg.astype(np.float64), x64 @ wu.astype(np.float64)
+    h = g / (1 + np.exp(-g)) * u
+    return h @ wd.astype(np.float64) + x64
+
+
+def oracle_ffn(x, wg, wu, wd):
+    o = OracleInterpreter()
+    o.load(_cases.ffn_swiglu_4core(x.shape[0], x.shape[1], wg.shape[1]))
+    return o.execute_function("ffn_swiglu", x_ptr=x, wg_ptr=wg, wu_ptr=wu, wd_ptr=wd,
+                              out_ptr=np.zeros_like(x))["out_ptr"]
+
+
+def test_oracle_ffn_swiglu_4core():
+    """The 4-core SwiGLU FFN against a float64 model, at the tolerance of
+    the reference's own check of its 4-core FFN example
+    (tests/test_examples.py:932-1030: f16 matmuls and f16 folds)."""
+    x, wg, wu, wd = ffn_inputs()
+    np.testing.assert_allclose(oracle_ffn(x, wg, wu, wd).astype(np.float64), ffn_model(x, wg, wu, wd),
+                               rtol=2e-2, atol=2e-2)
