@@ -388,8 +388,9 @@ typedef struct ktir_attn {
   /* optional (0 / 0: not used): const int32_t* [2 * n_pairs] lanes run two
    * per workgroup ({lane, lane or -1}; paired lanes have equal k_base, v_base
    * and kpos0; every lane appears once).  Used in the cases that run P @ V
-   * in f16: one group of four wavefronts per lane, the two groups taking
-   * turns between MFMA work and softmax. */
+   * in f16 with scale > 0 and (under a mask) neg = -inf: one group of four
+   * wavefronts per lane, the two groups taking turns between MFMA work and
+   * softmax.  Other launches ignore the pairs and run one lane per workgroup. */
   uint64_t pairs;
   int64_t n_pairs;
 } ktir_attn_t;

@@ -96,8 +96,28 @@ __device__ __forceinline__ float other_half(float x) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// max / sum of x over the lane pair (l, l ^ 32): after v_permlane32_swap the
+// two results hold the pair's two values in either order, so one maximum or
+// add of them gives both lanes the same result (IEEE add commutes)
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __fadd_rn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // arith.maximumf: NaN-propagating maximum (v_maximum3_f32 on gfx950)
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmax3_nan(float a, float b, float c) { return fmax_nan(fmax_nan(a, b), c); }
+
+// x = -inf in the lanes of mask, in place (v_cndmask_b32 on x's own
+// register: the caller's S values keep the registers the MFMAs wrote)
+__device__ __forceinline__ float mask_ninf(float x, uint64_t mask) {
+  asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(-__builtin_inff()), "s"(mask));
+  return x;
+}
 
 // e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32)
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(__fmul_rn(x, LOG2E)); }
@@ -492,7 +512,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
   if (Tmax > 0) tile16_to_lds(K + kbase, d.k_row, K0s, w8, l);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const bool pos_scale = d.scale > 0.f;
   const float c1 = __fmul_rn(d.scale, LOG2E);
   const f32x16_t z16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   f32x16_t o0 = z16, o1 = z16, o2 = z16, o3 = z16;
@@ -557,40 +576,38 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
     __builtin_amdgcn_s_setprio(0);                                                                   \
   } while (0)
 
-  // vector phase V_j: softmax of S_j (online, base mr as in attn_kernel) into ph
+  // vector phase V_j: softmax of S_j (online, base mr as in attn_kernel) into
+  // ph.  The launch runs this kernel only for scale > 0 and, under a position
+  // mask, the fill value -inf: a score outside the kept positions becomes
+  // -inf in place, after which one form serves every tile (the maximum
+  // ignores -inf unless the whole row is masked, and 2^(-inf c1 + c0) = 0,
+  // exactly what exp(-inf - m) gives).
 #define PP_V(J)                                                                                      \
   do {                                                                                               \
     if ((J) >= 0 && (J) < T) {                                                                       \
       const int dbase = (int)(kpos00 + (int64_t)(J) * d.kpos_step - qpos);                           \
       const bool all_keep = !d.causal ||                                                             \
           (minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi));        \
-      const bool fast = pos_scale && __all(all_keep);                                                \
-      float mn;                                                                                      \
-      if (fast) {                                                                                    \
-        float x0 = fmax_nan(sc[0][0], sc[0][1]), x1 = fmax_nan(sc[1][0], sc[1][1]);                  \
-        float x2 = fmax_nan(sc[2][0], sc[2][1]), x3 = fmax_nan(sc[3][0], sc[3][1]);                  \
-        _Pragma("unroll") for (int i = 2; i < 16; i += 2) {                                          \
-          x0 = fmax_nan(x0, fmax_nan(sc[0][i], sc[0][i + 1]));                                       \
-          x1 = fmax_nan(x1, fmax_nan(sc[1][i], sc[1][i + 1]));                                       \
-          x2 = fmax_nan(x2, fmax_nan(sc[2][i], sc[2][i + 1]));                                       \
-          x3 = fmax_nan(x3, fmax_nan(sc[3][i], sc[3][i + 1]));                                       \
-        }                                                                                            \
-        float xm = fmax_nan(fmax_nan(x0, x1), fmax_nan(x2, x3));                                     \
-        xm = fmax_nan(xm, other_half(xm));                                                           \
-        mn = fmax_nan(m, __fmul_rn(d.scale, xm));                                                    \
-      } else {                                                                                       \
-        AT_S_LOOP(sc[kt][i] = __fmul_rn(d.scale, sc[kt][i]))                                         \
-        if (d.causal) {                                                                              \
-          AT_S_LOOP({                                                                                \
+      if (!__all(all_keep)) {                                                                        \
+        /* wait states between the MFMA writes of S and these VALU reads */                          \
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");                                  \
+        _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) {                                           \
+          _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                           \
             const int df = dbase + kt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);                         \
-            if ((df >= mlo && df <= mhi) == (bool)minv) sc[kt][i] = d.neg;                           \
-          })                                                                                         \
+            sc[kt][i] = mask_ninf(sc[kt][i], __builtin_amdgcn_ballot_w64((df >= mlo && df <= mhi) == (bool)minv)); \
+          }                                                                                          \
         }                                                                                            \
-        float xm = -__builtin_inff();                                                                \
-        AT_S_LOOP(xm = fmax_nan(xm, sc[kt][i]))                                                      \
-        xm = fmax_nan(xm, other_half(xm));                                                           \
-        mn = fmax_nan(m, xm);                                                                        \
       }                                                                                              \
+      /* four chains of v_maximum3 (15 scores each), then the 4 left and the chains */               \
+      float x[4];                                                                                    \
+      _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) {                                             \
+        x[kt] = fmax3_nan(sc[kt][0], sc[kt][1], sc[kt][2]);                                          \
+        _Pragma("unroll") for (int i = 3; i < 15; i += 2) x[kt] = fmax3_nan(x[kt], sc[kt][i], sc[kt][i + 1]); \
+      }                                                                                              \
+      const float y0 = fmax3_nan(x[0], sc[0][15], sc[1][15]);                                        \
+      const float y1 = fmax3_nan(x[1], sc[2][15], sc[3][15]);                                        \
+      const float xm = pair_max(fmax_nan(fmax3_nan(y0, y1, x[2]), x[3]));                            \
+      const float mn = fmax_nan(m, __fmul_rn(d.scale, xm));                                          \
       const bool up = mn > __fadd_rn(mr, 8.0f);                                                      \
       if (__any(up)) {                                                                               \
         const float al = up ? exp_f(__fsub_rn(mr, mn)) : 1.f;                                        \
@@ -603,12 +620,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
         lsum = __fmul_rn(lsum, al);                                                                  \
         mr = up ? mn : mr;                                                                           \
       }                                                                                              \
-      if (fast) {                                                                                    \
-        const float c0 = -__fmul_rn(mr, LOG2E);                                                      \
-        AT_S_LOOP(sc[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][i], c1, c0)))             \
-      } else {                                                                                       \
-        AT_S_LOOP(sc[kt][i] = exp_f(__fsub_rn(sc[kt][i], mr)))                                       \
-      }                                                                                              \
+      const float c0 = -__fmul_rn(mr, LOG2E);                                                        \
+      AT_S_LOOP(sc[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][i], c1, c0)))               \
       m = mn;                                                                                        \
       /* the row sum from the f16 P the product uses: two values per dot2 */                        \
       float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;                                                  \
@@ -624,8 +637,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
         s3 = dot2_one(bh1, s3);                                                                      \
         ph[ks] = make_uint4(ah0, ah1, bh0, bh1);                                                     \
       }                                                                                              \
-      const float ls = __fadd_rn(__fadd_rn(s0, s1), __fadd_rn(s2, s3));                              \
-      lsum = __fadd_rn(lsum, __fadd_rn(ls, other_half(ls)));                                         \
+      lsum = __fadd_rn(lsum, pair_sum(__fadd_rn(__fadd_rn(s0, s1), __fadd_rn(s2, s3))));             \
     }                                                                                                \
   } while (0)
 
@@ -782,7 +794,10 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
   // its error there is at most 2^-12 max|V| per element, while an
   // unnormalised acc would carry it l times over
   const bool norm = d->o_ptr && !d->acc_out;
-  const bool pp = norm && d->pairs && d->n_pairs > 0 && d->n_pairs < (int64_t)0x7fffffff;
+  // the two-group kernel's one softmax form needs scale > 0 and, under a
+  // mask, the fill value -inf; anything else runs attn_kernel
+  const bool pp = norm && d->pairs && d->n_pairs > 0 && d->n_pairs < (int64_t)0x7fffffff && d->scale > 0.f &&
+                  (!d->causal || d->neg == -__builtin_inff());
   const dim3 pgrid((unsigned)(pp ? d->n_pairs : 1));
   if (d->dtype == KTIR_BF16 && d->v16_ptr && norm) {
     if (!d->v16_flag || (d->v16_lo | d->v16_n) & 7 || d->v16_lo < 0 || d->v16_n <= 0 || (d->v16_ptr & 15))

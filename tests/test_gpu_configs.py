@@ -270,6 +270,24 @@ def test_flash_attention_fused_v_beyond_f16(big):
     np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("fill,sign,dt", [("-1.0e4", 1, "bf16"), ("-1.0e4", 1, "f16"), ("0xFF800000", -1, "bf16"),
+                                          ("-3.0", -1, "f16")])
+def test_flash_attention_fused_other_fill_or_scale(fill, sign, dt):
+    """A finite mask fill value or a negative scale (the two-group kernel
+    takes only -inf and scale > 0) still runs as one fused launch, on the
+    one-lane-per-workgroup kernel, and matches the oracle."""
+    src, fn, kw = _cases.flash_attention(S=512, D=128, blk=128, dt=dt)
+    src = src.replace("%neg_inf = arith.constant 0xFF800000 : f32",
+                      f"%neg_inf = arith.constant 0xFF800000 : f32\n    %fill = arith.constant {fill} : f32")
+    src = src.replace("%r = arith.select %keep, %sv, %neg_inf : f32", "%r = arith.select %keep, %sv, %fill : f32")
+    kw["scale"] = sign * kw["scale"]
+    print(f"[attn] fill {fill} scale sign {sign} {dt}", flush=True)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts().get("attn") == 1
+    f = bf16_from_bits if dt == "bf16" else (lambda x: x.astype(np.float32))
+    np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+
+
 def test_flash_attention_unfused_epilogue():
     """An epilogue other than acc / l stays a separate program after the fused loop."""
     src, fn, kw = _cases.flash_attention(S=256, D=128, blk=128)
