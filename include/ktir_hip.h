@@ -373,7 +373,11 @@ typedef struct ktir_attn {
    * to o_dtype and written at o_ptr + o_base[l] + row * o_row + d */
   uint64_t o_ptr, o_base;              /* 0: no epilogue; o_base: const int64_t* [lanes] */
   int64_t o_row;
-  int32_t o_dtype, pad2;
+  int32_t o_dtype;
+  /* nonzero: v16_ptr and v16_flag still hold the copy and verdict of this V
+   * range from an earlier launch, and V has not changed since (the caller
+   * vouches for it), so the conversion is skipped */
+  int32_t v16_ready;
   /* optional f16 copy of V for bf16 operands (0: not used): the launch first
    * converts elements [v16_lo, v16_lo + v16_n) of V into v16_ptr (f16, same
    * order; v16_lo and v16_n multiples of 8) and sets the device int32 at

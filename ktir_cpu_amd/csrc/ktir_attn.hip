@@ -805,9 +805,11 @@ extern "C" int ktir_launch_attention(const ktir_attn_t* d) {
                        (long long)d->v16_lo, (long long)d->v16_n);
     const int64_t n8 = d->v16_n / 8;
     const int64_t blocks = n8 / 256 + 1 < 16384 ? n8 / 256 + 1 : 16384;
-    hipLaunchKernelGGL(attn_v16_clear, dim3(1), dim3(1), 0, stream(), (int*)d->v16_flag);
-    hipLaunchKernelGGL(attn_v16, dim3((unsigned)blocks), dim3(256), 0, stream(),
-                       (const uint16_t*)d->v_ptr + d->v16_lo, (uint16_t*)d->v16_ptr, n8, (int*)d->v16_flag);
+    if (!d->v16_ready) {
+      hipLaunchKernelGGL(attn_v16_clear, dim3(1), dim3(1), 0, stream(), (int*)d->v16_flag);
+      hipLaunchKernelGGL(attn_v16, dim3((unsigned)blocks), dim3(256), 0, stream(),
+                         (const uint16_t*)d->v_ptr + d->v16_lo, (uint16_t*)d->v16_ptr, n8, (int*)d->v16_flag);
+    }
     if (pp)
       hipLaunchKernelGGL((attn_pp<true>), pgrid, dim3(512), 0, stream(), *d, lo, hi, inv);
     else

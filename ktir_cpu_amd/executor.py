@@ -487,6 +487,18 @@ def _all_comparable(ids: set, insts: Instances) -> bool:
 # launch plan
 # ---------------------------------------------------------------------------
 
+class V16Copy:
+    """The f16 copy of a bf16 V range that an attention launch makes: valid
+    on a replay when no launch of the plan stores into V (`ok`, set when the
+    walk ends) and the buffer holding V has had no host write since the
+    launch that made it (`gen`)."""
+
+    def __init__(self, alloc, buf):
+        self.alloc, self.buf = alloc, buf
+        self.ok = False
+        self.gen = None
+
+
 class Plan:
     """The recorded launch sequence of one execute_function call."""
 
@@ -497,6 +509,7 @@ class Plan:
         self.ran_during_walk = False     # launches already ran as they were walked
         self.mode = "lockstep"
         self.fallback_reason = None
+        self.v16: Dict[int, V16Copy] = {}   # id(attention descriptor) -> its V copy
 
     def add(self, kind, desc, keep=()):
         # a list stays shared with the caller, who may still append buffers
@@ -506,7 +519,13 @@ class Plan:
     def run(self):
         L = rt.lib()
         for kind, desc, _ in self.launches:
-            _launch(L, kind, desc)
+            c = self.v16.get(id(desc)) if kind == "attn" else None
+            if c is not None:
+                desc.v16_ready = int(c.ok and c.gen is not None and c.gen == c.buf.host_writes)
+                _launch(L, kind, desc)
+                c.gen = c.buf.host_writes
+            else:
+                _launch(L, kind, desc)
 
     def counts(self) -> Dict[str, int]:
         out: Dict[str, int] = {}

@@ -20,7 +20,7 @@ from typing import List, Optional
 import numpy as np
 
 from .affine import Box
-from .executor import ATile, NeedEager, Tile
+from .executor import ATile, NeedEager, Tile, V16Copy
 
 _SCALAR_OPS_PREFIX = ("arith.",)
 _SKIP = {"ktdp.load", "arith.extf", "linalg.matmul", "scf.yield"}
@@ -859,6 +859,10 @@ def _attention_loop(ex, op, lb, st, trips, inits):
                 flag = ex.pool.temp(4)
                 keep += [v16, flag]
                 d.v16_ptr, d.v16_flag, d.v16_lo, d.v16_n = v16.ptr, flag.ptr, lo_, hi_ - lo_
+                valloc = tiles["v"][0]
+                if any(a is valloc for a in ex.arena.allocs):
+                    # replays may reuse the copy (executor.V16Copy says when)
+                    ex.plan.v16[id(d)] = V16Copy(valloc, valloc.buf if valloc.buf is not None else ex.arena.buf)
     d.order = up(_xcd_order(trips, tiles["k"][1], tiles["v"][1]))
     pairs = _pp_pairs(trips, tiles["k"][1], tiles["v"][1], ck0.astype(np.int64))
     if len(pairs):

@@ -113,7 +113,7 @@ class ATTN(C.Structure):
                 ("dtype", C.c_int32), ("pad", C.c_int32),
                 ("m_out", C.c_uint64), ("l_out", C.c_uint64), ("acc_out", C.c_uint64),
                 ("o_ptr", C.c_uint64), ("o_base", C.c_uint64), ("o_row", C.c_int64), ("o_dtype", C.c_int32),
-                ("pad2", C.c_int32), ("v16_ptr", C.c_uint64), ("v16_flag", C.c_uint64), ("v16_lo", C.c_int64),
+                ("v16_ready", C.c_int32), ("v16_ptr", C.c_uint64), ("v16_flag", C.c_uint64), ("v16_lo", C.c_int64),
                 ("v16_n", C.c_int64), ("pairs", C.c_uint64), ("n_pairs", C.c_int64)]
 
 
@@ -204,7 +204,7 @@ def device_info() -> dict:
 class DeviceBuffer:
     """One device allocation; freed explicitly or when garbage collected."""
 
-    __slots__ = ("ptr", "nbytes", "_pool", "__weakref__")
+    __slots__ = ("ptr", "nbytes", "_pool", "host_writes", "__weakref__")
 
     def __init__(self, nbytes: int, pool: Optional["BufferPool"] = None):
         p = C.c_uint64()
@@ -212,6 +212,7 @@ class DeviceBuffer:
         self.ptr = p.value
         self.nbytes = int(nbytes)
         self._pool = pool
+        self.host_writes = 0         # uploads and fills from the host so far (device copies it caches check it)
 
     def free(self):
         if self.ptr:
@@ -221,6 +222,7 @@ class DeviceBuffer:
     def upload(self, arr: np.ndarray, offset: int = 0):
         a = np.ascontiguousarray(arr)
         assert offset + a.nbytes <= self.nbytes
+        self.host_writes += 1
         check(lib().ktir_memcpy_h2d(self.ptr + offset, a.ctypes.data, a.nbytes), "ktir_memcpy_h2d")
 
     def download_into(self, dst: np.ndarray, offset: int = 0):
@@ -232,6 +234,7 @@ class DeviceBuffer:
     def memset(self, value: int = 0, offset: int = 0, nbytes: Optional[int] = None):
         n = self.nbytes - offset if nbytes is None else int(nbytes)
         assert offset + n <= self.nbytes
+        self.host_writes += 1
         check(lib().ktir_memset(self.ptr + offset, int(value), n), "ktir_memset")
 
     def download(self, nbytes: int, offset: int = 0) -> bytes:

@@ -331,12 +331,21 @@ class Executor:
         self.n_cores = nx * ny * nz
         self.insts = Instances(self.n_cores)
         self.accesses: List[Access] = []
+        self.stored: set = set()     # id() of every allocation a launch stores into
         self.lx_capacity = lx_size_mb * 1024 * 1024
         self.use_counts = _use_counts(fn.operations)
         self._linalg_shape: List[Tuple[int, ...]] = []
 
     # -- driver -------------------------------------------------------------
     def run(self):
+        plan = self._run_grid()
+        # a device copy of an input stays valid across replays only if no
+        # launch of the plan stores into the input
+        for c in plan.v16.values():
+            c.ok = id(c.alloc) not in self.stored
+        return plan
+
+    def _run_grid(self):
         if self.sequential:
             for c in range(self.n_cores):
                 lanes = Lanes(np.array([c], dtype=np.int64), np.array([c], dtype=np.int64))
@@ -629,6 +638,8 @@ class Executor:
         self.log(alloc, store, rel, shape, strides, mask=mask)
 
     def log(self, alloc, store, base, shape, strides, whole=False, group=None, mask=None):
+        if store and alloc is not None:
+            self.stored.add(id(alloc))
         if self.sequential:
             return
         inst = self.lanes.inst.copy()

@@ -288,6 +288,47 @@ def test_flash_attention_fused_other_fill_or_scale(fill, sign, dt):
     np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
 
 
+def test_flash_attention_replay_reuses_v_copy():
+    """Replays of a prepared bf16 attention reuse the f16 copy of V while no
+    host write has reached the arena; a new V written through memory.hbm
+    makes the next replay convert again, and its result is the oracle's for
+    the new V; reset_inputs restores the first result."""
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    from oracle.interp import bf16_bits
+    src, fn, kw = _cases.flash_attention(S=512, D=128, blk=128)
+    print("[attn] replay with the f16 copy of V", flush=True)
+    g = KTIRInterpreter()
+    g.load(src)
+    prep = g.prepare(fn, **{k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in kw.items()})
+    out0 = prep.outputs()["o_ptr"]
+    attn = [d for k, d, _ in prep.plan.launches if k == "attn"]
+    assert len(attn) == 1 and len(prep.plan.v16) == 1
+    assert next(iter(prep.plan.v16.values())).ok
+    prep.run()
+    assert attn[0].v16_ready == 1
+    np.testing.assert_array_equal(prep.outputs()["o_ptr"], out0)
+    # a different V through the interpreter's HBM (a host write into the arena)
+    v2 = bf16_bits(bf16_from_bits(kw["v_ptr"])[..., ::-1] * 0.5)
+    a = next(x for x in prep.arena.allocs if x.name == "v_ptr")
+    g.memory.hbm.write(a.addr // 128, v2.reshape(-1))
+    prep.run()
+    assert attn[0].v16_ready == 0
+    o = OracleInterpreter()
+    o.load(src)
+    kw2 = dict(kw, v_ptr=v2, o_ptr=np.zeros_like(kw["o_ptr"]))
+    ref2 = o.execute_function(fn, **kw2)["o_ptr"]
+    out2 = prep.outputs()["o_ptr"]
+    np.testing.assert_allclose(bf16_from_bits(out2), bf16_from_bits(ref2), rtol=1e-2, atol=1e-3)
+    assert not np.array_equal(out2, out0)
+    prep.run()
+    assert attn[0].v16_ready == 1
+    np.testing.assert_array_equal(prep.outputs()["o_ptr"], out2)
+    prep.reset_inputs()
+    prep.run()
+    assert attn[0].v16_ready == 0
+    np.testing.assert_array_equal(prep.outputs()["o_ptr"], out0)
+
+
 def test_flash_attention_unfused_epilogue():
     """An epilogue other than acc / l stays a separate program after the fused loop."""
     src, fn, kw = _cases.flash_attention(S=256, D=128, blk=128)
