@@ -1474,10 +1474,13 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
     h2 a = {-__builtin_inff16(), -__builtin_inff16()}, b = a;
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, c[i][0]));
-      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, c[i][1]));
-      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, c[i][2]));
-      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, c[i][3]));
+      // the words through scalars: this clang lowers __builtin_bit_cast of a
+      // vector element (c[i][k]) as a read of element 0
+      const uint32_t w0 = c[i][0], w1 = c[i][1], w2 = c[i][2], w3 = c[i][3];
+      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, w0));
+      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, w1));
+      a = __builtin_elementwise_maximum(a, __builtin_bit_cast(h2, w2));
+      b = __builtin_elementwise_maximum(b, __builtin_bit_cast(h2, w3));
     }
     a = __builtin_elementwise_maximum(a, b);
     mx = __builtin_elementwise_maximum((float)a.x, (float)a.y);
@@ -1514,26 +1517,18 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   const float c0 = -__fmul_rn(m, 1.44269504088896341f);
   const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
   float s0 = 0.f, s1 = 0.f;
-  if (near) {
+  {
+    // one loop for both forms: near, x - 0 (exact) into the FMA with c0;
+    // far, x - m' first and no addend (the same roundings as either form alone)
+    const float msub = near ? 0.f : m, c0u = near ? c0 : 0.f;
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       float v[8];
       rf_unpack<DT>(c[i], v);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const f2 x = {__builtin_amdgcn_exp2f(__builtin_fmaf(v[2 * k], 1.44269504088896341f, c0)),
-                      __builtin_amdgcn_exp2f(__builtin_fmaf(v[2 * k + 1], 1.44269504088896341f, c0))};
-        ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      float v[8];
-      rf_unpack<DT>(c[i], v);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const f2 x = {exp_hw(__fsub_rn(v[2 * k], m)), exp_hw(__fsub_rn(v[2 * k + 1], m))};
+        const f2 x = {__builtin_amdgcn_exp2f(__builtin_fmaf(__fsub_rn(v[2 * k], msub), 1.44269504088896341f, c0u)),
+                      __builtin_amdgcn_exp2f(__builtin_fmaf(__fsub_rn(v[2 * k + 1], msub), 1.44269504088896341f, c0u))};
         ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
       }
     }
@@ -1544,6 +1539,20 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
     s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q + 1]), one, s1, false);
   }
   float sum = __fadd_rn(s0, s1);
+  // v_dot2_f32_f16 does not carry a NaN operand into its sum as an f32 add
+  // would.  An exponential is NaN only if the row max is NaN or m' is not
+  // finite (x - m' is NaN only for x NaN or x = m' = +-inf), so only then are
+  // the f16 values checked; a NaN among them makes the lane's part NaN, and
+  // the adds below carry it into the row sum.
+  if (mx != mx || !(fabsf(m) <= 3.40282347e38f)) {
+    bool nan_e = false;
+#pragma unroll
+    for (int q = 0; q < NQ * 4; ++q) {
+      const h2 w = __builtin_bit_cast(h2, ep[q]);
+      nan_e = nan_e || w.x != w.x || w.y != w.y;
+    }
+    if (nan_e) sum = __builtin_nanf("");
+  }
 #pragma unroll
   for (int sh = 32; sh >= 1; sh >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, sh));
   rr.set(F.fold1, sum);
