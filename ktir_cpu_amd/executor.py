@@ -516,9 +516,11 @@ class Plan:
         # that a later rewrite of `desc` points at
         self.launches.append((kind, desc, keep if isinstance(keep, list) else tuple(keep)))
 
-    def run(self):
+    def run(self, after=None):
+        """Replay every launch; `after(i)`, if given, runs after launch i is
+        queued (the bench records a HIP event there)."""
         L = rt.lib()
-        for kind, desc, _ in self.launches:
+        for i, (kind, desc, _) in enumerate(self.launches):
             c = self.v16.get(id(desc)) if kind == "attn" else None
             if c is not None:
                 desc.v16_ready = int(c.ok and c.gen is not None and c.gen == c.buf.host_writes)
@@ -526,6 +528,8 @@ class Plan:
                 c.gen = c.buf.host_writes
             else:
                 _launch(L, kind, desc)
+            if after is not None:
+                after(i)
 
     def counts(self) -> Dict[str, int]:
         out: Dict[str, int] = {}
