@@ -27,6 +27,30 @@ def gather_scatter_add(rows=1024, dim=32, n_idx=512, cores=4, chunk=32, seed=42,
             dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((rows, dim), np.float32)))
 
 
+def scatter_add_two_index(rows=1024, dim=32, n_idx=512, cores=4, chunk=32, seed=42, hot=None):
+    """out[didx[i], :] = out[didx[i], :] + extf(table[sidx[i], :]): the
+    gather + scatter-add kernel with its source rows named by a second index
+    tensor, so updates of one destination row add different rows and their
+    order shows in the f32 sums.  `hot`: destination indices drawn from
+    [0, hot) (long chains)."""
+    rng = np.random.default_rng(seed)
+    src = configs.gather_scatter_add(rows, dim, n_idx, cores, chunk)
+    sig = "%table_ptr: index, %idx_ptr: index, %out_ptr: index)"
+    assert src.count(sig) == 1
+    src = src.replace(sig, "%table_ptr: index, %idx_ptr: index, %out_ptr: index, %sidx_ptr: index)")
+    view = configs._view("idx_view", "idx_ptr", [n_idx], [1], "i32")
+    assert src.count(view) == 1
+    src = src.replace(view, view + "\n" + configs._view("sidx_view", "sidx_ptr", [n_idx], [1], "i32"))
+    g = "%table_view[ind(%idx_view[%row0 + %r]), (%c)]"
+    assert src.count(g) == 1
+    src = src.replace(g, "%table_view[ind(%sidx_view[%row0 + %r]), (%c)]")
+    table = rng.standard_normal((rows, dim)).astype(np.float16)
+    didx = rng.integers(0, hot or rows, n_idx).astype(np.int32)
+    sidx = rng.integers(0, rows, n_idx).astype(np.int32)
+    out = rng.standard_normal((rows, dim)).astype(np.float32)
+    return src, "gather_scatter_add", dict(table_ptr=table, idx_ptr=didx, out_ptr=out, sidx_ptr=sidx)
+
+
 def _half(x, dt):
     """f32 values as the element type's storage: f16 values, or bf16 bit patterns."""
     return x.astype(np.float16) if dt == "f16" else bf16_bits(x.astype(np.float32))

@@ -59,6 +59,20 @@ def test_gather_scatter_add_heavy_duplicates(rows, dim):
     assert g.last_plan.rmw_variants() == [_rmw_kernel(dim)]
 
 
+@pytest.mark.parametrize("dim", [32, 128, 256])
+@pytest.mark.parametrize("hot", [None, 24])
+def test_scatter_add_two_index_bit_exact(dim, hot):
+    """Source rows from a second index tensor: the updates of one destination
+    row add different rows, in the reference's order (last writer inside a
+    chunk, instance after instance), bit-exact; with `hot`, every destination
+    row takes a long chain (the chain path of the row-order kernel)."""
+    print(f"[rmw] two-index dim {dim} hot {hot}", flush=True)
+    ref, out, g = _run(_cases.scatter_add_two_index(dim=dim, hot=hot))
+    np.testing.assert_array_equal(out["out_ptr"], ref["out_ptr"])
+    assert g.last_plan.counts() == {"rmw": 1}
+    assert g.last_plan.rmw_variants() == [_rmw_kernel(dim)]
+
+
 @pytest.mark.parametrize("dim", [32, 128])
 def test_gather_scatter_add_rows_past_allocation(dim):
     """Indices past the end of the table read zero rows, and a destination

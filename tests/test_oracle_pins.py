@@ -291,3 +291,29 @@ def test_oracle_gather_scatter_add_against_brute_force(rows, dim, n_idx, cores, 
     np.testing.assert_array_equal(got, want)
     # a last-writer-wins mistake (accumulating in-chunk repeats) would differ
     assert len(np.unique(kw["idx_ptr"][:chunk])) < chunk or hot >= n_idx
+
+
+@pytest.mark.parametrize("dim,hot", [(8, 6), (16, 96)])
+def test_oracle_scatter_add_two_index_against_brute_force(dim, hot):
+    """The same kernel with the source rows named by a second index tensor:
+    the updates of one destination row add different table rows, so a wrong
+    order (or a wrong source) shows in the f32 sums.  Against a per-row loop:
+    each chunk reads its destination rows before any of its stores, the last
+    position of a row in a chunk writes, chunks and cores follow in order."""
+    src, fn, kw = _cases.scatter_add_two_index(rows=96, dim=dim, n_idx=64, cores=2, chunk=8, seed=dim, hot=hot)
+    d, s = kw["idx_ptr"], kw["sidx_ptr"]
+    table = kw["table_ptr"].astype(np.float32)
+    want = kw["out_ptr"].astype(np.float32).copy()
+    per_core = len(d) // 2
+    for c in range(2):
+        for b in range(c * per_core, (c + 1) * per_core, 8):
+            new = {}
+            before = {int(r): want[r].copy() for r in d[b:b + 8]}
+            for k in range(b, b + 8):
+                new[int(d[k])] = (before[int(d[k])] + table[int(s[k])]).astype(np.float32)
+            for r, v in new.items():
+                want[r] = v
+    got = _exec((src, fn, kw))["out_ptr"]
+    np.testing.assert_array_equal(got, want)
+    # the sources of one destination row differ (else this would not test the order)
+    assert any(len(set(s[d == r])) > 1 for r in np.unique(d))
