@@ -328,6 +328,29 @@ def test_flash_attention_fused_other_fill_or_scale(fill, sign, dt):
     np.testing.assert_allclose(f(out["o_ptr"]), f(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_flash_attention_fused_non_finite_inputs(dt):
+    """A NaN in one query row and an infinity in one key: NaN exactly where
+    the oracle has NaN (the NaN row; the rows whose maximum the infinite key
+    sets), the other rows within tolerance."""
+    from oracle.interp import bf16_bits
+    src, fn, kw = _cases.flash_attention(S=512, D=128, blk=128, dt=dt)
+    f = bf16_from_bits if dt == "bf16" else (lambda x: x.astype(np.float32))
+    back = (lambda x: bf16_bits(x.astype(np.float32))) if dt == "bf16" else (lambda x: x.astype(np.float16))
+    q, k = f(kw["q_ptr"]).copy(), f(kw["k_ptr"]).copy()
+    q[0, 1, 200, 7] = np.nan
+    k[0, 0, 300, 3] = np.inf
+    kw["q_ptr"], kw["k_ptr"] = back(q), back(k)
+    print(f"[attn] non-finite inputs {dt}", flush=True)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts().get("attn") == 1
+    got, want = f(out["o_ptr"]), f(ref["o_ptr"])
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    assert np.isnan(want).any()
+    ok = ~np.isnan(want)
+    np.testing.assert_allclose(got[ok], want[ok], rtol=1e-2, atol=1e-3)
+
+
 def test_flash_attention_replay_reuses_v_copy():
     """Replays of a prepared bf16 attention reuse the f16 copy of V while no
     host write has reached the arena; a new V written through memory.hbm
