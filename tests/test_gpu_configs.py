@@ -173,6 +173,31 @@ def test_softmax_fixed_form_large_and_non_finite_rows(cols, dt):
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 4096])
+def test_rmsnorm_non_finite_and_zero_rows(cols, dt):
+    """RMSNorm rows holding +inf or NaN, an all-zero row, and (bf16) values
+    whose squares overflow f32: equal to the oracle bit for bit, NaN where it
+    has NaN."""
+    from oracle.interp import bf16_bits
+    src, fn, kw = _cases.rmsnorm(rows=48, cols=cols, cores=4, dt=dt, wide=True)
+    x = _half_f32(kw["x_ptr"], dt).astype(np.float64)
+    x[2, 5] = np.inf
+    x[9, 0] = np.nan
+    x[13, :] = 0.0
+    if dt == "bf16":
+        x[17, 3] = 3.0e38
+        x[21, :8] = -2.0e30
+    kw["x_ptr"] = x.astype(np.float16) if dt == "f16" else bf16_bits(x.astype(np.float32))
+    print(f"[rmsnorm] non-finite rows {cols} {dt}", flush=True)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts() == {"prog": 1}
+    got, want = _half_f32(out["y_ptr"], dt), _half_f32(ref["y_ptr"], dt)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok], want[ok])
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("cols", [512, 1024, 2048, 4096])
 def test_rmsnorm_bit_exact(cols, dt):
     """RMSNorm with magnitudes over eight decades: every step is a correctly
