@@ -147,13 +147,14 @@ def test_softmax_fixed_form(cols, dt):
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-@pytest.mark.parametrize("cols", [512, 4096])
+@pytest.mark.parametrize("cols", [512, 4096, 256, 3000])
 def test_softmax_fixed_form_large_and_non_finite_rows(cols, dt):
     """Rows whose maximum is 2048 or more (the exponent then takes x - m'
     first), rows holding +inf or NaN (a sum that is not finite: the plain
     quotient per element), a row whose maximum (40) only a max over every
     element finds (a smaller one would overflow the f16 exponentials), next to
-    ordinary rows; NaN where the oracle has NaN."""
+    ordinary rows; NaN where the oracle has NaN.  256 and 3000 columns take
+    the general row kernels."""
     from oracle.interp import bf16_bits
     src, fn, kw = _cases.softmax(rows=48, cols=cols, cores=4, dt=dt)
     x = _half_f32(kw["x_ptr"], dt).astype(np.float64)
@@ -166,7 +167,8 @@ def test_softmax_fixed_form_large_and_non_finite_rows(cols, dt):
     kw["x_ptr"] = x.astype(np.float16) if dt == "f16" else bf16_bits(x.astype(np.float32))
     print(f"[softmax] large / non-finite rows {cols} {dt}", flush=True)
     ref, out, g = _run((src, fn, kw))
-    assert g.last_plan.counts() == {"prog": 1}
+    if cols in (512, 4096):
+        assert g.last_plan.counts() == {"prog": 1}
     got, want = _half_f32(out["y_ptr"], dt), _half_f32(ref["y_ptr"], dt)
     np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
     np.testing.assert_allclose(np.nan_to_num(got), np.nan_to_num(want), rtol=1e-2, atol=1e-3)
