@@ -61,18 +61,27 @@ __device__ __forceinline__ float combine(int op, int order, int dt, float dst, f
 }
 
 constexpr int RMW_MAXK = 1024;
-constexpr int RMW_TBL = 4096;   // LDS hash slots for the last-position test (>= 4 * RMW_MAXK)
 
+// LDS hash slots for the last-position test: a power of two, at least 64
+// and at least 4 per position
+__host__ __device__ __forceinline__ int rmw_table_slots(int K) {
+  int tb = 64;
+  while (tb < 4 * K) tb <<= 1;
+  return tb;
+}
+
+// The launch sizes the LDS to K (positions, then hash slots), so that at the
+// usual K = 128 (2.5 KB) many more workgroups share a CU than a fixed
+// RMW_MAXK-sized table would allow.
 __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
-  __shared__ int32_t rows[RMW_MAXK];
-  __shared__ int32_t tbl[RMW_TBL];
+  extern __shared__ int32_t rmw_lds[];
+  const int K = (int)d.K;
+  const int tb = rmw_table_slots(K);
+  int32_t* rows = rmw_lds;
+  int32_t* tbl = rmw_lds + K;
   const int64_t inst = blockIdx.x;
   const int64_t p0 = ((const int64_t*)d.dst_pos)[inst];
   const int64_t q0 = ((const int64_t*)d.src_pos)[inst];
-  const int K = (int)d.K;
-  // table size: a power of two, at least 4 slots per position
-  int tb = 64;
-  while (tb < 4 * K) tb <<= 1;
   const int tshift = 32 - __builtin_ctz(tb);
   bool bad = false;
   for (int i = threadIdx.x; i < tb; i += blockDim.x) tbl[i] = -1;
@@ -514,7 +523,8 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
 static int rmw_launch(const ktir_rmw_t* d) {
   if (d->n_inst == 0) return KTIR_OK;
   const int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
-  hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), 0, stream(), *d, device_error_flag());
+  const size_t lds = (size_t)(d->K + rmw_table_slots((int)d->K)) * sizeof(int32_t);
+  hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), lds, stream(), *d, device_error_flag());
   const int64_t total = d->n_inst * d->K;
   const int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
   if (rmw_rows_form(d)) {
