@@ -30,6 +30,7 @@ namespace ktir {
 typedef float gf4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gu2 __attribute__((ext_vector_type(2)));
 typedef int32_t gi2 __attribute__((ext_vector_type(2)));
+typedef int32_t gi4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int64_t read_index(uint64_t ptr, int dt, int64_t e, int64_t hi, bool* bad) {
   if (e < 0 || e >= hi) return 0;   // over-read of the index tensor reads zeros
@@ -70,24 +71,29 @@ __host__ __device__ __forceinline__ int rmw_table_slots(int K) {
   return tb;
 }
 
-// The launch sizes the LDS to K (positions, then hash slots), so that at the
-// usual K = 128 (2.5 KB) many more workgroups share a CU than a fixed
-// RMW_MAXK-sized table would allow.
+// The launch sizes the LDS to K (destination rows, source rows, then hash
+// slots), so that at the usual K = 128 (3 KB) many more workgroups share a
+// CU than a fixed RMW_MAXK-sized table would allow.
 __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
   extern __shared__ int32_t rmw_lds[];
   const int K = (int)d.K;
   const int tb = rmw_table_slots(K);
   int32_t* rows = rmw_lds;
-  int32_t* tbl = rmw_lds + K;
+  int32_t* srcs = rmw_lds + K;
+  int32_t* tbl = rmw_lds + 2 * K;
   const int64_t inst = blockIdx.x;
   const int64_t p0 = ((const int64_t*)d.dst_pos)[inst];
   const int64_t q0 = ((const int64_t*)d.src_pos)[inst];
   const int tshift = 32 - __builtin_ctz(tb);
   bool bad = false;
   for (int i = threadIdx.x; i < tb; i += blockDim.x) tbl[i] = -1;
+  // both index views are read at every position, as the instance's gather
+  // and scatter tiles read them (a negative value anywhere is an error)
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    int64_t r = read_index(d.dst_idx_ptr, d.dst_idx_dtype, p0 + k, d.dst_idx_hi, &bad);
+    const int64_t r = read_index(d.dst_idx_ptr, d.dst_idx_dtype, p0 + k, d.dst_idx_hi, &bad);
+    const int64_t s = read_index(d.src_idx_ptr, d.src_idx_dtype, q0 + k, d.src_idx_hi, &bad);
     rows[k] = (r >= 0 && r < d.n_rows) ? (int32_t)r : -1;
+    srcs[k] = (int32_t)(s < 0x7fffffff ? s : 0x7fffffff);
   }
   __syncthreads();
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
@@ -112,8 +118,7 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
     }
     int32_t code = -1, s32 = 0;
     if (last) {
-      const int64_t s = read_index(d.src_idx_ptr, d.src_idx_dtype, q0 + k, d.src_idx_hi, &bad);
-      s32 = (int32_t)(s < 0x7fffffff ? s : 0x7fffffff);
+      s32 = srcs[k];
       const int32_t prev = atomicExch(&((int32_t*)d.head)[r], (int32_t)e);
       // heads hold entries of this call only (-1 between calls); the bound
       // keeps a corrupted head from turning into a stray write
@@ -307,6 +312,20 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
   const int64_t hw = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 32;
   const int hl = threadIdx.x % 32;
   const int64_t e0 = hw * RMW_NE;
+  // When the head table is at most 8 slots per entry, every thread first
+  // sets four consecutive heads to -1 (the launch has 16 threads per entry,
+  // so the grid covers the table): one coalesced pass instead of a 4-byte
+  // write at a random address per owner.  Nothing in this kernel reads the
+  // heads; rmw_link of this call has finished with them.
+  const bool dense = d.n_rows <= 8 * n_entries;
+  if (dense) {
+    KTIR_G(int32_t)* hd = (KTIR_G(int32_t)*)d.head;
+    const int64_t h0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (h0 + 4 <= d.n_rows && (d.head & 15) == 0)
+      *(KTIR_G(gi4)*)(hd + h0) = gi4{-1, -1, -1, -1};
+    else
+      for (int64_t i = h0; i < h0 + 4 && i < d.n_rows; ++i) hd[i] = -1;
+  }
   if (e0 >= n_entries) return;
   const int64_t D = D128 ? 128 : d.D;
   const KTIR_G(gi2)* rec = (const KTIR_G(gi2)*)d.rows;
@@ -364,7 +383,7 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
       if (nx[j].x >= 0 && !second_first)
         for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g2[j][q]);
       if (hl == 0 && c + 128 >= D) {    // the row's last column group: leave its head and slot empty
-        head[r[j]] = -1;
+        if (!dense) head[r[j]] = -1;
         if (nx[j].x >= 0) nxt[e0 + j] = gi2{-1, -1};
       }
       *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + d.dst_base + (int64_t)r[j] * d.dst_row + c) =
@@ -523,7 +542,7 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
 static int rmw_launch(const ktir_rmw_t* d) {
   if (d->n_inst == 0) return KTIR_OK;
   const int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
-  const size_t lds = (size_t)(d->K + rmw_table_slots((int)d->K)) * sizeof(int32_t);
+  const size_t lds = (size_t)(2 * d->K + rmw_table_slots((int)d->K)) * sizeof(int32_t);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), lds, stream(), *d, device_error_flag());
   const int64_t total = d->n_inst * d->K;
   const int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
