@@ -290,6 +290,55 @@ def test_gemm_bf16(shape):
     np.testing.assert_allclose(bf16_from_bits(out["c_ptr"]), bf16_from_bits(ref["c_ptr"]), rtol=1e-2, atol=1e-3)
 
 
+def _plant_non_finite(a, b, inf, ninf, nan):
+    """Planted values whose products decide the result's non-finite entries
+    in any summation order: row 3 of A holds +inf (C row 3 = +-inf by the
+    sign of B row 5), row 17 is zero but for one NaN (C row 17 all NaN),
+    B[9, 33] = -inf (column 33), and column 70 of B is zero but for +inf at
+    k = 100, with A[50, 100] = 0 (C[50, 70] = 0 * inf = NaN)."""
+    a[3, 5] = inf
+    a[17, :] = 0
+    a[17, 40] = nan
+    b[9, 33] = ninf
+    b[:, 70] = 0
+    b[100, 70] = inf
+    a[50, 100] = 0
+
+
+def _check_non_finite(o, r):
+    np.testing.assert_array_equal(np.isnan(o), np.isnan(r))
+    np.testing.assert_array_equal(np.isposinf(o), np.isposinf(r))
+    np.testing.assert_array_equal(np.isneginf(o), np.isneginf(r))
+    fin = np.isfinite(r)
+    assert np.isnan(r).any() and np.isinf(r).any() and fin.mean() > 0.9
+    np.testing.assert_allclose(o[fin], r[fin], rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.filterwarnings("ignore:invalid value encountered in matmul")
+@pytest.mark.parametrize("shape,out_dt", [((256, 256, 256, 64, 64, 32, 2, 2), "f16"),   # generic tile path
+                                          (_MFMA_SHAPES[0], "f16"), (_MFMA_SHAPES[0], "f32"),
+                                          (_MFMA_SHAPES[1], "f32")])
+def test_gemm_non_finite_inputs(shape, out_dt):
+    """+-inf and NaN operands: the result is NaN, +inf or -inf exactly where
+    the oracle's is (those follow from the products alone, whatever the
+    order of the sums), and within tolerance elsewhere."""
+    src, fn, kw = _cases.gemm(*shape, out_dt=out_dt)
+    _plant_non_finite(kw["a_ptr"], kw["b_ptr"], np.inf, -np.inf, np.nan)
+    ref, out, g = _run((src, fn, kw))
+    assert set(g.last_plan.counts()) == {"mm"}
+    _check_non_finite(out["c_ptr"].astype(np.float32), ref["c_ptr"].astype(np.float32))
+
+
+@pytest.mark.filterwarnings("ignore:invalid value encountered in matmul")
+@pytest.mark.parametrize("shape", _MFMA_SHAPES)
+def test_gemm_bf16_non_finite_inputs(shape):
+    src, fn, kw = _cases.gemm_bf16(*shape)
+    _plant_non_finite(kw["a_ptr"], kw["b_ptr"], 0x7F80, 0xFF80, 0x7FC0)
+    ref, out, g = _run((src, fn, kw))
+    assert set(g.last_plan.counts()) == {"mm"}
+    _check_non_finite(bf16_from_bits(out["c_ptr"]), bf16_from_bits(ref["c_ptr"]))
+
+
 def test_flash_attention_generic_path():
     """D = 32, 64-row blocks: not the fused kernel's shape, op-by-op launches."""
     ref, out, g = _run(_cases.flash_attention())
