@@ -165,13 +165,50 @@ __device__ __forceinline__ void store4(const ktir_rmw_t& d, int64_t e0, int64_t 
   }
 }
 
+// The rows form's element access (unit column stride, f32 destination, f16
+// or f32 source): 4 columns [c, c + 4) from element e0, zeros outside
+// [0, hi); the dtype is a template constant, so no per-element dtype switch.
+template <int DT>
+__device__ __forceinline__ void rows_get4(uint64_t ptr, int64_t e0, int64_t c, int64_t D, int64_t hi, float* v) {
+  if (e0 >= 0 && e0 + 4 <= hi) {
+    if (DT == KTIR_F16) {
+      const uint2 w = __builtin_bit_cast(uint2, *(const KTIR_G(gu2)*)((const KTIR_G(uint16_t)*)ptr + e0));
+      v[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x & 0xffffu));
+      v[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x >> 16));
+      v[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y & 0xffffu));
+      v[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y >> 16));
+    } else {
+      const gf4 w = *(const KTIR_G(gf4)*)((const KTIR_G(float)*)ptr + e0);
+      v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
+    }
+    return;
+  }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t x = e0 + i;
+    const bool in = c + i < D && x >= 0 && x < hi;
+    v[i] = !in ? 0.f
+               : (DT == KTIR_F16 ? (float)((const KTIR_G(_Float16)*)ptr)[x] : ((const KTIR_G(float)*)ptr)[x]);
+  }
+}
+
+__device__ __forceinline__ void rows_put4(const ktir_rmw_t& d, int64_t e0, int64_t c, const float* v) {
+  if (e0 >= 0 && e0 + 4 <= d.dst_hi) {
+    *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + e0) = gf4{v[0], v[1], v[2], v[3]};
+    return;
+  }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t x = e0 + i;
+    if (c + i < d.D && x >= 0 && x < d.dst_hi) ((KTIR_G(float)*)d.dst_ptr)[x] = v[i];
+  }
+}
+
 // A chain of three or more entries (rare): starting from the owner (entry e,
 // source s), the successor slots list the others in arrival order; apply
 // them in ascending entry order by repeated selection (bounded walks).
 // Each arrival links only to an earlier one, so chains are acyclic and at most
 // n_entries long: that bound never cuts a chain short.
 template <typename SRC4>
-__device__ __forceinline__ void apply_long_chain(const ktir_rmw_t& d, int32_t e, int32_t s, int2 nx, int dt,
+__device__ __forceinline__ void apply_long_chain(const ktir_rmw_t& d, int op, int32_t e, int32_t s, int2 nx, int dt,
                                                  float* x, SRC4 src4) {
   const int2* nxt = (const int2*)d.link;
   const int64_t bound = d.n_inst * d.K + 1;
@@ -186,7 +223,7 @@ __device__ __forceinline__ void apply_long_chain(const ktir_rmw_t& d, int32_t e,
     prevm = m;
     float g[4];
     src4(sm, g);
-    for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, dt, x[q], g[q]);
+    for (int q = 0; q < 4; ++q) x[q] = combine(op, d.order, dt, x[q], g[q]);
   }
 }
 
@@ -230,8 +267,8 @@ __device__ __forceinline__ void rmw_src4(const ktir_rmw_t& d, int64_t se, float*
 constexpr int RMW_CH = 8;
 
 template <int SDT, bool D128>
-__device__ __forceinline__ bool apply_short_chain(const ktir_rmw_t& d, int32_t r, int32_t e, int32_t s, int2 nx,
-                                                  int2 n2, int64_t n_entries, int hl) {
+__device__ __forceinline__ bool apply_short_chain(const ktir_rmw_t& d, int op, int32_t r, int32_t e, int32_t s,
+                                                  int2 nx, int2 n2, int64_t n_entries, int hl) {
   const KTIR_G(gi2)* nxt = (const KTIR_G(gi2)*)d.link;
   int32_t ce[RMW_CH], cs[RMW_CH];
   ce[0] = e; cs[0] = s;
@@ -282,7 +319,7 @@ __device__ __forceinline__ bool apply_short_chain(const ktir_rmw_t& d, int32_t r
       float g[4];
       rmw_src4<SDT>(d, d.src_base + (int64_t)os[it] * d.src_row + c, g);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) x[k] = combine(d.op, d.order, KTIR_F32, x[k], g[k]);
+      for (int k = 0; k < 4; ++k) x[k] = combine(op, d.order, KTIR_F32, x[k], g[k]);
     }
     *(KTIR_G(gf4)*)((KTIR_G(float)*)d.dst_ptr + de + c) = gf4{x[0], x[1], x[2], x[3]};
   }
@@ -304,11 +341,15 @@ __device__ __forceinline__ bool apply_short_chain(const ktir_rmw_t& d, int32_t r
 // half-wave takes RMW_NE consecutive entries; lane l covers columns
 // 4l .. 4l + 3 of each 128-column group.  An owner's record, its successor
 // slot, its destination row and every source row of a one- or two-entry
-// chain are loaded before anything is combined.
+// chain are loaded before anything is combined.  OPT >= 0 fixes the combining
+// op at compile time (the launcher instantiates the add, the common case):
+// the per-element op switch then disappears from the hot path, which keeps
+// the kernel a fifth of its size; OPT = -1 reads the op from the descriptor.
 constexpr int RMW_NE = 2;
 
-template <int SDT, bool D128>
+template <int SDT, bool D128, int OPT>
 __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_t n_entries) {
+  const int op = OPT >= 0 ? OPT : d.op;
   const int64_t hw = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 32;
   const int hl = threadIdx.x % 32;
   const int64_t e0 = hw * RMW_NE;
@@ -378,10 +419,10 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
       float x[4] = {v[j][0], v[j][1], v[j][2], v[j][3]};
       const bool second_first = nx[j].x >= 0 && nx[j].x < e0 + j;
       if (second_first)
-        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g2[j][q]);
-      for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g[j][q]);
+        for (int q = 0; q < 4; ++q) x[q] = combine(op, d.order, KTIR_F32, x[q], g2[j][q]);
+      for (int q = 0; q < 4; ++q) x[q] = combine(op, d.order, KTIR_F32, x[q], g[j][q]);
       if (nx[j].x >= 0 && !second_first)
-        for (int q = 0; q < 4; ++q) x[q] = combine(d.op, d.order, KTIR_F32, x[q], g2[j][q]);
+        for (int q = 0; q < 4; ++q) x[q] = combine(op, d.order, KTIR_F32, x[q], g2[j][q]);
       if (hl == 0 && c + 128 >= D) {    // the row's last column group: leave its head and slot empty
         if (!dense) head[r[j]] = -1;
         if (nx[j].x >= 0) nxt[e0 + j] = gi2{-1, -1};
@@ -397,15 +438,15 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
   for (int j = 0; j < RMW_NE; ++j) {
     if (r[j] < 0 || (fast[j] && n2[j].x < 0)) continue;
     const int32_t e = (int32_t)(e0 + j);
-    if (fast[j] && apply_short_chain<SDT, D128>(d, r[j], e, s[j], nx[j], n2[j], n_entries, hl)) continue;
+    if (fast[j] && apply_short_chain<SDT, D128>(d, op, r[j], e, s[j], nx[j], n2[j], n_entries, hl)) continue;
     const int64_t de = d.dst_base + (int64_t)r[j] * d.dst_row;
     for (int64_t c = (int64_t)hl * 4; c < D; c += 128) {
       float x[4];
-      load4(d, true, de + c, c, true, x);
-      apply_long_chain(d, e, s[j], nx[j], KTIR_F32, x, [&](int32_t sm, float* gg) {
-        load4(d, false, d.src_base + (int64_t)sm * d.src_row + c, c, true, gg);
+      rows_get4<KTIR_F32>(d.dst_ptr, de + c, c, D, d.dst_hi, x);
+      apply_long_chain(d, op, e, s[j], nx[j], KTIR_F32, x, [&](int32_t sm, float* gg) {
+        rows_get4<SDT>(d.src_ptr, d.src_base + (int64_t)sm * d.src_row + c, c, D, d.src_hi, gg);
       });
-      store4(d, de + c, c, true, x);
+      rows_put4(d, de + c, c, x);
     }
     rmw_reset(d, r[j], e, nx[j], hl);
   }
@@ -436,7 +477,7 @@ __global__ __launch_bounds__(256) void rmw_apply(const ktir_rmw_t d, int64_t n_e
     for (int64_t c = (int64_t)hl * 4; c < d.D; c += 128) {
       float x[4];
       load4(d, true, de + c * d.dst_col, c, vec, x);
-      apply_long_chain(d, e, s, nx, d.dt, x, [&](int32_t sm, float* gg) {
+      apply_long_chain(d, d.op, e, s, nx, d.dt, x, [&](int32_t sm, float* gg) {
         load4(d, false, d.src_base + (int64_t)sm * d.src_row + c * d.src_col, c, vec, gg);
       });
       store4(d, de + c * d.dst_col, c, vec, x);
@@ -547,13 +588,24 @@ static int rmw_launch(const ktir_rmw_t* d) {
   const int64_t total = d->n_inst * d->K;
   const int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
   if (rmw_rows_form(d)) {
-    const bool d128 = d->D == 128;
+    const bool d128 = d->D == 128, add = d->op == KTIR_OP_ADDF;
+    const dim3 g((unsigned)blocks), b(256);
     if (d->src_dtype == KTIR_F16) {
-      if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
-      else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+      if (add) {
+        if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, true, KTIR_OP_ADDF>), g, b, 0, stream(), *d, total);
+        else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, false, KTIR_OP_ADDF>), g, b, 0, stream(), *d, total);
+      } else {
+        if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, true, -1>), g, b, 0, stream(), *d, total);
+        else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F16, false, -1>), g, b, 0, stream(), *d, total);
+      }
     } else {
-      if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, true>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
-      else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, false>), dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
+      if (add) {
+        if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, true, KTIR_OP_ADDF>), g, b, 0, stream(), *d, total);
+        else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, false, KTIR_OP_ADDF>), g, b, 0, stream(), *d, total);
+      } else {
+        if (d128) hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, true, -1>), g, b, 0, stream(), *d, total);
+        else hipLaunchKernelGGL((rmw_apply_rows<KTIR_F32, false, -1>), g, b, 0, stream(), *d, total);
+      }
     }
   } else {
     hipLaunchKernelGGL(rmw_apply, dim3((unsigned)blocks), dim3(256), 0, stream(), *d, total);
