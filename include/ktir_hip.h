@@ -216,7 +216,8 @@ int ktir_memcpy_d2d(uint64_t dst, uint64_t src, uint64_t bytes);
 int ktir_memset(uint64_t dst, int value, uint64_t bytes);
 int ktir_sync(void);
 int ktir_check_error_flag(void);  /* device-side errors (negative indices) raised since the last call */
-/* HIP events on the library's stream, for timing launches */
+/* HIP events on the library's stream, for timing launches (created without the
+   system-scope fence at record time: timestamps only, not synchronisation) */
 int ktir_event_create(uint64_t* ev);
 int ktir_event_record(uint64_t ev);
 int ktir_event_elapsed_ms(uint64_t start, uint64_t stop, float* ms);

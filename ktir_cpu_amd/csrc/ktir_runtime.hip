@@ -126,9 +126,13 @@ extern "C" int ktir_check_error_flag(void) {
   return KTIR_OK;
 }
 
+// Timing events: no system-scope fence when one is recorded, so recording
+// it does not write back and invalidate the caches between the launches it
+// separates (elapsed times only need the timestamps; ktir_sync or
+// ktir_event_elapsed_ms waits for completion).
 extern "C" int ktir_event_create(uint64_t* ev) {
   hipEvent_t e;
-  KTIR_HIP_CHECK(hipEventCreate(&e));
+  KTIR_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
   *ev = (uint64_t)e;
   return KTIR_OK;
 }
