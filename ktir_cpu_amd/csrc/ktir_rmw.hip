@@ -64,29 +64,39 @@ __device__ __forceinline__ float combine(int op, int order, int dt, float dst, f
 constexpr int RMW_MAXK = 1024;
 
 // LDS hash slots for the last-position test: a power of two, at least 64
-// and at least 4 per position
+// and at least 4 per position (so at most a quarter of them are taken)
 __host__ __device__ __forceinline__ int rmw_table_slots(int K) {
   int tb = 64;
   while (tb < 4 * K) tb <<= 1;
   return tb;
 }
 
-// The launch sizes the LDS to K (destination rows, source rows, then hash
-// slots), so that at the usual K = 128 (3 KB) many more workgroups share a
-// CU than a fixed RMW_MAXK-sized table would allow.
+// The launch sizes the LDS to K (destination rows, source rows, then the
+// hash table's keys and values), so that at the usual K = 128 (5 KB) many
+// more workgroups share a CU than a fixed RMW_MAXK-sized table would allow.
+// The table is open addressing with linear probing: a position claims its
+// row's slot (compare-and-swap of the key from -1) or finds it, and raises
+// the slot's value to its position; a lookup probes to the row's key.  Each
+// row has exactly one slot, and with at most a quarter of the slots taken
+// the probe sequences stay short (the table never fills, so they end).
 __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
   extern __shared__ int32_t rmw_lds[];
   const int K = (int)d.K;
   const int tb = rmw_table_slots(K);
   int32_t* rows = rmw_lds;
   int32_t* srcs = rmw_lds + K;
-  int32_t* tbl = rmw_lds + 2 * K;
+  int32_t* keys = rmw_lds + 2 * K;
+  int32_t* last_pos = keys + tb;
   const int64_t inst = blockIdx.x;
   const int64_t p0 = ((const int64_t*)d.dst_pos)[inst];
   const int64_t q0 = ((const int64_t*)d.src_pos)[inst];
   const int tshift = 32 - __builtin_ctz(tb);
+  const uint32_t tmask = (uint32_t)tb - 1;
   bool bad = false;
-  for (int i = threadIdx.x; i < tb; i += blockDim.x) tbl[i] = -1;
+  for (int i = threadIdx.x; i < tb; i += blockDim.x) {
+    keys[i] = -1;
+    last_pos[i] = -1;
+  }
   // both index views are read at every position, as the instance's gather
   // and scatter tiles read them (a negative value anywhere is an error)
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
@@ -98,7 +108,15 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
   __syncthreads();
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
     const int32_t r = rows[k];
-    if (r >= 0) atomicMax(&tbl[((uint32_t)r * 2654435761u) >> tshift], k);
+    if (r < 0) continue;
+    uint32_t h = ((uint32_t)r * 2654435761u) >> tshift;
+    for (int probe = 0; probe < tb; ++probe, h = (h + 1) & tmask) {
+      const int32_t owner = atomicCAS(&keys[h], -1, r);
+      if (owner == -1 || owner == r) {
+        atomicMax(&last_pos[h], k);
+        break;
+      }
+    }
   }
   __syncthreads();
   int2* rec = (int2*)d.rows;
@@ -108,13 +126,9 @@ __global__ __launch_bounds__(256) void rmw_link(const ktir_rmw_t d, int* err) {
     const int32_t r = rows[k];
     bool last = false;
     if (r >= 0) {
-      const int w = tbl[((uint32_t)r * 2654435761u) >> tshift];
-      if (w == k) {
-        last = true;
-      } else if (rows[w] != r) {     // the slot's winner is another row: look for a later position of r
-        last = true;
-        for (int j = k + 1; j < K && last; ++j) last = rows[j] != r;
-      }
+      uint32_t h = ((uint32_t)r * 2654435761u) >> tshift;
+      for (int probe = 0; probe < tb && keys[h] != r; ++probe) h = (h + 1) & tmask;
+      last = last_pos[h] == k;
     }
     int32_t code = -1, s32 = 0;
     if (last) {
@@ -583,7 +597,7 @@ extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
 static int rmw_launch(const ktir_rmw_t* d) {
   if (d->n_inst == 0) return KTIR_OK;
   const int t1 = d->K >= 256 ? 256 : (int)((d->K + 63) / 64 * 64);
-  const size_t lds = (size_t)(2 * d->K + rmw_table_slots((int)d->K)) * sizeof(int32_t);
+  const size_t lds = (size_t)(2 * d->K + 2 * rmw_table_slots((int)d->K)) * sizeof(int32_t);
   hipLaunchKernelGGL(rmw_link, dim3((unsigned)d->n_inst), dim3(t1), lds, stream(), *d, device_error_flag());
   const int64_t total = d->n_inst * d->K;
   const int64_t blocks = (total + 8 * RMW_NE - 1) / (8 * RMW_NE);
