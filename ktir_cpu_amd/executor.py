@@ -516,14 +516,16 @@ class Plan:
         # that a later rewrite of `desc` points at
         self.launches.append((kind, desc, keep if isinstance(keep, list) else tuple(keep)))
 
-    def run(self, after=None):
+    def run(self, after=None, reuse_v16=True):
         """Replay every launch; `after(i)`, if given, runs after launch i is
-        queued (the bench records a HIP event there)."""
+        queued (the bench records a HIP event there).  With reuse_v16 false
+        every attention launch converts its V again, as a call with a new V
+        does."""
         L = rt.lib()
         for i, (kind, desc, _) in enumerate(self.launches):
             c = self.v16.get(id(desc)) if kind == "attn" else None
             if c is not None:
-                desc.v16_ready = int(c.ok and c.gen is not None and c.gen == c.buf.host_writes)
+                desc.v16_ready = int(reuse_v16 and c.ok and c.gen is not None and c.gen == c.buf.host_writes)
                 _launch(L, kind, desc)
                 c.gen = c.buf.host_writes
             else:
