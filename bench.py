@@ -161,10 +161,9 @@ def _traffic(config, kind):
     if not t:
         return None
     pats = _LAUNCH_KERNELS.get(kind, ())
-    # the kernels of that launch that run on every replay (not the attention
-    # launch's f16 copy of V, which a replay reuses)
-    b = [v["bytes"] for k, v in t.get("kernels", {}).items()
-         if any(p in k for p in pats) and v.get("every_run", True)]
+    # every kernel of that launch runs on each timed replay (the attention
+    # launch converts V on each one)
+    b = [v["bytes"] for k, v in t.get("kernels", {}).items() if any(p in k for p in pats)]
     return round(sum(b)) if b else None
 
 
@@ -408,14 +407,13 @@ def collect_traffic(root):
         (f, nf), (w, _) = per_kernel(config, "FETCH_SIZE"), per_kernel(config, "WRITE_SIZE")
         if not f:
             continue
-        # the launch of a replay: the kernels dispatched on every run of the
-        # plan; one dispatched less often (the attention launch's f16 copy of
-        # V, made by a run whose V is new, skipped by replays) is listed apart
-        top = max(nf.values())
-        ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0), "dispatches": nf[k], "every_run": nf[k] == top,
+        # the launch of a timed replay: every kernel dispatched (the
+        # attention launch's f16 copy of V included: each timed replay makes
+        # it; the bench's reuse figure adds dispatches without it, which the
+        # per-dispatch medians leave out of the bytes)
+        ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0), "dispatches": nf[k],
                   "bytes": f[k] * 1024 * fscale + w.get(k, 0.0) * 1024 * wscale} for k in f}
-        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values() if v["every_run"]),
-                                  "kernels": ks}
+        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values()), "kernels": ks}
     path = os.path.join(ROOT, "profiles", "traffic.json")
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1)
