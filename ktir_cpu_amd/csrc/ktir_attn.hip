@@ -721,10 +721,15 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
     ((float*)d.l_out)[lane * AT + row] = lsum;
   }
   const int64_t ob = uni(((const int64_t*)d.o_base)[lane]) + (int64_t)row * d.o_row + 4 * h;
+  // O = acc / l as acc * (1 / l): one correctly rounded reciprocal per row
+  // instead of 64 IEEE divisions per lane (within 1.5 ulp of the quotient,
+  // before the result's own rounding; l = 0, inf or NaN give the quotient's
+  // inf / 0 / NaN as well)
+  const float rl = __frcp_rn(lsum);
 #define PP_EPI(o, dt)                                                                            \
   _Pragma("unroll") for (int gg = 0; gg < 4; ++gg) {                                             \
-    const float q0 = __fdiv_rn(o[4 * gg], lsum), q1 = __fdiv_rn(o[4 * gg + 1], lsum);            \
-    const float q2 = __fdiv_rn(o[4 * gg + 2], lsum), q3 = __fdiv_rn(o[4 * gg + 3], lsum);        \
+    const float q0 = __fmul_rn(o[4 * gg], rl), q1 = __fmul_rn(o[4 * gg + 1], rl);                \
+    const float q2 = __fmul_rn(o[4 * gg + 2], rl), q3 = __fmul_rn(o[4 * gg + 3], rl);            \
     const int64_t e = ob + 32 * dt + 8 * gg;                                                     \
     if (d.o_dtype == KTIR_F32)                                                                   \
       *(float4*)((float*)d.o_ptr + e) = make_float4(q0, q1, q2, q3);                             \
