@@ -5,10 +5,11 @@ prints ONE JSON line.  A step is one replay of the recorded launch plan of a
 config's KTIR kernel over inputs already resident in HBM (the host IR walk
 and the host<->device copies are outside the timed region).  Timing uses HIP
 events on the library's stream, with an event after every launch, so the
-dominant launch's own time gives `roofline.achieved`.  Every timed replay
-does a whole call's work: the attention launch converts V to f16 on each
-one (replays of an unchanged V may reuse the copy; that figure is reported
-beside it as `v16_reuse`, never as the value).  By default the line's
+dominant launch's own time gives `roofline.achieved`.  A replay of the
+attention launch reuses the f16 copy of its V while V is unchanged (the
+plan tracks writes to V); the figure with V converted again on every step,
+as a call with a new V does, is reported beside it as `v16_new`.  By
+default the line's
 top-level fields are the gather + scatter-add config
 and `per_config` holds the same measurement for every config; each entry also
 reports the host side of a real call (copies in and out, one end-to-end
@@ -161,9 +162,10 @@ def _traffic(config, kind):
     if not t:
         return None
     pats = _LAUNCH_KERNELS.get(kind, ())
-    # every kernel of that launch runs on each timed replay (the attention
-    # launch converts V on each one)
-    b = [v["bytes"] for k, v in t.get("kernels", {}).items() if any(p in k for p in pats)]
+    # the kernels of that launch that run on every replay (not the attention
+    # launch's f16 copy of V, which a replay of an unchanged V reuses)
+    b = [v["bytes"] for k, v in t.get("kernels", {}).items()
+         if any(p in k for p in pats) and v.get("every_run", True)]
     return round(sum(b)) if b else None
 
 
@@ -212,9 +214,7 @@ def cpu_baseline(cfg, budget_s=2.5, repeats=3):
 
 def _instrumented_steps(prep, steps):
     """K replays of the plan with a HIP event after every launch (library
-    stream): returns (ms per step, mean ms of each launch).  Every replay
-    does a whole call's work: an attention launch converts V to f16 again
-    (a replay may otherwise reuse the copy of an unchanged V)."""
+    stream): returns (ms per step, mean ms of each launch)."""
     from ktir_cpu_amd import runtime as rt
     plan = prep.plan
     n = len(plan.launches)
@@ -224,13 +224,13 @@ def _instrumented_steps(prep, steps):
     # one untimed replay ahead of the start event keeps the GPU busy while
     # the host queues the timed ones, so the region does not open with the
     # GPU idle, waiting for the first launch to be submitted
-    plan.run(reuse_v16=False)
+    plan.run()
     e0.record()
     for s_ in range(steps):
         if instrument:
-            plan.run(after=lambda i, row=evs[s_]: row[i].record(), reuse_v16=False)
+            plan.run(after=lambda i, row=evs[s_]: row[i].record())
         else:
-            plan.run(reuse_v16=False)
+            plan.run()
     e1.record()
     rt.sync()
     ms = e0.elapsed_ms(e1) / steps
@@ -262,18 +262,18 @@ def measure(name, steps, warmup, with_cpu):
         prep.run()
     rt.sync()
     ms, durs = _instrumented_steps(prep, steps)
-    reuse_ms = None
+    new_ms = None
     if plan.v16:
-        # the same replays letting attention reuse the f16 copy of its
-        # unchanged V (reported beside the figure, never as it)
+        # the same replays with attention converting V to f16 on each one, as
+        # a call whose V is new does (reported beside the figure)
         e0, e1 = rt.Event(), rt.Event()
-        plan.run()
+        plan.run(reuse_v16=False)
         e0.record()
         for _ in range(steps):
-            plan.run()
+            plan.run(reuse_v16=False)
         e1.record()
         rt.sync()
-        reuse_ms = e0.elapsed_ms(e1) / steps
+        new_ms = e0.elapsed_ms(e1) / steps
     n = len(plan.launches)
     dom = int(np.argmax(durs)) if n else 0
     dom_ms = float(durs[dom]) if n and durs.any() else ms
@@ -303,8 +303,8 @@ def measure(name, steps, warmup, with_cpu):
            "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                         "frac": round(achieved / peak, 4), "traffic": _traffic(name, kind),
                         "dominant_launch": kind, "dominant_ms": round(dom_ms, 6)},
-           **({"v16_reuse": {"ms_per_step": round(reuse_ms, 6),
-                             "value": round(units / (reuse_ms * 1e-3) / scale, 3)}} if reuse_ms else {}),
+           **({"v16_new": {"ms_per_step": round(new_ms, 6),
+                           "value": round(units / (new_ms * 1e-3) / scale, 3)}} if new_ms else {}),
            "host": {"prepare_s": round(prepare_s, 3), "h2d_s": round(h2d_s, 4), "d2h_s": round(d2h_s, 4),
                     "execute_function_s": round(e2e_s, 3),
                     "execute_function_rate": round(units / e2e_s / scale, 4)}}
@@ -363,8 +363,8 @@ def main():
                    "plan_mode": h["plan_mode"]},
         "roofline": h["roofline"],
     }
-    if "v16_reuse" in h:
-        out["v16_reuse"] = h["v16_reuse"]
+    if "v16_new" in h:
+        out["v16_new"] = h["v16_new"]
     if "cpu_baseline" in h:
         out["cpu_baseline"] = h["cpu_baseline"]
     out["host"] = h["host"]
@@ -407,13 +407,14 @@ def collect_traffic(root):
         (f, nf), (w, _) = per_kernel(config, "FETCH_SIZE"), per_kernel(config, "WRITE_SIZE")
         if not f:
             continue
-        # the launch of a timed replay: every kernel dispatched (the
-        # attention launch's f16 copy of V included: each timed replay makes
-        # it; the bench's reuse figure adds dispatches without it, which the
-        # per-dispatch medians leave out of the bytes)
-        ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0), "dispatches": nf[k],
+        # the launch of a replay: the kernels dispatched on every run of the
+        # plan; one dispatched less often (the attention launch's f16 copy of
+        # V, made by a run whose V is new, skipped by replays) is listed apart
+        top = max(nf.values())
+        ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0), "dispatches": nf[k], "every_run": nf[k] == top,
                   "bytes": f[k] * 1024 * fscale + w.get(k, 0.0) * 1024 * wscale} for k in f}
-        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values()), "kernels": ks}
+        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values() if v["every_run"]),
+                                  "kernels": ks}
     path = os.path.join(ROOT, "profiles", "traffic.json")
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1)
