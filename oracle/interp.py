@@ -29,6 +29,12 @@ How each part is pinned (``tests/test_golden.py``, ``tests/test_oracle_pins.py``
 - attention (matmul, mask, max, exp, sum, divide as composed by the KTIR
   loop): the closed form for Q = 0, where softmax is uniform and O[i] is the
   mean of the V rows row i may see (causal and full);
+- the parser and affine evaluator it shares with the product
+  (``ktir_cpu_amd.parser``, ``ktir_cpu_amd.affine``): maps and sets against
+  MLIR's integer semantics from their definitions on negative operands,
+  set membership and box lowering against brute-force enumeration, parsed
+  kernels against their structure written out by hand
+  (``tests/test_affine_parser_pins.py``);
 - LX-overflow accounting (``grid.py:255-350``): the reference's golden peak
   of 622592 bytes for its K-loop matmul kernel
   (``tests/test_lx_scoping.py:1095-1185``): capacity equal to it runs, one
