@@ -8,9 +8,9 @@
 // its last position (computed from the row as it was before the instance).
 //
 //   pass 1 (rmw_link, one workgroup per instance): the instance's last
-//     position of every destination row survives (an LDS table keyed by a
-//     hash of the row keeps the largest position; a slot won by another row
-//     falls back to a scan).  A survivor e of row r exchanges itself into
+//     position of every destination row survives (an LDS hash table with
+//     open addressing keeps each row's largest position).  A survivor e of
+//     row r exchanges itself into
 //     head[r]; the entry that finds head[r] empty is the row's owner, and
 //     every later arrival writes (its entry, its source row) into its
 //     predecessor's successor slot.  The record of entry e is the pair
