@@ -317,3 +317,37 @@ def test_oracle_scatter_add_two_index_against_brute_force(dim, hot):
     np.testing.assert_array_equal(got, want)
     # the sources of one destination row differ (else this would not test the order)
     assert any(len(set(s[d == r])) > 1 for r in np.unique(d))
+
+
+def _splat_kernel(dt, const):
+    return f"""module {{
+  func.func @splat_kernel(%out_ptr: index) attributes {{grid = [1, 1]}} {{
+    %c = arith.constant {const} : {dt}
+    %z = arith.constant 0 : index
+    %v = ktdp.construct_memory_view %out_ptr, sizes: [4, 8], strides: [8, 1] {{
+      coordinate_set = affine_set<(d0, d1) : (d0 >= 0, -d0 + 3 >= 0, d1 >= 0, -d1 + 7 >= 0)>, memory_space = #ktdp.memory_space<global>
+    }} : memref<4x8x{dt}>
+    %t = tensor.splat %c : tensor<4x8x{dt}>
+    %tile = ktdp.construct_access_tile %v[%z, %z] {{
+      access_tile_set = affine_set<(d0, d1) : (d0 >= 0, -d0 + 3 >= 0, d1 >= 0, -d1 + 7 >= 0)>,
+      access_tile_order = affine_map<(d0, d1) -> (d0, d1)>
+    }} : memref<4x8x{dt}> -> !ktdp.access_tile<4x8xindex>
+    ktdp.store %t, %tile : tensor<4x8x{dt}>, !ktdp.access_tile<4x8xindex>
+    return
+  }}
+}}
+"""
+
+
+@pytest.mark.parametrize("dt,const,np_dt", [("f32", "2.5", np.float32), ("f16", "0.1", np.float16),
+                                            ("i32", "-7", np.int32)])
+def test_oracle_splat_takes_shape_and_dtype_from_result_type(dt, const, np_dt):
+    """tensor.splat fills the result type's shape with the scalar in the
+    result's dtype (reference dialects/tensor_ops.py:57-84): every stored
+    element equals np.full of that shape (0.1 rounded once to f16)."""
+    o = OracleInterpreter()
+    o.load(_splat_kernel(dt, const))
+    out = o.execute_function("splat_kernel", out_ptr=np.full((4, 8), 99, np_dt))["out_ptr"]
+    want = np.full((4, 8), np_dt(float(const)) if np_dt is not np.int32 else int(const), np_dt)
+    assert out.dtype == np_dt
+    np.testing.assert_array_equal(out, want)
