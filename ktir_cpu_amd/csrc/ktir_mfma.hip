@@ -425,6 +425,37 @@ __device__ __forceinline__ void q256_out(uint64_t ptr, int64_t cb, int64_t cs, i
         mm_put<DT>(ptr, cb + (32 * i + 8 * (e >> 2) + 4 * h + (e & 3)) * cs + 32 * j + r32, __fadd_rn(acc[i][j][e], z));
 }
 
+// The same 128 x 128 result rounded to a 16-bit dtype, staged through this
+// wavefront's 32 KB of LDS (row-major, 128 halfs a row) and written as
+// 16-byte row pieces: 32 stores per lane instead of 256 two-byte ones.
+// Needs 16-byte aligned result rows (the caller checks).
+typedef uint32_t q256_u4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ void q256_out16(uint16_t* lds, uint64_t ptr, int64_t cb, int64_t cs, int h, int r32, int l,
+                                           const f32x16 (&acc)[4][4], float z) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = __fadd_rn(acc[i][j][e], z);
+        const uint16_t b = DT == KTIR_F16 ? __builtin_bit_cast(uint16_t, (_Float16)v)
+                                          : (uint16_t)(__float_as_uint(round_bf16(v)) >> 16);
+        lds[(32 * i + 8 * (e >> 2) + 4 * h + (e & 3)) * 128 + 32 * j + r32] = b;
+      }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  KTIR_G(uint16_t)* c = (KTIR_G(uint16_t)*)ptr + cb;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const int row = 4 * it + (l >> 4), col = 8 * (l & 15);
+    const q256_u4 v = *(const q256_u4*)&lds[row * 128 + col];
+    __builtin_nontemporal_store(v, (KTIR_G(q256_u4)*)(c + row * cs + col));
+  }
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
   __shared__ __align__(16) uint16_t P0[4 * QT];
@@ -537,12 +568,22 @@ __global__ __launch_bounds__(256, 1) void mm_mfma_256(const ktir_mm_t d) {
   // result dtype (the only forms launched here)
   const int64_t cb = lane_offset(d.c, ln), cs = d.c.strides[0];
   const float z = d.accumulate == 2 ? 0.f : -0.f;
-  if (d.c.dtype == KTIR_F32)
+  if (d.c.dtype == KTIR_F32) {
     q256_out<KTIR_F32>(d.c.ptr, cb, cs, h, r32, acc, z);
-  else if (d.c.dtype == KTIR_F16)
-    q256_out<KTIR_F16>(d.c.ptr, cb, cs, h, r32, acc, z);
-  else
-    q256_out<KTIR_BF16>(d.c.ptr, cb, cs, h, r32, acc, z);
+  } else {
+    // every wavefront's DMA has landed (waited above) and every wavefront is
+    // past its last read of the stages: the LDS is free for the result
+    __syncthreads();
+    uint16_t* stage = (w < 2 ? P0 : P1) + (w & 1) * (2 * QT);
+    const bool vec = ((d.c.ptr + 2 * (uint64_t)cb) & 15) == 0 && (cs & 7) == 0;
+    if (d.c.dtype == KTIR_F16) {
+      if (vec) q256_out16<KTIR_F16>(stage, d.c.ptr, cb, cs, h, r32, l, acc, z);
+      else q256_out<KTIR_F16>(d.c.ptr, cb, cs, h, r32, acc, z);
+    } else {
+      if (vec) q256_out16<KTIR_BF16>(stage, d.c.ptr, cb, cs, h, r32, l, acc, z);
+      else q256_out<KTIR_BF16>(d.c.ptr, cb, cs, h, r32, acc, z);
+    }
+  }
 }
 
 }  // namespace ktir
