@@ -5,11 +5,12 @@ prints ONE JSON line.  A step is one replay of the recorded launch plan of a
 config's KTIR kernel over inputs already resident in HBM (the host IR walk
 and the host<->device copies are outside the timed region).  Timing uses HIP
 events on the library's stream, with an event after every launch, so the
-dominant launch's own time gives `roofline.achieved`.  A replay of the
-attention launch reuses the f16 copy of its V while V is unchanged (the
-plan tracks writes to V); the figure with V converted again on every step,
-as a call with a new V does, is reported beside it as `v16_new`.  By
-default the line's
+dominant launch's own time gives `roofline.achieved`.  Every timed
+attention replay converts V to f16 again, as a call with a new V does; the
+figure for replays that reuse the f16 copy of an unchanged V (the plan
+tracks writes to V) is reported beside it as `v16_reuse`.  For the
+memory-bound configs `cold` times replays that each follow a 1 GiB fill, so
+that no input is left in L2 or the Infinity Cache.  By default the line's
 top-level fields are the gather + scatter-add config
 and `per_config` holds the same measurement for every config; each entry also
 reports the host side of a real call (copies in and out, one end-to-end
@@ -80,7 +81,7 @@ def _gather():
     kw = dict(table_ptr=table, idx_ptr=idx, out_ptr=np.zeros((rows, dim), np.float32))
     alg = 4 * n_idx + n_idx * dim * 2 + 2 * dim * 4 * n_uniq
     return dict(src=configs.gather_scatter_add(rows, dim, n_idx, cores, chunk), fn="gather_scatter_add", kw=kw,
-                cores=cores, bytes=alg, flops=n_idx * dim, bound="hbm", dtype="f16->f32",
+                cores=cores, bytes=alg, flops=n_idx * dim, bound="hbm", dtype="f16 table, f32 out (f32 adds)",
                 workload=f"gather_scatter_add table={rows}x{dim} f16 idx={n_idx} i32 (10% dup) out f32 "
                          f"grid={cores} chunk={chunk}")
 
@@ -92,7 +93,8 @@ def _softmax():
     x = (rng.standard_normal((rows, cols), dtype=np.float32) * 2).astype(np.float16)
     kw = dict(x_ptr=x, y_ptr=np.zeros_like(x))
     return dict(src=configs.softmax(rows, cols, cores, rblk), fn="softmax_kernel", kw=kw, cores=cores,
-                bytes=4 * rows * cols, flops=5 * rows * cols, bound="hbm", dtype="f16/f32",
+                bytes=4 * rows * cols, flops=5 * rows * cols, bound="hbm",
+                dtype="f16 in/out; f32 max, sum and 1/sum; exp(x - max) held in f16",
                 workload=f"softmax {rows}x{cols} f16 grid={cores} rows/step={rblk}")
 
 
@@ -104,7 +106,8 @@ def _rmsnorm():
     w = rng.uniform(0.5, 1.5, cols).astype(np.float16)
     kw = dict(x_ptr=x, w_ptr=w, y_ptr=np.zeros_like(x), eps=1e-6)
     return dict(src=configs.rmsnorm(rows, cols, cores, rblk), fn="rmsnorm_kernel", kw=kw, cores=cores,
-                bytes=4 * rows * cols + 2 * cols, flops=4 * rows * cols, bound="hbm", dtype="f16/f32",
+                bytes=4 * rows * cols + 2 * cols, flops=4 * rows * cols, bound="hbm",
+                dtype="f16 in/out; f32 squares, sum, rsqrt and scaling",
                 workload=f"rmsnorm {rows}x{cols} f16 grid={cores} rows/step={rblk}")
 
 
@@ -116,7 +119,7 @@ def _gemm():
     b = (rng.standard_normal((K, N), dtype=np.float32) * K ** -0.5).astype(np.float16)
     kw = dict(a_ptr=a, b_ptr=b, c_ptr=np.zeros((M, N), np.float16))
     return dict(src=configs.gemm(M, N, K, 128, 128, 64, 8, 8), fn="gemm_kernel", kw=kw, cores=64,
-                bytes=3 * M * N * 2, flops=2 * M * N * K, bound="mfma", dtype="f16 (f32 acc)",
+                bytes=3 * M * N * 2, flops=2 * M * N * K, bound="mfma", dtype="f16 MFMA, f32 accumulate, f16 out",
                 workload=f"gemm {M}x{N}x{K} f16 tiles 128x128x64 grid=8x8")
 
 
@@ -135,7 +138,8 @@ def _attention():
     q, k, v = (_bf16_bits(rng.standard_normal((B, H, S, D), dtype=np.float32)) for _ in range(3))
     kw = dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D))
     return dict(src=configs.flash_attention(B, H, S, D, 128), fn="flash_attention", kw=kw, cores=B * H * S // 128,
-                bytes=4 * B * H * S * D * 2, flops=4 * B * H * S * S * D // 2, bound="mfma", dtype="bf16 (f32 acc)",
+                bytes=4 * B * H * S * D * 2, flops=4 * B * H * S * S * D // 2, bound="mfma",
+                dtype="bf16 Q K^T MFMA, f32 scores / m / l / acc; P and V rounded to f16 for the f16 P V MFMA; bf16 out",
                 f32_blas=True,
                 workload=f"flash_attention causal B={B} H={H} S={S} D={D} kv_tile=128")
 
@@ -212,7 +216,7 @@ def cpu_baseline(cfg, budget_s=2.5, repeats=3):
     return t_full, {"k": kk, "t_k": t_k, "t_fixed": t_fixed}
 
 
-def _instrumented_steps(prep, steps):
+def _instrumented_steps(prep, steps, reuse_v16=True):
     """K replays of the plan with a HIP event after every launch (library
     stream): returns (ms per step, mean ms of each launch)."""
     from ktir_cpu_amd import runtime as rt
@@ -224,13 +228,13 @@ def _instrumented_steps(prep, steps):
     # one untimed replay ahead of the start event keeps the GPU busy while
     # the host queues the timed ones, so the region does not open with the
     # GPU idle, waiting for the first launch to be submitted
-    plan.run()
+    plan.run(reuse_v16=reuse_v16)
     e0.record()
     for s_ in range(steps):
         if instrument:
-            plan.run(after=lambda i, row=evs[s_]: row[i].record())
+            plan.run(after=lambda i, row=evs[s_]: row[i].record(), reuse_v16=reuse_v16)
         else:
-            plan.run()
+            plan.run(reuse_v16=reuse_v16)
     e1.record()
     rt.sync()
     ms = e0.elapsed_ms(e1) / steps
@@ -243,6 +247,29 @@ def _instrumented_steps(prep, steps):
                 prev = evs[s_][i]
         durs /= steps
     return ms, durs
+
+
+FLUSH_BYTES = 1 << 30
+
+
+def _cold_steps(prep, steps):
+    """K replays, each preceded (outside its own events) by a fill of a
+    1 GiB scratch buffer on the library stream, which evicts the L2 caches
+    and MI355X's 256 MB Infinity Cache: the mean ms of one replay whose
+    inputs are in HBM only."""
+    from ktir_cpu_amd import runtime as rt
+    scratch = rt.DeviceBuffer(FLUSH_BYTES)
+    plan = prep.plan
+    evs = [(rt.Event(), rt.Event()) for _ in range(steps)]
+    for s_, (a, b) in enumerate(evs):
+        scratch.memset(s_ & 0xFF)
+        a.record()
+        plan.run()
+        b.record()
+    rt.sync()
+    ms = float(np.mean([a.elapsed_ms(b) for a, b in evs]))
+    scratch.free()
+    return ms
 
 
 def measure(name, steps, warmup, with_cpu):
@@ -261,19 +288,14 @@ def measure(name, steps, warmup, with_cpu):
     for _ in range(warmup):
         prep.run()
     rt.sync()
-    ms, durs = _instrumented_steps(prep, steps)
-    new_ms = None
+    # attention converts V to f16 on every timed replay, as a call whose V is
+    # new does; the replays that reuse the copy of an unchanged V are
+    # reported beside the value
+    ms, durs = _instrumented_steps(prep, steps, reuse_v16=False)
+    reuse_ms = None
     if plan.v16:
-        # the same replays with attention converting V to f16 on each one, as
-        # a call whose V is new does (reported beside the figure)
-        e0, e1 = rt.Event(), rt.Event()
-        plan.run(reuse_v16=False)
-        e0.record()
-        for _ in range(steps):
-            plan.run(reuse_v16=False)
-        e1.record()
-        rt.sync()
-        new_ms = e0.elapsed_ms(e1) / steps
+        reuse_ms, _ = _instrumented_steps(prep, steps, reuse_v16=True)
+    cold_ms = _cold_steps(prep, steps) if cfg["bound"] == "hbm" else None
     n = len(plan.launches)
     dom = int(np.argmax(durs)) if n else 0
     dom_ms = float(durs[dom]) if n and durs.any() else ms
@@ -303,8 +325,12 @@ def measure(name, steps, warmup, with_cpu):
            "roofline": {"bound": cfg["bound"], "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                         "frac": round(achieved / peak, 4), "traffic": _traffic(name, kind),
                         "dominant_launch": kind, "dominant_ms": round(dom_ms, 6)},
-           **({"v16_new": {"ms_per_step": round(new_ms, 6),
-                           "value": round(units / (new_ms * 1e-3) / scale, 3)}} if new_ms else {}),
+           **({"v16_reuse": {"ms_per_step": round(reuse_ms, 6),
+                             "value": round(units / (reuse_ms * 1e-3) / scale, 3)}} if reuse_ms else {}),
+           **({"cold": {"ms_per_step": round(cold_ms, 6), "value": round(units / (cold_ms * 1e-3) / scale, 3),
+                        "frac": round(units / (cold_ms * 1e-3) / scale / peak, 4),
+                        "how": f"each replay after a {FLUSH_BYTES >> 20} MiB fill (outside the timed region) "
+                               "that evicts L2 and the 256 MB Infinity Cache"}} if cold_ms else {}),
            "host": {"prepare_s": round(prepare_s, 3), "h2d_s": round(h2d_s, 4), "d2h_s": round(d2h_s, 4),
                     "execute_function_s": round(e2e_s, 3),
                     "execute_function_rate": round(units / e2e_s / scale, 4)}}
@@ -363,8 +389,9 @@ def main():
                    "plan_mode": h["plan_mode"]},
         "roofline": h["roofline"],
     }
-    if "v16_new" in h:
-        out["v16_new"] = h["v16_new"]
+    for k in ("cold", "v16_reuse"):
+        if k in h:
+            out[k] = h[k]
     if "cpu_baseline" in h:
         out["cpu_baseline"] = h["cpu_baseline"]
     out["host"] = h["host"]

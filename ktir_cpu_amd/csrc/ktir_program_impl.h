@@ -53,29 +53,62 @@ __device__ __forceinline__ float binop_f(int op, int dt, float x, float y) {
   return round_to(r, dt);
 }
 
+// Integer semantics are NumPy's on int32 tiles, as the reference computes
+// them on an x86-64 host:
+// * floor_divide / remainder by 0 give 0; INT_MIN // -1 wraps to INT_MIN;
+// * divsi and ceildivsi go through float64 (trunc / ceil of a / b, exact for
+//   int32 operands), and a float64 that int32 cannot hold (a / 0 = +-inf or
+//   NaN, INT_MIN / -1 = 2^31) converts to INT_MIN, as cvttsd2si does;
+// * remsi is a - divsi(a, b) * b in wrapping int32 (so remsi(a, 0) = a);
+// * shifts by an amount outside [0, 32) give 0 (shli, shrui) or the sign
+//   fill (shrsi).
+__device__ __forceinline__ int neg_i(int x) { return (int)(0u - (uint32_t)x); }
+
 __device__ __forceinline__ int floordiv_i(int x, int y) {
   if (y == 0) return 0;
+  if (y == -1) return neg_i(x);
   int q = x / y;
   if ((x % y != 0) && ((x < 0) != (y < 0))) --q;
   return q;
 }
+
+__device__ __forceinline__ int truncdiv_i(int x, int y) {
+  if (y == 0 || (y == -1 && x == INT_MIN)) return INT_MIN;
+  return y == -1 ? -x : x / y;
+}
+
+__device__ __forceinline__ int truncrem_i(int x, int y) {
+  return (int)((uint32_t)x - (uint32_t)truncdiv_i(x, y) * (uint32_t)y);
+}
+
+__device__ __forceinline__ int ceildiv_i(int x, int y) {
+  if (y == 0 || (y == -1 && x == INT_MIN)) return INT_MIN;
+  if (y == -1) return -x;
+  int q = x / y;
+  if ((x % y != 0) && ((x < 0) == (y < 0))) ++q;
+  return q;
+}
+
+__device__ __forceinline__ int shl_i(int x, int y) { return (uint32_t)y < 32u ? (int)((uint32_t)x << y) : 0; }
+__device__ __forceinline__ int shrs_i(int x, int y) { return (uint32_t)y < 32u ? x >> y : (x < 0 ? -1 : 0); }
+__device__ __forceinline__ int shru_i(int x, int y) { return (uint32_t)y < 32u ? (int)((uint32_t)x >> y) : 0; }
 
 __device__ __forceinline__ int binop_i(int op, int x, int y) {
   switch (op) {
     case KTIR_OP_ADDI: return (int)((uint32_t)x + (uint32_t)y);
     case KTIR_OP_SUBI: return (int)((uint32_t)x - (uint32_t)y);
     case KTIR_OP_MULI: return (int)((uint32_t)x * (uint32_t)y);
-    case KTIR_OP_DIVSI: return y ? x / y : 0;
-    case KTIR_OP_REMSI: return y ? x % y : 0;
+    case KTIR_OP_DIVSI: return truncdiv_i(x, y);
+    case KTIR_OP_REMSI: return truncrem_i(x, y);
     case KTIR_OP_FLOORDIVSI: return floordiv_i(x, y);
-    case KTIR_OP_FLOORREMSI: return y ? x - floordiv_i(x, y) * y : 0;
-    case KTIR_OP_CEILDIVSI: return y ? -floordiv_i(-x, y) : 0;
+    case KTIR_OP_FLOORREMSI: return y ? (int)((uint32_t)x - (uint32_t)floordiv_i(x, y) * (uint32_t)y) : 0;
+    case KTIR_OP_CEILDIVSI: return ceildiv_i(x, y);
     case KTIR_OP_ANDI: return x & y;
     case KTIR_OP_ORI: return x | y;
     case KTIR_OP_XORI: return x ^ y;
-    case KTIR_OP_SHLI: return (int)((uint32_t)x << (y & 31));
-    case KTIR_OP_SHRSI: return x >> (y & 31);
-    case KTIR_OP_SHRUI: return (int)((uint32_t)x >> (y & 31));
+    case KTIR_OP_SHLI: return shl_i(x, y);
+    case KTIR_OP_SHRSI: return shrs_i(x, y);
+    case KTIR_OP_SHRUI: return shru_i(x, y);
     case KTIR_OP_MAXSI: return x > y ? x : y;
     case KTIR_OP_MINSI: return x < y ? x : y;
   }
@@ -128,7 +161,9 @@ __device__ __forceinline__ float cast_val(float x, int src, int dst) {
   if (fs && fd) return round_to(x, dst);
   if (fs) {
     if (dst == KTIR_I1) return __int_as_float(x != 0.f);
-    int i = (x != x) ? 0 : (int)truncf(fminf(fmaxf(x, -2147483648.f), 2147483520.f));
+    // NaN and values int32 cannot hold convert to INT_MIN (NumPy's astype on
+    // x86-64, cvttss2si)
+    int i = (x != x || !(x < 2147483648.f && x >= -2147483648.f)) ? INT_MIN : (int)x;
     if (dst == KTIR_I8) i = (int8_t)i;
     if (dst == KTIR_I16) i = (int16_t)i;
     return __int_as_float(i);
@@ -160,7 +195,7 @@ __device__ __forceinline__ float unop(int op, int dt, float x) {
     case KTIR_OP_CEIL: r = ceilf(x); break;
     case KTIR_OP_FLOOR: r = floorf(x); break;
     case KTIR_OP_NOTI: return __int_as_float(__float_as_int(x) ? 0 : 1);
-    case KTIR_OP_ABSI: { int i = __float_as_int(x); return __int_as_float(i < 0 ? -i : i); }
+    case KTIR_OP_ABSI: { int i = __float_as_int(x); return __int_as_float(i < 0 ? neg_i(i) : i); }
     default: r = 0.f;
   }
   return round_to(r, dt);
@@ -351,7 +386,7 @@ __device__ __forceinline__ float unop_simple(int op, int dt, float x) {
     case KTIR_OP_CEIL: r = ceilf(x); break;
     case KTIR_OP_FLOOR: r = floorf(x); break;
     case KTIR_OP_NOTI: return __int_as_float(__float_as_int(x) ? 0 : 1);
-    case KTIR_OP_ABSI: { int i = __float_as_int(x); return __int_as_float(i < 0 ? -i : i); }
+    case KTIR_OP_ABSI: { int i = __float_as_int(x); return __int_as_float(i < 0 ? neg_i(i) : i); }
     default: r = 0.f;
   }
   return round_to(r, dt);
@@ -381,9 +416,9 @@ __device__ __forceinline__ int binop_i_simple(int op, int x, int y) {
     case KTIR_OP_ANDI: return x & y;
     case KTIR_OP_ORI: return x | y;
     case KTIR_OP_XORI: return x ^ y;
-    case KTIR_OP_SHLI: return (int)((uint32_t)x << (y & 31));
-    case KTIR_OP_SHRSI: return x >> (y & 31);
-    case KTIR_OP_SHRUI: return (int)((uint32_t)x >> (y & 31));
+    case KTIR_OP_SHLI: return shl_i(x, y);
+    case KTIR_OP_SHRSI: return shrs_i(x, y);
+    case KTIR_OP_SHRUI: return shru_i(x, y);
     case KTIR_OP_MAXSI: return x > y ? x : y;
     case KTIR_OP_MINSI: return x < y ? x : y;
   }

@@ -424,7 +424,8 @@ __global__ __launch_bounds__(256) void rmw_apply_rows(const ktir_rmw_t d, int64_
       if (nx[j].x >= 0) {
         rmw_src4<SDT>(d, d.src_base + (int64_t)nx[j].y * d.src_row + c, g2[j]);
         const gi2 t = nxt[nx[j].x];
-        n2[j] = make_int2(t.x, t.y);
+        // checked like nx: a slot outside this call's entries is not followed
+        n2[j] = t.x >= 0 && t.x < n_entries ? make_int2(t.x, t.y) : make_int2(-1, -1);
       }
     }
 #pragma unroll
@@ -591,6 +592,9 @@ extern "C" int ktir_launch_row_rmw_noalloc(const ktir_rmw_t* d) {
 extern "C" int ktir_launch_row_rmw(const ktir_rmw_t* d) {
   const int rc = rmw_check(d, "ktir_launch_row_rmw");
   if (rc != KTIR_OK) return rc;
+  if (d->n_inst > 0 && (!d->head || !d->link || !d->rows))
+    return set_error(KTIR_E_ARG, "ktir_launch_row_rmw: head, link and rows scratch must be given "
+                                 "(head: n_rows int32 of -1; link: 2 * n_inst * K int32 of -1)");
   return rmw_launch(d);
 }
 

@@ -1504,15 +1504,21 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
   const float m = rr.get(F.m);
   rf_fence<NQ>(c);
-  // exp(x - m') rounded to f16 (at most 1: x <= m'), kept packed for the
-  // store pass (half the registers of f32 values); the row sum adds the same
-  // f16 values two per dot2.  Against the reference's f32 values this moves
-  // each output by at most about 2^-11 of itself, inside softmax's tolerance.
+  // exp(x - m') (at most 1: x <= m').  An f16 row keeps the exponentials
+  // rounded to f16 and packed for the store pass (half the registers of f32
+  // values), and the row sum adds those f16 values two per dot2: an
+  // exponential below f16's normal range (x - m' < -9.7) loses relative
+  // precision, but the output e / s (s >= 1) is then below f16's normal range
+  // too, so the error stays under one f16 ulp of the output (2^-11 of it in
+  // the normal range).  A bf16 row keeps f32 exponentials: bf16 outputs hold
+  // their relative precision far below f16's range.
   // While |m'| < 2048 the exponent is one FMA into exp2 (the rounding of
   // m' log2 e is then below 2^-12 of it); else the difference first.
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   typedef float f2 __attribute__((ext_vector_type(2)));
-  uint32_t ep[NQ * 4];
+  constexpr bool PACK = DT == KTIR_F16;
+  constexpr int NE = PACK ? NQ * 4 : NQ * 8;
+  uint32_t ep[NE];                 // f16 pairs (PACK) or f32 bit patterns
   const bool near = fabsf(m) < 2048.f;
   const float c0 = -__fmul_rn(m, 1.44269504088896341f);
   const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -1529,14 +1535,27 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
       for (int k = 0; k < 4; ++k) {
         const f2 x = {__builtin_amdgcn_exp2f(__builtin_fmaf(__fsub_rn(v[2 * k], msub), 1.44269504088896341f, c0u)),
                       __builtin_amdgcn_exp2f(__builtin_fmaf(__fsub_rn(v[2 * k + 1], msub), 1.44269504088896341f, c0u))};
-        ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+        if constexpr (PACK) {
+          ep[4 * i + k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+        } else {
+          ep[8 * i + 2 * k] = __float_as_uint(x.x);
+          ep[8 * i + 2 * k + 1] = __float_as_uint(x.y);
+        }
       }
     }
   }
+  if constexpr (PACK) {
 #pragma unroll
-  for (int q = 0; q < NQ * 4; q += 2) {
-    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q]), one, s0, false);
-    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q + 1]), one, s1, false);
+    for (int q = 0; q < NE; q += 2) {
+      s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q]), one, s0, false);
+      s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ep[q + 1]), one, s1, false);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NE; q += 2) {
+      s0 = __fadd_rn(s0, __uint_as_float(ep[q]));
+      s1 = __fadd_rn(s1, __uint_as_float(ep[q + 1]));
+    }
   }
   float sum = __fadd_rn(s0, s1);
   // v_dot2_f32_f16 does not carry a NaN operand into its sum as an f32 add
@@ -1544,14 +1563,16 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
   // finite (x - m' is NaN only for x NaN or x = m' = +-inf), so only then are
   // the f16 values checked; a NaN among them makes the lane's part NaN, and
   // the adds below carry it into the row sum.
-  if (mx != mx || !(fabsf(m) <= 3.40282347e38f)) {
-    bool nan_e = false;
+  if constexpr (PACK) {
+    if (mx != mx || !(fabsf(m) <= 3.40282347e38f)) {
+      bool nan_e = false;
 #pragma unroll
-    for (int q = 0; q < NQ * 4; ++q) {
-      const h2 w = __builtin_bit_cast(h2, ep[q]);
-      nan_e = nan_e || w.x != w.x || w.y != w.y;
+      for (int q = 0; q < NE; ++q) {
+        const h2 w = __builtin_bit_cast(h2, ep[q]);
+        nan_e = nan_e || w.x != w.x || w.y != w.y;
+      }
+      if (nan_e) sum = __builtin_nanf("");
     }
-    if (nan_e) sum = __builtin_nanf("");
   }
 #pragma unroll
   for (int sh = 32; sh >= 1; sh >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, sh));
@@ -1573,7 +1594,12 @@ __device__ __forceinline__ void rf_softmax(const RfPlan& F, gu4 (&c)[NQ], const 
       float y[8];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const f2 e = __builtin_convertvector(__builtin_bit_cast(h2, ep[4 * i + k]), f2);
+        f2 e;
+        if constexpr (PACK) {
+          e = __builtin_convertvector(__builtin_bit_cast(h2, ep[4 * i + k]), f2);
+        } else {
+          e = f2{__uint_as_float(ep[8 * i + 2 * k]), __uint_as_float(ep[8 * i + 2 * k + 1])};
+        }
         y[2 * k] = div(e.x);
         y[2 * k + 1] = div(e.y);
       }

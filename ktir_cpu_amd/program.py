@@ -366,7 +366,10 @@ def compile_program(root: Expr, lanes: int, dest: LeafSpec) -> Tuple[rt.Prog, li
     def row_leaf(spec: LeafSpec) -> LeafSpec:
         k = id(spec)
         if k not in row_specs:
-            row_specs[k] = spec.with_strides(tuple(spec.strides) + (0,))
+            # a 1-D row space has one value per lane: a 0-d leaf (kept as
+            # one element with strides (1,)) reads or writes that element
+            base = () if R == 1 else tuple(spec.strides)
+            row_specs[k] = spec.with_strides(base + (0,))
         return row_specs[k]
 
     def is_row(n: Expr) -> bool:

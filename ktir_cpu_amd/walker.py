@@ -144,6 +144,88 @@ def E_scalar(v: np.ndarray, dt: str, shape) -> Expr:
     return Expr("lane", dt, shape, attr=np.asarray(v, dtype=np.float64))
 
 
+def _strides_injective(shape, strides) -> bool:
+    """Whether distinct positions of a box of `shape` over `strides` always
+    reach distinct elements (sufficient test: every stride, smallest first,
+    exceeds the span of the smaller ones).  A store through a box that fails
+    it can write one element twice, and then the later position in
+    row-major order must win, as in the reference's fancy-index write."""
+    span = 0
+    for s, n in sorted((abs(int(s)), int(n)) for s, n in zip(strides, shape) if int(n) > 1):
+        if s <= span:
+            return False
+        span += s * (n - 1)
+    return True
+
+
+def _collapse_dims(e: Expr, dest: LeafSpec, max_dims: int):
+    """Rewrite a fold-free expression stored through `dest` over fewer
+    dimensions: dims of extent 1 are dropped (their index is 0), then
+    adjacent dims d, d + 1 merge where every leaf (and `dest`) has
+    stride[d] == stride[d + 1] * extent[d + 1] and no linalg.index reads
+    either.  Gather leaves (offset lists) are laid out over the flattened
+    positions, so they keep contiguous strides.  Returns (e, dest) of rank
+    <= max_dims, or None."""
+    shape = tuple(e.shape)
+    nodes = topo(e)
+    if any(n.kind in ("fold", "rowval") for n in nodes):
+        return None
+    specs = [n.attr for n in nodes if n.kind == "ld"] + [dest]
+    if any(len(sp.strides) != len(shape) for sp in specs):
+        return None
+    if any(sp.offsets is not None and tuple(sp.strides) != _cstrides(shape) for sp in specs):
+        return None
+    idx_dims = {int(n.attr) for n in nodes if n.kind == "idx"}
+    # groups of old dims that become one new dim
+    groups = [[d] for d in range(len(shape)) if shape[d] != 1]
+    if not groups:
+        groups = [[len(shape) - 1]]
+    k = 0
+    while len(groups) > max_dims and k < len(groups) - 1:
+        a, b = groups[k], groups[k + 1]
+        ok = not (set(a) | set(b)) & idx_dims
+        for sp in specs:
+            if ok and int(sp.strides[a[-1]]) != int(sp.strides[b[-1]]) * _prod([shape[d] for d in b]):
+                ok = False
+        if ok:
+            groups[k:k + 2] = [a + b]
+        else:
+            k += 1
+    if len(groups) > max_dims:
+        return None
+    nshape = tuple(_prod([shape[d] for d in g]) for g in groups)
+    pos = {g[0]: i for i, g in enumerate(groups)}
+
+    def lf(spec):
+        if spec.offsets is not None:
+            return spec.with_strides(_cstrides(nshape))
+        return spec.with_strides(tuple(int(spec.strides[g[-1]]) for g in groups))
+
+    def idxf(d):
+        if d in pos:
+            return Expr("idx", "i32", nshape, attr=pos[d])
+        return E_const(0, "i32", nshape)
+
+    memo = {}
+
+    def rebuild(x):
+        k2 = id(x)
+        if k2 in memo:
+            return memo[k2]
+        if x.kind == "ld":
+            r = Expr("ld", x.dtype, nshape, attr=lf(x.attr))
+        elif x.kind == "idx":
+            r = idxf(int(x.attr))
+        elif x.kind in ("const", "lane"):
+            r = Expr(x.kind, x.dtype, nshape, attr=x.attr)
+        else:
+            r = Expr(x.kind, x.dtype, nshape, [rebuild(a) for a in x.args], x.attr)
+        memo[k2] = r
+        return r
+
+    return rebuild(e), lf(dest)
+
+
 def _map_leaf_idx(e: Expr, shape, leaf_fn, idx_fn, memo=None) -> Expr:
     """Rebuild `e` over a new iteration space.  leaf_fn(spec) -> spec maps
     strided leaves; idx_fn(dim) -> Expr builds the new index of an old dim."""
@@ -669,6 +751,12 @@ class Executor:
         return out
 
     def _emit_store(self, e: Expr, dest: LeafSpec, depth=0):
+        if len(e.shape) > rt.MAX_DIMS and not e.has_fold:
+            c = _collapse_dims(e, dest, rt.MAX_DIMS)
+            if c is None:
+                raise NotImplementedError(f"a tile expression of rank {len(e.shape)} whose dims do not collapse "
+                                          f"to {rt.MAX_DIMS}")
+            e, dest = c
         try:
             prog, keep = compile_program(e, self.L, dest)
         except CompileError:
@@ -692,11 +780,16 @@ class Executor:
         if not cands:
             raise CompileError("cannot split expression")
         best = max(cands, key=lambda n: sizes[id(n)]) if not e.has_fold else cands[0]
-        if best.kind == "fold" or len(best.shape) < len(e.shape) or best.has_fold:
-            mt = self.materialize(Tile(best))
-            leaf = mt.e
-        else:
+        # a sub-expression that cannot compile either splits again; bound the
+        # nesting (materialize starts a fresh _emit_store for it)
+        self._split_depth = getattr(self, "_split_depth", 0) + 1
+        try:
+            if self._split_depth > 16:
+                raise NotImplementedError(f"a tile expression that no split fits into one program "
+                                          f"(shape {tuple(e.shape)})")
             leaf = self.materialize(Tile(best)).e
+        finally:
+            self._split_depth -= 1
         return _replace(e, best, leaf)
 
     def hazard_flush(self, alloc: Alloc, keep: Optional[Tile] = None):
@@ -845,7 +938,7 @@ class Executor:
             return self.distributed_load(at, tuple(rs) if rs is not None else tuple(at.shape))
         v = at.view
         cs, co = at.cs, at.co
-        if isinstance(cs, Box) and co is None:
+        if isinstance(cs, Box) and co is None and _strides_injective(cs.extent, v.strides):
             lo_off = sum(int(l) * int(s) for l, s in zip(cs.lo, v.strides))
             shape = cs.extent
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
@@ -886,7 +979,7 @@ class Executor:
             return None
         v = at.view
         cs, co = at.cs, at.co
-        if isinstance(cs, Box) and co is None:
+        if isinstance(cs, Box) and co is None and _strides_injective(cs.extent, v.strides):
             lo_off = sum(int(l) * int(s) for l, s in zip(cs.lo, v.strides))
             shape = cs.extent
             spec, alloc, rel = self._hbm_leaf(v, at.origin + lo_off, shape, v.strides)
@@ -1817,6 +1910,12 @@ class Executor:
             perm = [d for d in range(nd) if d != dim] + [dim]
             t = self.transpose(t, perm)
         n = t.shape[-1]
+        if nd > rt.MAX_DIMS:
+            # a row space of more dims than a program has: fold a contiguous
+            # (rows, n) copy, then give the rows their shape back
+            lead = tuple(t.shape[:-1])
+            flat = self.reshape(self.materialize(t), (_prod(lead), n))
+            return self.reshape(self.fold(flat, 1, region), lead)
         if self.lat is not None:
             # the reference runs the combiner once per halving level on the
             # two halves (linalg_ops.py:114-131): charge those runs

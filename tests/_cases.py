@@ -186,7 +186,7 @@ def elementwise(body, ins, out_dt, n=4096, cores=4, name="ew_kernel"):
         lines.append(configs._view(f"{x}_view", f"{x}_ptr", [n], [1], dt))
         lines.append(configs._tile(f"{x}_t", f"{x}_view", ["%off"], [blk], [n], dt))
         lines.append(f"    %{x} = ktdp.load %{x}_t : {at} -> {configs._t([blk], dt)}")
-    types = {f"T_{dt}": configs._t([blk], dt) for dt in ("f16", "bf16", "f32", "i1", "i32")}
+    types = {f"T_{dt}": configs._t([blk], dt) for dt in ("f16", "bf16", "f32", "i1", "i32", "i64")}
     lines += ["    " + ln.format(**types) for ln in body]
     lines.append(configs._view("r_view", "r_ptr", [n], [1], out_dt))
     lines.append(configs._tile("r_t", "r_view", ["%off"], [blk], [n], out_dt))
@@ -797,3 +797,327 @@ def ffn_swiglu_4core(seq=4, d=256, f=1024, cores=4):
   }}
 }}
 """
+
+
+# ---------------------------------------------------------------------------
+# linalg.reduce over other axes, several axes and all axes; linalg.generic
+# with reduction iterators; linalg.batch_matmul
+# ---------------------------------------------------------------------------
+
+def _nd_box(shape):
+    dims = ", ".join(f"d{i}" for i in range(len(shape)))
+    cons = ", ".join(f"d{i} >= 0, -d{i} + {s - 1} >= 0" for i, s in enumerate(shape))
+    return f"affine_set<({dims}) : ({cons})>", f"affine_map<({dims}) -> ({dims})>"
+
+
+def _core_tile(name, view, shape, full, dt, row="%row0"):
+    """Access tile of `shape` at row `row` of a view of shape `full`."""
+    idx = [row] + ["%c0"] * (len(shape) - 1)
+    return configs._tile(name, view, idx, list(shape), list(full), dt)
+
+
+def reduce_kernel(shape=(3, 4, 2), dims=(0, 2), dt="f32", init=0.0, combiner="arith.addf", cores=2,
+                  region=False):
+    """Each core loads its `shape` block of x (blocks stacked on axis 0),
+    reduces it over `dims` (None: every axis, to a scalar) with outs
+    initialised to `init`, and stores the result (a scalar through a
+    one-element tensor.splat).  `region` writes the combiner as an explicit
+    region instead of the shorthand."""
+    nd = len(shape)
+    full = (shape[0] * cores,) + tuple(shape[1:])
+    rshape = tuple(s for i, s in enumerate(shape) if dims is not None and i not in dims)
+    rfull = (rshape[0] * cores,) + rshape[1:] if rshape else (cores,)
+    T = configs._t(list(shape), dt)
+    if region:
+        comb = (f"(%in: {dt}, %acc: {dt}) {{\n        %cmb = {combiner} %in, %acc : {dt}\n"
+                f"        linalg.yield %cmb : {dt}\n      }}")
+        head, tail = "", f"\n      {comb}"
+    else:
+        head, tail = f" {{ {combiner} }}", ""
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %c_rows = arith.constant {shape[0]} : index",
+             "    %row0 = arith.muli %core_id, %c_rows : index",
+             f"    %c_orows = arith.constant {rshape[0] if rshape else 1} : index",
+             "    %orow0 = arith.muli %core_id, %c_orows : index",
+             configs._view("x_view", "x_ptr", list(full), list(_cstr(full)), dt),
+             configs._view("y_view", "y_ptr", list(rfull), list(_cstr(rfull)), dt),
+             _core_tile("xt", "x_view", shape, full, dt),
+             f"    %x = ktdp.load %xt : !ktdp.access_tile<{'x'.join(map(str, shape))}xindex> -> {T}",
+             f"    %iv = arith.constant {init!r} : {dt}"]
+    if dims is None or not rshape:
+        dd = "" if dims is None else f" dimensions = {list(dims)}"
+        lines += [f"    %init = tensor.splat %iv : tensor<{dt}>",
+                  f"    %s = linalg.reduce{head} ins(%x : {T}) outs(%init : tensor<{dt}>){dd}{tail}",
+                  f"    %r = tensor.splat %s : tensor<1x{dt}>",
+                  configs._tile("yt", "y_view", ["%core_id"], [1], [cores], dt),
+                  f"    ktdp.store %r, %yt : tensor<1x{dt}>, !ktdp.access_tile<1xindex>"]
+    else:
+        R = configs._t(list(rshape), dt)
+        lines += [f"    %init = tensor.splat %iv : {R}",
+                  f"    %r = linalg.reduce{head} ins(%x : {T}) outs(%init : {R}) dimensions = {list(dims)}{tail}",
+                  _core_tile("yt", "y_view", rshape, rfull, dt, row="%orow0"),
+                  f"    ktdp.store %r, %yt : {R}, !ktdp.access_tile<{'x'.join(map(str, rshape))}xindex>"]
+    src = (f"module {{\n  func.func @reduce_kernel(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{\n"
+           + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "reduce_kernel", full, rfull
+
+
+def _cstr(shape):
+    st, acc = [], 1
+    for s in reversed(shape):
+        st.append(acc)
+        acc *= s
+    return tuple(reversed(st))
+
+
+def generic_contraction(M=3, N=4, K=5, dt="f32", cores=2, combiner="arith.addf"):
+    """C = A @ B + C0 written as a linalg.generic with a reduction iterator
+    (the reference's tests/test_dialects_exec.py:1222-1277 contraction), one
+    (M, K) @ (K, N) block per core."""
+    a_full, b_full, c_full = (M * cores, K), (K * cores, N), (M * cores, N)
+    TA, TB, TC = (configs._t(list(s), dt) for s in ((M, K), (K, N), (M, N)))
+    mul = "arith.mulf" if dt.startswith(("f", "b")) else "arith.muli"
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %cm = arith.constant {M} : index", f"    %ck = arith.constant {K} : index",
+             "    %am = arith.muli %core_id, %cm : index", "    %bk = arith.muli %core_id, %ck : index",
+             configs._view("a_view", "a_ptr", list(a_full), [K, 1], dt),
+             configs._view("b_view", "b_ptr", list(b_full), [N, 1], dt),
+             configs._view("c_view", "c_ptr", list(c_full), [N, 1], dt),
+             configs._tile("at", "a_view", ["%am", "%c0"], [M, K], list(a_full), dt),
+             configs._tile("bt", "b_view", ["%bk", "%c0"], [K, N], list(b_full), dt),
+             configs._tile("ct", "c_view", ["%am", "%c0"], [M, N], list(c_full), dt),
+             f"    %a = ktdp.load %at : !ktdp.access_tile<{M}x{K}xindex> -> {TA}",
+             f"    %b = ktdp.load %bt : !ktdp.access_tile<{K}x{N}xindex> -> {TB}",
+             f"    %c = ktdp.load %ct : !ktdp.access_tile<{M}x{N}xindex> -> {TC}",
+             "    %r = linalg.generic {indexing_maps = [affine_map<(d0, d1, d2) -> (d0, d2)>, "
+             "affine_map<(d0, d1, d2) -> (d2, d1)>, affine_map<(d0, d1, d2) -> (d0, d1)>],",
+             '                         iterator_types = ["parallel", "parallel", "reduction"]}',
+             f"        ins(%a, %b : {TA}, {TB}) outs(%c : {TC}) {{",
+             f"      ^bb0(%aa: {dt}, %bb: {dt}, %cc: {dt}):",
+             f"        %mul = {mul} %aa, %bb : {dt}",
+             f"        %acc = {combiner} %mul, %cc : {dt}",
+             f"        linalg.yield %acc : {dt}",
+             f"    }} -> {TC}",
+             f"    ktdp.store %r, %ct : {TC}, !ktdp.access_tile<{M}x{N}xindex>"]
+    src = (f"module {{\n  func.func @generic_red(%a_ptr: index, %b_ptr: index, %c_ptr: index) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "generic_red", a_full, b_full, c_full
+
+
+def generic_stick_contraction(cores=2):
+    """The stickified contraction of the reference's issue-174 test
+    (tests/test_dialects_exec.py:1279-1330): iteration (d0..d4) = (n_stick 1,
+    m 4, k_stick 2, k_elem 4, n_elem 4), reductions over d2 and d3, A read
+    through a permuted map (d2, d1, d3) and W through the computed map
+    (d0, d2 * 4 + d3, d4).  One block per core."""
+    a_s, w_s, c_s = (2, 4, 4), (1, 8, 4), (1, 4, 4)
+    full = {k: (s[0] * cores,) + s[1:] for k, s in (("a", a_s), ("w", w_s), ("c", c_s))}
+    T = {k: configs._t(list(s), "f32") for k, s in (("a", a_s), ("w", w_s), ("c", c_s))}
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index", "    %c1 = arith.constant 1 : index",
+             "    %c2 = arith.constant 2 : index",
+             "    %r2 = arith.muli %core_id, %c2 : index"]
+    for k, s, r in (("a", a_s, "%r2"), ("w", w_s, "%core_id"), ("c", c_s, "%core_id")):
+        lines.append(configs._view(f"{k}_view", f"{k}_ptr", list(full[k]), list(_cstr(full[k])), "f32"))
+        lines.append(configs._tile(f"{k}t", f"{k}_view", [r, "%c0", "%c0"], list(s), list(full[k]), "f32"))
+        lines.append(f"    %{k} = ktdp.load %{k}t : !ktdp.access_tile<{'x'.join(map(str, s))}xindex> -> {T[k]}")
+    lines += ["    %r = linalg.generic {indexing_maps = [affine_map<(d0, d1, d2, d3, d4) -> (d2, d1, d3)>, "
+              "affine_map<(d0, d1, d2, d3, d4) -> (d0, d2 * 4 + d3, d4)>, "
+              "affine_map<(d0, d1, d2, d3, d4) -> (d0, d1, d4)>],",
+              '                         iterator_types = ["parallel", "parallel", "reduction", "reduction", '
+              '"parallel"]}',
+              f"        ins(%a, %w : {T['a']}, {T['w']}) outs(%c : {T['c']}) {{",
+              "      ^bb0(%aa: f32, %ww: f32, %cc: f32):",
+              "        %mul = arith.mulf %aa, %ww : f32",
+              "        %acc = arith.addf %mul, %cc : f32",
+              "        linalg.yield %acc : f32",
+              f"    }} -> {T['c']}",
+              f"    ktdp.store %r, %ct : {T['c']}, !ktdp.access_tile<1x4x4xindex>"]
+    src = (f"module {{\n  func.func @stick_red(%a_ptr: index, %w_ptr: index, %c_ptr: index) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "stick_red", full
+
+
+def batch_matmul(Bt=3, M=16, N=32, K=64, dt="f16", out_dt="f32", cores=2):
+    """C = C0 + A @ B per batch with linalg.batch_matmul, one (Bt, M, K) x
+    (Bt, K, N) block per core (blocks stacked on the batch axis)."""
+    a_full, b_full, c_full = (Bt * cores, M, K), (Bt * cores, K, N), (Bt * cores, M, N)
+    TA, TB = configs._t([Bt, M, K], dt), configs._t([Bt, K, N], dt)
+    TC = configs._t([Bt, M, N], out_dt)
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %cb = arith.constant {Bt} : index",
+             "    %b0 = arith.muli %core_id, %cb : index",
+             configs._view("a_view", "a_ptr", list(a_full), list(_cstr(a_full)), dt),
+             configs._view("b_view", "b_ptr", list(b_full), list(_cstr(b_full)), dt),
+             configs._view("c_view", "c_ptr", list(c_full), list(_cstr(c_full)), out_dt),
+             configs._tile("at", "a_view", ["%b0", "%c0", "%c0"], [Bt, M, K], list(a_full), dt),
+             configs._tile("bt", "b_view", ["%b0", "%c0", "%c0"], [Bt, K, N], list(b_full), dt),
+             configs._tile("ct", "c_view", ["%b0", "%c0", "%c0"], [Bt, M, N], list(c_full), out_dt),
+             f"    %a = ktdp.load %at : !ktdp.access_tile<{Bt}x{M}x{K}xindex> -> {TA}",
+             f"    %b = ktdp.load %bt : !ktdp.access_tile<{Bt}x{K}x{N}xindex> -> {TB}",
+             f"    %c = ktdp.load %ct : !ktdp.access_tile<{Bt}x{M}x{N}xindex> -> {TC}",
+             f"    %r = linalg.batch_matmul ins(%a, %b : {TA}, {TB}) outs(%c : {TC}) -> {TC}",
+             f"    ktdp.store %r, %ct : {TC}, !ktdp.access_tile<{Bt}x{M}x{N}xindex>"]
+    src = (f"module {{\n  func.func @bmm(%a_ptr: index, %b_ptr: index, %c_ptr: index) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "bmm", a_full, b_full, c_full
+
+
+# ---------------------------------------------------------------------------
+# general indirect path: direct_expr subscripts, a permuted
+# variables_space_order, its error paths
+# ---------------------------------------------------------------------------
+
+def _box2(m, k):
+    return f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {m - 1} >= 0, d1 >= 0, -d1 + {k - 1} >= 0)>"
+
+
+def iat_direct_expr(cores=2, rows=64, cols=128, E=4, M=60):
+    """Y[e, m] = X[IDX[e], 2 m + 1] (the reference's direct_expr case,
+    tests/test_blocked_indirect_fast_path.py:360-391), E index rows per core."""
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %ce = arith.constant {E} : index",
+             "    %e0 = arith.muli %core_id, %ce : index",
+             configs._view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16"),
+             configs._view("i_view", "i_ptr", [E * cores], [1], "i32"),
+             configs._view("y_view", "y_ptr", [E * cores, M], [M, 1], "f16"),
+             "    %g = ktdp.construct_indirect_access_tile intermediate_variables(%e, %m)",
+             "        %x_view[ind(%i_view[%e0 + %e]), (2 * %m + 1)] {",
+             f"      variables_space_set = {_box2(E, M)},",
+             "      variables_space_order = affine_map<(d0, d1) -> (d0, d1)>",
+             f"    }} : memref<{rows}x{cols}xf16>, memref<{E * cores}xi32> -> !ktdp.access_tile<{E}x{M}xindex>",
+             f"    %v = ktdp.load %g : !ktdp.access_tile<{E}x{M}xindex> -> tensor<{E}x{M}xf16>",
+             configs._tile("yt", "y_view", ["%e0", "%c0"], [E, M], [E * cores, M], "f16"),
+             f"    ktdp.store %v, %yt : tensor<{E}x{M}xf16>, !ktdp.access_tile<{E}x{M}xindex>"]
+    src = (f"module {{\n  func.func @iat_expr(%x_ptr: index, %i_ptr: index, %y_ptr: index) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "iat_expr"
+
+
+def iat_permuted(M=4, K=8, rows=16, cols=16, cores=2, scatter=False, vso="(d1, d0)", store_shape=None):
+    """Two-index gather (or scatter) Y[m, k] <-> X[I1[m, k], I2[m, k]] over an
+    M x K variable space visited in the order of `vso` (a permutation of
+    (d0, d1)); each core uses its own M rows of I1 / I2 / Y.  A scatter
+    stores Y's tile (of `store_shape`, default M x K) through the IAT."""
+    ss = store_shape or (M, K)
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %cm = arith.constant {M} : index",
+             "    %m0 = arith.muli %core_id, %cm : index",
+             configs._view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16"),
+             configs._view("i1_view", "i1_ptr", [M * cores, K], [K, 1], "i32"),
+             configs._view("i2_view", "i2_ptr", [M * cores, K], [K, 1], "i32"),
+             configs._view("y_view", "y_ptr", [M * cores, K], [K, 1], "f16"),
+             "    %g = ktdp.construct_indirect_access_tile intermediate_variables(%m, %k)",
+             "        %x_view[ind(%i1_view[%m0 + %m, %k]), ind(%i2_view[%m0 + %m, %k])] {",
+             f"      variables_space_set = {_box2(M, K)},",
+             f"      variables_space_order = affine_map<(d0, d1) -> {vso}>",
+             f"    }} : memref<{rows}x{cols}xf16>, memref<{M * cores}x{K}xi32>, memref<{M * cores}x{K}xi32> "
+             f"-> !ktdp.access_tile<{M}x{K}xindex>"]
+    yt = configs._tile("yt", "y_view", ["%m0", "%c0"], [M, K], [M * cores, K], "f16")
+    if scatter:
+        T = configs._t(list(ss), "f16")
+        lines += [yt, f"    %v0 = ktdp.load %yt : !ktdp.access_tile<{M}x{K}xindex> -> {configs._t([M, K], 'f16')}"]
+        if tuple(ss) != (M, K):
+            lines.append(f"    %v = tensor.collapse_shape %v0 [[0, 1]] : {configs._t([M, K], 'f16')} into "
+                         f"{configs._t([M * K], 'f16')}")
+            T = configs._t([M * K], "f16")
+        else:
+            lines.append(f"    %v = arith.addf %v0, %v0 : {T}")
+        lines.append(f"    ktdp.store %v, %g : {T}, !ktdp.access_tile<{M}x{K}xindex>")
+    else:
+        lines += [f"    %v = ktdp.load %g : !ktdp.access_tile<{M}x{K}xindex> -> tensor<{M}x{K}xf16>", yt,
+                  f"    ktdp.store %v, %yt : tensor<{M}x{K}xf16>, !ktdp.access_tile<{M}x{K}xindex>"]
+    src = (f"module {{\n  func.func @iat_perm(%x_ptr: index, %i1_ptr: index, %i2_ptr: index, %y_ptr: index) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "iat_perm"
+
+
+# ---------------------------------------------------------------------------
+# memory views with SSA sizes / strides and symbolic coordinate sets
+# ---------------------------------------------------------------------------
+
+def dyn_vector_add(block=1024, cores=1, dt="f32"):
+    """out = x + y over views whose size is the i32 argument n (a symbolic
+    coordinate set bound to it), with a fixed `block`-element access tile per
+    core: positions past the n-element allocations read zero and their
+    writes are dropped (after examples/triton-ktir/vector_add_dynamic_ktir.mlir)."""
+    T = configs._t([block], dt)
+    view = lambda name, ptr: (f"    %{name} = ktdp.construct_memory_view %{ptr}, sizes: [%n], strides: [1] {{\n"
+                              f"      coordinate_set = affine_set<(d0)[s0] : (d0 >= 0, -d0 + s0 - 1 >= 0)>, "
+                              f"memory_space = #ktdp.memory_space<global>\n    }} : memref<?x{dt}>")
+    tile = lambda name, v: (f"    %{name} = ktdp.construct_access_tile %{v}[%off] {{\n"
+                            f"      access_tile_set = affine_set<(d0) : (d0 >= 0, -d0 + {block - 1} >= 0)>,\n"
+                            f"      access_tile_order = affine_map<(d0) -> (d0)>\n"
+                            f"    }} : memref<?x{dt}> -> !ktdp.access_tile<{block}xindex>")
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             f"    %cb = arith.constant {block} : index",
+             "    %off = arith.muli %core_id, %cb : index",
+             "    %n = arith.index_cast %n_elements : i32 to index",
+             view("x_view", "x_ptr"), view("y_view", "y_ptr"), view("o_view", "out_ptr"),
+             tile("xt", "x_view"), tile("yt", "y_view"), tile("ot", "o_view"),
+             f"    %x = ktdp.load %xt : !ktdp.access_tile<{block}xindex> -> {T}",
+             f"    %y = ktdp.load %yt : !ktdp.access_tile<{block}xindex> -> {T}",
+             f"    %o = arith.addf %x, %y : {T}",
+             f"    ktdp.store %o, %ot : {T}, !ktdp.access_tile<{block}xindex>"]
+    src = (f"module {{\n  func.func @add_dyn(%x_ptr: index, %y_ptr: index, %out_ptr: index, %n_elements: i32) "
+           f"attributes {{grid = [{cores}, 1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "add_dyn"
+
+
+def dyn_distributed_copy(rows=64, tile_cols=32, merge_rows=False):
+    """B = A where A is two partitions with a symbolic column extent s0 (an
+    i32 argument) and SSA row strides, composed into one distributed view;
+    B's view has SSA size and stride 2 s0 (or, with merge_rows, the two
+    partitions split the rows and share the symbolic columns).  A loop
+    with an SSA trip count walks rows x tile_cols tiles across the global
+    domain (after examples/rfc/distributed-view-copy-dynamic.mlir)."""
+    if merge_rows:
+        p0 = f"affine_set<(d0, d1)[s0] : (d0 >= 0, -d0 + {rows - 1} >= 0, d1 >= 0, -d1 + s0 - 1 >= 0)>"
+        p1 = (f"affine_set<(d0, d1)[s0] : (d0 - {rows} >= 0, -d0 + {2 * rows - 1} >= 0, d1 >= 0, "
+              f"-d1 + s0 - 1 >= 0)>")
+        bset = f"affine_set<(d0, d1)[s0] : (d0 >= 0, -d0 + {2 * rows - 1} >= 0, d1 >= 0, -d1 + s0 - 1 >= 0)>"
+        grows, bsize, bstride, ub, row_tiles = 2 * rows, f"[{2 * rows}, %s0]", "[%s0, 1]", "%s0", 2
+    else:
+        p0 = f"affine_set<(d0, d1)[s0] : (d0 >= 0, -d0 + {rows - 1} >= 0, d1 >= 0, -d1 + s0 - 1 >= 0)>"
+        p1 = f"affine_set<(d0, d1)[s0] : (d0 >= 0, -d0 + {rows - 1} >= 0, d1 - s0 >= 0, -d1 + 2*s0 - 1 >= 0)>"
+        bset = f"affine_set<(d0, d1)[s0] : (d0 >= 0, -d0 + {rows - 1} >= 0, d1 >= 0, -d1 + s0 - 1 >= 0)>"
+        grows, bsize, bstride, ub, row_tiles = rows, "[%s0x2]", "[%s0x2, 1]", "%s0x2", 1
+    tset = f"affine_set<(d0, d1) : (d0 >= 0, -d0 + {rows - 1} >= 0, d1 >= 0, -d1 + {tile_cols - 1} >= 0)>"
+    mt = f"memref<{rows}x?xf16>"
+    gt = f"memref<{grows}x?xf16>"
+    bs = f"[{rows}, %s0x2]" if not merge_rows else f"[{2 * rows}, %s0]"
+    lines = ["    %c0 = arith.constant 0 : index", "    %c1 = arith.constant 1 : index",
+             "    %c2 = arith.constant 2 : index", f"    %ct = arith.constant {tile_cols} : index",
+             f"    %crows = arith.constant {rows} : index",
+             "    %s0 = arith.index_cast %s0_in : i32 to index",
+             "    %s0x2 = arith.muli %s0, %c2 : index",
+             f"    %a0 = ktdp.construct_memory_view %a0_ptr, sizes: [{rows}, %s0], strides: [%s0, 1] {{",
+             f"      coordinate_set = {p0}, memory_space = #ktdp.memory_space<global>", f"    }} : {mt}",
+             f"    %a1 = ktdp.construct_memory_view %a1_ptr, sizes: [{rows}, %s0], strides: [%s0, 1] {{",
+             f"      coordinate_set = {p1}, memory_space = #ktdp.memory_space<global>", f"    }} : {mt}",
+             f"    %a = ktdp.construct_distributed_memory_view (%a0, %a1 : {mt}, {mt}) : {gt}",
+             f"    %b = ktdp.construct_memory_view %b_ptr, sizes: {bs}, strides: {bstride if merge_rows else '[%s0x2, 1]'} {{",
+             f"      coordinate_set = {bset}, memory_space = #ktdp.memory_space<global>", f"    }} : {gt}",
+             f"    scf.for %r = %c0 to %c{row_tiles} step %c1 {{" if merge_rows else "    scf.for %r = %c0 to %c1 step %c1 {",
+             "      %roff = arith.muli %r, %crows : index",
+             f"      scf.for %off = %c0 to {ub} step %ct {{",
+             "        %at = ktdp.construct_access_tile %a[%roff, %off] {",
+             f"          access_tile_set = {tset}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>",
+             f"        }} : {gt} -> !ktdp.access_tile<{rows}x{tile_cols}xindex>",
+             "        %bt = ktdp.construct_access_tile %b[%roff, %off] {",
+             f"          access_tile_set = {tset}, access_tile_order = affine_map<(d0, d1) -> (d0, d1)>",
+             f"        }} : {gt} -> !ktdp.access_tile<{rows}x{tile_cols}xindex>",
+             f"        %d = ktdp.load %at : !ktdp.access_tile<{rows}x{tile_cols}xindex> -> tensor<{rows}x{tile_cols}xf16>",
+             f"        ktdp.store %d, %bt : tensor<{rows}x{tile_cols}xf16>, !ktdp.access_tile<{rows}x{tile_cols}xindex>",
+             "      }", "    }"]
+    if merge_rows:
+        lines.insert(0, "    %c2r = arith.constant 2 : index")
+        lines = [ln.replace("%c2 step %c1", "%c2r step %c1") for ln in lines]
+    src = (f"module {{\n  func.func @dyn_copy(%a0_ptr: index, %a1_ptr: index, %b_ptr: index, %s0_in: i32) "
+           f"attributes {{grid = [1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "dyn_copy"

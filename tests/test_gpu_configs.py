@@ -176,6 +176,33 @@ def test_softmax_fixed_form_large_and_non_finite_rows(cols, dt):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("cols", [512, 4096])
+def test_softmax_fixed_form_wide_range_relative_error(cols, dt):
+    """Rows spanning 30 (exponentials down to e^-30, far below f16's normal
+    range): a bf16 output is within rtol 1e-2 of every nonzero reference
+    output with no absolute term (the kernel keeps f32 exponentials for
+    bf16); an f16 output is within rtol 1e-2 plus one subnormal step 2^-24
+    (its f16 exponentials lose relative precision only where the output
+    itself is subnormal)."""
+    from oracle.interp import bf16_bits
+    src, fn, kw = _cases.softmax(rows=48, cols=cols, cores=4, dt=dt)
+    rng = np.random.default_rng(21)
+    x = rng.uniform(-30.0, 0.0, (48, cols))
+    kw["x_ptr"] = x.astype(np.float16) if dt == "f16" else bf16_bits(x.astype(np.float32))
+    print(f"[softmax] wide-range rows {cols} {dt}", flush=True)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts() == {"prog": 1}
+    got, want = _half_f32(out["y_ptr"], dt).astype(np.float64), _half_f32(ref["y_ptr"], dt).astype(np.float64)
+    if dt == "bf16":
+        nz = want != 0
+        assert nz.mean() > 0.99
+        assert np.all(np.abs(got[nz] - want[nz]) <= 1e-2 * np.abs(want[nz])), \
+            np.max(np.abs(got[nz] - want[nz]) / np.abs(want[nz]))
+    else:
+        assert np.all(np.abs(got - want) <= 1e-2 * np.abs(want) + 2.0 ** -24)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("cols", [512, 4096])
 def test_rmsnorm_non_finite_and_zero_rows(cols, dt):
     """RMSNorm rows holding +inf or NaN, an all-zero row, and (bf16) values
     whose squares overflow f32: equal to the oracle bit for bit, NaN where it
@@ -288,6 +315,31 @@ def test_gemm_bf16(shape):
     ref, out, g = _run(_cases.gemm_bf16(*shape))
     assert set(g.last_plan.counts()) == {"mm"}
     np.testing.assert_allclose(bf16_from_bits(out["c_ptr"]), bf16_from_bits(ref["c_ptr"]), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("out_dt", ["f16", "bf16"])
+@pytest.mark.parametrize("pad", [3, 8])
+def test_gemm_256_block_into_wider_rows(out_dt, pad):
+    """C is a 256 x 256 view into rows of 256 + pad elements: with pad 3 the
+    rows are not 16-byte aligned, so the 256 x 256 MFMA kernel's epilogue
+    takes its direct-store path instead of the LDS-staged one (pad 8 keeps
+    the staged path); the padding columns stay untouched."""
+    M = N = 256
+    if out_dt == "f16":
+        src, fn, kw = _cases.gemm(M, N, 512, 128, 128, 64, 2, 2)
+    else:
+        src, fn, kw = _cases.gemm_bf16(M, N, 512, 128, 128, 64, 2, 2)
+    old = f"%c_view = ktdp.construct_memory_view %c_ptr, sizes: [{M}, {N}], strides: [{N}, 1]"
+    assert old in src
+    src = src.replace(old, f"%c_view = ktdp.construct_memory_view %c_ptr, sizes: [{M}, {N}], strides: [{N + pad}, 1]")
+    c = np.full((M, N + pad), 7.0, np.float16)
+    kw["c_ptr"] = c if out_dt == "f16" else np.full((M, N + pad), 0x40E0, np.uint16)   # bf16 7.0
+    ref, out, g = _run((src, fn, kw))
+    assert set(g.last_plan.counts()) == {"mm"}
+    got, want = out["c_ptr"], ref["c_ptr"]
+    np.testing.assert_array_equal(got[:, N:], want[:, N:])
+    f = (lambda x: x.astype(np.float32)) if out_dt == "f16" else bf16_from_bits
+    np.testing.assert_allclose(f(got[:, :N]), f(want[:, :N]), rtol=1e-2, atol=1e-3)
 
 
 def _plant_non_finite(a, b, inf, ninf, nan):

@@ -158,3 +158,54 @@ def test_mm_quads_xcd_blocks():
         for r in range(4):
             tl = q[128 * x + 32 * r:128 * x + 32 * r + 32, 0]
             assert len(set((mi[tl] // 2).tolist())) == 4 and len(set((ni[tl] // 2).tolist())) == 8
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_strides_injective_is_sufficient_against_brute_force(seed):
+    """Whenever the store path's test says a box is injective, no two
+    positions reach one element (brute force over small boxes); and the
+    layouts that overlap (a row tile wider than the row stride, a zero
+    stride) are reported as not injective."""
+    from ktir_cpu_amd.walker import _strides_injective
+    rng = np.random.default_rng(seed)
+    nd = int(rng.integers(1, 4))
+    shape = tuple(int(x) for x in rng.integers(1, 6, nd))
+    strides = tuple(int(x) for x in rng.integers(-3, 40, nd))
+    offs = [sum(i * s for i, s in zip(p, strides)) for p in np.ndindex(*shape)]
+    if _strides_injective(shape, strides):
+        assert len(set(offs)) == len(offs), (shape, strides)
+    assert _strides_injective((64, 32), (32, 1)) and not _strides_injective((64, 32), (16, 1))
+    assert not _strides_injective((4, 3), (0, 1)) and _strides_injective((1, 3), (0, 1))
+
+
+def test_collapse_dims_keeps_every_element_offset():
+    """A 5-d expression with a unit dim and mergeable dims compiles over <= 4
+    dims: each leaf and the destination address the same elements, in the
+    same flattened order, and linalg.index dims keep their values."""
+    from ktir_cpu_amd.program import Expr, LeafSpec
+    from ktir_cpu_amd.walker import _collapse_dims, _cstrides
+    shape = (1, 4, 2, 4, 4)
+    a = LeafSpec(0, "f32", LaneOff(0, 32), (0, 4, 16, 1, 0), 0, 1 << 20)
+    g = LeafSpec(0, "f32", LaneOff(0, 128), _cstrides(shape), 0, 1 << 20)
+    g.offsets = object()                       # an offset-list (gather) leaf
+    dest = LeafSpec(0, "f32", LaneOff(0, 128), _cstrides(shape), 0, 1 << 20)
+    e = Expr("bin", "f32", shape, [Expr("ld", "f32", shape, attr=a), Expr("ld", "f32", shape, attr=g)], 0)
+    e = Expr("bin", "f32", shape, [e, Expr("idx", "i32", shape, attr=4)], 0)
+    out = _collapse_dims(e, dest, 4)
+    assert out is not None
+    e2, d2 = out
+    assert len(e2.shape) <= 4 and int(np.prod(e2.shape)) == int(np.prod(shape))
+    pts_old = list(np.ndindex(*shape))
+    pts_new = list(np.ndindex(*e2.shape))
+    leaves = [n for n in [e2.args[0].args[0], e2.args[0].args[1]]]
+    for old, new in zip((a, g, dest), (leaves[0].attr, leaves[1].attr, d2)):
+        o = [sum(i * s for i, s in zip(p, old.strides)) for p in pts_old]
+        n = [sum(i * s for i, s in zip(p, new.strides)) for p in pts_new]
+        assert o == n
+    idx = e2.args[1]
+    assert idx.kind == "idx" and [p[idx.attr] for p in pts_new] == [p[4] for p in pts_old]
+    # a linalg.index over a merged pair blocks that merge
+    e3 = Expr("bin", "f32", (2, 3, 4, 5, 6), [Expr("idx", "i32", (2, 3, 4, 5, 6), attr=d) for d in (0, 1)], 0)
+    d3 = LeafSpec(0, "f32", LaneOff(0, 720), _cstrides((2, 3, 4, 5, 6)), 0, 1 << 20)
+    e4, _ = _collapse_dims(e3, d3, 4)
+    assert e4.shape == (2, 3, 20, 6)          # merges only until the rank fits
