@@ -9,7 +9,7 @@ dominant launch's own time gives `roofline.achieved`.  Every timed
 attention replay converts V to f16 again, as a call with a new V does; the
 figure for replays that reuse the f16 copy of an unchanged V (the plan
 tracks writes to V) is reported beside it as `v16_reuse`.  For the
-memory-bound configs `cold` times replays that each follow a 1 GiB fill, so
+memory-bound configs `cold` times replays that each follow a 1 GiB read, so
 that no input is left in L2 or the Infinity Cache.  By default the line's
 top-level fields are the gather + scatter-add config
 and `per_config` holds the same measurement for every config; each entry also
@@ -166,10 +166,11 @@ def _traffic(config, kind):
     if not t:
         return None
     pats = _LAUNCH_KERNELS.get(kind, ())
-    # the kernels of that launch that run on every replay (not the attention
-    # launch's f16 copy of V, which a replay of an unchanged V reuses)
+    # the kernels of that launch that run on every timed replay: the
+    # attention launch's f16 copy of V included, since every timed replay
+    # converts V as a call with a new V does
     b = [v["bytes"] for k, v in t.get("kernels", {}).items()
-         if any(p in k for p in pats) and v.get("every_run", True)]
+         if any(p in k for p in pats) and (v.get("every_run", True) or kind == "attn")]
     return round(sum(b)) if b else None
 
 
@@ -249,26 +250,61 @@ def _instrumented_steps(prep, steps, reuse_v16=True):
     return ms, durs
 
 
-FLUSH_BYTES = 1 << 30
+FLUSH_ROWS, FLUSH_COLS = 65536, 4096      # 1 GiB of f32 read by the flush
+
+
+def _flush_plan():
+    """A KTIR row sum over a 1 GiB f32 array (1024 cores x 64 rows of 4096):
+    replayed on the library stream it reads 1 GiB and writes 256 KB, which
+    evicts the L2 caches and MI355X's 256 MB Infinity Cache and leaves them
+    holding clean lines (a fill would leave dirty lines, whose write-back
+    the timed launch would then pay)."""
+    from ktir_cpu_amd import configs
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    rows, cols, cores = FLUSH_ROWS, FLUSH_COLS, 1024      # 1 MiB of LX per core
+    blk = rows // cores
+    T, V = configs._t([blk, cols], "f32"), configs._t([blk], "f32")
+    src = f"""module {{
+  func.func @flush(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %B = arith.constant {blk} : index
+    %r0 = arith.muli %core_id, %B : index
+    %zero = arith.constant 0.0 : f32
+{configs._view("x_view", "x_ptr", [rows, cols], [cols, 1], "f32")}
+{configs._view("y_view", "y_ptr", [rows], [1], "f32")}
+{configs._tile("xt", "x_view", ["%r0", "%c0"], [blk, cols], [rows, cols], "f32")}
+{configs._tile("yt", "y_view", ["%r0"], [blk], [rows], "f32")}
+    %x = ktdp.load %xt : !ktdp.access_tile<{blk}x{cols}xindex> -> {T}
+    %init = tensor.splat %zero : {V}
+    %s = linalg.reduce {{ arith.addf }} ins(%x : {T}) outs(%init : {V}) dimensions = [1]
+    ktdp.store %s, %yt : {V}, !ktdp.access_tile<{blk}xindex>
+    return
+  }}
+}}
+"""
+    it = KTIRInterpreter()
+    it.load(src)
+    prep = it.prepare("flush", x_ptr=np.ones((rows, cols), np.float32), y_ptr=np.zeros(rows, np.float32))
+    return it, prep
 
 
 def _cold_steps(prep, steps):
-    """K replays, each preceded (outside its own events) by a fill of a
-    1 GiB scratch buffer on the library stream, which evicts the L2 caches
-    and MI355X's 256 MB Infinity Cache: the mean ms of one replay whose
-    inputs are in HBM only."""
+    """K replays, each preceded (outside its own events, on the same stream)
+    by the flush plan: the mean ms of one replay whose inputs come from HBM
+    only."""
     from ktir_cpu_amd import runtime as rt
-    scratch = rt.DeviceBuffer(FLUSH_BYTES)
+    _it, flush = _flush_plan()
     plan = prep.plan
     evs = [(rt.Event(), rt.Event()) for _ in range(steps)]
-    for s_, (a, b) in enumerate(evs):
-        scratch.memset(s_ & 0xFF)
+    for a, b in evs:
+        flush.plan.run()
         a.record()
         plan.run()
         b.record()
     rt.sync()
     ms = float(np.mean([a.elapsed_ms(b) for a, b in evs]))
-    scratch.free()
+    del flush, _it
     return ms
 
 
@@ -329,8 +365,9 @@ def measure(name, steps, warmup, with_cpu):
                              "value": round(units / (reuse_ms * 1e-3) / scale, 3)}} if reuse_ms else {}),
            **({"cold": {"ms_per_step": round(cold_ms, 6), "value": round(units / (cold_ms * 1e-3) / scale, 3),
                         "frac": round(units / (cold_ms * 1e-3) / scale / peak, 4),
-                        "how": f"each replay after a {FLUSH_BYTES >> 20} MiB fill (outside the timed region) "
-                               "that evicts L2 and the 256 MB Infinity Cache"}} if cold_ms else {}),
+                        "how": f"each replay after a row sum that reads {FLUSH_ROWS * FLUSH_COLS * 4 >> 20} MiB "
+                               "(outside the timed region, same stream), which evicts L2 and the 256 MB "
+                               "Infinity Cache"}} if cold_ms else {}),
            "host": {"prepare_s": round(prepare_s, 3), "h2d_s": round(h2d_s, 4), "d2h_s": round(d2h_s, 4),
                     "execute_function_s": round(e2e_s, 3),
                     "execute_function_rate": round(units / e2e_s / scale, 4)}}
@@ -368,9 +405,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--collect-traffic", metavar="DIR",
                     help="build profiles/traffic.json from rocprofv3 FETCH_SIZE/WRITE_SIZE runs under DIR")
+    ap.add_argument("--collect-counters", metavar="DIR",
+                    help="build profiles/counters.json from rocprofv3 --pmc runs (COUNTER_PASSES) under DIR")
     args = ap.parse_args()
     if args.collect_traffic:
         collect_traffic(args.collect_traffic)
+        return
+    if args.collect_counters:
+        for r in collect_counters(args.collect_counters):
+            print(json.dumps(r))
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this backend runs on one GPU; multi-GPU runs are not part of this build",
@@ -398,6 +441,65 @@ def main():
     if args.config == "all":
         out["per_config"] = results
     print(json.dumps(out))
+
+
+COUNTER_PASSES = {
+    "mfma": ["SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES",
+             "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "GRBM_GUI_ACTIVE"],
+    "lds": ["SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS",
+            "GRBM_GUI_ACTIVE"],
+}
+SIMDS, XCDS, PEAK_GHZ = 1024, 8, 2.4
+
+
+def collect_counters(root):
+    """profiles/counters.md from rocprofv3 --pmc runs under
+    ROOT/counters_<config>_<pass>/ (passes in COUNTER_PASSES), for the MFMA
+    kernels of the gemm and attention configs: MFMA busy (the MfmaUtil
+    expression: SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs), VALU
+    co-executing with MFMA, instruction counts, LDS bank conflicts per active
+    LDS cycle, and the shader clock (GRBM_GUI_ACTIVE per XCD over the
+    dispatch's duration), beside the MFMA fraction of 2.5 PF scaled to that
+    clock."""
+    import csv
+    import glob
+    rows = []
+    for config, kern, flops in (("gemm", "mm_mfma_256", 2 * 8192 ** 3),
+                                ("attention", "attn_pp", 4 * 4 * 32 * 8192 * 8192 * 128 // 2)):
+        vals, durs = {}, {}
+        for pas in COUNTER_PASSES:
+            for fn in glob.glob(os.path.join(root, f"counters_{config}_{pas}", "**", "*counter_collection.csv"),
+                                recursive=True):
+                with open(fn) as f:
+                    for r in csv.DictReader(f):
+                        if kern not in r.get("Kernel_Name", ""):
+                            continue
+                        name = r["Kernel_Name"]
+                        vals.setdefault((name, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+                        if r["Counter_Name"] == "GRBM_GUI_ACTIVE":
+                            durs.setdefault(name, []).append(
+                                (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) * 1e-9)
+        for name in sorted(durs):
+            v = {c: float(np.median(x)) for (n, c), x in vals.items() if n == name}
+            # the MFMA pass and the LDS pass each give GRBM_GUI_ACTIVE; both
+            # runs' dispatches are pooled for the clock
+            t = float(np.median(durs[name]))
+            ghz = v["GRBM_GUI_ACTIVE"] / XCDS / t / 1e9
+            tf = flops / t / 1e12
+            rows.append({
+                "config": config, "kernel": name, "dispatches": len(durs[name]), "duration_us": t * 1e6,
+                "clock_ghz": ghz, "tflops": tf, "frac_2_5pf": tf / MFMA_F16_TFLOPS,
+                "frac_at_clock": tf / (MFMA_F16_TFLOPS * ghz / PEAK_GHZ),
+                "mfma_busy": v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / (v["GRBM_GUI_ACTIVE"] / XCDS * SIMDS),
+                "coexec_of_busy": v.get("SQ_VALU_MFMA_COEXEC_CYCLES", 0) / max(v.get("SQ_VALU_MFMA_BUSY_CYCLES", 1), 1),
+                "mfma_insts": v.get("SQ_INSTS_MFMA"), "valu_insts": v.get("SQ_INSTS_VALU"),
+                "trans_insts": v.get("SQ_INSTS_VALU_TRANS_F32"),
+                "lds_conflict_rate": v.get("SQ_LDS_BANK_CONFLICT", 0) / max(v.get("SQ_LDS_IDX_ACTIVE", 1), 1),
+                "lds_bank_conflict": v.get("SQ_LDS_BANK_CONFLICT"), "lds_insts": v.get("SQ_INSTS_LDS")})
+    path = os.path.join(ROOT, "profiles", "counters.json")
+    with open(path, "w") as fh:
+        json.dump(rows, fh, indent=1)
+    return rows
 
 
 def collect_traffic(root):

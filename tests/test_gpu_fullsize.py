@@ -69,6 +69,31 @@ def test_softmax_full_size_sampled_cores():
     assert np.all(np.abs(s - 1) < 0.02), (s.min(), s.max())
 
 
+def test_softmax_full_size_against_float64():
+    """All 32 768 rows at 4096 columns against float64 softmax of the same f16
+    inputs: within rtol 1e-2 / atol 1e-3 everywhere, and, in f16 ulps of the
+    float64 result rounded to f16, at most 2 apart on every output in f16's
+    normal range (the kernel keeps exp(x - max) in f16 and multiplies by a
+    correctly rounded 1 / sum).  Records the worst errors at this size."""
+    cfg = bench.CONFIGS["softmax"]()
+    out, g = _gpu(cfg)
+    assert g.last_plan.counts() == {"prog": 1}
+    x = cfg["kw"]["x_ptr"].astype(np.float64)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    ref = e / e.sum(axis=1, keepdims=True)
+    got = out["y_ptr"].astype(np.float64)
+    worst = float(np.max(np.abs(got - ref) / (1e-3 + 1e-2 * np.abs(ref))))
+    normal = ref >= 2.0 ** -14
+    r16 = ref.astype(np.float16)
+    ulps = np.abs(out["y_ptr"].view(np.int16).astype(np.int32) - r16.view(np.int16).astype(np.int32))
+    rel = np.abs(got - ref)[normal] / ref[normal]
+    print(f"softmax full size: worst |err| / (atol + rtol |ref|) = {worst:.4f}; outputs in f16's normal range: "
+          f"max {int(ulps[normal].max())} f16 ulps from float64 rounded to f16, max relative error {rel.max():.3e}; "
+          f"all outputs: max {int(ulps.max())} ulps", flush=True)
+    assert worst <= 1.0
+    assert ulps[normal].max() <= 2
+
+
 def test_rmsnorm_full_size_sampled_cores_bit_exact():
     cfg = bench.CONFIGS["rmsnorm"]()
     out, g = _gpu(cfg)
