@@ -1039,6 +1039,9 @@ def _b_reshape(op, toks, aliases):
     into = _idx(toks, "into", kind="ident")
     if into < 0:
         into = _idx(toks, "to", kind="ident")
+    if into < 0 and c >= 0:
+        # tensor.reshape %src(%shape) : (T, tensor<Nxindex>) -> T'
+        into = _idx(toks, "->", start=c + 1)
     op.operand_types = _types_after(toks, c + 1) if c >= 0 else []
     op.result_types = _types_after(toks, into + 1) if into >= 0 else []
     if not op.result_types:
@@ -1081,8 +1084,10 @@ def _b_slice(op, toks, aliases):
                 vals.append(int(p[0].text))
         statics.append(vals)
     c = _last_top(toks, ":")
-    to = _idx(toks, "to", kind="ident")
-    into = _idx(toks, "into", kind="ident")
+    # the type separator after the colon (insert_slice also has the
+    # `%src into %dst` before it)
+    to = _idx(toks, "to", start=c + 1, kind="ident")
+    into = _idx(toks, "into", start=c + 1, kind="ident")
     sep = to if to >= 0 else into
     op.operand_types = _types_after(toks, c + 1)
     op.result_types = _types_after(toks, sep + 1) if sep >= 0 else op.operand_types[-1:]

@@ -1121,3 +1121,68 @@ def dyn_distributed_copy(rows=64, tile_cols=32, merge_rows=False):
     src = (f"module {{\n  func.func @dyn_copy(%a0_ptr: index, %a1_ptr: index, %b_ptr: index, %s0_in: i32) "
            f"attributes {{grid = [1]}} {{\n" + "\n".join(lines) + "\n    return\n  }\n}\n")
     return src, "dyn_copy"
+
+
+# ---------------------------------------------------------------------------
+# tensor.extract_slice / insert_slice / generate / from_elements / reshape
+# ---------------------------------------------------------------------------
+
+def tensor_ops(cores=4, R=4, C=16):
+    """Each core loads its R x C f32 block X of x and stores:
+    a = X[1:3, 2:10] (extract_slice, static);
+    b = X[k, 1:14:3] (extract_slice, dynamic row k = core mod R, stride 3,
+        rank-reduced to 5 elements);
+    c = zeros with a inserted at [2, k2 : k2 + 8] (insert_slice, dynamic
+        column k2 = 2 (core mod 4));
+    g = (i >= j) as f16 over R x C (tensor.generate yielding cmpi);
+    r = X reshaped to (R C / 32) x 32 through a from_elements shape tensor."""
+    T = configs._t([R, C], "f32")
+    rr = R * C // 32
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %cR = arith.constant {R} : index",
+             "    %c2 = arith.constant 2 : index", "    %c4 = arith.constant 4 : index",
+             f"    %crr = arith.constant {rr} : index", "    %c32 = arith.constant 32 : index",
+             "    %row0 = arith.muli %core_id, %cR : index",
+             "    %k = arith.remui %core_id, %cR : index",
+             "    %m4 = arith.remui %core_id, %c4 : index",
+             "    %k2 = arith.muli %m4, %c2 : index",
+             "    %zero = arith.constant 0.0 : f32"]
+    outs = {"x": ([R * cores, C], "f32"), "a": ([2 * cores, 8], "f32"), "b": ([5 * cores], "f32"),
+            "c": ([R * cores, C], "f32"), "g": ([R * cores, C], "f16"), "r": ([rr * cores, 32], "f32")}
+    for n, (shape, dt) in outs.items():
+        lines.append(configs._view(f"{n}_view", f"{n}_ptr", shape, list(_cstr(shape)), dt))
+    lines += [configs._tile("xt", "x_view", ["%row0", "%c0"], [R, C], [R * cores, C], "f32"),
+              f"    %x = ktdp.load %xt : !ktdp.access_tile<{R}x{C}xindex> -> {T}",
+              f"    %a = tensor.extract_slice %x[1, 2] [2, 8] [1, 1] : {T} to tensor<2x8xf32>",
+              f"    %b = tensor.extract_slice %x[%k, 1] [1, 5] [1, 3] : {T} to tensor<5xf32>",
+              f"    %z = tensor.splat %zero : {T}",
+              f"    %c = tensor.insert_slice %a into %z[2, %k2] [2, 8] [1, 1] : tensor<2x8xf32> into {T}",
+              "    %g = tensor.generate {",
+              "    ^bb0(%i: index, %j: index):",
+              "      %cmp = arith.cmpi sge, %i, %j : index",
+              "      tensor.yield %cmp : i1",
+              f"    }} : tensor<{R}x{C}xf16>",
+              "    %shape = tensor.from_elements %crr, %c32 : tensor<2xindex>",
+              f"    %r = tensor.reshape %x(%shape) : ({T}, tensor<2xindex>) -> tensor<{rr}x32xf32>",
+              "    %a0 = arith.muli %core_id, %c2 : index",
+              "    %c5 = arith.constant 5 : index",
+              "    %b0 = arith.muli %core_id, %c5 : index",
+              "    %r0 = arith.muli %core_id, %crr : index",
+              configs._tile("at", "a_view", ["%a0", "%c0"], [2, 8], [2 * cores, 8], "f32"),
+              configs._tile("bt", "b_view", ["%b0"], [5], [5 * cores], "f32"),
+              configs._tile("ct", "c_view", ["%row0", "%c0"], [R, C], [R * cores, C], "f32"),
+              configs._tile("gt", "g_view", ["%row0", "%c0"], [R, C], [R * cores, C], "f16"),
+              configs._tile("rt", "r_view", ["%r0", "%c0"], [rr, 32], [rr * cores, 32], "f32"),
+              "    ktdp.store %a, %at : tensor<2x8xf32>, !ktdp.access_tile<2x8xindex>",
+              "    ktdp.store %b, %bt : tensor<5xf32>, !ktdp.access_tile<5xindex>",
+              f"    ktdp.store %c, %ct : {T}, !ktdp.access_tile<{R}x{C}xindex>",
+              f"    ktdp.store %g, %gt : tensor<{R}x{C}xf16>, !ktdp.access_tile<{R}x{C}xindex>",
+              f"    ktdp.store %r, %rt : tensor<{rr}x32xf32>, !ktdp.access_tile<{rr}x32xindex>"]
+    args = ", ".join(f"%{n}_ptr: index" for n in outs)
+    src = (f"module {{\n  func.func @tensor_ops({args}) attributes {{grid = [{cores}, 1]}} {{\n"
+           + "\n".join(lines) + "\n    return\n  }\n}\n")
+    rng = np.random.default_rng(17)
+    kw = {f"{n}_ptr": (rng.standard_normal(shape).astype(np.float32) if n == "x"
+              else np.zeros(shape, np.float16 if dt == "f16" else np.float32)) for n, (shape, dt) in outs.items()}
+    return src, "tensor_ops", kw

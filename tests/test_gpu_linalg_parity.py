@@ -128,3 +128,52 @@ def test_batch_matmul_random_within_tolerance(dt):
     C0 = rng.standard_normal(c).astype(np.float32)
     got, ref = _both(src, fn, "c_ptr", a_ptr=A, b_ptr=B, c_ptr=C0)
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-3)
+
+
+def test_tensor_slices_generate_from_elements_reshape_bit_exact():
+    from tests.test_oracle_linalg_pins import tensor_ops_brute
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    src, fn, kw = C.tensor_ops()
+    o = OracleInterpreter()
+    o.load(src)
+    ref = o.execute_function(fn, **{k: v.copy() for k, v in kw.items()})
+    g = KTIRInterpreter()
+    g.load(src)
+    got = g.execute_function(fn, **kw)
+    print(fn, g.last_plan.mode, g.last_plan.counts(), flush=True)
+    for k, v in tensor_ops_brute(kw).items():
+        np.testing.assert_array_equal(got[k], ref[k], err_msg=k)
+        np.testing.assert_array_equal(got[k], v, err_msg=k)
+
+
+@pytest.mark.parametrize("rows,cols,rblk", [(16, 256, 4), (64, 16, 16), (64, 512, 8)])
+def test_softmax_rows_that_expose_the_broadcast_axis(rows, cols, rblk):
+    """The oracle's closed-form softmax case on the GPU: exact where the
+    closed form is exact (1 / k at the top entries, 0 elsewhere)."""
+    from tests.test_oracle_linalg_pins import broadcast_softmax_rows
+    src, fn, kw = C.softmax(rows=rows, cols=cols, cores=4, rblk=rblk)
+    kw["x_ptr"] = broadcast_softmax_rows(rows, cols).astype(np.float16)
+    got, ref = _both(src, fn, "y_ptr", **kw)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,cols,rblk", [(16, 512, 4), (64, 16, 16)])
+def test_rmsnorm_constant_rows_column_weights_bit_exact(dt, rows, cols, rblk):
+    from oracle.interp import bf16_bits
+    c = np.array([(-1) ** r * 0.25 * (r % 16 + 1) * (1 + r // 16) for r in range(rows)])
+    x = np.repeat(c[:, None], cols, axis=1)
+    w = np.linspace(0.5, 1.5, cols)
+    src, fn, kw = C.rmsnorm(rows=rows, cols=cols, cores=4, rblk=rblk, dt=dt)
+    if dt == "f16":
+        kw["x_ptr"], kw["w_ptr"] = x.astype(np.float16), w.astype(np.float16)
+    else:
+        kw["x_ptr"], kw["w_ptr"] = bf16_bits(x.astype(np.float32)), bf16_bits(w.astype(np.float32))
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    o = OracleInterpreter()
+    o.load(src)
+    ref = o.execute_function(fn, **{k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in kw.items()})["y_ptr"]
+    g = KTIRInterpreter()
+    g.load(src)
+    got = g.execute_function(fn, **kw)["y_ptr"]
+    np.testing.assert_array_equal(got, ref)

@@ -165,3 +165,92 @@ def test_oracle_batch_matmul_exact(out_dt):
     got = _run(src, fn, a_ptr=A, b_ptr=B, c_ptr=C0)["c_ptr"]
     want = np.einsum("bij,bjk->bik", A.astype(np.int64), B.astype(np.int64)) + C0.astype(np.int64)
     np.testing.assert_array_equal(got, want)
+
+
+def broadcast_softmax_rows(rows=16, cols=256):
+    """Rows that make a wrong broadcast visible: row r holds r + 1 entries
+    equal to its base and the rest 30 below it; the bases are -150, -50, 50,
+    150 in turn, so the maximum of another row subtracted from this one
+    overflows exp (inf / inf = NaN), and another row's sum gives the wrong
+    fraction.  The exact result is 1 / (r + 1) at the r + 1 top entries and
+    e^-30 / (r + 1) (0 in f16) elsewhere."""
+    x = np.full((rows, cols), -30.0)
+    for r in range(rows):
+        x[r, np.arange(min(r + 1, cols)) * 7 % cols] = 0.0
+        x[r] += -150.0 + 100.0 * (r % 4)
+    return x
+
+
+@pytest.mark.parametrize("rows,cols,rblk", [(16, 256, 4), (64, 16, 16)])
+def test_oracle_softmax_config_closed_form_pins_broadcast(rows, cols, rblk):
+    """The softmax config kernel (two row reductions broadcast back along
+    dimension 1 by linalg.broadcast) against the closed form; the square
+    16 x 16 blocks are where a broadcast along the wrong axis would not fail
+    on shape and would transpose silently."""
+    x = broadcast_softmax_rows(rows, cols).astype(np.float16)
+    src, fn, kw = C.softmax(rows=rows, cols=cols, cores=4, rblk=rblk)
+    kw["x_ptr"] = x
+    got = _run(src, fn, **kw)["y_ptr"].astype(np.float64)
+    for r in range(rows):
+        top = np.zeros(cols, bool)
+        top[np.arange(min(r + 1, cols)) * 7 % cols] = True
+        np.testing.assert_array_equal(got[r, top], np.float16(1.0 / top.sum()))
+        np.testing.assert_array_equal(got[r, ~top], 0.0)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,cols,rblk", [(16, 512, 4), (64, 16, 16)])
+def test_oracle_rmsnorm_config_closed_form_pins_broadcast(dt, rows, cols, rblk):
+    """The RMSNorm config kernel on rows that are each one constant c_r
+    (a different one per row) with a weight that varies by column: every
+    output is c_r w_j / sqrt(c_r^2 + eps), within one ulp of the output type.
+    The mean of squares is exact here (equal terms, pairwise halving), so a
+    broadcast of the row scale or of w along the wrong axis fails."""
+    from oracle.interp import bf16_bits, bf16_from_bits
+    c = np.array([(-1) ** r * 0.25 * (r % 16 + 1) * (1 + r // 16) for r in range(rows)])
+    w = np.linspace(0.5, 1.5, cols)
+    x = np.repeat(c[:, None], cols, axis=1)
+    src, fn, kw = C.rmsnorm(rows=rows, cols=cols, cores=4, rblk=rblk, dt=dt)
+    if dt == "f16":
+        kw["x_ptr"], kw["w_ptr"] = x.astype(np.float16), w.astype(np.float16)
+        cq, wq = kw["x_ptr"][:, 0].astype(np.float64), kw["w_ptr"].astype(np.float64)
+    else:
+        kw["x_ptr"], kw["w_ptr"] = bf16_bits(x.astype(np.float32)), bf16_bits(w.astype(np.float32))
+        cq, wq = bf16_from_bits(kw["x_ptr"][:, 0]).astype(np.float64), bf16_from_bits(kw["w_ptr"]).astype(np.float64)
+    got = _run(src, fn, **kw)["y_ptr"]
+    want = cq[:, None] * wq[None, :] / np.sqrt(cq[:, None] ** 2 + 1e-6)
+    if dt == "f16":
+        g16, w16 = got, want.astype(np.float16)
+        d = np.abs(g16.view(np.int16).astype(np.int32) - w16.view(np.int16).astype(np.int32))
+    else:
+        w16 = bf16_bits(want.astype(np.float32))
+        d = np.abs(got.view(np.int16).astype(np.int32) - w16.view(np.int16).astype(np.int32))
+    assert d.max() <= 1, d.max()
+
+
+def tensor_ops_brute(kw, cores=4):
+    """The tensor_ops kernel's outputs by NumPy slicing, per core (the
+    reference's semantics, dialects/tensor_ops.py:133-359)."""
+    X = kw["x_ptr"]
+    want = {k: np.zeros_like(v) for k, v in kw.items() if k != "x_ptr"}
+    i, j = np.meshgrid(np.arange(4), np.arange(16), indexing="ij")
+    for c in range(cores):
+        Xc = X[4 * c:4 * c + 4]
+        k, k2 = c % 4, 2 * (c % 4)
+        want["a_ptr"][2 * c:2 * c + 2] = Xc[1:3, 2:10]
+        want["b_ptr"][5 * c:5 * c + 5] = Xc[k, 1:14:3]
+        want["c_ptr"][4 * c + 2:4 * c + 4, k2:k2 + 8] = Xc[1:3, 2:10]
+        want["g_ptr"][4 * c:4 * c + 4] = (i >= j).astype(np.float16)
+        want["r_ptr"][2 * c:2 * c + 2] = Xc.reshape(2, 32)
+    return want
+
+
+def test_oracle_tensor_slices_generate_from_elements_reshape():
+    """extract_slice (static; dynamic offset with stride 3, rank-reduced),
+    insert_slice at a dynamic offset, generate (the reference's 2-d cmpi
+    case, tests/test_dialects_exec.py:1700-1716), from_elements feeding
+    reshape, each against NumPy slicing."""
+    src, fn, kw = C.tensor_ops()
+    got = _run(src, fn, **kw)
+    for k, v in tensor_ops_brute(kw).items():
+        np.testing.assert_array_equal(got[k], v, err_msg=k)

@@ -170,3 +170,19 @@ def test_oracle_powf_and_fma():
     # exactly a * a + c = 2^-24, but a * a = 1 + 2^-11 + 2^-24 is a tie that
     # rounds to 1 + 2^-11 in f32 first, so unfused it is 0
     np.testing.assert_array_equal(got, np.zeros(512, np.float32))
+
+
+@pytest.mark.parametrize("op,fn", [("math.ceil", math.ceil), ("math.floor", math.floor)])
+def test_oracle_ceil_floor_against_math(op, fn):
+    x = T.float_cast_operands(n=1024, seed=17)
+    x = x[np.isfinite(x)]
+    got = _run([f"%r = {op} %a : {{T_f32}}"], ["f32"], "f32", [x[:1024 // 4 * 4]], cores=1)
+    want = np.array([float(fn(v)) for v in x[:len(got)].tolist()], np.float64)
+    np.testing.assert_array_equal(got.astype(np.float64), np.where(want == 0, 0.0, want))
+
+
+def test_oracle_absi_against_python_abs():
+    """|x| wrapped to int32 (|INT_MIN| stays INT_MIN)."""
+    a, _ = T.int_operands("arith.addi", n=1024, seed=19)
+    got = _run(["%r = math.absi %a : {T_i32}"], ["i32"], "i32", [a])
+    np.testing.assert_array_equal(got.astype(np.int64), np.array([T.wrap32(abs(v)) for v in a.tolist()]))
