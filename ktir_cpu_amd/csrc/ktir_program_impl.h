@@ -162,8 +162,10 @@ __device__ __forceinline__ float cast_val(float x, int src, int dst) {
   if (fs) {
     if (dst == KTIR_I1) return __int_as_float(x != 0.f);
     // NaN and values int32 cannot hold convert to INT_MIN (NumPy's astype on
-    // x86-64, cvttss2si)
-    int i = (x != x || !(x < 2147483648.f && x >= -2147483648.f)) ? INT_MIN : (int)x;
+    // x86-64, cvttss2si): |x| < 2^31 (0x4f000000) on the magnitude bits, which
+    // NaN and infinities fail, or x exactly -2^31
+    const uint32_t u = __float_as_uint(x);
+    int i = ((u & 0x7fffffffu) < 0x4f000000u) ? (int)x : INT_MIN;
     if (dst == KTIR_I8) i = (int8_t)i;
     if (dst == KTIR_I16) i = (int16_t)i;
     return __int_as_float(i);
