@@ -3,7 +3,9 @@
 `python bench.py [--config NAME|all] [--steps K] [--warmup W] [--no-cpu]`
 prints ONE JSON line.  A step is one replay of the recorded launch plan of a
 config's KTIR kernel over inputs already resident in HBM (the host IR walk
-and the host<->device copies are outside the timed region).  Timing uses HIP
+and the host<->device copies are outside the timed region).  Untimed
+warm-up replays (at least W, and at least 0.5 s of them unless W is 0) come
+first, so the GPU's clocks have settled when timing starts.  Timing uses HIP
 events on the library's stream, with an event after every launch, so the
 dominant launch's own time gives `roofline.achieved`.  Every timed
 attention replay converts V to f16 again, as a call with a new V does; the
@@ -251,6 +253,7 @@ def _instrumented_steps(prep, steps, reuse_v16=True):
 
 
 FLUSH_ROWS, FLUSH_COLS = 65536, 4096      # 1 GiB of f32 read by the flush
+WARMUP_S = 0.5                            # least warm-up time per workload
 
 
 def _flush_plan():
@@ -321,8 +324,16 @@ def measure(name, steps, warmup, with_cpu):
     prep = interp.prepare(cfg["fn"], **cfg["kw"])          # copies in, host walk, first launch
     prepare_s = time.perf_counter() - t0
     plan = prep.plan
-    for _ in range(warmup):
+    # at least W replays and at least WARMUP_S seconds of them (none for
+    # W = 0, as the counter runs ask): the GPU's clocks take tens of
+    # milliseconds of load to settle, and a few replays of a
+    # millisecond-scale launch end before they do
+    t0, k = time.perf_counter(), 0
+    while k < warmup or (warmup and time.perf_counter() - t0 < WARMUP_S):
         prep.run()
+        k += 1
+        if k % 4 == 0:
+            rt.sync()
     rt.sync()
     # attention converts V to f16 on every timed replay, as a call whose V is
     # new does; the replays that reuse the copy of an unchanged V are
@@ -426,6 +437,7 @@ def main():
     out = {
         "metric": "achieved HBM GB/s & MFMA TFLOP/s per KTIR kernel (% of roofline) vs NumPy",
         "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "warmup_min_s": WARMUP_S,
         "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": h["dtype"], "data": "synthetic (seed 42)",
         "config": {"workload": h["workload"], "launches_per_step": h["launches_per_step"],
@@ -536,13 +548,15 @@ def collect_traffic(root):
         (f, nf), (w, _) = per_kernel(config, "FETCH_SIZE"), per_kernel(config, "WRITE_SIZE")
         if not f:
             continue
-        # the launch of a replay: the kernels dispatched on every run of the
-        # plan; one dispatched less often (the attention launch's f16 copy of
-        # V, made by a run whose V is new, skipped by replays) is listed apart
+        # the launch of a timed replay: the kernels dispatched on every run
+        # of the plan, plus the attention launch's f16 copy of V (made by a
+        # run whose V is new and skipped by a replay that reuses it; every
+        # timed replay converts V, as a call with a new V does)
         top = max(nf.values())
         ks = {k: {"fetch_kib": f[k], "write_kib": w.get(k, 0.0), "dispatches": nf[k], "every_run": nf[k] == top,
                   "bytes": f[k] * 1024 * fscale + w.get(k, 0.0) * 1024 * wscale} for k in f}
-        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for v in ks.values() if v["every_run"]),
+        out["configs"][config] = {"traffic_bytes": sum(v["bytes"] for k, v in ks.items()
+                                                       if v["every_run"] or "attn_v16" in k),
                                   "kernels": ks}
     path = os.path.join(ROOT, "profiles", "traffic.json")
     with open(path, "w") as fh:
