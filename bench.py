@@ -113,6 +113,33 @@ def _rmsnorm():
                 workload=f"rmsnorm {rows}x{cols} f16 grid={cores} rows/step={rblk}")
 
 
+def _softmax_extract():
+    from ktir_cpu_amd import configs
+    rows, cols, cores = 32768, 4096, 512
+    rng = np.random.default_rng(42)
+    x = (rng.standard_normal((rows, cols), dtype=np.float32) * 2).astype(np.float16)
+    kw = dict(x_ptr=x, y_ptr=np.zeros_like(x), n_rows=rows)
+    return dict(src=configs.softmax_extract(rows, cols, cores), fn="softmax_fwd", kw=kw, cores=cores,
+                bytes=4 * rows * cols, flops=5 * rows * cols, bound="hbm",
+                dtype="f16 (the reference example's f16 max, exp, sum and divide)",
+                workload=f"softmax {rows}x{cols} f16 grid={cores}, one row per loop step, row max and sum "
+                         f"read by tensor.extract (the reference's triton-ktir softmax_fwd form)")
+
+
+def _rmsnorm_extract():
+    from ktir_cpu_amd import configs
+    rows, cols, cores = 32768, 4096, 512
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((rows, cols), dtype=np.float32).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, (1, cols)).astype(np.float16)
+    kw = dict(x_ptr=x, w_ptr=w, y_ptr=np.zeros_like(x), n_rows=rows, eps=1e-3)
+    return dict(src=configs.rmsnorm_extract(rows, cols, cores), fn="rmsnorm_fwd", kw=kw, cores=cores,
+                bytes=4 * rows * cols + 2 * cols, flops=4 * rows * cols, bound="hbm",
+                dtype="f16 (the reference example's f16 squares, sum and scalar math)",
+                workload=f"rmsnorm {rows}x{cols} f16 grid={cores}, one row per loop step, sum of squares read "
+                         f"by tensor.extract, then scalar divf / addf / rsqrt (the reference's latency-example form)")
+
+
 def _gemm():
     from ktir_cpu_amd import configs
     M = N = K = 8192
@@ -147,7 +174,8 @@ def _attention():
 
 
 CONFIGS = {"vector_add": _vector_add, "vector_add_4096": _vector_add_4096, "copy": _copy, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
-           "gemm": _gemm, "attention": _attention}
+           "gemm": _gemm, "attention": _attention, "softmax_extract": _softmax_extract,
+           "rmsnorm_extract": _rmsnorm_extract}
 
 
 # kernels that make up each kind of launch (the HIP kernel names)
@@ -403,7 +431,8 @@ def measure(name, steps, warmup, with_cpu):
 
 
 HEADLINE = "gather"
-PER_CONFIG = ["vector_add", "gather", "softmax", "rmsnorm", "gemm", "attention", "vector_add_4096"]
+PER_CONFIG = ["vector_add", "gather", "softmax", "rmsnorm", "gemm", "attention", "softmax_extract", "rmsnorm_extract",
+              "vector_add_4096"]
 
 
 def main():

@@ -266,6 +266,87 @@ def rmsnorm(rows: int = 32768, cols: int = 4096, cores: int = 512, rblk: int = 8
 """
 
 
+def _strided_rows(fn, args, rows, cols, cores, body):
+    """A kernel whose core c handles rows c, c + cores, ... one (1 x cols)
+    row per loop step, as the reference's triton-ktir examples do."""
+    return f"""module {{
+  func.func @{fn}({args}) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %step = arith.constant {cores} : index
+{_view("x_view", "x_ptr", [rows, cols], [cols, 1], "f16")}
+{_view("y_view", "y_ptr", [rows, cols], [cols, 1], "f16")}
+{body}
+  }}
+}}
+"""
+
+
+def softmax_extract(rows: int = 4096, cols: int = 1024, cores: int = 32) -> str:
+    """Softmax in the form of the reference's triton-ktir softmax_fwd
+    example: f16 math, and the row max and row sum read out of a
+    tensor<1xf16> by tensor.extract, then spread over the row by
+    tensor.splat (a scalar per row held on the device)."""
+    T, V = _t([1, cols], "f16"), _t([1], "f16")
+    at = f"!ktdp.access_tile<1x{cols}xindex>"
+    body = f"""    %neg_inf = arith.constant 0xFC00 : f16
+    %zero = arith.constant 0.0 : f16
+    scf.for %row = %core_id to %n_rows step %step : index {{
+{_tile("x_acc", "x_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      %x = ktdp.load %x_acc : {at} -> {T}
+      %mx_init = tensor.splat %neg_inf : {V}
+      %mx = linalg.reduce {{ arith.maxnumf }} ins(%x : {T}) outs(%mx_init : {V}) dimensions = [1]
+      %m = tensor.extract %mx[%c0] : {V}
+      %mb = tensor.splat %m : {T}
+      %d = arith.subf %x, %mb : {T}
+      %e = math.exp %d : {T}
+      %s_init = tensor.splat %zero : {V}
+      %s = linalg.reduce {{ arith.addf }} ins(%e : {T}) outs(%s_init : {V}) dimensions = [1]
+      %sv = tensor.extract %s[%c0] : {V}
+      %sb = tensor.splat %sv : {T}
+      %p = arith.divf %e, %sb : {T}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      ktdp.store %p, %y_acc : {T}, {at}
+      scf.yield
+    }}
+    return"""
+    return _strided_rows("softmax_fwd", "%x_ptr: index, %y_ptr: index, %n_rows: index", rows, cols, cores, body)
+
+
+def rmsnorm_extract(rows: int = 4096, cols: int = 1024, cores: int = 32) -> str:
+    """RMSNorm in the form of the reference's latency examples: f16 math,
+    the row's sum of squares read by tensor.extract, then scalar f16 ops
+    (divide by the row length, add eps, rsqrt) before tensor.splat spreads
+    the result over the row."""
+    T, V = _t([1, cols], "f16"), _t([1], "f16")
+    at = f"!ktdp.access_tile<1x{cols}xindex>"
+    body = f"""{_view("w_view", "w_ptr", [1, cols], [cols, 1], "f16")}
+{_tile("w_acc", "w_view", ["%c0", "%c0"], [1, cols], [1, cols], "f16")}
+    %w = ktdp.load %w_acc : {at} -> {T}
+    %zero = arith.constant 0.0 : f16
+    %nf = arith.constant {float(cols)} : f16
+    scf.for %row = %core_id to %n_rows step %step : index {{
+{_tile("x_acc", "x_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      %x = ktdp.load %x_acc : {at} -> {T}
+      %sq = arith.mulf %x, %x : {T}
+      %ss_init = tensor.splat %zero : {V}
+      %ss = linalg.reduce {{ arith.addf }} ins(%sq : {T}) outs(%ss_init : {V}) dimensions = [1]
+      %sv = tensor.extract %ss[%c0] : {V}
+      %ms = arith.divf %sv, %nf : f16
+      %mse = arith.addf %ms, %eps : f16
+      %rs = math.rsqrt %mse : f16
+      %rb = tensor.splat %rs : {T}
+      %xn = arith.mulf %x, %rb : {T}
+      %y = arith.mulf %xn, %w : {T}
+{_tile("y_acc", "y_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      ktdp.store %y, %y_acc : {T}, {at}
+      scf.yield
+    }}
+    return"""
+    return _strided_rows("rmsnorm_fwd", "%x_ptr: index, %w_ptr: index, %y_ptr: index, %n_rows: index, %eps: f16",
+                         rows, cols, cores, body)
+
+
 # ---------------------------------------------------------------------------
 # 4. GEMM
 # ---------------------------------------------------------------------------

@@ -30,6 +30,17 @@ __device__ __forceinline__ float round_bf16(float x) {
 
 __device__ __forceinline__ float round_f16(float x) { return (float)(_Float16)x; }
 
+// x * y in f32, for a product that may be rounded to f16 next.  The
+// compiler turns an f32 product narrowed to f16 into one mixed-precision
+// fused multiply-add with a +0 addend (v_fma_mix), which gives +0 for a
+// product of -0: the empty asm keeps the product a separate f32 result, so
+// the narrowing sees -0 and keeps its sign.
+__device__ __forceinline__ float mul_keep(float x, float y) {
+  float r = __fmul_rn(x, y);
+  __asm__ volatile("" : "+v"(r));
+  return r;
+}
+
 // Round a float result to the KTIR dtype it is declared with.
 __device__ __forceinline__ float round_to(float x, int dt) {
   if (dt == KTIR_F16) return round_f16(x);

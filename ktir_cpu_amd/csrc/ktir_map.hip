@@ -142,7 +142,7 @@ __device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t i
   switch (op) {
     case KTIR_OP_ADDF: EACH(round_to(__fadd_rn(x, y), dt))
     case KTIR_OP_SUBF: EACH(round_to(__fsub_rn(x, y), dt))
-    case KTIR_OP_MULF: EACH(round_to(__fmul_rn(x, y), dt))
+    case KTIR_OP_MULF: EACH(round_to(mul_keep(x, y), dt))
     case KTIR_OP_DIVF: EACH(round_to(__fdiv_rn(x, y), dt))
     case KTIR_OP_CAST: EACH(cast_val(x, in.aux, dt))
     case KTIR_OP_CONST: EACH(__int_as_float(in.imm))
@@ -215,7 +215,7 @@ __device__ __forceinline__ void map_binop(int op, int dt, bool swap, const float
   switch (op) {
     case KTIR_OP_ADDF: MB(__fadd_rn(x, y))
     case KTIR_OP_SUBF: MB(__fsub_rn(x, y))
-    case KTIR_OP_MULF: MB(__fmul_rn(x, y))
+    case KTIR_OP_MULF: MB(mul_keep(x, y))
     case KTIR_OP_DIVF: MB(__fdiv_rn(x, y))
   }
 #undef MB

@@ -40,7 +40,7 @@ __device__ __forceinline__ float binop_f(int op, int dt, float x, float y) {
   switch (op) {
     case KTIR_OP_ADDF: r = __fadd_rn(x, y); break;
     case KTIR_OP_SUBF: r = __fsub_rn(x, y); break;
-    case KTIR_OP_MULF: r = __fmul_rn(x, y); break;
+    case KTIR_OP_MULF: r = mul_keep(x, y); break;
     case KTIR_OP_DIVF: r = __fdiv_rn(x, y); break;
     case KTIR_OP_REMF: r = py_fmod(x, y); break;
     case KTIR_OP_MAXIMUMF: r = (x != x || y != y) ? __int_as_float(0x7fc00000) : fmaxf(x, y); break;
@@ -399,7 +399,7 @@ __device__ __forceinline__ float binop_f_simple(int op, int dt, float x, float y
   switch (op) {
     case KTIR_OP_ADDF: r = __fadd_rn(x, y); break;
     case KTIR_OP_SUBF: r = __fsub_rn(x, y); break;
-    case KTIR_OP_MULF: r = __fmul_rn(x, y); break;
+    case KTIR_OP_MULF: r = mul_keep(x, y); break;
     case KTIR_OP_DIVF: r = __fdiv_rn(x, y); break;
     case KTIR_OP_MAXIMUMF: r = (x != x || y != y) ? __int_as_float(0x7fc00000) : fmaxf(x, y); break;
     case KTIR_OP_MINIMUMF: r = (x != x || y != y) ? __int_as_float(0x7fc00000) : fminf(x, y); break;

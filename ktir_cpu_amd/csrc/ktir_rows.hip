@@ -124,14 +124,21 @@ static int row_op_reads(int op) {
   return 1;
 }
 
-// Chain ops the kernel implements (straight-line code per op keeps the kernel
-// small): f32 arithmetic and f32 -> f16 / bf16 / f32 rounding casts.
+// Chain ops the kernels implement (straight-line code per op keeps them
+// small): float arithmetic, and f32 -> f16 / bf16 / f32 rounding casts.  An
+// f16 / bf16 op is kept as its f32 op followed by a rounding cast to its
+// type (the general kernels' arithmetic: f32, then rounded), except a narrow
+// rsqrt, whose root is rounded before the division.
+static bool chain_dt(int dt) { return dt == KTIR_F32 || dt == KTIR_F16 || dt == KTIR_BF16; }
+
 static bool chain_unary(const ktir_instr_t& x) {
   switch (x.op) {
-    case KTIR_OP_NEGF: case KTIR_OP_ABSF: case KTIR_OP_EXP: case KTIR_OP_SQRT: case KTIR_OP_RSQRT:
+    case KTIR_OP_NEGF: case KTIR_OP_ABSF: case KTIR_OP_EXP: case KTIR_OP_SQRT:
+      return chain_dt(x.dt);
+    case KTIR_OP_RSQRT:
       return x.dt == KTIR_F32;
     case KTIR_OP_CAST:
-      return x.aux == KTIR_F32 && (x.dt == KTIR_F32 || x.dt == KTIR_F16 || x.dt == KTIR_BF16);
+      return x.aux == KTIR_F32 && chain_dt(x.dt);
   }
   return false;
 }
@@ -139,10 +146,29 @@ static bool chain_unary(const ktir_instr_t& x) {
 static bool chain_binary(const ktir_instr_t& x) {
   switch (x.op) {
     case KTIR_OP_ADDF: case KTIR_OP_SUBF: case KTIR_OP_MULF: case KTIR_OP_DIVF: case KTIR_OP_MAXIMUMF:
-    case KTIR_OP_MINIMUMF:
-      return x.dt == KTIR_F32;
+    case KTIR_OP_MINIMUMF: case KTIR_OP_MAXNUMF: case KTIR_OP_MINNUMF:
+      return chain_dt(x.dt);
   }
   return false;
+}
+
+// a pass plan of f32 folds combined by the arithmetic or NaN-propagating
+// ops, with no NaN-ignoring min / max and no exact division among its chain
+// ops: the only plans the fixed-form kernels take.  The row-wave kernel
+// takes the others in its FOLDX instantiations (folds of any op, rounded to
+// f16 / bf16 at every level where the fold is of that type).
+static bool plan_plain(const RcPlan& R) {
+  for (int i = 0; i < R.n_steps; ++i) {
+    const RcStep& S = R.steps[i];
+    if (S.kind != 1) continue;
+    if (S.end == 0 && (S.fold_dt != KTIR_F32 || S.fold_op == KTIR_OP_MAXNUMF || S.fold_op == KTIR_OP_MINNUMF))
+      return false;
+    for (int k = 0; k < S.n_ops; ++k) {
+      const RcOp& o = S.ops[k];
+      if (o.op == KTIR_OP_MAXNUMF || o.op == KTIR_OP_MINNUMF || (o.op == KTIR_OP_DIVF && o.aux)) return false;
+    }
+  }
+  return true;
 }
 
 static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
@@ -226,7 +252,15 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
       } else if (chain_unary(x)) {
         if (kind[x.a] == K_LEAF && !start(x.a)) return false;
         if (x.a != acc) return false;
-        if (!add(RcOp{x.op, x.dt, (int8_t)x.aux, 0, 0, 0, {0, 0}})) return false;
+        if (x.op == KTIR_OP_CAST || x.dt == KTIR_F32) {
+          if (!add(RcOp{x.op, x.dt, (int8_t)x.aux, 0, 0, 0, {0, 0}})) return false;
+        } else {
+          // a narrow op: its f32 op, then (unless exact, as a sign change is) the rounding
+          if (!add(RcOp{x.op, KTIR_F32, 0, 0, 0, 0, {0, 0}})) return false;
+          if (x.op != KTIR_OP_NEGF && x.op != KTIR_OP_ABSF &&
+              !add(RcOp{KTIR_OP_CAST, x.dt, KTIR_F32, 0, 0, 0, {0, 0}}))
+            return false;
+        }
         acc = x.dst;
       } else if (chain_binary(x)) {
         int a = x.a, b = x.b;
@@ -239,7 +273,9 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
             return false;
           }
         }
-        RcOp o{x.op, x.dt, 0, 0, 0, 0, {0, 0}};
+        // a narrow op: its f32 op (a division correctly rounded), then the rounding
+        const bool narrow = x.dt != KTIR_F32;
+        RcOp o{x.op, KTIR_F32, (int8_t)(narrow && x.op == KTIR_OP_DIVF), 0, 0, 0, {0, 0}};
         if (a == acc && b == acc) {
           o.kind = 3;
         } else {
@@ -257,6 +293,10 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
           }
         }
         if (!add(o)) return false;
+        // min / max give one of their operands: nothing to round
+        if (narrow && x.op != KTIR_OP_MAXIMUMF && x.op != KTIR_OP_MINIMUMF && x.op != KTIR_OP_MAXNUMF &&
+            x.op != KTIR_OP_MINNUMF && !add(RcOp{KTIR_OP_CAST, x.dt, KTIR_F32, 0, 0, 0, {0, 0}}))
+          return false;
         acc = x.dst;
       } else if (x.op == KTIR_OP_RED || x.op == KTIR_OP_ST) {
         if (kind[x.a] == K_LEAF && acc < 0 && !start(x.a)) return false;
@@ -282,7 +322,8 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
       if (pc >= P.n_instr || P.instr[pc].op != KTIR_OP_FOLD) return false;
       const ktir_instr_t& f = P.instr[pc];
       if (f.dst < 0 || f.dst >= KTIR_NREG || f.aux >= KTIR_OP_ADDI) return false;
-      if (f.aux != KTIR_OP_ADDF && f.aux != KTIR_OP_MULF && f.aux != KTIR_OP_MAXIMUMF && f.aux != KTIR_OP_MINIMUMF)
+      if (f.aux != KTIR_OP_ADDF && f.aux != KTIR_OP_MULF && f.aux != KTIR_OP_MAXIMUMF && f.aux != KTIR_OP_MINIMUMF &&
+          f.aux != KTIR_OP_MAXNUMF && f.aux != KTIR_OP_MINNUMF)
         return false;
       if (f.dt != KTIR_F32 && f.dt != KTIR_F16 && f.dt != KTIR_BF16) return false;
       S.fold_op = (int8_t)f.aux;
@@ -308,14 +349,14 @@ static bool analyze_rows(const ktir_prog_t& P, RcPlan& R) {
     if (S.kind != 1) continue;
     const RcOp* o = S.ops;
     if (S.n_ops >= 2 && o[0].op == KTIR_OP_SUBF && o[0].kind == 1 && !o[0].swap && o[1].op == KTIR_OP_EXP &&
-        o[1].kind == 0) {
+        o[1].kind == 0 && o[0].dt == KTIR_F32 && o[1].dt == KTIR_F32) {
       S.head = 1;
       if (last_subexp >= 0 && R.steps[last_subexp].src == S.src && R.steps[last_subexp].ops[0].idx == o[0].idx) {
         R.steps[last_subexp].save = 1;
         S.reuse = 1;
       }
       last_subexp = i;
-    } else if (S.n_ops >= 1 && o[0].op == KTIR_OP_MULF && o[0].kind == 3) {
+    } else if (S.n_ops >= 1 && o[0].op == KTIR_OP_MULF && o[0].kind == 3 && o[0].dt == KTIR_F32) {
       S.head = 2;
     }
     // so does a fold into the subtracted register
@@ -431,7 +472,11 @@ __device__ __forceinline__ float div_by(float x, float s, float r) {
 }
 
 // one chain op over the E chain values; the opcode and operand kind are
-// uniform, so both are dispatched once outside the element loops
+// uniform, so both are dispatched once outside the element loops.  Ops are
+// f32: an f16 / bf16 op of the program arrives here as its f32 op and a
+// rounding cast (analyze_rows), and a division marked exact (aux 1) is
+// the correctly rounded one, so that the rounding to the narrow type sees
+// the f32 result the general kernels compute.
 template <int E>
 __device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, const float (&c0)[E],
                                          const float (&c1)[E]) {
@@ -459,9 +504,12 @@ __device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, c
       case KTIR_OP_MULF: RC_S(__fmul_rn(x, s))
       case KTIR_OP_MAXIMUMF: RC_S(maxnan(x, s))
       case KTIR_OP_MINIMUMF: RC_S(minnan(x, s))
+      case KTIR_OP_MAXNUMF: RC_S(fmaxf(x, s))
+      case KTIR_OP_MINNUMF: RC_S(fminf(x, s))
       case KTIR_OP_SUBF: if (o.swap) RC_S(__fsub_rn(s, x)) else RC_S(__fsub_rn(x, s))
       case KTIR_OP_DIVF:
         if (o.swap) RC_S(__fdiv_rn(s, x))
+        if (o.aux) RC_S(__fdiv_rn(x, s))
         {
           const float r = __fdiv_rn(1.f, s);
           const float as = fabsf(s);
@@ -505,6 +553,8 @@ __device__ __forceinline__ void apply_op(const RcOp o, float (&v)[E], float s, c
     case KTIR_OP_DIVF: RC_B(__fdiv_rn(l, r))
     case KTIR_OP_MAXIMUMF: RC_B(maxnan(l, r))
     case KTIR_OP_MINIMUMF: RC_B(minnan(l, r))
+    case KTIR_OP_MAXNUMF: RC_B(fmaxf(l, r))
+    case KTIR_OP_MINNUMF: RC_B(fminf(l, r))
   }
 #undef RC_B
 }
@@ -514,8 +564,10 @@ template <int OP, int DT>
 __device__ __forceinline__ float fold_op(float x, float y) {
   float r;
   if (OP == KTIR_OP_ADDF) r = __fadd_rn(x, y);
-  else if (OP == KTIR_OP_MULF) r = __fmul_rn(x, y);
+  else if (OP == KTIR_OP_MULF) r = DT == KTIR_F32 ? __fmul_rn(x, y) : mul_keep(x, y);
   else if (OP == KTIR_OP_MAXIMUMF) return maxnan(x, y);
+  else if (OP == KTIR_OP_MAXNUMF) return fmaxf(x, y);   // an operand's value: no rounding
+  else if (OP == KTIR_OP_MINNUMF) return fminf(x, y);
   else return minnan(x, y);
   return DT == KTIR_F32 ? r : (DT == KTIR_F16 ? round_f16(r) : round_bf16(r));
 }
@@ -564,6 +616,8 @@ __device__ __forceinline__ float fold_group(float (&v)[E], int op, int dt, int t
     case KTIR_OP_ADDF: return fold_group_d<E, KTIR_OP_ADDF>(v, dt, tpr, xch);
     case KTIR_OP_MULF: return fold_group_d<E, KTIR_OP_MULF>(v, dt, tpr, xch);
     case KTIR_OP_MAXIMUMF: return fold_group_d<E, KTIR_OP_MAXIMUMF>(v, dt, tpr, xch);
+    case KTIR_OP_MAXNUMF: return fold_group_d<E, KTIR_OP_MAXNUMF>(v, dt, tpr, xch);
+    case KTIR_OP_MINNUMF: return fold_group_d<E, KTIR_OP_MINNUMF>(v, dt, tpr, xch);
     default: return fold_group_d<E, KTIR_OP_MINIMUMF>(v, dt, tpr, xch);
   }
 }
@@ -774,6 +828,20 @@ __device__ __forceinline__ float fold_rt(int op, float x, float y) {
   }
 }
 
+// a fold combine of any fold op in the fold's dtype (sums and products
+// rounded to f16 / bf16 at every level, as the reference's tree fold on a
+// narrow tile does; a min / max is one of its operands)
+__device__ __forceinline__ float fold_any(int op, int dt, float x, float y) {
+  switch (op) {
+    case KTIR_OP_ADDF: return round_to(__fadd_rn(x, y), dt);
+    case KTIR_OP_MULF: return round_to(mul_keep(x, y), dt);
+    case KTIR_OP_MAXIMUMF: return maxnan(x, y);
+    case KTIR_OP_MINIMUMF: return minnan(x, y);
+    case KTIR_OP_MAXNUMF: return fmaxf(x, y);
+    default: return fminf(x, y);
+  }
+}
+
 // Pairs k = c NB + q (c < B) of a cached row in LDS: v[2c], v[2c + 1] are the
 // elements 128 k + 2 l + {0, 1}.
 template <int B, int NB>
@@ -827,6 +895,8 @@ __device__ __forceinline__ void rw_binary(int op, bool swap, float (&v)[E], cons
     case KTIR_OP_DIVF: RW_B(__fdiv_rn(x, y))
     case KTIR_OP_MAXIMUMF: RW_B(maxnan(x, y))
     case KTIR_OP_MINIMUMF: RW_B(minnan(x, y))
+    case KTIR_OP_MAXNUMF: RW_B(fmaxf(x, y))
+    case KTIR_OP_MINNUMF: RW_B(fminf(x, y))
   }
 #undef RW_B
 }
@@ -845,6 +915,39 @@ __device__ __forceinline__ void rw_fold_step(float (&v)[2 * B]) {
   }
 }
 
+// the same halving tree for any fold op and dtype (op and dtype dispatched
+// once; a min / max needs no rounding, so its dtype does not matter)
+template <int B, int OP, int DT>
+__device__ __forceinline__ void rw_fold_step_t(float (&v)[2 * B]) {
+#pragma unroll
+  for (int h = B / 2; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int c = 0; c < h; ++c) {
+      v[2 * c] = fold_op<OP, DT>(v[2 * c], v[2 * (c + h)]);
+      v[2 * c + 1] = fold_op<OP, DT>(v[2 * c + 1], v[2 * (c + h) + 1]);
+    }
+  }
+}
+
+template <int B, int OP>
+__device__ __forceinline__ void rw_fold_step_dt(float (&v)[2 * B], int dt) {
+  if (dt == KTIR_F16) rw_fold_step_t<B, OP, KTIR_F16>(v);
+  else if (dt == KTIR_BF16) rw_fold_step_t<B, OP, KTIR_BF16>(v);
+  else rw_fold_step_t<B, OP, KTIR_F32>(v);
+}
+
+template <int B>
+__device__ __forceinline__ void rw_fold_exact(float (&v)[2 * B], int op, int dt) {
+  switch (op) {
+    case KTIR_OP_ADDF: rw_fold_step_dt<B, KTIR_OP_ADDF>(v, dt); return;
+    case KTIR_OP_MULF: rw_fold_step_dt<B, KTIR_OP_MULF>(v, dt); return;
+    case KTIR_OP_MAXIMUMF: rw_fold_step_t<B, KTIR_OP_MAXIMUMF, KTIR_F32>(v); return;
+    case KTIR_OP_MINIMUMF: rw_fold_step_t<B, KTIR_OP_MINIMUMF, KTIR_F32>(v); return;
+    case KTIR_OP_MAXNUMF: rw_fold_step_t<B, KTIR_OP_MAXNUMF, KTIR_F32>(v); return;
+    default: rw_fold_step_t<B, KTIR_OP_MINNUMF, KTIR_F32>(v); return;
+  }
+}
+
 // One pass of a row.  Lane l holds the K pairs k of its row (elements
 // 128 k + 2 l + {0, 1}) as NB steps of B pairs, step q holding k = c NB + q:
 // the whole step's values are in registers, so every op of the pass is
@@ -852,7 +955,7 @@ __device__ __forceinline__ void rw_fold_step(float (&v)[2 * B]) {
 // tree over c (the tree's levels over the high bits of k), the NB <= 4 step
 // roots by its levels over the low bits of k (the bits of q), then lanes
 // l ^ 32 .. l ^ 1, then the two elements of the pair.  A store pass writes every pair.
-template <int K>
+template <int K, bool FOLDX>
 __device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const uint8_t* s0, int d0,
                                          const uint8_t* s1, int d1, const RowRegs& rr, const RwOut& SL,
                                          bool out_in_range, int l) {
@@ -861,6 +964,7 @@ __device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const
   static_assert(NB <= 4, "at most four steps per row");
   const bool fold = S.end == 0;
   const int fop = S.fold_op;
+  const int fdt = S.fold_dt;
   const int n_ops = S.n_ops;
   const uint8_t* sp = S.src ? s1 : s0;
   const int dp = S.src ? d1 : d0;
@@ -919,11 +1023,15 @@ __device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const
       }
       continue;
     }
-    switch (fop) {
-      case KTIR_OP_ADDF: rw_fold_step<B, KTIR_OP_ADDF>(v); break;
-      case KTIR_OP_MULF: rw_fold_step<B, KTIR_OP_MULF>(v); break;
-      case KTIR_OP_MAXIMUMF: rw_fold_step<B, KTIR_OP_MAXIMUMF>(v); break;
-      default: rw_fold_step<B, KTIR_OP_MINIMUMF>(v); break;
+    if constexpr (FOLDX) {
+      rw_fold_exact<B>(v, fop, fdt);
+    } else {
+      switch (fop) {
+        case KTIR_OP_ADDF: rw_fold_step<B, KTIR_OP_ADDF>(v); break;
+        case KTIR_OP_MULF: rw_fold_step<B, KTIR_OP_MULF>(v); break;
+        case KTIR_OP_MAXIMUMF: rw_fold_step<B, KTIR_OP_MAXIMUMF>(v); break;
+        default: rw_fold_step<B, KTIR_OP_MINIMUMF>(v); break;
+      }
     }
     ra[q] = v[0];
     rb[q] = v[1];
@@ -934,17 +1042,17 @@ __device__ __forceinline__ float rw_pass(const RwHead& S, const RcOp* ops, const
   for (int h = NB / 2; h >= 1; h >>= 1) {
 #pragma unroll
     for (int q = 0; q < h; ++q) {
-      ra[q] = fold_rt(fop, ra[q], ra[q + h]);
-      rb[q] = fold_rt(fop, rb[q], rb[q + h]);
+      ra[q] = FOLDX ? fold_any(fop, fdt, ra[q], ra[q + h]) : fold_rt(fop, ra[q], ra[q + h]);
+      rb[q] = FOLDX ? fold_any(fop, fdt, rb[q], rb[q + h]) : fold_rt(fop, rb[q], rb[q + h]);
     }
   }
   float a = ra[0], b = rb[0];
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) {
-    a = fold_rt(fop, a, __shfl_xor(a, s));
-    b = fold_rt(fop, b, __shfl_xor(b, s));
+    a = FOLDX ? fold_any(fop, fdt, a, __shfl_xor(a, s)) : fold_rt(fop, a, __shfl_xor(a, s));
+    b = FOLDX ? fold_any(fop, fdt, b, __shfl_xor(b, s)) : fold_rt(fop, b, __shfl_xor(b, s));
   }
-  return fold_rt(fop, a, b);
+  return FOLDX ? fold_any(fop, fdt, a, b) : fold_rt(fop, a, b);
 }
 
 // Position of row r: its lane (core) and its index in each outer dim.  Rows,
@@ -1079,7 +1187,7 @@ __device__ __forceinline__ void rw_row_exec(const PL& SP, const ktir_instr_t in,
 template <int K, int NQ>
 constexpr int rw_waves() { return (K == 32 && NQ == 8) || (K == 16 && NQ == 4) || K <= 8 ? 3 : 2; }
 
-template <int K, int NQ>
+template <int K, int NQ, bool FOLDX = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(rw_waves<K, NQ>()))) void prog_rowwave(const RwPlan Pk, int64_t total_rows) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ RwPlan SP;
@@ -1144,7 +1252,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(rw_waves<K, 
         SL = RwOut{L.ptr, L.lo, L.hi, rw_row_base(L, pos), L.dtype};
         in_range = SL.base >= SL.lo && SL.base + inner <= SL.hi;
       }
-      const float f = rw_pass<K>(S, SP.steps[si].ops, s0, d0, s1, d1, rr, SL, in_range, l);
+      const float f = rw_pass<K, FOLDX>(S, SP.steps[si].ops, s0, d0, s1, d1, rr, SL, in_range, l);
       if (S.end == 0) rr.set(S.dst, __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f))));
     }
     // the row's LDS reads are done (LDS operations of a wavefront complete in order)
@@ -1170,12 +1278,12 @@ int64_t row_grid_limit(int64_t blocks) {
 // One resident wavefront per row stream: as many workgroups as the device
 // holds at once (so no second, partial round of workgroups), each taking an
 // equal share of the rows.
-template <int K, int NQ>
+template <int K, int NQ, bool FOLDX = false>
 static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows) {
   static int cached_lds = -1, cached_resident = 0;
   if (cached_lds != lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prog_rowwave<K, NQ>, 64, lds_bytes) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prog_rowwave<K, NQ, FOLDX>, 64, lds_bytes) != hipSuccess ||
         hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 || cus < 1) {
       per_cu = 1;
@@ -1186,13 +1294,21 @@ static void launch_rowwave(const RwPlan& W, int lds_bytes, int64_t rows) {
   }
   const int64_t per_block = (rows + cached_resident - 1) / cached_resident;
   const int64_t blocks = row_grid_limit((rows + per_block - 1) / per_block);
-  hipLaunchKernelGGL((prog_rowwave<K, NQ>), dim3((unsigned)blocks), dim3(64), lds_bytes, stream(), W, rows);
+  hipLaunchKernelGGL((prog_rowwave<K, NQ, FOLDX>), dim3((unsigned)blocks), dim3(64), lds_bytes, stream(), W, rows);
 }
 
 template <int K>
-static bool pick_nq(int nq, const RwPlan& W, int lds_bytes, int64_t rows) {
+static bool pick_nq(int nq, const RwPlan& W, int lds_bytes, int64_t rows, bool foldx) {
   // K/4 chunks: one 16-bit slot; K/2: one f32 slot or two 16-bit slots; K: more (at most 16 chunks)
   constexpr int A = K / 4 > 0 ? K / 4 : 1, B = K / 2, C = K;
+  if (foldx) {
+    // plans with f16 / bf16 or NaN-ignoring folds: one or two row slots
+    if (nq <= A) { launch_rowwave<K, A, true>(W, lds_bytes, rows); return true; }
+    if constexpr (B <= 16) {
+      if (nq <= B) { launch_rowwave<K, B, true>(W, lds_bytes, rows); return true; }
+    }
+    return false;
+  }
   if (nq <= A) { launch_rowwave<K, A>(W, lds_bytes, rows); return true; }
   if constexpr (B <= 16) {
     if (nq <= B) { launch_rowwave<K, B>(W, lds_bytes, rows); return true; }
@@ -1218,7 +1334,7 @@ static RwLeaf rw_leaf(const ktir_prog_t& P, int leaf) {
   return o;
 }
 
-static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t rows, int64_t inner) {
+static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t rows, int64_t inner, bool foldx) {
   if (inner % 128 || inner / 128 < 4 || inner / 128 > 64) return false;
   if (rows > INT32_MAX) return false;   // row positions use 32-bit arithmetic
   for (int d = 0; d < P.ndim; ++d)
@@ -1250,7 +1366,7 @@ static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t ro
     const RcStep& S = R.steps[i];
     RwStep& D = W.steps[i];
     D.kind = S.kind;
-    if (S.kind == 1 && S.end == 0 && S.fold_dt != KTIR_F32) return false;
+    if (S.kind == 1 && S.end == 0 && S.fold_dt != KTIR_F32 && !foldx) return false;
     if (S.kind == 0 || S.kind == 2) D.ins = P.instr[S.pc];
     if (S.kind == 2 || (S.kind == 1 && S.end == 1)) {
       if (n_leaves == 4) return false;
@@ -1269,11 +1385,11 @@ static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t ro
   W.n_leaves = n_leaves;
   if (off > 64 * 1024 || nq > 16) return false;
   switch (inner / 128) {
-    case 4: return pick_nq<4>(nq, W, off, rows);
-    case 8: return pick_nq<8>(nq, W, off, rows);
-    case 16: return pick_nq<16>(nq, W, off, rows);
-    case 32: return pick_nq<32>(nq, W, off, rows);
-    case 64: return pick_nq<64>(nq, W, off, rows);
+    case 4: return pick_nq<4>(nq, W, off, rows, foldx);
+    case 8: return pick_nq<8>(nq, W, off, rows, foldx);
+    case 16: return pick_nq<16>(nq, W, off, rows, foldx);
+    case 32: return pick_nq<32>(nq, W, off, rows, foldx);
+    case 64: return pick_nq<64>(nq, W, off, rows, foldx);
   }
   return false;
 }
@@ -1740,7 +1856,9 @@ static bool rf_invariant(const ktir_prog_t& P, const ktir_leaf_t& L) {
   return inv;
 }
 
-static bool rf_op(const RcOp& o, int op, int kind) { return o.op == op && o.dt == KTIR_F32 && o.kind == kind; }
+static bool rf_op(const RcOp& o, int op, int kind) {
+  return o.op == op && o.dt == KTIR_F32 && o.kind == kind && (op != KTIR_OP_DIVF || o.aux == 0);
+}
 
 // Match the pass plan against the two fixed forms and launch; false leaves
 // the program to the general row kernels.
@@ -1851,8 +1969,9 @@ bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
   }
   RcPlan R;
   if (!analyze_rows(P, R)) return false;
-  if (try_launch_rowfix(P, R, rows, inner)) return true;
-  if (try_launch_rowwave(P, R, rows, inner)) return true;
+  const bool plain = plan_plain(R);
+  if (plain && try_launch_rowfix(P, R, rows, inner)) return true;
+  if (try_launch_rowwave(P, R, rows, inner, !plain)) return true;
   // threads per row and elements per thread: n = tpr * E, E in {2..32}, tpr in {32..256}
   int tpr = (int)(inner / 16);
   if (tpr > 256) tpr = 256;

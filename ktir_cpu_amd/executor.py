@@ -15,9 +15,11 @@ Reordering work across lanes is only valid when lanes do not communicate
 through HBM.  The walk therefore *records* launches and HBM accesses first;
 ``verify`` checks that no two lanes that the reference orders differently
 touch the same bytes with a store involved.  If they might, or if the
-function needs device data to continue the walk (``tensor.extract``), the
-executor falls back to running one core at a time, in core-id order, still
-entirely on the GPU, which is the reference's order by construction.
+function needs device data to continue the walk (an integer read from a
+tile by ``tensor.extract``, or a scalar read from a tile and then used as
+an address, a bound or a condition), the executor falls back to running one
+core at a time, in core-id order, still entirely on the GPU, which is the
+reference's order by construction.
 """
 
 from __future__ import annotations
@@ -318,6 +320,29 @@ class Tile:
         for s in self.shape:
             n *= s
         return n * rt.ELEM_BYTES.get(self.dtype, 4)
+
+
+class DevScalar:
+    """A per-lane float scalar that stays on the device: the one element of
+    `t`, a tile of shape () or (1,), read from tile data by tensor.extract
+    or a reduction over every axis (reference dialects/tensor_ops.py:88-102,
+    dialects/linalg_ops.py:197-240).  tensor.extract gives the reference a
+    NumPy scalar of the tile's type: `t.dtype` is that type ("f16" or "f32";
+    a bf16 element is held as f32), which decides how later scalar ops
+    round.  A reduction over every axis gives it a Python float (`weak`):
+    `t` holds its value exactly, and ops that would compute on it in
+    float64 read it on the host.  Host code that needs the value reads it
+    (Executor.get_value)."""
+
+    __slots__ = ("t", "weak")
+
+    def __init__(self, t: Tile, weak: bool = False):
+        self.t = t
+        self.weak = weak
+
+    @property
+    def dtype(self):
+        return self.t.dtype
 
 
 @dataclass

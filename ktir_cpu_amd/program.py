@@ -404,10 +404,12 @@ def compile_program(root: Expr, lanes: int, dest: LeafSpec) -> Tuple[rt.Prog, li
         if u[0] == "rows":
             todo = [n for n in u[1] if id(n) not in regs]
             if todo:
-                ids = {id(n) for n in todo}
-                _emit_block(b, todo, regs, ids, row_leaf)
-                for n in todo:
-                    row_held[id(n)] = regs[id(n)]
+                # row values a later unit reads stay held; the rest (constants,
+                # intermediate steps of a scalar chain) free their registers
+                # at their last use here
+                keep = {id(n) for n in todo if id(n) in needed_after[ui]}
+                held = _emit_block(b, todo, regs, keep, row_leaf)
+                row_held.update(held)
         else:
             elem, f = u[1], u[2]
             start = b.emit(O["ELEM"])

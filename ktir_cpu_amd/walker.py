@@ -16,8 +16,8 @@ import numpy as np
 
 from . import runtime as rt
 from .affine import AffineMap, AffineSet, Box, evaluate
-from .executor import (Access, Alloc, Arena, ATile, DistATile, DistView, IATile, Instances, Lanes, NeedEager, Plan, Pool, Tile,
-                       View, _launch, verify)
+from .executor import (Access, Alloc, Arena, ATile, DevScalar, DistATile, DistView, IATile, Instances, Lanes, NeedEager,
+                       Plan, Pool, Tile, View, _launch, verify)
 from .ir import IRFunction, Operation, Region
 from .program import CompileError, Expr, LaneOff, LeafSpec, compile_program, is_float, round_host, topo
 
@@ -105,6 +105,31 @@ def _elem_of(t) -> Optional[str]:
 
 def _is_scalar(v) -> bool:
     return isinstance(v, np.ndarray)
+
+
+def _narrow_scalar(v, target, op_name) -> np.ndarray:
+    """A scalar float cast (reference ops/arith_ops.py:38-87): a value that
+    is already of the target type is kept; a finite value that becomes
+    infinite raises OverflowError."""
+    a = np.asarray(v)
+    if a.dtype == target:
+        return a
+    with np.errstate(over="ignore"):
+        r = a.astype(target)
+    bad = np.isinf(r) & np.isfinite(a.astype(np.float64))
+    if np.any(bad):
+        raise OverflowError(f"{op_name}: {a[bad].flat[0]} overflows {np.dtype(target).name}")
+    return r
+
+
+def _scalar_kind(v) -> Optional[str]:
+    """The NumPy float type of a scalar operand ("f16" / "f32"), or None for
+    one that acts as a Python number (a constant, a float64 value, a
+    reduction's Python float) and takes the other operand's type."""
+    if isinstance(v, DevScalar):
+        return None if v.weak else v.dtype
+    dt = np.asarray(v).dtype
+    return {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32"}.get(dt)
 
 
 class _Yield:
@@ -353,6 +378,8 @@ def take_value(v, idx: np.ndarray):
         return v[idx]
     if isinstance(v, Tile):
         return Tile(remap_lanes(v.e, idx))
+    if isinstance(v, DevScalar):
+        return DevScalar(Tile(remap_lanes(v.t.e, idx)), v.weak)
     if isinstance(v, (View, ATile, IATile, DistView, DistATile, _Future)):
         return v.take(idx)
     if isinstance(v, tuple):
@@ -531,7 +558,11 @@ class Executor:
             if not unch:
                 self.lx_used -= t.nbytes()
 
-    def get_value(self, name, peek=False):
+    def get_value(self, name, peek=False, dev=False):
+        """The value of SSA name `name` on the current lanes.  A scalar that
+        lives on the device (DevScalar) is returned as it is only to callers
+        that keep it there (`dev`); any other caller gets its per-lane host
+        values."""
         for fr in reversed(self.frames):
             if name in fr.vals:
                 v = fr.vals[name]
@@ -541,8 +572,24 @@ class Executor:
                     self._release(v)
                 if fr.level != len(self.levels) - 1:
                     v = take_value(v, self._idx_to(fr.level))
+                if isinstance(v, DevScalar) and not dev:
+                    v = self.host_scalar(v)
                 return v
         raise KeyError(f"Value '{name}' not found")
+
+    def host_scalar(self, v: DevScalar) -> np.ndarray:
+        """Per-lane host values of a device scalar, as the NumPy scalar type
+        the reference holds.  Reading device data needs the work recorded so
+        far to have run: a lockstep walk starts again core by core (or, where
+        cores meet at a ring reduce, launches from here on as it walks)."""
+        if not self.eager:
+            if not self.collective:
+                raise NeedEager("a scalar read from tile data is used on the host")
+            self._go_eager()
+        data = self.read_tile(v.t).reshape(self.L)
+        if v.weak:
+            return data.astype(np.float64)
+        return data.astype(np.float16 if v.dtype == "f16" else np.float32)
 
     def has_value(self, name) -> bool:
         return any(name in fr.vals for fr in self.frames)
@@ -560,7 +607,7 @@ class Executor:
         lat_ops = None
         if self.lat is not None:
             # operands as they were before the op (reference interpreter.py:209-217)
-            lat_ops = [self.get_value(n, peek=True) if self.has_value(n) else None for n in op.operands]
+            lat_ops = [self.get_value(n, peek=True, dev=True) if self.has_value(n) else None for n in op.operands]
             self._lat_mem = None
         if h is not None:
             res = h(op)
@@ -1378,6 +1425,11 @@ class Executor:
         the reference's `np.float16(scalar)` coercion when float_scalar)."""
         if isinstance(v, Tile):
             return self.broadcast_to(v, shape).e if tuple(v.shape) != tuple(shape) else v.e
+        if isinstance(v, DevScalar):
+            if is_float(dt):
+                t = self._cast_tile(v.t, "f16") if float_scalar else v.t
+                return self._ds_broadcast(self._cast_tile(t, "f32"), shape).e
+            v = self.host_scalar(v)
         arr = np.asarray(v)
         if float_scalar and is_float(dt):
             arr = arr.astype(np.float64)
@@ -1388,8 +1440,12 @@ class Executor:
         return E_scalar(arr.astype(np.int64), "i32", shape)
 
     def float_binop(self, op, code):
-        a, b = self.get_value(op.operands[0]), self.get_value(op.operands[1])
+        a, b = self.get_value(op.operands[0], dev=True), self.get_value(op.operands[1], dev=True)
         if not isinstance(a, Tile) and not isinstance(b, Tile):
+            if isinstance(a, DevScalar) or isinstance(b, DevScalar):
+                # both scalars rounded to f16, an f16 result (dialects/_helpers.py:47-50)
+                ea, eb = self._scalar_operand(a, "f16"), self._scalar_operand(b, "f16")
+                return DevScalar(Tile(Expr("bin", "f16", (1,), [ea, eb], rt.op(code))))
             fn = SCALAR_FLOAT[op.op_type]
             with np.errstate(all="ignore"):
                 return np.asarray(fn(np.asarray(a, dtype=np.float16), np.asarray(b, dtype=np.float16)),
@@ -1402,9 +1458,19 @@ class Executor:
         return Tile(Expr("bin", dt, shape, [ea, eb], rt.op(code)))
 
     def minmax(self, op):
-        a, b = self.get_value(op.operands[0]), self.get_value(op.operands[1])
+        a, b = self.get_value(op.operands[0], dev=True), self.get_value(op.operands[1], dev=True)
         f = SCALAR_MINMAX[op.op_type]
         if not isinstance(a, Tile) and not isinstance(b, Tile):
+            if isinstance(a, DevScalar) or isinstance(b, DevScalar):
+                # NumPy's promotion of two scalars: a NumPy float scalar keeps
+                # its type against a Python float, the wider of two NumPy types wins
+                kinds = [_scalar_kind(x) for x in (a, b)]
+                if kinds == [None, None]:
+                    a, b = (self.host_scalar(x) if isinstance(x, DevScalar) else x for x in (a, b))
+                    return f(a, b)
+                dt = "f32" if "f32" in kinds else "f16"
+                ea, eb = self._scalar_operand(a, dt), self._scalar_operand(b, dt)
+                return DevScalar(Tile(Expr("bin", dt, (1,), [ea, eb], rt.op(MINMAX_F[op.op_type]))))
             return f(a, b)
         ref = a if isinstance(a, Tile) else b
         shape = _bshape(a, b)
@@ -1435,7 +1501,12 @@ class Executor:
         return Tile(Expr("bin", ref.dtype, shape, [ea, eb], rt.op(INT_BIN[op.op_type])))
 
     def math_unary(self, op):
-        v = self.get_value(op.operands[0])
+        v = self.get_value(op.operands[0], dev=True)
+        if isinstance(v, DevScalar):
+            if not v.weak:
+                # a NumPy float scalar keeps its type (ops/_helpers.py:59-60)
+                return DevScalar(Tile(Expr("un", v.dtype, v.t.shape, [v.t.e], rt.op(MATH_UN[op.op_type]))))
+            v = self.host_scalar(v)      # a Python float: float64 math
         if not isinstance(v, Tile):
             x = np.asarray(v)
             if not np.issubdtype(x.dtype, np.floating):
@@ -1445,11 +1516,15 @@ class Executor:
         return Tile(Expr("un", v.dtype, v.shape, [v.e], rt.op(MATH_UN[op.op_type])))
 
     def h_arith_negf(self, op):
-        v = self.get_value(op.operands[0])
+        v = self.get_value(op.operands[0], dev=True)
+        if isinstance(v, DevScalar):
+            return DevScalar(Tile(Expr("un", v.dtype, v.t.shape, [v.t.e], rt.op("NEGF"))), v.weak)
         return Tile(Expr("un", v.dtype, v.shape, [v.e], rt.op("NEGF"))) if isinstance(v, Tile) else -v
 
     def h_arith_absf(self, op):
-        v = self.get_value(op.operands[0])
+        v = self.get_value(op.operands[0], dev=True)
+        if isinstance(v, DevScalar):
+            return DevScalar(Tile(Expr("un", v.dtype, v.t.shape, [v.t.e], rt.op("ABSF"))), v.weak)
         return Tile(Expr("un", v.dtype, v.shape, [v.e], rt.op("ABSF"))) if isinstance(v, Tile) else np.abs(v)
 
     h_math_absf = h_arith_absf
@@ -1531,20 +1606,30 @@ class Executor:
         return Tile(Expr("cast", dt, v.shape, [v.e], v.dtype))
 
     def h_arith_extf(self, op):
-        v = self.get_value(op.operands[0])
+        v = self.get_value(op.operands[0], dev=True)
+        if isinstance(v, DevScalar):
+            # from f16 or f32: exact, never overflows
+            return DevScalar(self._cast_tile(v.t, "f32"))
         if isinstance(v, Tile):
             return self._cast_tile(v, "f32")
-        return np.asarray(v, dtype=np.float32)
+        return _narrow_scalar(v, np.float32, "extf")
 
     def h_arith_truncf(self, op):
-        v = self.get_value(op.operands[0])
         dt = _elem_of(op.result_type) or "f16"
         dt = "bf16" if dt == "bf16" else "f16"
+        v = self.get_value(op.operands[0], dev=True)
+        if isinstance(v, DevScalar):
+            if dt == "bf16":
+                return DevScalar(self._cast_tile(self._cast_tile(v.t, "bf16"), "f32"))
+            if v.dtype == "f16" and not v.weak:
+                return v
+            # an f32 value that f16 cannot hold raises: read it on the host
+            v = self.host_scalar(v)
         if isinstance(v, Tile):
             return self._cast_tile(v, dt)
         if dt == "bf16":
             return np.asarray([round_host(float(x), "bf16") for x in np.asarray(v).ravel()], dtype=np.float32)
-        return np.asarray(v, dtype=np.float16)
+        return _narrow_scalar(v, np.float16, "truncf")
 
     def h_arith_extsi(self, op):
         v = self.get_value(op.operands[0])
@@ -1609,13 +1694,21 @@ class Executor:
         return Tile(E_const(0, dt, shape))
 
     def h_tensor_splat(self, op):
-        s = self.get_value(op.operands[0])
+        s = self.get_value(op.operands[0], dev=True)
         if isinstance(s, Tile):
-            raise NeedEager("tensor.splat of a tile element")
+            # the reference splats the tile's first element
+            if not is_float(s.dtype):
+                raise NeedEager("tensor.splat of an integer tile element")
+            s = DevScalar(self._element(s, []))
         shape = tuple(op.attributes.get("shape", ()))
         dt = _canon(op.attributes.get("dtype", "f16"))
         if not shape:
             shape = (1,)
+        if isinstance(s, DevScalar):
+            if is_float(dt) or dt == "i32":
+                # np.full: one conversion of the scalar to the tile's type
+                return self._cast_tile(self._ds_broadcast(s.t, shape), dt)
+            s = self.host_scalar(s)
         arr = np.asarray(s)
         if np.issubdtype(arr.dtype, np.integer) and arr.dtype != np.bool_:
             return Tile(E_scalar(arr.astype(np.int64), "i32", shape))
@@ -1623,10 +1716,13 @@ class Executor:
         return Tile(E_scalar(vals, dt, shape))
 
     def h_tensor_extract(self, op):
-        src = self.get_value(op.operands[0])
+        src = self.get_value(op.operands[0], dev=True)
         idx = [self.get_value(o) for o in op.operands[1:]]
         if not isinstance(src, Tile):
             return src
+        if is_float(src.dtype):
+            # the element stays on the device; only a host use reads it
+            return DevScalar(self._element(src, idx))
         if not self.eager and self.collective:
             self._go_eager()
         if not self.eager:
@@ -1656,6 +1752,55 @@ class Executor:
         self.plan.replayable = False
         self.attn_pending = None
         self.mm_pending = None
+
+    def _element(self, src: Tile, idx) -> Tile:
+        """Element `idx` of every lane's `src` (per-lane host indices; a
+        negative index counts from the end, as in NumPy; none: the first
+        element) as a tile of shape () or (1,), in f16 for an f16 tile and
+        f32 otherwise (reference dialects/tensor_ops.py:88-102)."""
+        shape = tuple(src.shape)
+        L = self.L
+        if idx and len(idx) != len(shape):
+            raise IndexError(f"tensor.extract: {len(idx)} indices for a rank-{len(shape)} tensor")
+        ii = []
+        for k, n in enumerate(shape):
+            a = np.broadcast_to(np.asarray(idx[k] if idx else 0, dtype=np.int64), (L,))
+            if np.any((a < -n) | (a >= n)):
+                raise IndexError(f"tensor.extract: index out of range for dimension {k} of size {n}")
+            ii.append(np.where(a < 0, a + n, a))
+        ones = (1,) * len(shape)
+        if shape == ones:
+            t = src
+        elif all(L == 0 or np.all(a == a[0]) for a in ii):
+            t = Tile(self._slice_expr(src, [int(a[0]) if L else 0 for a in ii], ones, ones))
+        else:
+            m = src if src.e.kind == "ld" and src.e.attr.offsets is None else self.materialize(src)
+            spec = m.e.attr
+            delta = sum(a * int(st) for a, st in zip(ii, spec.strides))
+            t = Tile(Expr("ld", m.dtype, ones, attr=spec.with_strides(spec.strides, spec.lane.add(delta))))
+        if len(t.shape) > 1:
+            t = self.reshape(t, (1,))
+        return self._cast_tile(t, "f16" if src.dtype == "f16" else "f32")
+
+    def _ds_broadcast(self, t: Tile, shape) -> Tile:
+        """A device scalar's tile broadcast over `shape`.  A per-row fold
+        value spread along the row it folded stays one fused row program
+        (the 'rowval' form linalg.broadcast uses); anything else with a fold
+        in it is evaluated first."""
+        shape = tuple(shape)
+        e = t.e
+        if e.has_fold and len(shape) >= 1 and tuple(t.shape) == shape[:-1] and e._fold == shape[-1]:
+            return Tile(Expr("rowval", e.dtype, shape, [e]))
+        return self.broadcast_to(t, shape)
+
+    def _scalar_operand(self, v, dt: str) -> Expr:
+        """A scalar operand of a device-scalar op: a (1,)-shaped expression
+        holding `v` converted to `dt` (f32-typed, as scalars in tile
+        expressions are)."""
+        if isinstance(v, DevScalar):
+            return self.broadcast_to(self._cast_tile(self._cast_tile(v.t, dt), "f32"), (1,)).e
+        arr = np.broadcast_to(np.asarray(v, dtype=np.float64), (self.L,))
+        return E_scalar(arr.astype(NP_DTYPE[dt]).astype(np.float64), "f32", (1,))
 
     def read_tile(self, t: Tile) -> np.ndarray:
         m = self.materialize(t)
@@ -1875,8 +2020,12 @@ class Executor:
         return self.transpose(inp, perm)
 
     def h_linalg_fill(self, op):
-        s = self.get_value(op.operands[0])
+        s = self.get_value(op.operands[0], dev=True)
         out = self.get_value(op.operands[1])
+        if isinstance(s, DevScalar):
+            if is_float(out.dtype) or out.dtype == "i32":
+                return self._cast_tile(self._ds_broadcast(s.t, out.shape), out.dtype)
+            s = self.host_scalar(s)
         vals = np.asarray(s, dtype=np.float64)
         if is_float(out.dtype):
             vals = np.array([_round_val(float(x), out.dtype) for x in vals.ravel()])
@@ -2001,10 +2150,19 @@ class Executor:
             if isinstance(outs_tile, Tile):
                 o = outs_tile
                 if tuple(o.shape) != tuple(red.shape):
-                    if _prod(o.shape) == _prod(red.shape):
+                    if reduced_all and o.shape and _prod(o.shape) == 1:
+                        # a full reduction combined with a one-element outs of
+                        # rank >= 1 broadcasts to that shape: the reference
+                        # then holds a tile, not a scalar
+                        red = self.reshape(red, o.shape)
+                        reduced_all = False
+                    elif _prod(o.shape) == _prod(red.shape):
                         o = self.reshape(o, red.shape)
                 red = self._combine(region, red, o)
-            if reduced_all:
+            if reduced_all and is_float(tile.dtype):
+                # the reference's Python float: the reduced value, held exactly
+                result = DevScalar(self._cast_tile(red, "f16" if red.dtype == "f16" else "f32"), weak=True)
+            elif reduced_all:
                 if not self.eager:
                     raise NeedEager("reduction to a scalar")
                 v = self.read_tile(red).reshape(self.L)
@@ -2665,12 +2823,10 @@ def _expandable(ops) -> bool:
     """Iterations can run as lanes: no indirect stores, no host reads of tile
     data, no ops whose result depends on another iteration."""
     for op in ops:
-        if op.op_type in ("tensor.extract", "arith.index_cast", "arith.index_castui"):
+        if op.op_type in ("arith.index_cast", "arith.index_castui"):
             return False
         if op.op_type in ("ktdp.construct_indirect_access_tile", "ktdp.inter_tile_produce",
                           "ktdp.inter_tile_reduce"):
-            return False
-        if op.op_type == "linalg.reduce" and op.attributes.get("dimensions") is None:
             return False
         for r in op.regions:
             if not _expandable(r.ops):

@@ -103,16 +103,27 @@ def flash_attention(B=1, H=2, S=256, D=32, blk=64, seed=42, dt="bf16", causal=Tr
             dict(q_ptr=q, k_ptr=k, v_ptr=v, o_ptr=np.zeros_like(q), scale=1.0 / math.sqrt(D)))
 
 
-def row_reduce(rows=32, cols=4096, rblk=4, combiner="arith.addf", dt="f32", seed=5):
+def row_reduce(rows=32, cols=4096, rblk=4, combiner="arith.addf", dt="f32", seed=5, nans=False, decades=6):
     """out[r] = fold of x[r, :] with `combiner` (the reference's pairwise-halving
-    linalg.reduce), one core per rblk-row block; values spread over 12 decades so
-    the summation order shows in the result bits."""
+    linalg.reduce), one core per rblk-row block; values spread over 2 x
+    `decades` decades so the summation order shows in the result bits;
+    `nans` puts a NaN in every other row."""
     rng = np.random.default_rng(seed)
-    x = (rng.standard_normal((rows, cols)) * 10.0 ** rng.uniform(-6, 6, (rows, cols))).astype(np.float32)
-    x = x.astype(np.float16) if dt == "f16" else x
+    x = (rng.standard_normal((rows, cols)) * 10.0 ** rng.uniform(-decades, decades, (rows, cols))).astype(np.float32)
+    if nans:
+        # a NaN in every other row: the NaN-ignoring folds skip it, the others propagate it
+        x[::2, rng.integers(0, cols, rows // 2 + rows % 2)] = np.nan
+    if dt == "f16":
+        x = x.astype(np.float16)
+    elif dt == "bf16":
+        from oracle.interp import bf16_bits
+        x = bf16_bits(x)
     cores = rows // rblk
     T, V = configs._t([rblk, cols], dt), configs._t([rblk], dt)
-    init = {"arith.addf": "0.0", "arith.maximumf": "0xFF800000", "arith.mulf": "1.0"}[combiner]
+    ninf = {"f32": "0xFF800000", "f16": "0xFC00", "bf16": "0xFF80"}[dt]
+    pinf = {"f32": "0x7F800000", "f16": "0x7C00", "bf16": "0x7F80"}[dt]
+    init = {"arith.addf": "0.0", "arith.maximumf": ninf, "arith.maxnumf": ninf, "arith.minnumf": pinf,
+            "arith.mulf": "1.0"}[combiner]
     src = f"""module {{
   func.func @row_reduce(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{
     %core_id = ktdp.get_compute_tile_id : index
@@ -1186,3 +1197,50 @@ def tensor_ops(cores=4, R=4, C=16):
     kw = {f"{n}_ptr": (rng.standard_normal(shape).astype(np.float32) if n == "x"
               else np.zeros(shape, np.float16 if dt == "f16" else np.float32)) for n, (shape, dt) in outs.items()}
     return src, "tensor_ops", kw
+
+
+# ---------------------------------------------------------------------------
+# scalars read from tile data (tensor.extract, reductions over every axis)
+# ---------------------------------------------------------------------------
+
+def scalar_chain(body, dt="f32", out_dt="f32", cores=4, C=16, idx="%c0", fill=False):
+    """Each core loads row `core_id` of x (cores x C, `dt`) and reads three
+    scalars from it: %s = x[core, idx] and %t = x[core, C - 1]
+    (tensor.extract: NumPy scalars of the tile's type) and %u, the sum of
+    the row (linalg.reduce over every axis into a 0-d outs: a Python
+    float); %v is the same sum reduced into a tensor<1x..> outs, which the
+    reference holds as a one-element tile.  `body`
+    ({dt} is replaced by `dt`) computes the scalar %r, which tensor.splat
+    (linalg.fill with `fill`) spreads over the core's row of y (cores x C,
+    `out_dt`); a body that defines the tile %rb itself stores that."""
+    T, O = configs._t([1, C], dt), configs._t([1, C], out_dt)
+    at = f"!ktdp.access_tile<1x{C}xindex>"
+    lines = ["    %core_id = ktdp.get_compute_tile_id : index",
+             "    %c0 = arith.constant 0 : index",
+             f"    %cC = arith.constant {C} : index",
+             f"    %cl = arith.constant {C - 1} : index",
+             "    %i_core = arith.remui %core_id, %cC : index",
+             configs._view("x_view", "x_ptr", [cores, C], [C, 1], dt),
+             configs._view("y_view", "y_ptr", [cores, C], [C, 1], out_dt),
+             configs._tile("xt", "x_view", ["%core_id", "%c0"], [1, C], [cores, C], dt),
+             f"    %x = ktdp.load %xt : {at} -> {T}",
+             f"    %s = tensor.extract %x[%c0, {idx}] : {T}",
+             f"    %t = tensor.extract %x[%c0, %cl] : {T}",
+             f"    %z = arith.constant 0.0 : {dt}",
+             f"    %u_e = tensor.empty() : tensor<{dt}>",
+             f"    %u_init = linalg.fill ins(%z : {dt}) outs(%u_e : tensor<{dt}>) -> tensor<{dt}>",
+             f"    %u = linalg.reduce {{ arith.addf }} ins(%x : {T}) outs(%u_init : tensor<{dt}>)",
+             f"    %v_init = tensor.splat %z : tensor<1x{dt}>",
+             f"    %v = linalg.reduce {{ arith.addf }} ins(%x : {T}) outs(%v_init : tensor<1x{dt}>)",
+             body.replace("{dt}", dt)]
+    if "%rb =" not in body:
+        if fill:
+            lines += [f"    %e = tensor.empty() : {O}",
+                      f"    %rb = linalg.fill ins(%r : {dt}) outs(%e : {O}) -> {O}"]
+        else:
+            lines.append(f"    %rb = tensor.splat %r : {O}")
+    lines += [configs._tile("yt", "y_view", ["%core_id", "%c0"], [1, C], [cores, C], out_dt),
+              f"    ktdp.store %rb, %yt : {O}, {at}"]
+    src = (f"module {{\n  func.func @scalar_chain(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{\n"
+           + "\n".join(lines) + "\n    return\n  }\n}\n")
+    return src, "scalar_chain"

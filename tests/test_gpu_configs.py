@@ -283,6 +283,34 @@ def test_row_reduce_f16_bit_exact(cols):
     np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
 
 
+@pytest.mark.parametrize("cols", [256, 1024, 4096])
+@pytest.mark.parametrize("combiner", ["arith.addf", "arith.mulf", "arith.maxnumf", "arith.minnumf", "arith.maximumf"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_row_reduce_narrow_and_nan_ignoring_folds_bit_exact(dt, combiner, cols):
+    """f16 / bf16 folds (every level rounded to the tile's type) and the
+    NaN-ignoring max / min, with a NaN in every other row: the row-wave
+    kernel's instantiations for such folds (1024 and 4096 columns) and the
+    row-chain kernel (256), bit for bit against the oracle."""
+    ref, out, _ = _run(_cases.row_reduce(rows=16, cols=cols, dt=dt, combiner=combiner, nans=True,
+                                         decades=1 if combiner == "arith.mulf" else 3))
+    got, want = out["y_ptr"].view(np.uint16).astype(np.int64), ref["y_ptr"].view(np.uint16).astype(np.int64)
+    exp_bits, man_bits = (0x7C00, 0x03FF) if dt == "f16" else (0x7F80, 0x007F)
+
+    def is_nan(b):
+        return ((b & exp_bits) == exp_bits) & ((b & man_bits) != 0)
+
+    both = is_nan(got) & is_nan(want)          # any NaN matches any NaN
+    if combiner != "arith.addf" and combiner != "arith.mulf":
+        # a max / min of -0 and +0: IEEE 754 leaves the sign open; NumPy on x86
+        # keeps the first operand for f16 and the second for f32 (its SIMD
+        # loop), the kernels give +0 for a max and -0 for a min
+        sign = 0x8000
+        both |= ((got & ~sign) == 0) & ((want & ~sign) == 0)
+    np.testing.assert_array_equal(np.where(both, 0, got), np.where(both, 0, want))
+    if combiner in ("arith.maxnumf", "arith.minnumf"):
+        assert not is_nan(got).any()
+
+
 @pytest.mark.parametrize("shape", [(256, 256, 256, 64, 64, 32, 2, 2),      # generic tile path
                                    (256, 256, 512, 128, 128, 64, 2, 2),    # MFMA path, one tile per core
                                    (512, 256, 256, 128, 128, 64, 2, 1),    # MFMA path, 2x2 tiles per core
@@ -527,3 +555,27 @@ def test_flash_attention_unfused_epilogue():
     ref, out, g = _run((src, fn, kw))
     assert g.last_plan.counts() == {"attn": 1, "prog": 1}
     np.testing.assert_allclose(bf16_from_bits(out["o_ptr"]), bf16_from_bits(ref["o_ptr"]), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("cols", [256, 1024])
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_row_product_fold_keeps_the_sign_of_zero(dt, cols):
+    """Row products that are zeros of either sign: -0 times ones, +0 times
+    one -1, one -0 with one -1, and a row of -0s with one +0, bit for bit
+    (the sign is the parity of the negative factors, whatever the order)."""
+    src, fn, kw = _cases.row_reduce(rows=8, cols=cols, rblk=4, dt=dt, combiner="arith.mulf")
+    x = np.ones((8, cols), np.float32)
+    x[1, 0] = -0.0
+    x[2, 0], x[2, 1] = 0.0, -1.0
+    x[3, 5], x[3, 6] = -0.0, -1.0
+    x[4], x[4, 3] = -0.0, 0.0
+    if dt == "bf16":
+        from oracle.interp import bf16_bits
+        kw["x_ptr"] = bf16_bits(x)
+    else:
+        kw["x_ptr"] = x.astype(kw["x_ptr"].dtype)
+    ref, out, _ = _run((src, fn, kw))
+    u = np.uint32 if dt == "f32" else np.uint16
+    np.testing.assert_array_equal(out["y_ptr"].view(u), ref["y_ptr"].view(u))
+    bits = ref["y_ptr"].view(u).astype(np.int64)
+    assert list((bits[[1, 2, 3, 4]] >> (31 if dt == "f32" else 15)) & 1) == [1, 1, 0, 1]

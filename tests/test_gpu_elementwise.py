@@ -231,3 +231,18 @@ def test_cores_accumulating_through_hbm_run_in_core_order():
     for c in range(6):
         want = (want + x[c * 512:(c + 1) * 512]).astype(np.float32)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [1 << 15, 1 << 20])
+def test_f16_mulf_keeps_the_sign_of_a_zero_product(n):
+    """Products that round to a zero of either sign (tiny operands of mixed
+    signs, and signed zeros times finite values): the f16 result keeps the
+    sign.  An f32 product narrowed to f16 is otherwise compiled to one
+    mixed-precision multiply-add with a +0 addend, which turns -0 into +0."""
+    rng = np.random.default_rng(9)
+    a = (rng.choice([-1.0, 1.0], n) * rng.uniform(1e-4, 2e-4, n)).astype(np.float16)
+    b = (rng.choice([-1.0, 1.0], n) * rng.uniform(1e-4, 2e-4, n)).astype(np.float16)
+    a[:4], b[:4] = np.array([-0.0, 0.0, -0.0, 0.0], np.float16), np.array([1.0, -1.0, -2.0, 3.0], np.float16)
+    got, ref = _both(["%r = arith.mulf %a, %b : {T_f16}"], ["f16", "f16"], "f16", [a, b])
+    assert np.signbit(ref).sum() > n // 4          # the oracle's -0 results
+    _bits_equal(got, ref)
