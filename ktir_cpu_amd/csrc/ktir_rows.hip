@@ -154,9 +154,10 @@ static bool chain_binary(const ktir_instr_t& x) {
 
 // a pass plan of f32 folds combined by the arithmetic or NaN-propagating
 // ops, with no NaN-ignoring min / max and no exact division among its chain
-// ops: the only plans the fixed-form kernels take.  The row-wave kernel
-// takes the others in its FOLDX instantiations (folds of any op, rounded to
-// f16 / bf16 at every level where the fold is of that type).
+// ops.  The row-wave kernel takes the others in its FOLDX instantiations
+// (folds of any op, rounded to f16 / bf16 at every level where the fold is of
+// that type); of them, the fixed-form kernels take only the f16-math softmax
+// and norm-scale forms.
 static bool plan_plain(const RcPlan& R) {
   for (int i = 0; i < R.n_steps; ++i) {
     const RcStep& S = R.steps[i];
@@ -1412,11 +1413,23 @@ static bool try_launch_rowwave(const ktir_prog_t& P, const RcPlan& R, int64_t ro
 // layout: the chunk bits in registers, the lane bits by shuffles (lanes
 // l ^ 32 .. l ^ 1), the bits of j in registers.  The max fold's result does
 // not depend on the order: the largest element, or NaN if any element is NaN.
+//
+// The same two forms computed in f16, as the reference's own row loops
+// write them (every op on an f16 tile, so every step rounded to f16):
+//   softmax16: m <- max fold (maxnumf or maximumf) of x; d = f16(x - m');
+//              e = f16(exp d); s <- f16 add fold of e; y = f16(e / s');
+//   norm16:    a <- f16 add fold of f16(x * x); y = f16(f16(x * r) * w) (or
+//              w first, or no w).
+// NumPy's f16 add, sub and mul round the f32 result of two f16 values, which
+// is the correctly rounded f16 result (f32 has at least 2 * 11 + 2 bits), so
+// packed f16 instructions give the same bits; exp is the hardware exp2
+// rounded to f16 (within one f16 ulp of NumPy's, as the general kernels'
+// exp), and the division a quotient within one f32 ulp rounded to f16.
 constexpr int RF_MAX_ROW = 8;
-enum { RF_SOFTMAX = 1, RF_NORM = 2 };
+enum { RF_SOFTMAX = 1, RF_NORM = 2, RF_SOFTMAX16 = 3, RF_NORM16 = 4 };
 
 struct RfPlan {
-  int32_t nd, has_w, w_first, n_row0, n_row1, pad0;
+  int32_t nd, has_w, w_first, n_row0, n_row1, numf;   // numf: softmax16's max ignores NaN
   int64_t shape[KTIR_MAX_DIMS];
   uint64_t lane_scalars;
   int64_t n_lane_scalars;
@@ -1773,18 +1786,192 @@ __device__ __forceinline__ void rf_norm(const RfPlan& F, gu4 (&c)[NQ], const gu4
   }
 }
 
+typedef _Float16 rf_h2 __attribute__((ext_vector_type(2)));
+typedef float rf_f2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ rf_h2 rf_word(uint32_t u) { return __builtin_bit_cast(rf_h2, u); }
+__device__ __forceinline__ uint32_t rf_bits(rf_h2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// f16 add fold in the reference's halving order of the row's values, which
+// get(i, k) produces as word k (elements 2k, 2k + 1) of chunk i; every add
+// rounded to f16 (packed adds on the pairs)
+template <int NQ, typename G>
+__device__ __forceinline__ float rf_sum16(G get) {
+  constexpr int H = NQ > 1 ? NQ / 2 : 1;
+  rf_h2 t[H][4];
+#pragma unroll
+  for (int i = 0; i < H; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t[i][k] = NQ > 1 ? get(i, k) + get(i + H, k) : get(i, k);
+#pragma unroll
+  for (int h = H / 2; h >= 1; h >>= 1)
+#pragma unroll
+    for (int i = 0; i < h; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) t[i][k] = t[i][k] + t[i + h][k];
+  rf_h2 a[4] = {t[0][0], t[0][1], t[0][2], t[0][3]};
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = a[k] + rf_word((uint32_t)__shfl_xor((int)rf_bits(a[k]), s));
+  // the bits of j: j with j + 4 (word k with word k + 2), j + 2 (word 0 with 1), j + 1
+  a[0] = a[0] + a[2];
+  a[1] = a[1] + a[3];
+  a[0] = a[0] + a[1];
+  return (float)(_Float16)(a[0].x + a[0].y);
+}
+
+template <int NQ>
+__device__ __forceinline__ void rf_softmax16(const RfPlan& F, gu4 (&c)[NQ], const RwPos& p, RowLanes& rr, int l) {
+  // row max of the f16 values: the order does not change a max
+  rf_h2 a = {-__builtin_inff16(), -__builtin_inff16()}, b = a;
+  float mx;
+  if (__builtin_amdgcn_readfirstlane(F.numf)) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const uint32_t w0 = c[i][0], w1 = c[i][1], w2 = c[i][2], w3 = c[i][3];
+      a = __builtin_elementwise_max(a, rf_word(w0));
+      b = __builtin_elementwise_max(b, rf_word(w1));
+      a = __builtin_elementwise_max(a, rf_word(w2));
+      b = __builtin_elementwise_max(b, rf_word(w3));
+    }
+    a = __builtin_elementwise_max(a, b);
+    mx = fmaxf((float)a.x, (float)a.y);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
+  } else {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const uint32_t w0 = c[i][0], w1 = c[i][1], w2 = c[i][2], w3 = c[i][3];
+      a = __builtin_elementwise_maximum(a, rf_word(w0));
+      b = __builtin_elementwise_maximum(b, rf_word(w1));
+      a = __builtin_elementwise_maximum(a, rf_word(w2));
+      b = __builtin_elementwise_maximum(b, rf_word(w3));
+    }
+    a = __builtin_elementwise_maximum(a, b);
+    mx = __builtin_elementwise_maximum((float)a.x, (float)a.y);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, s));
+  }
+  rr.set(F.fold0, mx);
+  for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
+  const float m = rr.get(F.m);
+  // e = f16(exp(f16(x - m'))), kept packed for the store pass.  With m' an
+  // f16 value, f16(x - m') is one packed f16 subtraction (NumPy's f16
+  // subtraction rounds the f32 difference of two f16 values, the correctly
+  // rounded f16 difference); else the f32 difference, rounded.
+  uint32_t ep[NQ * 4];
+  const _Float16 mh = (_Float16)m;
+  const bool m16 = (float)mh == m || m != m;
+  const rf_h2 m2 = {mh, mh};
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      rf_f2 dr;
+      if (m16) {
+        dr = __builtin_convertvector(rf_word(c[i][k]) - m2, rf_f2);
+      } else {
+        const rf_f2 x = __builtin_convertvector(rf_word(c[i][k]), rf_f2);
+        const rf_f2 d = {__fsub_rn(x.x, m), __fsub_rn(x.y, m)};
+        dr = __builtin_convertvector(__builtin_convertvector(d, rf_h2), rf_f2);
+      }
+      const rf_f2 e = {exp_hw(dr.x), exp_hw(dr.y)};
+      ep[4 * i + k] = rf_bits(__builtin_convertvector(e, rf_h2));
+    }
+  }
+  const float sum = rf_sum16<NQ>([&](int i, int k) { return rf_word(ep[4 * i + k]); });
+  rr.set(F.fold1, sum);
+  for (int k = 0; k < F.n_row1; ++k) rw_row_exec(F, F.row1[k], rr, p.lane);
+  const float s = rr.get(F.s);
+  const int64_t e0 = rw_row_base(F.y, p);
+  const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
+  // f16(e / s'): the quotient within one f32 ulp (div_by: the correctly
+  // rounded 1 / s' and one fused correction) before the f16 rounding, which it
+  // changes only next to an f16 rounding midpoint; the plain quotient for a
+  // sum that is tiny, huge or not finite
+  const float r = __fdiv_rn(1.f, s);
+  const float as = fabsf(s);
+  const bool fast = as > 1e-30f && as < 1e30f && r == r;
+  auto out = [&](auto div) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      gu4 y;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const rf_f2 e = __builtin_convertvector(rf_word(ep[4 * i + k]), rf_f2);
+        const rf_f2 q = {div(e.x), div(e.y)};
+        y[k] = rf_bits(__builtin_convertvector(q, rf_h2));
+      }
+      rf_store(F.y, e0, in, i, l, y);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (fast) {
+    out([&](float e) { return div_by(e, s, r); });
+  } else {
+    out([&](float e) {
+      const float q = __fdiv_rn(e, s);
+      __builtin_amdgcn_sched_barrier(0);
+      return q;
+    });
+  }
+}
+
+// w: the weight row in LDS (lane l's own 16-byte pieces, at 1024 i + 16 l)
+template <int NQ>
+__device__ __forceinline__ void rf_norm16(const RfPlan& F, gu4 (&c)[NQ], const gu4* w, const RwPos& p, RowLanes& rr,
+                                          int l) {
+  rr.set(F.fold0, rf_sum16<NQ>([&](int i, int k) {
+    const rf_h2 x = rf_word(c[i][k]);
+    return x * x;
+  }));
+  for (int k = 0; k < F.n_row0; ++k) rw_row_exec(F, F.row0[k], rr, p.lane);
+  const float s = rr.get(F.s);
+  const int64_t e0 = rw_row_base(F.y, p);
+  const bool in = e0 >= F.y.lo && e0 + 512 * NQ <= F.y.hi;
+  // f16(x * s) as one packed f16 product when s is an f16 value (the f32
+  // product of two f16 values rounded once); else in f32, then rounded
+  const _Float16 sh = (_Float16)s;
+  const bool s16 = (float)sh == s || s != s;
+  const rf_h2 s2 = {sh, sh};
+  auto scale = [&](rf_h2 x) -> rf_h2 {
+    if (s16) return x * s2;
+    const rf_f2 xf = __builtin_convertvector(x, rf_f2);
+    return __builtin_convertvector(rf_f2{__fmul_rn(xf.x, s), __fmul_rn(xf.y, s)}, rf_h2);
+  };
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    gu4 y;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      rf_h2 x = rf_word(c[i][k]);
+      if (F.has_w) {
+        const rf_h2 wk = rf_word(w[64 * i + l][k]);
+        x = F.w_first ? scale(x * wk) : scale(x) * wk;
+      } else {
+        x = scale(x);
+      }
+      y[k] = rf_bits(x);
+    }
+    rf_store(F.y, e0, in, i, l, y);
+  }
+}
+
 template <int NQ, int RECIPE, int DT>
 __device__ __forceinline__ void rf_row(const RfPlan& F, gu4 (&c)[NQ], const gu4* w, const RwPos& p, RowLanes& rr,
                                        int l) {
   if (RECIPE == RF_SOFTMAX) rf_softmax<NQ, DT>(F, c, p, rr, l);
-  else rf_norm<NQ, DT>(F, c, w, p, rr, l);
+  else if (RECIPE == RF_NORM) rf_norm<NQ, DT>(F, c, w, p, rr, l);
+  else if (RECIPE == RF_SOFTMAX16) rf_softmax16<NQ>(F, c, p, rr, l);
+  else rf_norm16<NQ>(F, c, w, p, rr, l);
 }
 
 // Rows r = blockIdx.x + k gridDim.x, two row buffers in turn (no copy between
 // them, so the next row's loads stay in flight across the current row).
 template <int NQ, int RECIPE, int DT>
 __global__ __launch_bounds__(64) void prog_rowfix(const RfPlan F, int64_t total_rows) {
-  __shared__ gu4 w[RECIPE == RF_NORM ? 64 * NQ : 1];
+  __shared__ gu4 w[RECIPE == RF_NORM || RECIPE == RF_NORM16 ? 64 * NQ : 1];
   const int l = threadIdx.x;
   int64_t rows_per_lane = 1;
 #pragma unroll
@@ -1796,7 +1983,7 @@ __global__ __launch_bounds__(64) void prog_rowfix(const RfPlan F, int64_t total_
   if (r >= total_rows) return;
   gu4 ca[NQ], cb[NQ];
   RwPos pa = rw_pos(F, r, rpl);
-  if (RECIPE == RF_NORM && F.has_w) {
+  if ((RECIPE == RF_NORM || RECIPE == RF_NORM16) && F.has_w) {
     // the same row for every row; each lane reads back only what it wrote
     rf_load<NQ>(F.w, rw_row_base(F.w, pa), l, ca);
 #pragma unroll
@@ -1837,7 +2024,11 @@ static void launch_rowfix(const RfPlan& F, int64_t rows) {
 
 template <int NQ>
 static void rowfix_dt(const RfPlan& F, int recipe, int dt, int64_t rows) {
-  if (recipe == RF_SOFTMAX) {
+  if (recipe == RF_SOFTMAX16) {
+    launch_rowfix<NQ, RF_SOFTMAX16, KTIR_F16>(F, rows);
+  } else if (recipe == RF_NORM16) {
+    launch_rowfix<NQ, RF_NORM16, KTIR_F16>(F, rows);
+  } else if (recipe == RF_SOFTMAX) {
     if (dt == KTIR_F16) launch_rowfix<NQ, RF_SOFTMAX, KTIR_F16>(F, rows);
     else launch_rowfix<NQ, RF_SOFTMAX, KTIR_BF16>(F, rows);
   } else {
@@ -1891,11 +2082,13 @@ static bool try_launch_rowfix(const ktir_prog_t& P, const RcPlan& R, int64_t row
     return k;
   };
   const RcStep& A = R.steps[pass[0]];
-  if (A.end != 0 || A.fold_dt != KTIR_F32) return false;
+  // f16 folds: the f16-math forms (f16 rows only)
+  const bool m16 = A.fold_dt == KTIR_F16;
+  if (A.end != 0 || (A.fold_dt != KTIR_F32 && !m16)) return false;
   const int sx = A.src;
   const ktir_leaf_t& X = P.leaves[R.slot_leaf[sx]];
   const int dt = X.dtype;
-  if ((dt != KTIR_F16 && dt != KTIR_BF16) || !rf_leaf_ok(X, P.ndim, dt)) return false;
+  if ((dt != KTIR_F16 && dt != KTIR_BF16) || (m16 && dt != KTIR_F16) || !rf_leaf_ok(X, P.ndim, dt)) return false;
   F.x = rw_leaf(P, R.slot_leaf[sx]);
   const RcStep& Z = R.steps[pass[n_pass - 1]];   // the storing pass
   if (Z.end != 1 || Z.src != sx || !rf_leaf_ok(P.leaves[Z.st_leaf], P.ndim, dt) || gap[n_pass - 1] != 0) return false;
@@ -1905,8 +2098,62 @@ static bool try_launch_rowfix(const ktir_prog_t& P, const RcPlan& R, int64_t row
     return S.n_ops == n || (S.n_ops == n + 1 && S.ops[n].op == KTIR_OP_CAST && S.ops[n].kind == 0 &&
                             S.ops[n].aux == KTIR_F32 && S.ops[n].dt == dt);
   };
+  // an f16 op as analyze_rows keeps it: its f32 op, then the rounding to f16;
+  // the storing pass's last rounding may be left to the (f16) store
+  auto nop = [&](const RcStep& S, int i, int op, int kind) {
+    return i + 1 < S.n_ops && S.ops[i].op == op && S.ops[i].dt == KTIR_F32 && S.ops[i].kind == kind &&
+           S.ops[i + 1].op == KTIR_OP_CAST && S.ops[i + 1].kind == 0 && S.ops[i + 1].aux == KTIR_F32 &&
+           S.ops[i + 1].dt == KTIR_F16;
+  };
+  auto nlast = [&](const RcStep& S, int i, int op, int kind) {
+    return (S.n_ops == i + 2 && nop(S, i, op, kind)) ||
+           (S.n_ops == i + 1 && S.ops[i].op == op && S.ops[i].dt == KTIR_F32 && S.ops[i].kind == kind);
+  };
   int recipe;
-  if (n_pass == 3) {
+  if (n_pass == 3 && m16) {
+    const RcStep& B = R.steps[pass[1]];
+    if (R.n_slots != 1 || A.n_ops != 0 || (A.fold_op != KTIR_OP_MAXNUMF && A.fold_op != KTIR_OP_MAXIMUMF)) return false;
+    if (B.src != sx || B.end != 0 || B.n_ops != 4 || B.fold_op != KTIR_OP_ADDF || B.fold_dt != KTIR_F16) return false;
+    if (!nop(B, 0, KTIR_OP_SUBF, 1) || B.ops[0].swap || !nop(B, 2, KTIR_OP_EXP, 0)) return false;
+    if (!nop(Z, 0, KTIR_OP_SUBF, 1) || Z.ops[0].swap || Z.ops[0].idx != B.ops[0].idx || !nop(Z, 2, KTIR_OP_EXP, 0) ||
+        !nlast(Z, 4, KTIR_OP_DIVF, 1) || Z.ops[4].swap)
+      return false;
+    // e is computed once: m' must hold the same value in both passes
+    const int m = B.ops[0].idx;
+    if (B.dst == m) return false;
+    F.n_row1 = rows_of(1, F.row1);
+    for (int k = 0; k < F.n_row1; ++k)
+      if (F.row1[k].dst == m) return false;
+    F.fold1 = B.dst;
+    F.m = (int8_t)m;
+    F.s = Z.ops[4].idx;
+    F.numf = A.fold_op == KTIR_OP_MAXNUMF;
+    recipe = RF_SOFTMAX16;
+  } else if (n_pass == 2 && m16) {
+    if (A.n_ops != 2 || !nop(A, 0, KTIR_OP_MULF, 3) || A.fold_op != KTIR_OP_ADDF) return false;
+    const RcOp* o = Z.ops;
+    if (nlast(Z, 0, KTIR_OP_MULF, 1)) {
+      F.s = o[0].idx;
+    } else if (nop(Z, 0, KTIR_OP_MULF, 1) && nlast(Z, 2, KTIR_OP_MULF, 2) && o[2].idx != sx) {
+      F.s = o[0].idx;
+      F.has_w = 1;
+    } else if (nop(Z, 0, KTIR_OP_MULF, 2) && nlast(Z, 2, KTIR_OP_MULF, 1) && o[0].idx != sx) {
+      F.s = o[2].idx;
+      F.has_w = 1;
+      F.w_first = 1;
+    } else {
+      return false;
+    }
+    if (R.n_slots != 1 + F.has_w) return false;
+    if (F.has_w) {
+      const ktir_leaf_t& W = P.leaves[R.slot_leaf[1 - sx]];
+      if (!rf_leaf_ok(W, P.ndim, dt) || !rf_invariant(P, W)) return false;
+      F.w = rw_leaf(P, R.slot_leaf[1 - sx]);
+    }
+    recipe = RF_NORM16;
+  } else if (m16) {
+    return false;
+  } else if (n_pass == 3) {
     const RcStep& B = R.steps[pass[1]];
     if (R.n_slots != 1 || A.n_ops != 0 || A.fold_op != KTIR_OP_MAXIMUMF) return false;
     if (B.src != sx || B.end != 0 || B.n_ops != 2 || B.fold_op != KTIR_OP_ADDF || B.fold_dt != KTIR_F32) return false;
@@ -1970,7 +2217,9 @@ bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner) {
   RcPlan R;
   if (!analyze_rows(P, R)) return false;
   const bool plain = plan_plain(R);
-  if (plain && try_launch_rowfix(P, R, rows, inner)) return true;
+  // the fixed forms: the f32-math ones take plain plans, the f16-math ones
+  // f16 folds (try_launch_rowfix checks which)
+  if (try_launch_rowfix(P, R, rows, inner)) return true;
   if (try_launch_rowwave(P, R, rows, inner, !plain)) return true;
   // threads per row and elements per thread: n = tpr * E, E in {2..32}, tpr in {32..256}
   int tpr = (int)(inner / 16);

@@ -1427,8 +1427,9 @@ class Executor:
             return self.broadcast_to(v, shape).e if tuple(v.shape) != tuple(shape) else v.e
         if isinstance(v, DevScalar):
             if is_float(dt):
+                # registers hold f32: the f16 value needs no widening cast
                 t = self._cast_tile(v.t, "f16") if float_scalar else v.t
-                return self._ds_broadcast(self._cast_tile(t, "f32"), shape).e
+                return self._ds_broadcast(t, shape).e
             v = self.host_scalar(v)
         arr = np.asarray(v)
         if float_scalar and is_float(dt):
@@ -1795,10 +1796,10 @@ class Executor:
 
     def _scalar_operand(self, v, dt: str) -> Expr:
         """A scalar operand of a device-scalar op: a (1,)-shaped expression
-        holding `v` converted to `dt` (f32-typed, as scalars in tile
-        expressions are)."""
+        holding `v` converted to `dt`."""
         if isinstance(v, DevScalar):
-            return self.broadcast_to(self._cast_tile(self._cast_tile(v.t, dt), "f32"), (1,)).e
+            # rounded to dt; registers hold f32, so no widening cast after it
+            return self.broadcast_to(self._cast_tile(v.t, dt), (1,)).e
         arr = np.broadcast_to(np.asarray(v, dtype=np.float64), (self.L,))
         return E_scalar(arr.astype(NP_DTYPE[dt]).astype(np.float64), "f32", (1,))
 
@@ -2581,7 +2582,12 @@ class Executor:
         return res[0] if len(res) == 1 else tuple(res)
 
     def _expand(self, op, lb, st, trips):
-        """Run independent iterations as extra lanes (one lane per (lane, iteration))."""
+        """Run independent iterations as extra lanes (one lane per (lane,
+        iteration)).  Lanes go lane-major (a lane's iterations side by side)
+        unless the iteration values are then not affine in the lane and
+        iteration-major order makes them so: a loop that strides its lanes'
+        rows (row = core + j * cores) then addresses memory with one stride per
+        lane instead of an offset table."""
         L = self.L
         tot = int(trips.sum())
         if tot == 0:
@@ -2590,6 +2596,13 @@ class Executor:
         first = np.repeat(np.cumsum(trips) - trips, trips)
         j = np.arange(tot, dtype=np.int64) - first
         ivals = lb[parent] + j * st[parent]
+        if L > 1 and np.all(trips == trips[0]) and not _affine(ivals):
+            T = int(trips[0])
+            p2 = np.tile(np.arange(L, dtype=np.int64), T)
+            j2 = np.repeat(np.arange(T, dtype=np.int64), L)
+            iv2 = lb[p2] + j2 * st[p2]
+            if _affine(iv2):
+                parent, j, ivals = p2, j2, iv2
         cur = self.lanes
         new = Lanes(cur.cores[parent], self.insts.new(cur.inst[parent]))
         self.levels.append(_Level(new, parent))
@@ -2688,6 +2701,14 @@ class Executor:
 class _Wrap:
     def __init__(self, ptr):
         self.ptr = ptr
+
+
+def _affine(a: np.ndarray) -> bool:
+    """Whether the values step by one constant difference."""
+    if a.size < 3:
+        return True
+    d = np.diff(a)
+    return bool(np.all(d == d[0]))
 
 
 def _prod(s) -> int:
