@@ -12,7 +12,10 @@ Configurations (all shapes parameterised so tests can shrink them):
 1. ``vector_add``       out = x + y, f16, BLOCK elements per block.
 2. ``gather_scatter_add`` out[idx[i], :] += f32(table[idx[i], :]) through
    indirect access tiles, in chunks of CH rows per step.
-3. ``softmax`` / ``rmsnorm`` row kernels, f32 row reductions.
+3. ``softmax`` / ``rmsnorm`` row kernels, f32 row reductions;
+   ``softmax_extract`` / ``rmsnorm_extract`` / ``layernorm_extract`` the
+   same in the f16-math, one-row-per-step form of the reference's examples
+   (row statistics read by ``tensor.extract``).
 4. ``gemm``              C = A @ B, f16 in, f32 accumulate, f16 out.
 5. ``flash_attention``   causal attention, bf16 in/out, online softmax over
    KV tiles with f32 state.
@@ -345,6 +348,95 @@ def rmsnorm_extract(rows: int = 4096, cols: int = 1024, cores: int = 32) -> str:
     return"""
     return _strided_rows("rmsnorm_fwd", "%x_ptr: index, %w_ptr: index, %y_ptr: index, %n_rows: index, %eps: f16",
                          rows, cols, cores, body)
+
+
+def layernorm_extract(rows: int = 1151, cols: int = 8192, block: int = 1024, cores: int = 32) -> str:
+    """LayerNorm in the form of the reference's triton-ktir layernorm_fwd
+    example: f16 math, one row per loop step (rows core, core + cores, ...),
+    the row sum and the sum of squared deviations accumulated block by block
+    in a loop-carried f16 tile and folded, mean and rstd as one-element
+    tensors (mean = sum / N, rstd = 1 / sqrt(var / N + eps)) read by
+    tensor.extract and spread by tensor.splat, both also stored, then y =
+    (x - mean) * rstd * w + b block by block."""
+    T, V = _t([1, block], "f16"), _t([1], "f16")
+    at, a1 = f"!ktdp.access_tile<1x{block}xindex>", "!ktdp.access_tile<1xindex>"
+    views = "\n".join(_view(n, p, [rows, cols], [cols, 1], "f16") for n, p in
+                      (("x_view", "x_ptr"), ("y_view", "y_ptr"), ("w_view", "w_ptr"), ("b_view", "b_ptr")))
+    views += "\n" + "\n".join(_view(n, p, [rows], [1], "f16") for n, p in (("mean_view", "mean_ptr"),
+                                                                         ("rstd_view", "rstd_ptr")))
+
+    def blk(name, view):
+        return _tile(name, view, ["%row", "%col"], [1, block], [rows, cols], "f16", "          ")
+
+    return f"""module {{
+  func.func @layernorm_fwd(%x_ptr: index, %y_ptr: index, %w_ptr: index, %b_ptr: index, %mean_ptr: index,
+                           %rstd_ptr: index, %n_cols: index, %eps: f16, %blk: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %n_rows = arith.constant {rows} : index
+    %step = arith.constant {cores} : index
+    %one = arith.constant 1.0 : f16
+    %zero = arith.constant 0.0 : f16
+{views}
+    scf.for %row = %core_id to %n_rows step %step : index {{
+      %zb = arith.constant dense<0.0> : {T}
+      %acc = scf.for %col = %c0 to %n_cols step %blk iter_args(%a = %zb) -> {T} {{
+{blk("xa", "x_view")}
+        %x = ktdp.load %xa : {at} -> {T}
+        %a2 = arith.addf %a, %x : {T}
+        scf.yield %a2 : {T}
+      }}
+      %s0 = tensor.splat %zero : {V}
+      %sum = linalg.reduce {{ arith.addf }} ins(%acc : {T}) outs(%s0 : {V}) dimensions = [1]
+      %n_i = arith.index_cast %n_cols : index to i32
+      %n_h = arith.sitofp %n_i : i32 to f16
+      %n_t = tensor.splat %n_h : {V}
+      %mean = arith.divf %sum, %n_t : {V}
+      %m = tensor.extract %mean[%c0] : {V}
+      %mb = tensor.splat %m : {T}
+      %vacc = scf.for %col = %c0 to %n_cols step %blk iter_args(%v = %zb) -> {T} {{
+{blk("xb", "x_view")}
+        %x = ktdp.load %xb : {at} -> {T}
+        %d = arith.subf %x, %mb : {T}
+        %d2 = arith.mulf %d, %d : {T}
+        %v2 = arith.addf %v, %d2 : {T}
+        scf.yield %v2 : {T}
+      }}
+      %q0 = tensor.splat %zero : {V}
+      %ssq = linalg.reduce {{ arith.addf }} ins(%vacc : {T}) outs(%q0 : {V}) dimensions = [1]
+      %var = arith.divf %ssq, %n_t : {V}
+      %eps_t = tensor.splat %eps : {V}
+      %ve = arith.addf %var, %eps_t : {V}
+      %sd = math.sqrt %ve : {V}
+      %one_t = tensor.splat %one : {V}
+      %rstd = arith.divf %one_t, %sd : {V}
+      %r = tensor.extract %rstd[%c0] : {V}
+      %rb = tensor.splat %r : {T}
+{_tile("ma", "mean_view", ["%row"], [1], [rows], "f16", "      ")}
+{_tile("ra", "rstd_view", ["%row"], [1], [rows], "f16", "      ")}
+      ktdp.store %mean, %ma : {V}, {a1}
+      ktdp.store %rstd, %ra : {V}, {a1}
+      scf.for %col = %c0 to %n_cols step %blk {{
+{blk("xc", "x_view")}
+{blk("wc", "w_view")}
+{blk("bc", "b_view")}
+{blk("yc", "y_view")}
+        %x = ktdp.load %xc : {at} -> {T}
+        %w = ktdp.load %wc : {at} -> {T}
+        %b = ktdp.load %bc : {at} -> {T}
+        %xm = arith.subf %x, %mb : {T}
+        %xh = arith.mulf %xm, %rb : {T}
+        %xw = arith.mulf %xh, %w : {T}
+        %y = arith.addf %xw, %b : {T}
+        ktdp.store %y, %yc : {T}, {at}
+        scf.yield
+      }}
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
 
 
 # ---------------------------------------------------------------------------

@@ -2841,11 +2841,11 @@ def _has_op(ops, name: str) -> bool:
 
 
 def _expandable(ops) -> bool:
-    """Iterations can run as lanes: no indirect stores, no host reads of tile
-    data, no ops whose result depends on another iteration."""
+    """Iterations can run as lanes: no indirect stores, no ops whose result
+    depends on another iteration.  (A host read of tile data inside, such as
+    an index_cast of a tile element, raises NeedEager while the lanes are
+    walked, as it would without the expansion.)"""
     for op in ops:
-        if op.op_type in ("arith.index_cast", "arith.index_castui"):
-            return False
         if op.op_type in ("ktdp.construct_indirect_access_tile", "ktdp.inter_tile_produce",
                           "ktdp.inter_tile_reduce"):
             return False

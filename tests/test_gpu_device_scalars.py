@@ -252,3 +252,39 @@ def test_rmsnorm_extract_row_wave_bit_exact():
                            eps=1e-3)
     assert plan.mode == "lockstep" and plan.counts() == {"prog": 1}
     _bits_equal(got, ref, "rmsnorm_extract")
+
+
+@pytest.mark.parametrize("rows_,cols,blk,cores", [(70, 512, 128, 8), (1151, 8192, 1024, 32)])
+def test_layernorm_extract_bit_exact(rows_, cols, blk, cores):
+    """The reference's layernorm_fwd form: loop-carried f16 block sums,
+    mean and rstd as one-element tensors read by tensor.extract, both
+    stored, then the normalised rows; bit for bit against the oracle (on
+    sampled cores at the example's own size), within f16 rounding of the
+    float64 LayerNorm."""
+    from ktir_cpu_amd import configs
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    src = configs.layernorm_extract(rows_, cols, blk, cores)
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((rows_, cols)) * 2 + 1).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, (rows_, cols)).astype(np.float16)
+    b = rng.standard_normal((rows_, cols)).astype(np.float16)
+    kw = dict(x_ptr=x, y_ptr=np.zeros_like(x), w_ptr=w, b_ptr=b, mean_ptr=np.zeros(rows_, np.float16),
+              rstd_ptr=np.zeros(rows_, np.float16), n_cols=cols, eps=1e-5, blk=blk)
+    print("layernorm_extract", rows_, cols, blk, cores, flush=True)
+    g = KTIRInterpreter()
+    g.load(src)
+    got = g.execute_function("layernorm_fwd", **kw)
+    print("  ", g.last_plan.mode, g.last_plan.counts(), g.last_plan.fallback_reason, flush=True)
+    assert g.last_plan.mode == "lockstep"
+    o = OracleInterpreter()
+    o.load(src)
+    if rows_ > 100:
+        o.cores_to_run = [0, 17, 31]
+    ref = o.execute_function("layernorm_fwd", **{k: (v.copy() if isinstance(v, np.ndarray) else v)
+                                                 for k, v in kw.items()})
+    sel = np.concatenate([np.arange(c, rows_, cores) for c in (o.cores_to_run or range(cores))])
+    for k in ("y_ptr", "mean_ptr", "rstd_ptr"):
+        _bits_equal(got[k][sel], ref[k][sel], k)
+    xf = x.astype(np.float64)
+    want = (xf - xf.mean(1, keepdims=True)) / np.sqrt(xf.var(1, keepdims=True) + 1e-5) * w + b
+    np.testing.assert_allclose(got["y_ptr"].astype(np.float64), want, atol=0.05, rtol=0.02)
