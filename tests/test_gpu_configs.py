@@ -579,3 +579,44 @@ def test_row_product_fold_keeps_the_sign_of_zero(dt, cols):
     np.testing.assert_array_equal(out["y_ptr"].view(u), ref["y_ptr"].view(u))
     bits = ref["y_ptr"].view(u).astype(np.int64)
     assert list((bits[[1, 2, 3, 4]] >> (31 if dt == "f32" else 15)) & 1) == [1, 1, 0, 1]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_flash_attention_epilogue_reciprocal_within_one_ulp(dt):
+    """O = acc / l as acc times the correctly rounded 1 / l, against the
+    oracle's division, on scores that make every probability exactly 1 or 0:
+    query i is one-hot on dimension i % 7, key j is 200 on dimension j % 7,
+    so query i's kept keys (j <= i, j = i mod 7) score 200 and the others 0
+    (exp(-200) is 0 in f32).  Then l is the count k_i = i // 7 + 1 and acc
+    the exact sum of their integer V rows, so the only difference left is
+    the epilogue's rounding: at most one output ulp, none where k_i is a
+    power of two (1 / k_i exact)."""
+    from oracle.interp import bf16_bits
+    B, H, S, D = 1, 2, 512, 128
+    src, fn, kw = _cases.flash_attention(B=B, H=H, S=S, D=D, blk=128, dt=dt)
+    rng = np.random.default_rng(11)
+    q = np.zeros((B, H, S, D), np.float32)
+    k = np.zeros((B, H, S, D), np.float32)
+    idx = np.arange(S)
+    q[:, :, idx, idx % 7] = 1.0
+    k[:, :, idx, idx % 7] = 200.0
+    v = rng.integers(-8, 9, (B, H, S, D)).astype(np.float32)
+    enc = bf16_bits if dt == "bf16" else (lambda a: a.astype(np.float16))
+    kw.update(q_ptr=enc(q), k_ptr=enc(k), v_ptr=enc(v), o_ptr=np.zeros_like(enc(q)), scale=1.0)
+    ref, out, g = _run((src, fn, kw))
+    assert g.last_plan.counts().get("attn") == 1
+    u = np.int32
+    got = out["o_ptr"].view(np.int16).astype(u)
+    want = ref["o_ptr"].view(np.int16).astype(u)
+    d = np.abs(got - want)
+    assert d.max() <= 1, d.max()
+    kcount = idx // 7 + 1
+    pow2 = (kcount & (kcount - 1)) == 0
+    assert (d[..., pow2, :] == 0).all()
+    # the exact quotients, rounded once: the oracle holds them
+    exact = np.zeros((B, H, S, D))
+    for i in range(S):
+        keep = (idx <= i) & (idx % 7 == i % 7)
+        exact[:, :, i] = v[:, :, keep].sum(axis=2) / keep.sum()
+    want_exact = enc(exact.astype(np.float32)).view(np.int16).astype(u)
+    np.testing.assert_array_equal(want, want_exact)
