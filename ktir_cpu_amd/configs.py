@@ -633,3 +633,322 @@ def flash_attention(B: int = 4, H: int = 32, S: int = 8192, D: int = 128, blk: i
   }}
 }}
 """
+
+
+# ---------------------------------------------------------------------------
+# 6. paged attention (unified 2-D attention over a paged KV cache)
+# ---------------------------------------------------------------------------
+
+def _gen2(ins, maps, out_t, args, body, res, indent="      "):
+    """A two-dimensional parallel linalg.generic with a scalar body."""
+    m = ", ".join(f"affine_map<(d0, d1) -> ({x})>" for x in maps)
+    i = ", ".join(n for n, _ in ins)
+    it = ", ".join(t for _, t in ins)
+    lines = [f"linalg.generic {{indexing_maps = [{m}],",
+             '    iterator_types = ["parallel", "parallel"]}',
+             f"    ins({i} : {it}) outs({res} : {out_t}) {{",
+             f"  ^bb0({args}):"] + [f"    {b}" for b in body] + [f"}} -> {out_t}"]
+    return ("\n" + indent).join(lines)
+
+
+def _gen1(ins, out_t, args, body, res, indent="      "):
+    """A one-dimensional parallel linalg.generic with identity maps."""
+    m = ", ".join(["affine_map<(d0) -> (d0)>"] * (len(ins) + 1))
+    i = ", ".join(n for n, _ in ins)
+    it = ", ".join(t for _, t in ins)
+    lines = [f'linalg.generic {{indexing_maps = [{m}], iterator_types = ["parallel"]}}',
+             f"    ins({i} : {it}) outs({res} : {out_t}) {{",
+             f"  ^bb0({args}):"] + [f"    {b}" for b in body] + [f"}} -> {out_t}"]
+    return ("\n" + indent).join(lines)
+
+
+def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head: int = 128,
+                    page: int = 16, blocks: int = 64, max_pages: int = 16, block_q: int = 2,
+                    total_tokens: int = 0) -> str:
+    """Causal grouped-query attention over a paged KV cache, in the form of
+    the reference's unified 2-D attention example
+    (examples/triton-ktir/paged_attention.mlir, parameters in its header and
+    tests/conftest.py:222-236).
+
+    query/output [total_tokens (default tokens), q_heads, head] f16; key/value caches
+    [blocks, page, kv_heads, head] f16; block_tables [1, max_pages] i32.
+    Grid [tokens / block_q, kv_heads]: core (p0, p1) takes query tokens
+    [start + p0*block_q, +block_q) of the q_heads/kv_heads query heads that
+    share KV head p1 (BM = block_q * group rows), then for j < num_tiles
+    reads page block_tables[0, offset + j] of K and V through indirect access
+    tiles, masks key position j*page + c above context_len + token position,
+    and keeps the online-softmax state (row max M, row sum L starting at 1,
+    f32 accumulator).  Output = acc / L, truncated to f16.
+    """
+    g = q_heads // kv_heads
+    bm = block_q * g
+    D = head
+    qs, cs = [max(total_tokens, tokens), q_heads, D], [blocks, page, kv_heads, D]
+    qst, cst = [q_heads * D, D, 1], [page * kv_heads * D, kv_heads * D, D, 1]
+    Q3 = _t([block_q, g, D], "f16")
+    Qh, Qf = _t([bm, D], "f16"), _t([bm, D], "f32")
+    K4 = _t([1, page, 1, D], "f16")
+    Kh, Kf = _t([page, D], "f16"), _t([page, D], "f32")
+    KTh, KTf = _t([D, page], "f16"), _t([D, page], "f32")
+    Sf, Vf = _t([bm, page], "f32"), _t([bm], "f32")
+    at_q = f"!ktdp.access_tile<{block_q}x{g}x{D}xindex>"
+    at_kv = f"!ktdp.access_tile<1x{page}x1x{D}xindex>"
+    vss = (f"affine_set<(d0, d1, d2, d3) : (d0 >= 0, -d0 >= 0, d1 >= 0, -d1 + {page - 1} >= 0, "
+           f"d2 >= 0, -d2 >= 0, d3 >= 0, -d3 + {D - 1} >= 0)>")
+
+    def kv_tile(name, view):
+        return (f"      %{name} = ktdp.construct_indirect_access_tile intermediate_variables(%e0, %e1, %e2, %e3)\n"
+                f"          %{view}[ind(%bt_view[%c0, %bt_col + %e0]), (%e1), (%p1 + %e2), (%e3)] {{\n"
+                f"        variables_space_set = {vss},\n"
+                f"        variables_space_order = affine_map<(d0, d1, d2, d3) -> (d0, d1, d2, d3)>\n"
+                f"      }} : memref<{'x'.join(map(str, cs))}xf16>, memref<1x{max_pages}xi32> -> {at_kv}")
+
+    mask = _gen2([("%s", Sf)], ["d0, d1", "d0, d1"], Sf, "%sv: f32, %o: f32", [
+        "%r = linalg.index 0 : index",
+        "%cc = linalg.index 1 : index",
+        "%tok = arith.divui %r, %cG : index",
+        "%qpos = arith.addi %p0_q, %tok : index",
+        "%qabs = arith.addi %context_len, %qpos : index",
+        "%kpos = arith.addi %k0, %cc : index",
+        "%keep = arith.cmpi ule, %kpos, %qabs : index",
+        "%mv = arith.select %keep, %sv, %neg_inf : f32",
+        "linalg.yield %mv : f32"], "%sm_init")
+    m_new = _gen1([("%M", Vf), ("%rm", Vf)], Vf, "%a: f32, %b: f32, %o: f32",
+                  ["%mx = arith.maximumf %a, %b : f32", "linalg.yield %mx : f32"], "%mn_init")
+    p = _gen2([("%sm", Sf), ("%m_new", Vf)], ["d0, d1", "d0", "d0, d1"], Sf, "%sv: f32, %mv: f32, %o: f32",
+              ["%dd = arith.subf %sv, %mv : f32", "%ee = math.exp %dd : f32", "linalg.yield %ee : f32"], "%p_init")
+    alpha = _gen1([("%M", Vf), ("%m_new", Vf)], Vf, "%a: f32, %b: f32, %o: f32",
+                  ["%dd = arith.subf %a, %b : f32", "%ee = math.exp %dd : f32", "linalg.yield %ee : f32"],
+                  "%al_init")
+    accs = _gen2([("%acc", Qf), ("%alpha", Vf)], ["d0, d1", "d0", "d0, d1"], Qf, "%av: f32, %al: f32, %o: f32",
+                 ["%sc = arith.mulf %av, %al : f32", "linalg.yield %sc : f32"], "%accs_init")
+    l_new = _gen1([("%L", Vf), ("%alpha", Vf), ("%ls", Vf)], Vf, "%l: f32, %al: f32, %lj: f32, %o: f32",
+                  ["%la = arith.mulf %l, %al : f32", "%ln = arith.addf %la, %lj : f32", "linalg.yield %ln : f32"],
+                  "%ln_init")
+    fin = _gen2([("%acc_f", Qf), ("%L_f", Vf)], ["d0, d1", "d0", "d0, d1"], Qf, "%av: f32, %lv: f32, %o: f32",
+                ["%qq = arith.divf %av, %lv : f32", "linalg.yield %qq : f32"], "%fin_init", "    ")
+    return f"""module {{
+  func.func @kernel_unified_attention_spyre_2d(%output_ptr: index, %query_ptr: index, %key_cache_ptr: index,
+      %value_cache_ptr: index, %block_tables_ptr: index, %cur_batch_start_index: index,
+      %block_table_offset: index, %num_tiles: index, %context_len: index, %scale: f32)
+      attributes {{grid = [{tokens // block_q}, {kv_heads}]}} {{
+    %p0, %p1 = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %cBQ = arith.constant {block_q} : index
+    %cG = arith.constant {g} : index
+    %cP = arith.constant {page} : index
+    %p0_q = arith.muli %p0, %cBQ : index
+    %q_row = arith.addi %cur_batch_start_index, %p0_q : index
+    %head0 = arith.muli %p1, %cG : index
+{_view("q_view", "query_ptr", qs, qst, "f16")}
+{_view("k_view", "key_cache_ptr", cs, cst, "f16")}
+{_view("v_view", "value_cache_ptr", cs, cst, "f16")}
+{_view("bt_view", "block_tables_ptr", [1, max_pages], [max_pages, 1], "i32")}
+{_view("o_view", "output_ptr", qs, qst, "f16")}
+{_tile("q_acc", "q_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, "f16")}
+    %q3 = ktdp.load %q_acc : {at_q} -> {Q3}
+    %qh = tensor.collapse_shape %q3 [[0, 1], [2]] : {Q3} into {Qh}
+    %q = arith.extf %qh : {Qh} to {Qf}
+    %neg_bits = arith.constant 0xFF800000 : i32
+    %neg_inf = arith.bitcast %neg_bits : i32 to f32
+    %zero = arith.constant 0.0 : f32
+    %one = arith.constant 1.0 : f32
+    %M0 = tensor.splat %neg_inf : {Vf}
+    %L0 = tensor.splat %one : {Vf}
+    %acc0 = tensor.splat %zero : {Qf}
+    %M_f, %L_f, %acc_f = scf.for %j = %c0 to %num_tiles step %c1
+        iter_args(%M = %M0, %L = %L0, %acc = %acc0) -> ({Vf}, {Vf}, {Qf}) {{
+      %bt_col = arith.addi %block_table_offset, %j : index
+{kv_tile("k_acc", "k_view")}
+{kv_tile("v_acc", "v_view")}
+      %k4 = ktdp.load %k_acc : {at_kv} -> {K4}
+      %v4 = ktdp.load %v_acc : {at_kv} -> {K4}
+      %kh = tensor.collapse_shape %k4 [[0, 1], [2, 3]] : {K4} into {Kh}
+      %kt_init = tensor.empty() : {KTh}
+      %kth = linalg.transpose ins(%kh : {Kh}) outs(%kt_init : {KTh}) permutation = [1, 0]
+      %vh = tensor.collapse_shape %v4 [[0, 1], [2, 3]] : {K4} into {Kh}
+      %kt = arith.extf %kth : {KTh} to {KTf}
+      %v = arith.extf %vh : {Kh} to {Kf}
+      %s_init = tensor.splat %zero : {Sf}
+      %qk = linalg.matmul ins(%q, %kt : {Qf}, {KTf}) outs(%s_init : {Sf}) -> {Sf}
+      %scale_t = tensor.splat %scale : {Sf}
+      %s = arith.mulf %scale_t, %qk : {Sf}
+      %k0 = arith.muli %j, %cP : index
+      %sm_init = tensor.empty() : {Sf}
+      %sm = {mask}
+      %rm_init = tensor.splat %neg_inf : {Vf}
+      %rm = linalg.reduce ins(%sm : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
+        (%a: f32, %b: f32) {{
+          %mx = arith.maximumf %a, %b : f32
+          linalg.yield %mx : f32
+        }}
+      %mn_init = tensor.empty() : {Vf}
+      %m_new = {m_new}
+      %p_init = tensor.empty() : {Sf}
+      %p = {p}
+      %ls_init = tensor.splat %zero : {Vf}
+      %ls = linalg.reduce ins(%p : {Sf}) outs(%ls_init : {Vf}) dimensions = [1]
+        (%a: f32, %b: f32) {{
+          %sum = arith.addf %a, %b : f32
+          linalg.yield %sum : f32
+        }}
+      %al_init = tensor.empty() : {Vf}
+      %alpha = {alpha}
+      %accs_init = tensor.empty() : {Qf}
+      %accs = {accs}
+      %acc_n = linalg.matmul ins(%p, %v : {Sf}, {Kf}) outs(%accs : {Qf}) -> {Qf}
+      %ln_init = tensor.empty() : {Vf}
+      %L_n = {l_new}
+      scf.yield %m_new, %L_n, %acc_n : {Vf}, {Vf}, {Qf}
+    }}
+    %fin_init = tensor.empty() : {Qf}
+    %of = {fin}
+    %oh = arith.truncf %of : {Qf} to {Qh}
+    %o3 = tensor.expand_shape %oh [[0, 1], [2]] output_shape [{block_q}, {g}, {D}] : {Qh} into {Q3}
+{_tile("o_acc", "o_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, "f16")}
+    ktdp.store %o3, %o_acc : {Q3}, {at_q}
+    return
+  }}
+}}
+"""
+
+
+# ---------------------------------------------------------------------------
+# 7. single-tile attention with f16 arithmetic, and rotary embedding
+# ---------------------------------------------------------------------------
+
+def sdpa_f16(n: int = 32, d: int = 64, rows: int = 32) -> str:
+    """out = softmax(Q K^T * 0.125) V with every step in f16, in the form of
+    the reference's examples/triton-ktir/sdpa_2d.mlir (f16 matmuls into f16
+    outs, linalg.fill inits, linalg.broadcast of the row max and row sum).
+
+    Q, K, V, out are [n, d] f16; grid [n / rows]: core p takes query rows
+    [p * rows, (p + 1) * rows) against all n keys."""
+    Qt, Kt, KTt, St, Rt = (_t([rows, d], "f16"), _t([n, d], "f16"), _t([d, n], "f16"),
+                           _t([rows, n], "f16"), _t([rows], "f16"))
+    vs = [n, d]
+
+    def load(name, view, row, shape):
+        at = "x".join(map(str, shape))
+        return (_tile(f"{name}_acc", view, [row, "%c0"], shape, vs, "f16") + "\n"
+                f"    %{name} = ktdp.load %{name}_acc : !ktdp.access_tile<{at}xindex> -> {_t(shape, 'f16')}")
+
+    return f"""module {{
+  func.func @sdpa_kernel_2d(%q_ptr: index, %k_ptr: index, %v_ptr: index, %output_ptr: index)
+      attributes {{grid = [{n // rows}]}} {{
+    %pid = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %cR = arith.constant {rows} : index
+    %zero = arith.constant 0.0 : f16
+    %scale = arith.constant 1.25e-01 : f16
+    %neg_inf = arith.constant 0xFC00 : f16
+    %row0 = arith.muli %pid, %cR : index
+{_view("q_view", "q_ptr", vs, [d, 1], "f16")}
+{_view("k_view", "k_ptr", vs, [d, 1], "f16")}
+{_view("v_view", "v_ptr", vs, [d, 1], "f16")}
+{_view("o_view", "output_ptr", vs, [d, 1], "f16")}
+{load("q", "q_view", "%row0", [rows, d])}
+{load("k", "k_view", "%c0", [n, d])}
+    %kt_init = tensor.empty() : {KTt}
+    %kt = linalg.transpose ins(%k : {Kt}) outs(%kt_init : {KTt}) permutation = [1, 0]
+    %qk_init = tensor.empty() : {St}
+    %qk = linalg.matmul ins(%q, %kt : {Qt}, {KTt}) outs(%qk_init : {St}) -> {St}
+    %scale_t = tensor.splat %scale : {St}
+    %s = arith.mulf %qk, %scale_t : {St}
+    %m_init = tensor.empty() : {Rt}
+    %m_fill = linalg.fill ins(%neg_inf : f16) outs(%m_init : {Rt}) -> {Rt}
+    %m = linalg.reduce {{ arith.maximumf }} ins(%s : {St}) outs(%m_fill : {Rt}) dimensions = [1]
+    %mb_init = tensor.empty() : {St}
+    %mb = linalg.broadcast ins(%m : {Rt}) outs(%mb_init : {St}) dimensions = [1]
+    %sh = arith.subf %s, %mb : {St}
+    %p = math.exp %sh : {St}
+    %l_init = tensor.empty() : {Rt}
+    %l_fill = linalg.fill ins(%zero : f16) outs(%l_init : {Rt}) -> {Rt}
+    %l = linalg.reduce {{ arith.addf }} ins(%p : {St}) outs(%l_fill : {Rt}) dimensions = [1]
+    %lb_init = tensor.empty() : {St}
+    %lb = linalg.broadcast ins(%l : {Rt}) outs(%lb_init : {St}) dimensions = [1]
+    %pn = arith.divf %p, %lb : {St}
+{load("v", "v_view", "%c0", [n, d])}
+    %acc_init = tensor.empty() : {Qt}
+    %acc_fill = linalg.fill ins(%zero : f16) outs(%acc_init : {Qt}) -> {Qt}
+    %acc = linalg.matmul ins(%pn, %v : {St}, {Kt}) outs(%acc_fill : {Qt}) -> {Qt}
+{_tile("o_acc", "o_view", ["%row0", "%c0"], [rows, d], vs, "f16")}
+    ktdp.store %acc, %o_acc : {Qt}, !ktdp.access_tile<{rows}x{d}xindex>
+    return
+  }}
+}}
+"""
+
+
+def rope(heads: int = 40, seq: int = 4096, head: int = 128, grid_s: int = 4, grid_h: int = 2,
+         tile: int = 256) -> str:
+    """Rotary position embedding in half layout, f16, in the form of the
+    reference's examples/latency/rope_fwd_4x2.mlir:
+    y[:, :D/2] = x1 * cos - x2 * sin, y[:, D/2:] = x1 * sin + x2 * cos,
+    with x1 / x2 the two halves of each [seq, head] row block of one head.
+
+    x / out are [heads * seq, head] f16, cos / sin [seq, head / 2] f16.
+    Grid [grid_s, grid_h]: core (ps, ph) takes positions
+    [ps * seq / grid_s, +seq / grid_s) in tiles of `tile` rows, and for each
+    tile the heads [ph * heads / grid_h, +heads / grid_h)."""
+    half = head // 2
+    per_s, per_h = seq // grid_s, heads // grid_h
+    T = _t([tile, half], "f16")
+    at = f"!ktdp.access_tile<{tile}x{half}xindex>"
+    xs, cs = [heads * seq, head], [seq, half]
+
+    def tl(name, view, row, col, vshape, indent):
+        return _tile(name, view, [row, col], [tile, half], vshape, "f16", indent)
+
+    return f"""module {{
+  func.func @rope_fwd_kernel(%x_ptr: index, %cos_ptr: index, %sin_ptr: index, %out_ptr: index)
+      attributes {{grid = [{grid_s}, {grid_h}]}} {{
+    %ps, %ph = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %cH = arith.constant {half} : index
+    %cT = arith.constant {tile} : index
+    %cS = arith.constant {seq} : index
+    %n_tiles = arith.constant {per_s // tile} : index
+    %n_heads = arith.constant {per_h} : index
+    %cPS = arith.constant {per_s} : index
+    %s0 = arith.muli %ps, %cPS : index
+    %h0 = arith.muli %ph, %n_heads : index
+{_view("x_view", "x_ptr", xs, [head, 1], "f16")}
+{_view("cos_view", "cos_ptr", cs, [half, 1], "f16")}
+{_view("sin_view", "sin_ptr", cs, [half, 1], "f16")}
+{_view("o_view", "out_ptr", xs, [head, 1], "f16")}
+    scf.for %t = %c0 to %n_tiles step %c1 {{
+      %toff = arith.muli %t, %cT : index
+      %pos = arith.addi %s0, %toff : index
+{tl("cos_acc", "cos_view", "%pos", "%c0", cs, "      ")}
+      %cos = ktdp.load %cos_acc : {at} -> {T}
+{tl("sin_acc", "sin_view", "%pos", "%c0", cs, "      ")}
+      %sin = ktdp.load %sin_acc : {at} -> {T}
+      scf.for %h = %c0 to %n_heads step %c1 {{
+        %hh = arith.addi %h0, %h : index
+        %hb = arith.muli %hh, %cS : index
+        %row = arith.addi %hb, %pos : index
+{tl("x1_acc", "x_view", "%row", "%c0", xs, "        ")}
+        %x1 = ktdp.load %x1_acc : {at} -> {T}
+{tl("x2_acc", "x_view", "%row", "%cH", xs, "        ")}
+        %x2 = ktdp.load %x2_acc : {at} -> {T}
+        %a = arith.mulf %x1, %cos : {T}
+        %b = arith.mulf %x2, %sin : {T}
+        %y1 = arith.subf %a, %b : {T}
+{tl("y1_acc", "o_view", "%row", "%c0", xs, "        ")}
+        ktdp.store %y1, %y1_acc : {T}, {at}
+        %c = arith.mulf %x1, %sin : {T}
+        %e = arith.mulf %x2, %cos : {T}
+        %y2 = arith.addf %c, %e : {T}
+{tl("y2_acc", "o_view", "%row", "%cH", xs, "        ")}
+        ktdp.store %y2, %y2_acc : {T}, {at}
+        scf.yield
+      }}
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""

@@ -442,13 +442,21 @@ def verify(accesses: List[Access], insts: Instances) -> Optional[str]:
             ok = True
             for a in lst:
                 c = _decompose(a.base, shape, strides)
-                if c is None or np.any(c % np.maximum(np.asarray(shape, dtype=np.int64), 1) != 0):
+                if c is None:
                     ok = False
                     break
                 cells.append(c)
                 inst_all.append(a.inst)
                 store_all.append(np.full(len(a.inst), a.store))
-            if ok:
+            aligned = ok and not any(np.any(c % np.maximum(np.asarray(shape, dtype=np.int64), 1) != 0)
+                                     for c in cells)
+            if ok and not aligned and _no_carry(np.concatenate(cells), shape, strides):
+                why = _box_hazard(np.concatenate(cells), shape, np.concatenate(inst_all),
+                                  np.concatenate(store_all), insts, name)
+                if why is not None:
+                    return why
+                continue
+            if aligned:
                 cells = np.concatenate(cells)
                 inst_all = np.concatenate(inst_all)
                 store_all = np.concatenate(store_all)
@@ -494,6 +502,61 @@ def verify(accesses: List[Access], insts: Instances) -> Optional[str]:
                 i -= 1
                 if j - i > 64:
                     return f"{name!r}: overlapping accesses between lanes"
+    return None
+
+
+def _no_carry(c: np.ndarray, shape, strides) -> bool:
+    """Whether boxes of `shape` at digit coordinates `c` (rows, from
+    `_decompose`) stay inside each digit's range: then two boxes share an
+    element exactly when their coordinates differ by less than the shape in
+    every dimension."""
+    st = list(strides)
+    order = sorted(range(len(st)), key=lambda d: -st[d])
+    for p in range(1, len(order)):
+        d, up = order[p], order[p - 1]
+        if np.any(c[:, d] + shape[d] > st[up] // st[d]):
+            return False
+    return True
+
+
+def _box_hazard(c: np.ndarray, shape, inst: np.ndarray, store: np.ndarray, insts: Instances,
+                name) -> Optional[str]:
+    """Exact conflict test for equal boxes that need not sit on multiples of
+    their shape (a tile that starts at row 9 of 2-row tiles): each box
+    touches at most two shape-sized grid cells per dimension, boxes that
+    share no grid cell share no element, and the candidates that do share
+    one are compared coordinate by coordinate."""
+    shp = np.maximum(np.asarray(shape, dtype=np.int64), 1)
+    g = c // shp
+    un = np.flatnonzero(np.any(c % shp != 0, axis=0))
+    if len(un) > 6:
+        return f"{name!r}: overlapping accesses between lanes"
+    n = len(c)
+    keys = []
+    for bits in range(1 << len(un)):
+        gg = g.copy()
+        for k, d in enumerate(un):
+            if bits >> k & 1:
+                gg[:, d] += 1
+        keys.append(gg)
+    owner = np.tile(np.arange(n, dtype=np.int64), 1 << len(un))
+    _, kid = np.unique(np.concatenate(keys), axis=0, return_inverse=True)
+    kid = kid.reshape(-1)
+    order = np.argsort(kid, kind="stable")
+    kid, owner = kid[order], owner[order]
+    big = int(np.unique(kid, return_counts=True)[1].max())
+    if big > 64:
+        return f"{name!r}: many tiles shared between lanes"
+    for k in range(1, big):
+        same = kid[k:] == kid[:-k]
+        i, j = owner[:-k][same], owner[k:][same]
+        hit = (np.all(np.abs(c[i] - c[j]) < shp, axis=1) & (store[i] | store[j]) & (inst[i] != inst[j]))
+        pairs = np.flatnonzero(hit)
+        if len(pairs) > 4096:
+            return f"{name!r}: many tiles shared between lanes"
+        for q in pairs:
+            if not insts.comparable(int(inst[i[q]]), int(inst[j[q]])):
+                return f"{name!r}: overlapping accesses between lanes"
     return None
 
 

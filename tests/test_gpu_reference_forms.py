@@ -1,0 +1,74 @@
+"""GPU parity for the paged attention, single-tile f16 attention and rotary
+embedding forms of the reference's examples, on the kernels whose oracle
+results tests/test_oracle_example_pins.py pins against closed forms (and
+against the example files themselves).
+
+Bars: RoPE is f16 multiply / add / subtract only, so bit-exact; the two
+attention forms meet the north star's rtol 1e-2 / atol 1e-3 (matmul and
+softmax), the f16 one with every intermediate rounded to f16 as the oracle
+does."""
+import numpy as np
+import pytest
+
+from ktir_cpu_amd import configs
+from oracle.interp import OracleInterpreter
+from tests.test_oracle_example_pins import (PA_ARGS, PA_CASES, PA_FN, paged_inputs, rope_inputs, sdpa_inputs)
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(src, fn, kw, out):
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    o = OracleInterpreter()
+    o.load(src)
+    ref = o.execute_function(fn, **{k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in kw.items()})[out]
+    g = KTIRInterpreter()
+    g.load(src)
+    got = g.execute_function(fn, **kw)[out]
+    print("  ", g.last_plan.mode, g.last_plan.counts(), g.last_plan.fallback_reason, flush=True)
+    return got, ref, g.last_plan
+
+
+@pytest.mark.parametrize("gen,inp,args", [c[1:] for c in PA_CASES], ids=[c[0] for c in PA_CASES])
+def test_paged_attention_within_tolerance(gen, inp, args):
+    kw = dict(paged_inputs(**inp), **args)
+    got, ref, plan = _both(configs.paged_attention(**gen), PA_FN, kw, "output_ptr")
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+    # the output tiles of an odd batch start sit off the 2-row grid but are
+    # disjoint: the lanes still run together
+    assert plan.mode == "lockstep"
+
+
+def test_paged_attention_many_tokens_within_tolerance():
+    """64 tokens of one sequence over a 512-block cache: 32 x 8 cores, each
+    through 40 pages of the table (640 keys)."""
+    gen = dict(tokens=64, q_heads=32, kv_heads=8, head=128, page=16, blocks=512, max_pages=64, block_q=2)
+    kw = dict(paged_inputs(tokens=64, blocks=512, max_pages=64, seed=7),
+              **dict(PA_ARGS, num_tiles=40, context_len=576, block_table_offset=3))
+    got, ref, _ = _both(configs.paged_attention(**gen), PA_FN, kw, "output_ptr")
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("n,d,rows", [(32, 64, 32), (256, 128, 64)])
+def test_sdpa_f16_within_tolerance(n, d, rows):
+    kw = sdpa_inputs(n, d, seed=n)
+    got, ref, _ = _both(configs.sdpa_f16(n, d, rows), "sdpa_kernel_2d", kw, "output_ptr")
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("zero", [False, True], ids=["normal", "zero_input"])
+def test_rope_example_size_bit_exact(zero):
+    """The example's size: 40 heads x 4096 positions x 128, grid [4, 2]."""
+    kw = rope_inputs(zero=zero)
+    got, ref, plan = _both(configs.rope(), "rope_fwd_kernel", kw, "out_ptr")
+    np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
+    assert plan.mode == "lockstep"
+
+
+def test_rope_odd_grid_bit_exact():
+    H, S, D = 6, 768, 64
+    kw = rope_inputs(H, S, D, seed=9)
+    got, ref, _ = _both(configs.rope(H, S, D, grid_s=3, grid_h=3, tile=128), "rope_fwd_kernel", kw, "out_ptr")
+    np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))

@@ -62,6 +62,48 @@ def test_verify_data_dependent_store_needs_one_lane():
     assert verify([_acc(a, True, [0, 1], [0, 0], whole=True, group=7)], ins) is None
 
 
+def _brute_conflict(bases, stores, inst, shape, strides):
+    cells = []
+    for b in bases:
+        idx = np.indices(shape).reshape(len(shape), -1)
+        cells.append(set((b + np.tensordot(np.asarray(strides), idx, 1)).tolist()))
+    for i in range(len(bases)):
+        for j in range(i + 1, len(bases)):
+            if inst[i] != inst[j] and (stores[i] or stores[j]) and cells[i] & cells[j]:
+                return True
+    return False
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_verify_unaligned_equal_tiles_exact(seed):
+    """Equal tiles at arbitrary (not shape-aligned) starts: verify flags a
+    conflict exactly when two lanes' element sets meet and one of them
+    stores, checked by brute force on the element sets."""
+    rng = np.random.default_rng(seed)
+    shape = (2, 3) if seed % 2 else (2, 3, 4)
+    vshape = (12, 9) if seed % 2 else (6, 5, 8)
+    strides = tuple(int(np.prod(vshape[d + 1:])) for d in range(len(vshape)))
+    n = int(rng.integers(2, 6))
+    starts = [tuple(int(rng.integers(0, v - s + 1)) for v, s in zip(vshape, shape)) for _ in range(n)]
+    bases = [int(np.dot(st, strides)) for st in starts]
+    stores = [bool(rng.integers(0, 2)) or k == 0 for k in range(n)]
+    a = Alloc("y", "f16", 0x10000, 2 * int(np.prod(vshape)), vshape)
+    ins = Instances(n)
+    acc = [_acc(a, st, [k], [b], shape=shape, strides=strides) for k, (b, st) in enumerate(zip(bases, stores))]
+    want = _brute_conflict(bases, stores, list(range(n)), shape, strides)
+    assert (verify(acc, ins) is not None) == want
+
+
+def test_verify_unaligned_row_pairs_pass():
+    """Tiles of 2 rows x 4 heads starting at row 9 (an odd batch start), the
+    shape of the paged attention output store: disjoint, so accepted."""
+    a = Alloc("o", "f16", 0x10000, 2 * 20 * 32 * 128, (20, 32, 128))
+    ins = Instances(32)
+    bases = [(9 + 2 * p0) * 4096 + 4 * p1 * 128 for p0 in range(4) for p1 in range(8)]
+    acc = [_acc(a, True, list(range(32)), bases, shape=(2, 4, 128), strides=(4096, 128, 1))]
+    assert verify(acc, ins) is None
+
+
 @pytest.mark.parametrize("strides,old,new,expect", [
     ((8192 * 128, 128, 1), (1, 128, 128), (128, 128), (128, 1)),
     ((4096, 1), (8, 4096), (8 * 4096,), (1,)),
