@@ -173,9 +173,49 @@ def _attention():
                 workload=f"flash_attention causal B={B} H={H} S={S} D={D} kv_tile=128")
 
 
+def _rope():
+    from ktir_cpu_amd import configs
+    H, S, D = 40, 4096, 128
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((H * S, D), dtype=np.float32).astype(np.float16)
+    freq = 10000.0 ** (-np.arange(D // 2, dtype=np.float64) * 2.0 / D)
+    ang = np.outer(np.arange(S, dtype=np.float64), freq)
+    kw = dict(x_ptr=x, cos_ptr=np.cos(ang).astype(np.float16), sin_ptr=np.sin(ang).astype(np.float16),
+              out_ptr=np.zeros_like(x))
+    return dict(src=configs.rope(H, S, D, 4, 2, 256), fn="rope_fwd_kernel", kw=kw, cores=8,
+                bytes=2 * H * S * D * 2 + 2 * S * (D // 2) * 2, flops=6 * H * S * D // 2, bound="hbm",
+                dtype="f16 (products, sum and difference each rounded to f16)",
+                workload=f"rope H={H} S={S} D={D} f16 grid=4x2 seq tile 256 (the reference's "
+                         f"latency/rope_fwd_4x2 form)")
+
+
+def _paged_attention():
+    from ktir_cpu_amd import configs
+    T, HQ, HK, D, P, BQ, ctx = 256, 32, 8, 128, 16, 2, 1024
+    nt = (ctx + T + P - 1) // P
+    blocks, max_pages = 2 * nt, nt
+    rng = np.random.default_rng(42)
+    kw = dict(output_ptr=np.zeros((T, HQ, D), np.float16),
+              query_ptr=rng.standard_normal((T, HQ, D), dtype=np.float32).astype(np.float16),
+              key_cache_ptr=rng.standard_normal((blocks, P, HK, D), dtype=np.float32).astype(np.float16),
+              value_cache_ptr=rng.standard_normal((blocks, P, HK, D), dtype=np.float32).astype(np.float16),
+              block_tables_ptr=rng.permutation(blocks)[:max_pages].astype(np.int32).reshape(1, max_pages),
+              cur_batch_start_index=0, block_table_offset=0, num_tiles=nt, context_len=ctx,
+              scale=1.0 / math.sqrt(D))
+    # causal keys per token: ctx + t + 1; executed keys: all nt pages
+    keys = sum(ctx + t + 1 for t in range(T))
+    return dict(src=configs.paged_attention(T, HQ, HK, D, P, blocks, max_pages, BQ), fn="kernel_unified_attention_spyre_2d",
+                kw=kw, cores=(T // BQ) * HK, bytes=2 * HQ * T * D * 2 + 2 * blocks * P * HK * D * 2,
+                flops=4 * HQ * keys * D, bound="mfma",
+                dtype="f16 in/out; f32 Q K^T, scores, online-softmax state and P V",
+                workload=f"paged attention {T} tokens after a {ctx}-token context, {HQ} query / {HK} KV heads, "
+                         f"D={D}, page {P}, {BQ} tokens per core (the reference's triton-ktir paged_attention form)")
+
+
 CONFIGS = {"vector_add": _vector_add, "vector_add_4096": _vector_add_4096, "copy": _copy, "gather": _gather, "softmax": _softmax, "rmsnorm": _rmsnorm,
            "gemm": _gemm, "attention": _attention, "softmax_extract": _softmax_extract,
-           "rmsnorm_extract": _rmsnorm_extract}
+           "rmsnorm_extract": _rmsnorm_extract, "rope": _rope,
+           "paged_attention": _paged_attention}
 
 
 # kernels that make up each kind of launch (the HIP kernel names)

@@ -401,6 +401,40 @@ typedef struct ktir_attn {
 } ktir_attn_t;
 int ktir_launch_attention(const ktir_attn_t* d);
 
+/* ---- paged attention (reference examples/triton-ktir/paged_attention.mlir:194-392,
+ * executed op by op per core and iteration by dialects/linalg_ops.py:307-596) ----
+ * For every lane l, `trips[l]` iterations j of the online-softmax loop over
+ * pages of a K / V cache, starting from m = m0, l = l0, acc = 0:
+ *   page  = tbl[tbl_pos[l] + j * tbl_step]  (an index outside [tbl_lo, tbl_hi)
+ *           reads 0; a negative one sets the device error flag and reads 0)
+ *   K[c][x] = k[k_base[l] + page * k_page + c * k_row + x]   (c < N, x < D;
+ *           outside [k_lo, k_hi) reads 0), V likewise
+ *   s[r][c] = scale * sum_x Q[r][x] K[c][x], Q[r][x] = q[q_base[l] + r * q_row + x]
+ *   causal: s = neg unless pred(kpos0[l] + j * kpos_step + c, qpos0[l] + r / row_div)
+ *   m' = maximumf(m, max_c s); p = exp(s - m'); alpha = exp(m - m')
+ *   acc' = acc * alpha + p V; l' = l * alpha + sum_c p; m = m'
+ * all in f32.  Final m, l -> m_out / l_out [lanes, M], acc -> acc_out
+ * [lanes, M, D].  Limits: M * D <= 8192; LDS 4 * (M (D+1) + N (D+1) + N D +
+ * M N + 3 M) bytes <= 160 KiB. */
+typedef struct ktir_pattn {
+  int64_t lanes, M, N, D;
+  uint64_t q_ptr, q_base;              /* q_base: const int64_t* [lanes] */
+  int64_t q_row, q_lo, q_hi;
+  int32_t q_dtype, kv_dtype;           /* KTIR_F16, KTIR_BF16 or KTIR_F32 */
+  uint64_t k_ptr, v_ptr, k_base, v_base;
+  int64_t k_row, v_row, k_page, v_page, k_lo, k_hi, v_lo, v_hi;
+  uint64_t tbl_ptr, tbl_pos;           /* tbl_pos: const int64_t* [lanes] */
+  int64_t tbl_step, tbl_lo, tbl_hi;
+  int32_t tbl_dtype, pred;             /* KTIR_I8 / I16 / I32 / I64; KTIR_CMP_* keep predicate */
+  uint64_t trips;                      /* const int32_t* [lanes] */
+  uint64_t qpos0, kpos0;               /* const int64_t* [lanes] */
+  int64_t kpos_step, row_div;
+  int32_t causal, pad;
+  float scale, neg, m0, l0;
+  uint64_t m_out, l_out, acc_out;
+} ktir_pattn_t;
+int ktir_launch_paged_attention(const ktir_pattn_t* d);
+
 #ifdef __cplusplus
 }
 #endif

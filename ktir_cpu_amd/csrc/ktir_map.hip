@@ -6,7 +6,7 @@
 // flight before it computes.  The register ops still come from the
 // program, evaluated per element with the same semantics as the general
 // interpreter (ktir_program.hip).
-#include "ktir_program_impl.h"
+#include "ktir_regops.h"
 
 namespace ktir {
 
@@ -98,39 +98,16 @@ struct Reg4 {
   }
 };
 
-__device__ __forceinline__ void exec_reg4(const ktir_prog_t& P, const ktir_instr_t in, Reg4& R, int64_t lane) {
-  const int op = in.op;
-  const float a = R.get(in.a), b = R.get(in.b);
-  float v;
-  if (op >= KTIR_OP_NEGF && op < KTIR_OP_ADDF) {
-    v = unop_simple(op, in.dt, a);
-  } else if (op >= KTIR_OP_ADDF && op < KTIR_OP_ADDI) {
-    v = binop_f_simple(op, in.dt, a, b);
-  } else if (op >= KTIR_OP_ADDI) {
-    v = __int_as_float(binop_i_simple(op, __float_as_int(a), __float_as_int(b)));
-  } else {
-    switch (op) {
-      case KTIR_OP_CONST: v = __int_as_float(in.imm); break;
-      case KTIR_OP_LANE: {
-        double d = ((const double*)P.lane_scalars)[lane * P.n_lane_scalars + in.aux];
-        v = is_float_dt(in.dt) ? round_to((float)d, in.dt) : __int_as_float((int)(long long)d);
-        break;
-      }
-      case KTIR_OP_CAST: v = cast_val(a, in.aux, in.dt); break;
-      case KTIR_OP_BITCAST: v = a; break;
-      case KTIR_OP_SELECT: v = __float_as_int(a) ? b : R.get(in.c); break;
-      case KTIR_OP_FMA: v = round_to(__fadd_rn(__fmul_rn(a, b), R.get(in.c)), in.dt); break;
-      case KTIR_OP_CMPF: v = __int_as_float(cmp_f(in.aux, a, b)); break;
-      case KTIR_OP_CMPI: v = __int_as_float(cmp_i(in.aux, __float_as_int(a), __float_as_int(b))); break;
-      default: v = 0.f;
-    }
-  }
-  R.set(in.dst, v);
+template <class RG>
+__device__ __forceinline__ void exec_reg(const ktir_prog_t& P, const ktir_instr_t in, RG& R, int64_t lane) {
+  const bool third = in.op == KTIR_OP_SELECT || in.op == KTIR_OP_FMA;
+  R.set(in.dst, exec_val(P, in, R.get(in.a), R.get(in.b), third ? R.get(in.c) : 0.f, lane));
 }
 
 // One instruction over the 8 elements of a chunk; the opcode switch is
 // taken once (it is uniform), the common ops run as straight loops.
-__device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t in, Reg4 (&R)[8], int64_t lane) {
+template <class RG>
+__device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t in, RG (&R)[8], int64_t lane) {
   const int op = in.op, dt = in.dt;
 #define EACH(expr)                                                          \
   _Pragma("unroll") for (int e = 0; e < 8; ++e) {                           \
@@ -151,7 +128,7 @@ __device__ __forceinline__ void exec8(const ktir_prog_t& P, const ktir_instr_t i
   }
 #undef EACH
 #pragma unroll
-  for (int e = 0; e < 8; ++e) exec_reg4(P, in, R[e], lane);
+  for (int e = 0; e < 8; ++e) exec_reg(P, in, R[e], lane);
 }
 
 // element offsets of chunk vid in the two inputs and the output

@@ -192,7 +192,9 @@ __device__ void fold_row(float* red, int64_t n, int op, int dt) {
 
 template <int V>
 __global__ __launch_bounds__(256) void prog_rows(const ktir_prog_t P, int64_t total_rows) {
-  __shared__ float red[KTIR_MAX_ROW];
+  // one row's values for the fold: `inner` floats of dynamic LDS, so short
+  // rows leave room for many workgroups per CU
+  extern __shared__ float red[];
   const int nd = P.ndim;
   const int64_t inner = P.shape[nd - 1];
   int64_t rows_per_lane = 1;
@@ -242,6 +244,7 @@ using namespace ktir;
 
 namespace ktir {
 bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner);
+bool try_launch_tile(const ktir_prog_t& Q, int64_t lanes, int64_t per_lane, int64_t inner);
 bool try_launch_rows(const ktir_prog_t& P, int64_t rows, int64_t inner);
 int64_t row_grid_limit(int64_t blocks);
 }
@@ -282,6 +285,10 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
     }
     dim3 b(256);
     uint32_t nv = (uint32_t)vecs;
+    if (!full && try_launch_tile(*P, P->lanes, per_lane, inner)) {
+      KTIR_HIP_CHECK(hipGetLastError());
+      return KTIR_OK;
+    }
     if (lean) {
       if (try_launch_map(*P, rows, inner)) {
         KTIR_HIP_CHECK(hipGetLastError());
@@ -329,10 +336,11 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
     int64_t blocks = row_grid_limit(rows < 65536 ? rows : 65536);
     int64_t per = v4 ? inner / 4 : inner;
     int threads = per >= 256 ? 256 : (int)((per + 63) / 64 * 64);
+    const size_t lds = (size_t)inner * sizeof(float);
     if (v4)
-      hipLaunchKernelGGL(prog_rows<4>, dim3((unsigned)blocks), dim3(threads), 0, stream(), *P, rows);
+      hipLaunchKernelGGL(prog_rows<4>, dim3((unsigned)blocks), dim3(threads), lds, stream(), *P, rows);
     else
-      hipLaunchKernelGGL(prog_rows<1>, dim3((unsigned)blocks), dim3(threads), 0, stream(), *P, rows);
+      hipLaunchKernelGGL(prog_rows<1>, dim3((unsigned)blocks), dim3(threads), lds, stream(), *P, rows);
   }
   KTIR_HIP_CHECK(hipGetLastError());
   return KTIR_OK;

@@ -656,6 +656,8 @@ def _launch(L, kind, desc):
         rt.check(L.ktir_launch_row_rmw(C.byref(desc)), "ktir_launch_row_rmw")
     elif kind == "attn":
         rt.check(L.ktir_launch_attention(C.byref(desc)), "ktir_launch_attention")
+    elif kind == "pattn":
+        rt.check(L.ktir_launch_paged_attention(C.byref(desc)), "ktir_launch_paged_attention")
     elif kind == "memset":
         ptr, val, nbytes = desc
         rt.check(L.ktir_memset(ptr, val, nbytes), "ktir_memset")

@@ -20,7 +20,7 @@ from typing import List, Optional
 import numpy as np
 
 from .affine import Box
-from .executor import ATile, NeedEager, Tile, V16Copy
+from .executor import ATile, IATile, NeedEager, Tile, V16Copy
 
 _SCALAR_OPS_PREFIX = ("arith.",)
 _SKIP = {"ktdp.load", "arith.extf", "linalg.matmul", "scf.yield"}
@@ -479,10 +479,13 @@ def _peel(by_res, name):
 def _mask_lin(ex, mask_op, L):
     """Evaluate a causal-mask generic body on the host.
 
-    Index values are kept as ``c[lane] + a*row + b*col``; the body must be
-    ``select(cmpi(pred, kpos, qpos), s, neg)`` (either operand order of the
-    compare and of the select) with kpos = c_k + col and qpos = c_q + row.
-    Returns (pred, c_k, c_q, neg) or None."""
+    Index values are kept as ``c[lane] + a * (row // g) + b * col``; the
+    body must be ``select(cmpi(pred, kpos, qpos), s, neg)`` (either operand
+    order of the compare and of the select) with kpos = c_k + col and
+    qpos = c_q + row // g (g = 1 unless the row index is divided by a
+    constant: the query-token position of grouped query heads, as in
+    ``examples/triton-ktir/paged_attention.mlir:273-295``).
+    Returns (pred, c_k, c_q, neg, g) or None."""
     region = mask_op.regions[0]
     sv = region.args[0][0]
     env = {}
@@ -496,21 +499,24 @@ def _mask_lin(ex, mask_op, L):
         arr = np.broadcast_to(np.asarray(v), (L,))
         if not np.issubdtype(arr.dtype, np.integer):
             raise NeedEager("mask operand")
-        return (arr.astype(np.int64), 0, 0)
+        return (arr.astype(np.int64), 0, 0, 1)
 
     cmp = None
     try:
         for x in region.ops:
             t, r = x.op_type, (x.results[0] if x.results else None)
             if t == "linalg.index":
-                env[r] = (np.zeros(L, np.int64), 1, 0) if x.attributes.get("dim") == 0 else (np.zeros(L, np.int64), 0, 1)
+                env[r] = (np.zeros(L, np.int64), 1, 0, 1) if x.attributes.get("dim") == 0 \
+                    else (np.zeros(L, np.int64), 0, 1, 1)
             elif t == "arith.constant" and isinstance(x.attributes.get("value"), int) \
                     and not isinstance(x.attributes.get("value"), bool):
-                env[r] = (np.full(L, x.attributes["value"], np.int64), 0, 0)
+                env[r] = (np.full(L, x.attributes["value"], np.int64), 0, 0, 1)
             elif t in ("arith.addi", "arith.subi"):
                 a, b = val(x.operands[0]), val(x.operands[1])
+                if a[1] and b[1] and a[3] != b[3]:
+                    return None
                 sg = 1 if t == "arith.addi" else -1
-                env[r] = (a[0] + sg * b[0], a[1] + sg * b[1], a[2] + sg * b[2])
+                env[r] = (a[0] + sg * b[0], a[1] + sg * b[1], a[2] + sg * b[2], a[3] if a[1] else b[3])
             elif t == "arith.muli":
                 a, b = val(x.operands[0]), val(x.operands[1])
                 if a[1] == 0 and a[2] == 0 and np.all(a[0] == a[0][0]):
@@ -518,7 +524,20 @@ def _mask_lin(ex, mask_op, L):
                 if b[1] != 0 or b[2] != 0 or not np.all(b[0] == b[0][0]):
                     return None
                 k = int(b[0][0])
-                env[r] = (a[0] * k, a[1] * k, a[2] * k)
+                env[r] = (a[0] * k, a[1] * k, a[2] * k, a[3])
+            elif t in ("arith.divui", "arith.divsi", "arith.floordivsi"):
+                a, b = val(x.operands[0]), val(x.operands[1])
+                if b[1] != 0 or b[2] != 0 or not np.all(b[0] == b[0][0]) or int(b[0][0]) <= 0:
+                    return None
+                k = int(b[0][0])
+                if a[1] == 0 and a[2] == 0:
+                    if np.any(a[0] < 0) and t != "arith.floordivsi":
+                        return None
+                    env[r] = (a[0] // k, 0, 0, 1)
+                elif a[2] == 0 and a[1] == 1 and not np.any(a[0]):
+                    env[r] = (a[0], 1, 0, a[3] * k)     # (row // g) // k == row // (g k)
+                else:
+                    return None
             elif t in ("arith.index_cast", "arith.index_castui"):
                 env[r] = val(x.operands[0])
             elif t == "arith.cmpi":
@@ -547,7 +566,7 @@ def _mask_lin(ex, mask_op, L):
                 nv = np.asarray(ex.get_value(neg_n, peek=True), dtype=np.float64).ravel()
                 if nv.size == 0 or np.any(nv != nv[0]) and not np.all(np.isnan(nv)):
                     return None
-                env[r] = ("sel", p, kp[0], qp[0], float(nv[0]))
+                env[r] = ("sel", p, kp[0], qp[0], float(nv[0]), qp[3])
             elif t == "linalg.yield":
                 y = env.get(x.operands[0]) if len(x.operands) == 1 else None
                 if not isinstance(y, tuple) or y[0] != "sel":
@@ -717,7 +736,8 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     for o in body:
         if id(o) in matched:
             continue
-        if o.op_type in ("ktdp.construct_access_tile", "tensor.empty", "tensor.splat", "arith.constant") \
+        if o.op_type in ("ktdp.construct_access_tile", "ktdp.construct_indirect_access_tile", "tensor.empty", "tensor.splat",
+                         "arith.constant") \
                 or (o.op_type.startswith("arith.") and not o.regions and not _is_tensor(o)):
             continue
         return None
@@ -730,24 +750,16 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     L = ex.L
     if L == 0:
         return None
-    # initial state: m = -inf, l = 0, acc = 0
+    # initial state: m = -inf, acc = 0 and l = 0 (l may start at any constant
+    # in the paged form: examples/triton-ktir/paged_attention.mlir:222 sets 1)
     def const_of(v):
         return float(v.e.attr) if isinstance(v, Tile) and v.e.kind == "const" else None
-    if const_of(inits[im]) != -np.inf or const_of(inits[il]) != 0.0 or const_of(inits[ia]) != 0.0:
+    l0 = const_of(inits[il])
+    if const_of(inits[im]) != -np.inf or const_of(inits[ia]) != 0.0 or l0 is None:
         return None
     q = ex.get_value(q_name, peek=True)
     if not isinstance(q, Tile):
         return None
-    qe = q.e
-    if not (qe.kind == "cast" and qe.dtype == "f32" and qe.attr in ("f16", "bf16") and qe.args[0].kind == "ld"
-            and qe.args[0].attr.offsets is None):
-        return None
-    q_leaf = qe.args[0].attr
-    AT = 128
-    if tuple(q.shape) != (AT, AT) or len(q_leaf.strides) < 2 or q_leaf.strides[-1] != 1 \
-            or any(s != 0 for s in q_leaf.strides[:-2]):
-        return None
-    dtype = q_leaf.dtype
     probe = [o for o in body if id(o) not in matched]
     iv = op.attributes["iter_var"]
     k_ld, v_ld = pk[0], pv[0]
@@ -782,16 +794,31 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     if mask_op is not None:
         if p0["mask"] is None or p1["mask"] is None or pl["mask"] is None:
             return None
-        pred, ck0, cq0, neg = p0["mask"]
-        _, ck1, cq1, _ = p1["mask"]
-        _, ckl, cql, _ = pl["mask"]
+        pred, ck0, cq0, neg, row_div = p0["mask"]
+        _, ck1, cq1, _, g1 = p1["mask"]
+        _, ckl, cql, _, gl = pl["mask"]
         kstep = ck1 - ck0
         if np.any(kstep != kstep[0]) or not np.array_equal(cq0, cq1) or not np.array_equal(cq0, cql) \
-                or not np.array_equal(ckl, ck0 + tm1 * kstep[0]):
+                or not np.array_equal(ckl, ck0 + tm1 * kstep[0]) or not row_div == g1 == gl:
             return None
         kpos_step = int(kstep[0])
     else:
-        pred, ck0, cq0, neg, kpos_step = "EQ", np.zeros(L, np.int64), np.zeros(L, np.int64), 0.0, 0
+        pred, ck0, cq0, neg, kpos_step, row_div = "EQ", np.zeros(L, np.int64), np.zeros(L, np.int64), 0.0, 0, 1
+    if isinstance(p0["k"], IATile) and isinstance(p0["v"], IATile):
+        return _paged_attention(ex, trips, tm1, q, (p0, p1, pl), (pk, pv), l0, (im, il, ia),
+                                (mask_op is not None, pred, ck0, cq0, neg, kpos_step, row_div))
+    if l0 != 0.0 or row_div != 1:
+        return None
+    qe = q.e
+    if not (qe.kind == "cast" and qe.dtype == "f32" and qe.attr in ("f16", "bf16") and qe.args[0].kind == "ld"
+            and qe.args[0].attr.offsets is None):
+        return None
+    q_leaf = qe.args[0].attr
+    AT = 128
+    if tuple(q.shape) != (AT, AT) or len(q_leaf.strides) < 2 or q_leaf.strides[-1] != 1 \
+            or any(s != 0 for s in q_leaf.strides[:-2]):
+        return None
+    dtype = q_leaf.dtype
     # K and V tiles: base offsets at iteration 0, uniform step, in bounds for every iteration run
     tiles = {}
     for key, ld in (("k", k_ld), ("v", v_ld)):
@@ -892,6 +919,124 @@ def _attention_loop(ex, op, lb, st, trips, inits):
     res[im], res[il] = vec(m_buf), vec(l_buf)
     res[ia] = Tile(Expr("ld", "f32", (AT, AT), attr=LeafSpec(a_buf.ptr, "f32", LaneOff(0, AT * AT), (AT, 1), 0,
                                                                L * AT * AT, keep=(a_buf,))))
+    return res
+
+
+def _paged_attention(ex, trips, tm1, q, probes, peeled, l0, slots, mask):
+    """Lower the online-softmax loop whose K and V tiles are pages of a
+    cache read through a block table (indirect access tiles whose only
+    indirect subscript is the page, as in the reference's
+    ``examples/triton-ktir/paged_attention.mlir:239-262``) to one
+    ``ktir_launch_paged_attention`` launch.  Checked on the host from the
+    iterations 0, 1 and the last of every lane: each K / V tile is an N x D
+    row-major block at a fixed lane offset plus page * page stride, the
+    page's position in the table advances by one fixed step, and Q is one
+    strided M x D tile.  Returns the loop results or None (op-by-op walk)."""
+    from . import runtime as rt
+    from .program import LeafSpec, LaneOff, Expr
+    p0, p1, pl = probes
+    im, il, ia = slots
+    causal, pred, ck0, cq0, neg, kpos_step, row_div = mask
+    L = ex.L
+    qe = q.e
+    if qe.kind == "cast" and qe.dtype == "f32" and qe.attr in ("f16", "bf16") and qe.args[0].kind == "ld":
+        ql = qe.args[0].attr
+    elif qe.kind == "ld" and qe.dtype == "f32":
+        ql = qe.attr
+    else:
+        return None
+    if len(q.shape) != 2 or ql.offsets is not None or ql.winner is not None or len(ql.strides) != 2 \
+            or ql.strides[-1] != 1:
+        return None
+    M, D = (int(x) for x in q.shape)
+    kv = {}
+    for key, peel in (("k", peeled[0]), ("v", peeled[1])):
+        coll = [o for o in peel[1] if o.op_type == "tensor.collapse_shape"]
+        if len(coll) != 1 or tuple(getattr(coll[0].result_types[0], "shape", ())) [-1:] != (D,):
+            return None
+        N = int(coll[0].result_types[0].shape[0])
+        parts = []
+        for pr in (p0, p1, pl):
+            at = pr[key]
+            try:
+                n, direct, ind = ex.iat_parts(at)
+            except (ValueError, NotImplementedError):
+                return None
+            if n != N * D or len(ind) != 1:
+                return None
+            iv, pos, stride = ind[0]
+            direct = np.broadcast_to(direct, (L, n))
+            pos = np.broadcast_to(pos, (L, n))
+            if np.any(pos != pos[:, :1]):
+                return None
+            row = int(direct[0, D] - direct[0, 0]) if N > 1 else D
+            expect = direct[:, :1] + (np.arange(N)[:, None] * row + np.arange(D)[None, :]).reshape(1, -1)
+            if not np.array_equal(direct, expect):
+                return None
+            ibpe = rt.ELEM_BYTES[iv.dtype]
+            ibase = np.broadcast_to(np.asarray(iv.base, dtype=np.int64), (L,))
+            try:
+                ta = ex._alloc_of(ibase * ibpe)
+                _, alloc, rel = ex._hbm_leaf(at.parent, np.zeros(L, np.int64), (n,), (1,))
+            except NotImplementedError:
+                return None
+            parts.append((alloc, rel + direct[:, 0], row, int(stride), ta, ibase - ta.addr // ibpe + pos[:, 0],
+                          iv.dtype, at.parent.dtype, N))
+        x0, x1, xl = parts
+        if any(x[0] is not x0[0] or x[4] is not x0[4] or x[2:4] != x0[2:4] or not np.array_equal(x[1], x0[1])
+               for x in (x1, xl)):
+            return None
+        multi = trips > 1
+        step = 0
+        if np.any(multi):
+            d_ = (x1[5] - x0[5])[multi]
+            if np.any(d_ != d_[0]) or np.any((xl[5] != x0[5] + tm1 * int(d_[0]))[multi]):
+                return None
+            step = int(d_[0])
+        kv[key] = x0[:5] + (x0[5], step) + x0[6:]
+    k, v = kv["k"], kv["v"]
+    if k[4] is not v[4] or not np.array_equal(k[5], v[5]) or k[6] != v[6] or k[7] != v[7] or k[8] != v[8] \
+            or k[9] != v[9] or k[8] not in ("f16", "bf16", "f32") or k[7] not in ("i8", "i16", "i32", "i64"):
+        return None
+    N = k[9]
+    lds = 4 * (M * (D + 1) + N * (D + 1) + N * D + M * N + 3 * M)
+    if M * D > 8192 or lds > 160 * 1024:
+        return None
+    d = rt.PATTN()
+    d.lanes, d.M, d.N, d.D = L, M, N, D
+    keep = []
+
+    def up(arr):
+        b = ex.pool.upload(np.ascontiguousarray(arr))
+        keep.append(b)
+        return b.ptr
+
+    d.q_ptr, d.q_base = ql.ptr, up(ql.lane.values(L).astype(np.int64))
+    d.q_row, d.q_lo, d.q_hi = int(ql.strides[0]), int(ql.lo), int(ql.hi)
+    d.q_dtype, d.kv_dtype = rt.DTYPE_CODE[ql.dtype], rt.DTYPE_CODE[k[8]]
+    d.k_ptr, d.k_base, d.k_row, d.k_page = ex.arena.ptr_of(k[0]), up(k[1]), k[2], k[3]
+    d.v_ptr, d.v_base, d.v_row, d.v_page = ex.arena.ptr_of(v[0]), up(v[1]), v[2], v[3]
+    d.k_lo, d.k_hi, d.v_lo, d.v_hi = 0, k[0].n_elems, 0, v[0].n_elems
+    d.tbl_ptr, d.tbl_pos, d.tbl_step = ex.arena.ptr_of(k[4]), up(k[5]), k[6]
+    d.tbl_lo, d.tbl_hi, d.tbl_dtype = 0, k[4].n_elems, rt.DTYPE_CODE[k[7]]
+    d.trips = up(trips.astype(np.int32))
+    d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
+    d.kpos_step, d.row_div = kpos_step, row_div
+    d.causal, d.pred = int(causal), rt.K["KTIR_CMP_" + pred]
+    d.scale, d.neg, d.m0, d.l0 = p0["scale"], neg, -np.inf, l0
+    m_buf, l_buf, a_buf = ex.pool.temp(L * M * 4), ex.pool.temp(L * M * 4), ex.pool.temp(L * M * D * 4)
+    d.m_out, d.l_out, d.acc_out = m_buf.ptr, l_buf.ptr, a_buf.ptr
+    keep += [m_buf, l_buf, a_buf, ql]
+    zero = np.zeros(L, np.int64)
+    for alloc in (k[0], v[0], k[4]):
+        ex.log(alloc, False, zero, (1,), (1,), whole=True)
+    ex.launch("pattn", d, keep)
+    vec = lambda b: Tile(Expr("ld", "f32", (M,), attr=LeafSpec(b.ptr, "f32", LaneOff(0, M), (1,), 0, L * M,
+                                                                 keep=(b,))))
+    res = [None, None, None]
+    res[im], res[il] = vec(m_buf), vec(l_buf)
+    res[ia] = Tile(Expr("ld", "f32", (M, D), attr=LeafSpec(a_buf.ptr, "f32", LaneOff(0, M * D), (D, 1), 0,
+                                                             L * M * D, keep=(a_buf,))))
     return res
 
 

@@ -117,6 +117,21 @@ class ATTN(C.Structure):
                 ("v16_n", C.c_int64), ("pairs", C.c_uint64), ("n_pairs", C.c_int64)]
 
 
+class PATTN(C.Structure):
+    _fields_ = [("lanes", C.c_int64), ("M", C.c_int64), ("N", C.c_int64), ("D", C.c_int64),
+                ("q_ptr", C.c_uint64), ("q_base", C.c_uint64), ("q_row", C.c_int64), ("q_lo", C.c_int64),
+                ("q_hi", C.c_int64), ("q_dtype", C.c_int32), ("kv_dtype", C.c_int32),
+                ("k_ptr", C.c_uint64), ("v_ptr", C.c_uint64), ("k_base", C.c_uint64), ("v_base", C.c_uint64),
+                ("k_row", C.c_int64), ("v_row", C.c_int64), ("k_page", C.c_int64), ("v_page", C.c_int64),
+                ("k_lo", C.c_int64), ("k_hi", C.c_int64), ("v_lo", C.c_int64), ("v_hi", C.c_int64),
+                ("tbl_ptr", C.c_uint64), ("tbl_pos", C.c_uint64), ("tbl_step", C.c_int64), ("tbl_lo", C.c_int64),
+                ("tbl_hi", C.c_int64), ("tbl_dtype", C.c_int32), ("pred", C.c_int32), ("trips", C.c_uint64),
+                ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64), ("row_div", C.c_int64),
+                ("causal", C.c_int32), ("pad", C.c_int32), ("scale", C.c_float), ("neg", C.c_float),
+                ("m0", C.c_float), ("l0", C.c_float), ("m_out", C.c_uint64), ("l_out", C.c_uint64),
+                ("acc_out", C.c_uint64)]
+
+
 class KTIRDeviceError(RuntimeError):
     pass
 
@@ -142,7 +157,7 @@ def lib():
                      "ktir_launch_matmul", "ktir_event_create", "ktir_event_record",
                      "ktir_event_elapsed_ms", "ktir_event_destroy", "ktir_device_info",
                      "ktir_launch_row_rmw", "ktir_launch_attention", "ktir_rmw_variant", "ktir_shutdown", "ktir_set_row_grid_limit",
-                     "ktir_launch_row_rmw_noalloc"):
+                     "ktir_launch_row_rmw_noalloc", "ktir_launch_paged_attention"):
             getattr(L, name).restype = C.c_int
         L.ktir_malloc.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.ktir_free.argtypes = [C.c_uint64]
@@ -159,6 +174,7 @@ def lib():
         L.ktir_launch_row_rmw_noalloc.argtypes = [C.POINTER(RMW)]
         L.ktir_set_row_grid_limit.argtypes = [C.c_int64]
         L.ktir_launch_attention.argtypes = [C.POINTER(ATTN)]
+        L.ktir_launch_paged_attention.argtypes = [C.POINTER(PATTN)]
         L.ktir_event_create.argtypes = [C.POINTER(C.c_uint64)]
         L.ktir_event_record.argtypes = [C.c_uint64]
         L.ktir_event_elapsed_ms.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_float)]

@@ -1270,7 +1270,11 @@ class Executor:
             self._store_expr(val, spec, alloc, shape)
             self._log_mem(alloc, True, rel + lo_o, (int(np.max(hi_o - lo_o)),), (1,), dtype, mask=m)
 
-    def _iat_offsets(self, at: IATile) -> Tuple[rt.DeviceBuffer, int, LeafSpec, Alloc]:
+    def iat_parts(self, at: IATile):
+        """Host part of an indirect access tile: (n points, direct element
+        offsets [1 or lanes, n], [(index view, element positions in it
+        [1 or lanes, n], parent stride)] per indirect dimension), points in
+        the order of the variables space (reference ops/memory_ops.py:491-576)."""
         if at.vso is not None and not at.vso.is_permutation():
             raise ValueError("variables_space_order must permute its input dimensions")
         if at.parent.space != "HBM" or any(v.space != "HBM" for v in at.views):
@@ -1280,7 +1284,6 @@ class Executor:
             pts = sorted(pts, key=lambda p: at.vso.eval(p))
         P = np.asarray(pts, dtype=np.int64).reshape(len(pts), len(at.shape))
         n = len(P)
-        L = self.L
         outer = at.ssa.get("__outer__", {})
         cols = []
         for k in range(P.shape[1]):
@@ -1308,6 +1311,11 @@ class Executor:
                 ind.append((iv, pos, pst[d]))
         if len(ind) > 4:
             raise NotImplementedError("more than 4 indirect dimensions")
+        return n, direct, ind
+
+    def _iat_offsets(self, at: IATile) -> Tuple[rt.DeviceBuffer, int, LeafSpec, Alloc]:
+        n, direct, ind = self.iat_parts(at)
+        L = self.L
         d = rt.IAT()
         d.lanes, d.n = L, n
         direct = np.broadcast_to(direct, (direct.shape[0], n)).astype(np.int64)

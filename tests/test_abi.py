@@ -44,9 +44,9 @@ def test_library_loads_without_gpu():
 def test_struct_sizes_match_c(tmp_path):
     """Compile a tiny host program that prints sizeof() of every descriptor."""
     from ktir_cpu_amd import runtime as rt
-    src = '#include <stdio.h>\n#include "ktir_hip.h"\nint main(){printf("%zu %zu %zu %zu %zu %zu %zu\\n",' \
+    src = '#include <stdio.h>\n#include "ktir_hip.h"\nint main(){printf("%zu %zu %zu %zu %zu %zu %zu %zu\\n",' \
           'sizeof(ktir_leaf_t), sizeof(ktir_instr_t), sizeof(ktir_prog_t), sizeof(ktir_iat_t), ' \
-          'sizeof(ktir_mm_t), sizeof(ktir_rmw_t), sizeof(ktir_attn_t));return 0;}'
+          'sizeof(ktir_mm_t), sizeof(ktir_rmw_t), sizeof(ktir_attn_t), sizeof(ktir_pattn_t));return 0;}'
     tmp = str(tmp_path)
     with open(os.path.join(tmp, "s.c"), "w") as f:
         f.write(src)
@@ -56,7 +56,7 @@ def test_struct_sizes_match_c(tmp_path):
     assert r.returncode == 0, r.stderr
     sizes = [int(x) for x in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
     assert sizes == [C.sizeof(rt.Leaf), C.sizeof(rt.Instr), C.sizeof(rt.Prog), C.sizeof(rt.IAT),
-                     C.sizeof(rt.MM), C.sizeof(rt.RMW), C.sizeof(rt.ATTN)]
+                     C.sizeof(rt.MM), C.sizeof(rt.RMW), C.sizeof(rt.ATTN), C.sizeof(rt.PATTN)]
     assert C.sizeof(rt.Prog) < 4096   # travels in the kernel arguments
 
 

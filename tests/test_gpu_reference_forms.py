@@ -36,8 +36,9 @@ def test_paged_attention_within_tolerance(gen, inp, args):
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
     # the output tiles of an odd batch start sit off the 2-row grid but are
-    # disjoint: the lanes still run together
+    # disjoint: the lanes still run together, the KV loop as one launch
     assert plan.mode == "lockstep"
+    assert plan.counts().get("pattn") == 1
 
 
 def test_paged_attention_many_tokens_within_tolerance():
@@ -46,8 +47,9 @@ def test_paged_attention_many_tokens_within_tolerance():
     gen = dict(tokens=64, q_heads=32, kv_heads=8, head=128, page=16, blocks=512, max_pages=64, block_q=2)
     kw = dict(paged_inputs(tokens=64, blocks=512, max_pages=64, seed=7),
               **dict(PA_ARGS, num_tiles=40, context_len=576, block_table_offset=3))
-    got, ref, _ = _both(configs.paged_attention(**gen), PA_FN, kw, "output_ptr")
+    got, ref, plan = _both(configs.paged_attention(**gen), PA_FN, kw, "output_ptr")
     np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+    assert plan.counts().get("pattn") == 1
 
 
 @pytest.mark.parametrize("n,d,rows", [(32, 64, 32), (256, 128, 64)])
