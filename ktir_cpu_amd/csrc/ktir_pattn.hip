@@ -8,10 +8,12 @@
 // (dialects/linalg_ops.py:307-596, dialects/math_ops.py).
 //
 // One workgroup per lane (simulated core): Q (M x D, as f32) stays in LDS
-// for the whole loop; per page the K and V tiles (N x D) are read once into
-// LDS, S (M x N) is computed from LDS, each row's statistics by one thread,
-// and the accumulator (M x D, at most 32 elements per thread) stays in
-// registers.  Arithmetic is f32 in the order of the loop body: s = scale *
+// for the whole loop; the next page's K and V tiles (N x D) are read into
+// registers (16-byte loads) while the current page is computed, then
+// written to LDS as f32; S (M x N) is computed from LDS by groups of lanes
+// per (row, key) combined with shuffles, a row's statistics by N lanes with
+// shuffles (or one thread per row), and the accumulator (M x D, at most 32
+// elements per thread) stays in registers.  Arithmetic is f32 in the order of the loop body: s = scale *
 // (q . k), m' = max(m, max_c s), p = exp(s - m'), alpha = exp(m - m'),
 // acc' = acc * alpha + p . v, l' = l * alpha + sum_c p.
 #include <climits>
@@ -20,7 +22,7 @@
 namespace ktir {
 
 constexpr int PA_THREADS = 256;
-constexpr int PA_ACC = 32;                 // accumulator elements per thread (M * D <= 8192)
+constexpr int PA_ACC = 32;                 // largest accumulator per thread (M * D <= 8192)
 constexpr int64_t PA_MAX_LDS = 160 * 1024;
 
 __device__ __forceinline__ float max_nan(float a, float b) {
@@ -54,7 +56,45 @@ static int64_t pa_lds_floats(int64_t M, int64_t N, int64_t D) {
   return M * (D + 1) + N * (D + 1) + N * D + M * N + 3 * M;
 }
 
-__global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d, int* err) {
+constexpr int PA_PF = 4;                   // largest prefetch: 8-element vectors per thread and tensor (N * D <= 8192)
+
+// Prefetch of one page of K and V into registers: the vectorised form
+// (flag `vec`: 16-bit elements, rows of whole 16-byte aligned 8-element
+// vectors) issues 16-byte loads; a vector not wholly inside its allocation
+// window, and the unaligned form, read element by element when the page is
+// written to LDS.
+template <int PF>
+struct PagePf {
+  uint4 k[PF], v[PF];
+  int64_t k0, v0;
+};
+
+__device__ __forceinline__ int64_t page_of(const ktir_pattn_t& d, int64_t tp, int j, int* err, bool lead) {
+  const int64_t te = tp + (int64_t)j * d.tbl_step;
+  int64_t page = (te >= d.tbl_lo && te < d.tbl_hi) ? load_index(d.tbl_ptr, te, d.tbl_dtype) : 0;
+  if (page < 0) {
+    if (lead) *err = 1;
+    page = 0;
+  }
+  return page;
+}
+
+__device__ __forceinline__ void unpack8(uint4 w, int dt, float* o) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (dt == KTIR_BF16) {
+      o[2 * i] = __uint_as_float(u[i] << 16);
+      o[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    } else {
+      o[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xffffu));
+      o[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+    }
+  }
+}
+
+template <int ACC, int PF>
+__global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d, int vec, int* err) {
   extern __shared__ float sm[];
   const int M = (int)d.M, N = (int)d.N, D = (int)d.D, DP = D + 1;
   float* Qs = sm;                  // [M][D + 1]
@@ -76,66 +116,188 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
     mrow[r] = d.m0;
     lrow[r] = d.l0;
   }
-  float acc[PA_ACC];
+  float acc[ACC];
 #pragma unroll
-  for (int k = 0; k < PA_ACC; ++k) acc[k] = 0.f;
+  for (int k = 0; k < ACC; ++k) acc[k] = 0.f;
   const int trips = ((const int32_t*)d.trips)[lane];
   const int64_t kb = ((const int64_t*)d.k_base)[lane], vb = ((const int64_t*)d.v_base)[lane];
   const int64_t tp = ((const int64_t*)d.tbl_pos)[lane];
   const int64_t qp0 = ((const int64_t*)d.qpos0)[lane], kp0 = ((const int64_t*)d.kpos0)[lane];
+  const int nvec = N * D / 8;      // 8-element vectors of one page tile (vectorised form)
+  vec = vec && !(kb & 7) && !(vb & 7);   // this lane's tiles start on 16-byte boundaries
+  // S = Q K^T: TP threads per (row, key) pair, each a strided part of the
+  // dot product, combined by lane shuffles (TP a power of two <= 64)
+  int TP = PA_THREADS / (M * N);
+  if (TP < 1) TP = 1;
+  while (TP > 1 && (D % TP || (TP & (TP - 1)))) TP >>= 1;
+  // row statistics by N lanes per row when N is a power of two <= 64 and
+  // the rows fit the workgroup at once; otherwise one thread per row
+  const bool rows_par = (N & (N - 1)) == 0 && N <= 64 && M * N <= PA_THREADS;
+  // S and the row statistics in one pass when every row's lanes lie in one
+  // wavefront and all pairs fit the workgroup
+  const bool fused = rows_par && N * TP <= 64 && M * N * TP <= PA_THREADS;
+  PagePf<PF> pf;
+  auto prefetch = [&](int j) {
+    const int64_t page = page_of(d, tp, j, err, tid == 0);
+    pf.k0 = kb + page * d.k_page;
+    pf.v0 = vb + page * d.v_page;
+    if (vec) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int i = tid + u * PA_THREADS;
+        if (i < nvec) {
+          const int c = (i * 8) / D, x = i * 8 - c * D;
+          const int64_t ek = pf.k0 + (int64_t)c * d.k_row + x, ev = pf.v0 + (int64_t)c * d.v_row + x;
+          if (ek >= d.k_lo && ek + 8 <= d.k_hi) pf.k[u] = *(const uint4*)((const uint16_t*)d.k_ptr + ek);
+          if (ev >= d.v_lo && ev + 8 <= d.v_hi) pf.v[u] = *(const uint4*)((const uint16_t*)d.v_ptr + ev);
+        }
+      }
+    }
+  };
+  auto commit = [&]() {
+    if (vec) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int i = tid + u * PA_THREADS;
+        if (i < nvec) {
+          const int c = (i * 8) / D, x = i * 8 - c * D;
+          const int64_t ek = pf.k0 + (int64_t)c * d.k_row + x, ev = pf.v0 + (int64_t)c * d.v_row + x;
+          float kv[8], vv[8];
+          if (ek >= d.k_lo && ek + 8 <= d.k_hi) {
+            unpack8(pf.k[u], d.kv_dtype, kv);
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) kv[t] = (ek + t >= d.k_lo && ek + t < d.k_hi) ? load_elem(d.k_ptr, ek + t, d.kv_dtype) : 0.f;
+          }
+          if (ev >= d.v_lo && ev + 8 <= d.v_hi) {
+            unpack8(pf.v[u], d.kv_dtype, vv);
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) vv[t] = (ev + t >= d.v_lo && ev + t < d.v_hi) ? load_elem(d.v_ptr, ev + t, d.kv_dtype) : 0.f;
+          }
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            Ks[c * DP + x + t] = kv[t];
+            Vs[c * D + x + t] = vv[t];
+          }
+        }
+      }
+    } else {
+      for (int i = tid; i < N * D; i += PA_THREADS) {
+        const int c = i / D, x = i - c * D;
+        const int64_t ek = pf.k0 + (int64_t)c * d.k_row + x, ev = pf.v0 + (int64_t)c * d.v_row + x;
+        Ks[c * DP + x] = (ek >= d.k_lo && ek < d.k_hi) ? load_elem(d.k_ptr, ek, d.kv_dtype) : 0.f;
+        Vs[c * D + x] = (ev >= d.v_lo && ev < d.v_hi) ? load_elem(d.v_ptr, ev, d.kv_dtype) : 0.f;
+      }
+    }
+  };
+  if (trips > 0) prefetch(0);
   __syncthreads();
   for (int j = 0; j < trips; ++j) {
-    // the page of this iteration: an index read outside the table's
-    // allocation reads 0, a negative index raises (after the launch)
-    const int64_t te = tp + (int64_t)j * d.tbl_step;
-    int64_t page = (te >= d.tbl_lo && te < d.tbl_hi) ? load_index(d.tbl_ptr, te, d.tbl_dtype) : 0;
-    if (page < 0) {
-      if (tid == 0) *err = 1;
-      page = 0;
-    }
-    const int64_t k0 = kb + page * d.k_page, v0 = vb + page * d.v_page;
-    for (int i = tid; i < N * D; i += PA_THREADS) {
-      const int c = i / D, x = i - c * D;
-      const int64_t ek = k0 + (int64_t)c * d.k_row + x, ev = v0 + (int64_t)c * d.v_row + x;
-      Ks[c * DP + x] = (ek >= d.k_lo && ek < d.k_hi) ? load_elem(d.k_ptr, ek, d.kv_dtype) : 0.f;
-      Vs[c * D + x] = (ev >= d.v_lo && ev < d.v_hi) ? load_elem(d.v_ptr, ev, d.kv_dtype) : 0.f;
-    }
+    commit();
+    if (j + 1 < trips) prefetch(j + 1);    // next page's loads in flight during this page's compute
     __syncthreads();
-    for (int i = tid; i < M * N; i += PA_THREADS) {
-      const int r = i / N, c = i - r * N;
-      const float* q = Qs + r * DP;
-      const float* k = Ks + c * DP;
+    if (fused) {
+      // one pass: lane group (pair, part) computes its part of s[r][c]; the
+      // TP lanes of a pair sum by shuffles (each then holds s), the N pairs
+      // of a row (N * TP consecutive lanes of one wavefront) take the row
+      // max and the row sum by shuffles, counting each pair once
+      const int pair = tid / TP, part = tid - pair * TP;
+      const bool live = pair < M * N;
+      const int r = live ? pair / N : 0, c = pair - r * N;
       float s = 0.f;
-      for (int x = 0; x < D; ++x) s = __fmaf_rn(q[x], k[x], s);
+      if (live) {
+        const float* q = Qs + r * DP;
+        const float* k = Ks + c * DP;
+        for (int x = part; x < D; x += TP) s = __fmaf_rn(q[x], k[x], s);
+      }
+      for (int o = 1; o < TP; o <<= 1) s += __shfl_xor(s, o);
       s = __fmul_rn(d.scale, s);
       if (d.causal) {
         const int64_t kpos = kp0 + (int64_t)j * d.kpos_step + c;
         const int64_t qpos = qp0 + r / d.row_div;
         if (!keep_pos(d.pred, kpos, qpos)) s = d.neg;
       }
-      S[i] = s;
+      if (!live) s = -INFINITY;
+      float mx = s;
+      for (int o = TP; o < N * TP; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
+      const float mo = live ? mrow[r] : 0.f;
+      const float mn = max_nan(mo, mx);
+      const float p = expf(__fsub_rn(s, mn));
+      float sum = part == 0 ? p : 0.f;
+      for (int o = 1; o < N * TP; o <<= 1) sum += __shfl_xor(sum, o);
+      if (live && part == 0) S[pair] = p;
+      if (live && part == 0 && c == 0) {
+        const float al = expf(__fsub_rn(mo, mn));
+        arow[r] = al;
+        lrow[r] = __fadd_rn(__fmul_rn(lrow[r], al), sum);
+        mrow[r] = mn;
+      }
+    } else {
+    for (int base = 0; base < M * N * TP; base += PA_THREADS) {
+      const int g = base + tid;
+      const int pair = g / TP, part = g - pair * TP;
+      float s = 0.f;
+      if (pair < M * N) {
+        const int r = pair / N, c = pair - r * N;
+        const float* q = Qs + r * DP;
+        const float* k = Ks + c * DP;
+        for (int x = part; x < D; x += TP) s = __fmaf_rn(q[x], k[x], s);
+      }
+      for (int o = 1; o < TP; o <<= 1) s += __shfl_xor(s, o);
+      if (pair < M * N && part == 0) {
+        const int r = pair / N, c = pair - r * N;
+        s = __fmul_rn(d.scale, s);
+        if (d.causal) {
+          const int64_t kpos = kp0 + (int64_t)j * d.kpos_step + c;
+          const int64_t qpos = qp0 + r / d.row_div;
+          if (!keep_pos(d.pred, kpos, qpos)) s = d.neg;
+        }
+        S[pair] = s;
+      }
     }
     __syncthreads();
-    for (int r = tid; r < M; r += PA_THREADS) {
-      float* sr = S + r * N;
-      float mx = -INFINITY;
-      for (int c = 0; c < N; ++c) mx = max_nan(mx, sr[c]);
-      const float mo = mrow[r];
+    if (rows_par) {
+      const int r = tid / N, c = tid - r * N;
+      const bool live = tid < M * N;
+      const float sv = live ? S[tid] : -INFINITY;
+      float mx = sv;
+      for (int o = 1; o < N; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
+      const float mo = live ? mrow[r] : 0.f;
       const float mn = max_nan(mo, mx);
-      float sum = 0.f;
-      for (int c = 0; c < N; ++c) {
-        const float p = expf(__fsub_rn(sr[c], mn));
-        sr[c] = p;
-        sum = __fadd_rn(sum, p);
+      const float p = expf(__fsub_rn(sv, mn));
+      float sum = p;
+      for (int o = 1; o < N; o <<= 1) sum += __shfl_xor(sum, o);
+      if (live) S[tid] = p;
+      if (live && c == 0) {
+        const float al = expf(__fsub_rn(mo, mn));
+        arow[r] = al;
+        lrow[r] = __fadd_rn(__fmul_rn(lrow[r], al), sum);
+        mrow[r] = mn;
       }
-      const float al = expf(__fsub_rn(mo, mn));
-      arow[r] = al;
-      lrow[r] = __fadd_rn(__fmul_rn(lrow[r], al), sum);
-      mrow[r] = mn;
+    } else {
+      for (int r = tid; r < M; r += PA_THREADS) {
+        float* sr = S + r * N;
+        float mx = -INFINITY;
+        for (int c = 0; c < N; ++c) mx = max_nan(mx, sr[c]);
+        const float mo = mrow[r];
+        const float mn = max_nan(mo, mx);
+        float sum = 0.f;
+        for (int c = 0; c < N; ++c) {
+          const float p = expf(__fsub_rn(sr[c], mn));
+          sr[c] = p;
+          sum = __fadd_rn(sum, p);
+        }
+        const float al = expf(__fsub_rn(mo, mn));
+        arow[r] = al;
+        lrow[r] = __fadd_rn(__fmul_rn(lrow[r], al), sum);
+        mrow[r] = mn;
+      }
+    }
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < PA_ACC; ++k) {
+    for (int k = 0; k < ACC; ++k) {
       const int i = tid + k * PA_THREADS;
       if (i < M * D) {
         const int r = i / D, x = i - r * D;
@@ -152,7 +314,7 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
     ((float*)d.l_out)[lane * M + r] = lrow[r];
   }
 #pragma unroll
-  for (int k = 0; k < PA_ACC; ++k) {
+  for (int k = 0; k < ACC; ++k) {
     const int i = tid + k * PA_THREADS;
     if (i < M * D) ((float*)d.acc_out)[lane * M * D + i] = acc[k];
   }
@@ -185,11 +347,28 @@ extern "C" int ktir_launch_paged_attention(const ktir_pattn_t* d) {
   }
   if (d->lanes == 0) return KTIR_OK;
   if (d->lanes > INT_MAX) return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_paged_attention: too many lanes");
-  if (lds > 64 * 1024)
-    KTIR_HIP_CHECK(hipFuncSetAttribute((const void*)pattn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds));
-  hipLaunchKernelGGL(pattn_kernel, dim3((unsigned)d->lanes), dim3(PA_THREADS), (size_t)lds, stream(), *d,
-                     device_error_flag());
+  // the vectorised page reads: 16-bit K / V, rows of whole 8-element
+  // vectors, every row start a multiple of 8 elements, pointers 16-byte aligned
+  int vec = (d->kv_dtype == KTIR_F16 || d->kv_dtype == KTIR_BF16) && d->D % 8 == 0 && d->N * d->D <= 8 * PA_THREADS * PA_PF
+            && !((d->k_ptr | d->v_ptr) & 15) && !((d->k_row | d->v_row | d->k_page | d->v_page) & 7);
+  const int64_t per = (d->M * d->D + PA_THREADS - 1) / PA_THREADS;
+  const int64_t pfv = (d->N * d->D / 8 + PA_THREADS - 1) / PA_THREADS;
+  auto go = [&](auto kern) -> int {
+    if (lds > 64 * 1024)
+      KTIR_HIP_CHECK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL(kern, dim3((unsigned)d->lanes), dim3(PA_THREADS), (size_t)lds, stream(), *d, vec,
+                       device_error_flag());
+    return 0;
+  };
+  // accumulator and prefetch sized to the tile: fewer VGPRs, more
+  // workgroups per CU
+  if (per <= 4 && pfv <= 1) go(pattn_kernel<4, 1>);
+  else if (per <= 4 && pfv <= 2) go(pattn_kernel<4, 2>);
+  else if (per <= 4) go(pattn_kernel<4, 4>);
+  else if (per <= 8 && pfv <= 2) go(pattn_kernel<8, 2>);
+  else if (per <= 8) go(pattn_kernel<8, 4>);
+  else if (per <= 16) go(pattn_kernel<16, 4>);
+  else go(pattn_kernel<32, 4>);
   KTIR_HIP_CHECK(hipGetLastError());
   return KTIR_OK;
 }
