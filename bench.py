@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_TFLOPS = 2500.0
+FP32_TFLOPS = 157.3        # dense f32 (VALU FMA and MFMA alike)
 
 
 def _vector_add():
@@ -206,8 +207,9 @@ def _paged_attention():
     keys = sum(ctx + t + 1 for t in range(T))
     return dict(src=configs.paged_attention(T, HQ, HK, D, P, blocks, max_pages, BQ), fn="kernel_unified_attention_spyre_2d",
                 kw=kw, cores=(T // BQ) * HK, bytes=2 * HQ * T * D * 2 + 2 * blocks * P * HK * D * 2,
-                flops=4 * HQ * keys * D, bound="mfma",
-                dtype="f16 in/out; f32 Q K^T, scores, online-softmax state and P V",
+                flops=4 * HQ * keys * D, bound="fp32",
+                dtype="f16 in/out; f32 Q K^T, scores, online-softmax state and P V (f32 FMA, the reference's "
+                      "extf'd operands)",
                 workload=f"paged attention {T} tokens after a {ctx}-token context, {HQ} query / {HK} KV heads, "
                          f"D={D}, page {P}, {BQ} tokens per core (the reference's triton-ktir paged_attention form)")
 
@@ -220,7 +222,7 @@ CONFIGS = {"vector_add": _vector_add, "vector_add_4096": _vector_add_4096, "copy
 
 # kernels that make up each kind of launch (the HIP kernel names)
 _LAUNCH_KERNELS = {"mm": ("mm_mfma", "mm_generic"), "attn": ("attn_kernel", "attn_pp", "attn_v16"), "rmw": ("rmw_",),
-                   "prog": ("prog_",)}
+                   "prog": ("prog_",), "pattn": ("pattn_kernel",)}
 
 
 def _traffic(config, kind):
@@ -419,6 +421,8 @@ def measure(name, steps, warmup, with_cpu):
     # algorithmic units (all bytes moved / all flops)
     if cfg["bound"] == "hbm":
         units, unit, peak, scale = cfg["bytes"], "GB/s", HBM_PEAK_GBS, 1e9
+    elif cfg["bound"] == "fp32":
+        units, unit, peak, scale = cfg["flops"], "TFLOP/s", FP32_TFLOPS, 1e12
     else:
         units, unit, peak, scale = cfg["flops"], "TFLOP/s", MFMA_F16_TFLOPS, 1e12
     value = units / (ms * 1e-3) / scale
@@ -472,7 +476,7 @@ def measure(name, steps, warmup, with_cpu):
 
 HEADLINE = "gather"
 PER_CONFIG = ["vector_add", "gather", "softmax", "rmsnorm", "gemm", "attention", "softmax_extract", "rmsnorm_extract",
-              "vector_add_4096"]
+              "paged_attention", "rope", "vector_add_4096"]
 
 
 def main():

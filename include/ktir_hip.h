@@ -427,6 +427,7 @@ typedef struct ktir_pattn {
   int64_t tbl_step, tbl_lo, tbl_hi;
   int32_t tbl_dtype, pred;             /* KTIR_I8 / I16 / I32 / I64; KTIR_CMP_* keep predicate */
   uint64_t trips;                      /* const int32_t* [lanes] */
+  uint64_t order;                      /* const int32_t* [lanes]: workgroup -> lane, or 0 */
   uint64_t qpos0, kpos0;               /* const int64_t* [lanes] */
   int64_t kpos_step, row_div;
   int32_t causal, pad;

@@ -7,7 +7,9 @@
 // accumulator; the reference runs each of those ops per core and iteration
 // (dialects/linalg_ops.py:307-596, dialects/math_ops.py).
 //
-// One workgroup per lane (simulated core): Q (M x D, as f32) stays in LDS
+// One workgroup per lane (simulated core; the host orders workgroups so
+// that the lanes reading one KV head's pages share an XCD and its L2):
+// Q (M x D, as f32) stays in LDS
 // for the whole loop; the next page's K and V tiles (N x D) are read into
 // registers (16-byte loads) while the current page is computed, then
 // written to LDS as f32; S (M x N) is computed from LDS by groups of lanes
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
   float* mrow = S + M * N;         // [M]
   float* lrow = mrow + M;          // [M]
   float* arow = lrow + M;          // [M] alpha of the current page
-  const int64_t lane = blockIdx.x;
+  const int64_t lane = d.order ? ((const int32_t*)d.order)[blockIdx.x] : blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t qb = ((const int64_t*)d.q_base)[lane];
   for (int i = tid; i < M * D; i += PA_THREADS) {

@@ -1020,6 +1020,8 @@ def _paged_attention(ex, trips, tm1, q, probes, peeled, l0, slots, mask):
     d.tbl_ptr, d.tbl_pos, d.tbl_step = ex.arena.ptr_of(k[4]), up(k[5]), k[6]
     d.tbl_lo, d.tbl_hi, d.tbl_dtype = 0, k[4].n_elems, rt.DTYPE_CODE[k[7]]
     d.trips = up(trips.astype(np.int32))
+    # lanes of one KV stream (equal K / V lane offsets: one KV head) on one XCD
+    d.order = up(_xcd_order(trips, k[1], v[1]))
     d.qpos0, d.kpos0 = up(cq0.astype(np.int64)), up(ck0.astype(np.int64))
     d.kpos_step, d.row_div = kpos_step, row_div
     d.causal, d.pred = int(causal), rt.K["KTIR_CMP_" + pred]

@@ -126,7 +126,7 @@ class PATTN(C.Structure):
                 ("k_lo", C.c_int64), ("k_hi", C.c_int64), ("v_lo", C.c_int64), ("v_hi", C.c_int64),
                 ("tbl_ptr", C.c_uint64), ("tbl_pos", C.c_uint64), ("tbl_step", C.c_int64), ("tbl_lo", C.c_int64),
                 ("tbl_hi", C.c_int64), ("tbl_dtype", C.c_int32), ("pred", C.c_int32), ("trips", C.c_uint64),
-                ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64), ("row_div", C.c_int64),
+                ("order", C.c_uint64), ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64), ("row_div", C.c_int64),
                 ("causal", C.c_int32), ("pad", C.c_int32), ("scale", C.c_float), ("neg", C.c_float),
                 ("m0", C.c_float), ("l0", C.c_float), ("m_out", C.c_uint64), ("l_out", C.c_uint64),
                 ("acc_out", C.c_uint64)]
