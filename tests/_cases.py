@@ -1244,3 +1244,180 @@ def scalar_chain(body, dt="f32", out_dt="f32", cores=4, C=16, idx="%c0", fill=Fa
     src = (f"module {{\n  func.func @scalar_chain(%x_ptr: index, %y_ptr: index) attributes {{grid = [{cores}, 1]}} {{\n"
            + "\n".join(lines) + "\n    return\n  }\n}\n")
     return src, "scalar_chain"
+
+
+# ---------------------------------------------------------------------------
+# indirect forms of the reference's examples (pointer arguments and sizes of
+# our choosing; the structure of examples/triton-ktir/indexed_add.mlir,
+# examples/rfc/paged-tensor-copy.mlir, paged-tensor-write.mlir, and the
+# X[IDX[e], m, n] / page-table gathers of the reference's
+# tests/test_blocked_indirect_fast_path.py:234-360)
+# ---------------------------------------------------------------------------
+
+def _vsets(shape):
+    dims = ", ".join(f"d{i}" for i in range(len(shape)))
+    cons = ", ".join(f"d{i} >= 0, -d{i} + {s - 1} >= 0" for i, s in enumerate(shape))
+    return f"affine_set<({dims}) : ({cons})>", f"affine_map<({dims}) -> ({dims})>"
+
+
+def indexed_add(rows=16, d1=64, heads=8, D=128, width=32, seed=0, index=(3, 7), dim1_start=5):
+    """out[g0, :, g1, :] = x[index[g0], s : s + width, g1, :] + y[g0, :, g1, :]
+    (f16) with an i64 index tensor, grid [len(index), heads]: the x tile is an
+    indirect access tile whose other subscripts are SSA + variable
+    expressions (dim1_start + d1, g1 + d2)."""
+    G0 = len(index)
+    xs, ys = [rows, d1, heads, D], [G0, width, heads, D]
+    st = lambda sh: [int(np.prod(sh[i + 1:])) for i in range(len(sh))]
+    at4 = f"!ktdp.access_tile<1x{width}x1x{D}xindex>"
+    T4 = configs._t([1, width, 1, D], "f16")
+    vss, vso = _vsets([1, width, 1, D])
+    src = f"""module {{
+  func.func @indexed_add_kernel(%x_ptr: index, %y_ptr: index, %index_ptr: index, %output_ptr: index,
+      %dim1_start: index) attributes {{grid = [{G0}, {heads}]}} {{
+    %g0, %g1 = ktdp.get_compute_tile_id : index, index
+    %c0 = arith.constant 0 : index
+{configs._view("i_view", "index_ptr", [G0], [1], "i64")}
+{configs._view("x_view", "x_ptr", xs, st(xs), "f16")}
+{configs._view("y_view", "y_ptr", ys, st(ys), "f16")}
+{configs._view("o_view", "output_ptr", ys, st(ys), "f16")}
+    %x_tile = ktdp.construct_indirect_access_tile intermediate_variables(%e0, %e1, %e2, %e3)
+        %x_view[ind(%i_view[%g0 + %e0]), (%dim1_start + %e1), (%g1 + %e2), (%e3)] {{
+      variables_space_set = {vss},
+      variables_space_order = {vso}
+    }} : memref<{'x'.join(map(str, xs))}xf16>, memref<{G0}xi64> -> {at4}
+{configs._tile("y_tile", "y_view", ["%g0", "%c0", "%g1", "%c0"], [1, width, 1, D], ys, "f16")}
+    %x = ktdp.load %x_tile : {at4} -> {T4}
+    %y = ktdp.load %y_tile : {at4} -> {T4}
+    %o = arith.addf %x, %y : {T4}
+{configs._tile("o_tile", "o_view", ["%g0", "%c0", "%g1", "%c0"], [1, width, 1, D], ys, "f16")}
+    ktdp.store %o, %o_tile : {T4}, {at4}
+    return
+  }}
+}}
+"""
+    rng = np.random.default_rng(seed)
+    kw = dict(x_ptr=rng.standard_normal(xs).astype(np.float16), y_ptr=rng.standard_normal(ys).astype(np.float16),
+              index_ptr=np.asarray(index, np.int64), output_ptr=np.zeros(ys, np.float16), dim1_start=dim1_start)
+    return src, "indexed_add_kernel", kw
+
+
+def paged_tensor(write=False, Nb=2, Ntkv=256, Ptkv=64, Nhkv=4, Ndkv=64, Npages=24, seed=1, pages=None):
+    """The page-table copy of examples/rfc/paged-tensor-copy.mlir (write
+    False): Y[b, tkv, h, d] = X[Idx[b, tkv // Ptkv], h, tkv % Ptkv, d], the
+    gather an indirect access tile whose index and direct subscripts use
+    floordiv / mod of one variable, the store an access tile whose order
+    permutes (b, h, tkv, d) to Y's (b, tkv, h, d) layout; or its scatter dual
+    (paged-tensor-write.mlir, write True): Y[Idx[b, tkv // Ptkv], h,
+    tkv % Ptkv, d] = X[b, tkv, h, d].  One core; f16; Idx i32 [Nb, Ntkv / Ptkv]."""
+    npg = Ntkv // Ptkv
+    paged = [Npages, Nhkv, Ptkv, Ndkv]
+    flat = [Nb, Ntkv, Nhkv, Ndkv]
+    st = lambda sh: [int(np.prod(sh[i + 1:])) for i in range(len(sh))]
+    tile = [Nb, Nhkv, Ntkv, Ndkv]
+    vss, vso = _vsets(tile)
+    perm = "affine_map<(d0, d1, d2, d3) -> (d0, d2, d1, d3)>"
+    at = f"!ktdp.access_tile<{'x'.join(map(str, tile))}xindex>"
+    T = configs._t(tile, "f16")
+    src_view, dst_view = ("X_view", "Y_view")
+    iat = f"""    %P_tile = ktdp.construct_indirect_access_tile intermediate_variables(%b, %h, %t, %d)
+        %{'Y' if write else 'X'}_view[ind(%I_view[%b, %t floordiv {Ptkv}]), (%h), (%t mod {Ptkv}), (%d)] {{
+      variables_space_set = {vss},
+      variables_space_order = {vso}
+    }} : memref<{'x'.join(map(str, paged))}xf16>, memref<{Nb}x{npg}xi32> -> {at}"""
+    ftile = f"""    %F_tile = ktdp.construct_access_tile %{'X' if write else 'Y'}_view[%c0, %c0, %c0, %c0] {{
+      access_tile_set = {vss},
+      access_tile_order = {perm}
+    }} : memref<{'x'.join(map(str, flat))}xf16> -> {at}"""
+    body = (f"    %v = ktdp.load %F_tile : {at} -> {T}\n    ktdp.store %v, %P_tile : {T}, {at}" if write else
+            f"    %v = ktdp.load %P_tile : {at} -> {T}\n    ktdp.store %v, %F_tile : {T}, {at}")
+    name = "paged_tensor_write_1core" if write else "paged_tensor_copy_1core"
+    src = f"""module {{
+  func.func @{name}(%x_ptr: index, %idx_ptr: index, %y_ptr: index) {{
+    %c0 = arith.constant 0 : index
+{configs._view("I_view", "idx_ptr", [Nb, npg], [npg, 1], "i32")}
+{configs._view("X_view", "x_ptr", flat if write else paged, st(flat if write else paged), "f16")}
+{configs._view("Y_view", "y_ptr", paged if write else flat, st(paged if write else flat), "f16")}
+{iat}
+{ftile}
+{body}
+    return
+  }}
+}}
+"""
+    rng = np.random.default_rng(seed)
+    if pages is None:
+        pages = rng.permutation(Npages)[:Nb * npg]
+    idx = np.asarray(pages, np.int32).reshape(Nb, npg)
+    x = rng.standard_normal(flat if write else paged).astype(np.float16)
+    y = np.zeros(paged if write else flat, np.float16)
+    return src, name, dict(x_ptr=x, idx_ptr=idx, y_ptr=y)
+
+
+def expert_gather(E=32, M=8, N=64, sel=(0, 5, 9, 17, 22, 31), cores=2):
+    """X[IDX[e], m, n] (the reference's tests/test_blocked_indirect_fast_path.py:234-258
+    MoE pattern): each core gathers len(sel) // cores experts' [M, N] blocks
+    of an f16 weight tensor through an i32 index tensor and stores them."""
+    k = len(sel) // cores
+    xs, os_ = [E, M, N], [len(sel), M, N]
+    st = lambda sh: [int(np.prod(sh[i + 1:])) for i in range(len(sh))]
+    vss, vso = _vsets([k, M, N])
+    at = f"!ktdp.access_tile<{k}x{M}x{N}xindex>"
+    T = configs._t([k, M, N], "f16")
+    src = f"""module {{
+  func.func @expert_gather(%x_ptr: index, %idx_ptr: index, %out_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core = ktdp.get_compute_tile_id : index
+    %c0 = arith.constant 0 : index
+    %ck = arith.constant {k} : index
+    %e0 = arith.muli %core, %ck : index
+{configs._view("i_view", "idx_ptr", [len(sel)], [1], "i32")}
+{configs._view("x_view", "x_ptr", xs, st(xs), "f16")}
+{configs._view("o_view", "out_ptr", os_, st(os_), "f16")}
+    %g = ktdp.construct_indirect_access_tile intermediate_variables(%e, %m, %n)
+        %x_view[ind(%i_view[%e0 + %e]), (%m), (%n)] {{
+      variables_space_set = {vss},
+      variables_space_order = {vso}
+    }} : memref<{E}x{M}x{N}xf16>, memref<{len(sel)}xi32> -> {at}
+    %v = ktdp.load %g : {at} -> {T}
+{configs._tile("o_tile", "o_view", ["%e0", "%c0", "%c0"], [k, M, N], os_, "f16")}
+    ktdp.store %v, %o_tile : {T}, {at}
+    return
+  }}
+}}
+"""
+    rng = np.random.default_rng(2)
+    return src, "expert_gather", dict(x_ptr=rng.standard_normal(xs).astype(np.float16),
+                                      idx_ptr=np.asarray(sel, np.int32), out_ptr=np.zeros(os_, np.float16))
+
+
+def nested_yield(outer=2, inner=2, n=4):
+    """Nested scf.for loops with iter_args (the structure of the reference's
+    examples/ktir/nested_yield.ktir): the outer loop adds 1 per trip, the
+    inner loop's own sum is computed and discarded; the result, stored, is
+    `outer` in every element."""
+    T = configs._t([n], "f32")
+    src = f"""module {{
+  func.func @nested_yield(%out: index) attributes {{grid = [1]}} {{
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %cI = arith.constant {outer} : index
+    %cJ = arith.constant {inner} : index
+    %fone = arith.constant 1.0 : f32
+    %fzero = arith.constant 0.0 : f32
+    %one = tensor.splat %fone : {T}
+    %zero = tensor.splat %fzero : {T}
+{configs._view("o_view", "out", [n], [1], "f32")}
+    %sum = scf.for %i = %c0 to %cI step %c1 iter_args(%acc = %zero) -> ({T}) {{
+      %next = arith.addf %acc, %one : {T}
+      %inner = scf.for %j = %c0 to %cJ step %c1 iter_args(%iacc = %zero) -> ({T}) {{
+        %t = arith.addf %iacc, %one : {T}
+        scf.yield %t : {T}
+      }}
+      scf.yield %next : {T}
+    }}
+{configs._tile("o_tile", "o_view", ["%c0"], [n], [n], "f32")}
+    ktdp.store %sum, %o_tile : {T}, !ktdp.access_tile<{n}xindex>
+    return
+  }}
+}}
+"""
+    return src, "nested_yield", dict(out=np.zeros(n, np.float32))

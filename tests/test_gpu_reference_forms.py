@@ -74,3 +74,36 @@ def test_rope_odd_grid_bit_exact():
     kw = rope_inputs(H, S, D, seed=9)
     got, ref, _ = _both(configs.rope(H, S, D, grid_s=3, grid_h=3, tile=128), "rope_fwd_kernel", kw, "out_ptr")
     np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+from tests import _cases as C  # noqa: E402
+from tests.test_oracle_example_pins import _bits  # noqa: E402
+
+
+@pytest.mark.parametrize("index,dim1_start", [((3, 7), 5), ((15, 0, 9), 32)])
+def test_indexed_add_bit_exact(index, dim1_start):
+    src, fn, kw = C.indexed_add(index=index, dim1_start=dim1_start)
+    got, ref, _ = _both(src, fn, kw, "output_ptr")
+    np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("write,pages", [(False, None), (True, None), (True, [3, 7, 3, 1, 0, 7, 2, 5])],
+                         ids=["copy", "write", "write_repeated_pages"])
+def test_paged_tensor_bit_exact(write, pages):
+    src, fn, kw = C.paged_tensor(write=write, pages=pages)
+    got, ref, _ = _both(src, fn, kw, "y_ptr")
+    np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+def test_expert_gather_bit_exact():
+    src, fn, kw = C.expert_gather()
+    got, ref, _ = _both(src, fn, kw, "out_ptr")
+    np.testing.assert_array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("outer,inner", [(2, 2), (5, 3)])
+def test_nested_yield(outer, inner):
+    src, fn, kw = C.nested_yield(outer, inner)
+    got, ref, _ = _both(src, fn, kw, "out")
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(got, np.full(4, float(outer), np.float32))

@@ -225,3 +225,86 @@ def test_rope_generator_is_the_example():
     mine = oracle(configs.rope(), "rope_fwd_kernel", kw)["out_ptr"]
     ex = oracle(os.path.join(EXAMPLES, "latency/rope_fwd_4x2.mlir"), "rope_fwd_kernel", kw)["out_ptr"]
     np.testing.assert_array_equal(_bits(mine), _bits(ex))
+
+
+# ---------------------------------------------------------------------------
+# indirect forms: indexed add (i64 index), paged tensor copy and write,
+# expert gather; nested loops with iter_args
+# ---------------------------------------------------------------------------
+
+from tests import _cases as C  # noqa: E402
+
+
+def paged_copy_closed_form(kw, P):
+    x, idx = kw["x_ptr"], kw["idx_ptr"]
+    out = np.zeros_like(kw["y_ptr"])
+    for b in range(idx.shape[0]):
+        for t in range(idx.shape[1] * P):
+            out[b, t] = x[idx[b, t // P], :, t % P]
+    return out
+
+
+def paged_write_closed_form(kw, P):
+    """Later (b, h, t, d) points win where two pages repeat: the reference's
+    last writer in variables-space order (memory.py:290)."""
+    x, idx = kw["x_ptr"], kw["idx_ptr"]
+    out = kw["y_ptr"].copy()
+    for b in range(idx.shape[0]):
+        for h in range(x.shape[2]):
+            for t in range(idx.shape[1] * P):
+                out[idx[b, t // P], h, t % P] = x[b, t, h]
+    return out
+
+
+def test_indexed_add_closed_form():
+    src, fn, kw = C.indexed_add()
+    got = oracle(src, fn, kw)["output_ptr"]
+    s = kw["dim1_start"]
+    np.testing.assert_array_equal(_bits(got), _bits(kw["x_ptr"][kw["index_ptr"]][:, s:s + 32] + kw["y_ptr"]))
+
+
+@pytest.mark.skipif(not os.path.isdir(EXAMPLES), reason="reference example kernels not present")
+def test_indexed_add_generator_is_the_example():
+    """At the example's shapes (x [128, 64, 8, 128], grid [2, 8], 32 rows
+    from dim1_start) with the reference test's index (3, 7)."""
+    src, fn, kw = C.indexed_add(rows=128, d1=64, heads=8, D=128, width=32, index=(3, 7), dim1_start=0)
+    mine = oracle(src, fn, kw)["output_ptr"]
+    ex = oracle(os.path.join(EXAMPLES, "triton-ktir/indexed_add.mlir"), fn, kw)["output_ptr"]
+    np.testing.assert_array_equal(_bits(mine), _bits(ex))
+
+
+@pytest.mark.parametrize("write", [False, True], ids=["copy", "write"])
+def test_paged_tensor_closed_form(write):
+    src, fn, kw = C.paged_tensor(write=write)
+    got = oracle(src, fn, kw)["y_ptr"]
+    want = (paged_write_closed_form if write else paged_copy_closed_form)(kw, 64)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
+
+
+def test_paged_tensor_write_repeated_page_last_writer():
+    """A page named twice in the table: the later table entry's rows win."""
+    pages = [3, 7, 3, 1, 0, 7, 2, 5]
+    src, fn, kw = C.paged_tensor(write=True, pages=pages)
+    got = oracle(src, fn, kw)["y_ptr"]
+    np.testing.assert_array_equal(_bits(got), _bits(paged_write_closed_form(kw, 64)))
+    first_wins = kw["y_ptr"].copy()
+    x, idx = kw["x_ptr"], kw["idx_ptr"]
+    for b in reversed(range(idx.shape[0])):
+        for h in range(x.shape[2]):
+            for t in reversed(range(idx.shape[1] * 64)):
+                first_wins[idx[b, t // 64], h, t % 64] = x[b, t, h]
+    assert not np.array_equal(_bits(got), _bits(first_wins))
+
+
+def test_expert_gather_closed_form():
+    src, fn, kw = C.expert_gather()
+    got = oracle(src, fn, kw)["out_ptr"]
+    np.testing.assert_array_equal(_bits(got), _bits(kw["x_ptr"][kw["idx_ptr"]]))
+
+
+def test_nested_yield_value():
+    """The reference test's value (tests/test_examples.py:1197-1209): 2.0."""
+    src, fn, kw = C.nested_yield()
+    np.testing.assert_array_equal(oracle(src, fn, kw)["out"], np.full(4, 2.0, np.float32))
+    src, fn, kw = C.nested_yield(outer=5, inner=3)
+    np.testing.assert_array_equal(oracle(src, fn, kw)["out"], np.full(4, 5.0, np.float32))
