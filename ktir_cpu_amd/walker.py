@@ -2083,6 +2083,23 @@ class Executor:
                 for c in self.lanes.cores:
                     self.lat.record_op(int(c), comb, n_elems=other * half)
                 m = half + (m % 2)
+        if n > rt.MAX_ROW:
+            # a row longer than the row kernels fold in LDS: the first halving
+            # levels of the same pairwise fold run as elementwise programs on
+            # the two halves (an odd last element carried), the rest as a row
+            # program; the combiner runs are already charged above
+            lat, self.lat = self.lat, None
+            try:
+                while n > rt.MAX_ROW:
+                    half = n // 2
+                    comb_t = self._combine(region, self._take_range(t, nd - 1, 0, half),
+                                           self._take_range(t, nd - 1, half, 2 * half))
+                    if n % 2:
+                        comb_t = self._concat(comb_t, self._take_range(t, nd - 1, 2 * half, n), nd - 1)
+                    t = comb_t
+                    n = t.shape[-1]
+            finally:
+                self.lat = lat
         e = t.e
         if e.has_fold and (e._fold != n or len(_fold_space(e)) != len(t.shape)):
             e = self.materialize(t).e

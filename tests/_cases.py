@@ -1421,3 +1421,79 @@ def nested_yield(outer=2, inner=2, n=4):
 }}
 """
     return src, "nested_yield", dict(out=np.zeros(n, np.float32))
+
+
+def softmax_wide(rows=2, cols=4096, cores=1):
+    """The row softmax of the reference's examples/ktir/softmax_wide.mlir:
+    rows [start, min(start + chunk, R)) per core, a whole row per step in
+    f16, `maxnumf` row max and sum read by tensor.extract.  At its own width
+    (262144) one row's tile exceeds the 2 MiB LX scratchpad and the run
+    raises the reference's overflow error."""
+    chunk = -(-rows // cores)
+    T = configs._t([1, cols], "f16")
+    at = f"!ktdp.access_tile<1x{cols}xindex>"
+    src = f"""module {{
+  func.func @softmax_kernel(%output_ptr: index, %input_ptr: index) attributes {{grid = [{cores}, 1]}} {{
+    %core_id = ktdp.get_compute_tile_id : index
+    %c_chunk = arith.constant {chunk} : index
+    %c_R = arith.constant {rows} : index
+    %c1 = arith.constant 1 : index
+    %start = arith.muli %core_id, %c_chunk : index
+    %end_raw = arith.addi %start, %c_chunk : index
+    %cmp = arith.cmpi slt, %end_raw, %c_R : index
+    %end = arith.select %cmp, %end_raw, %c_R : index
+{configs._view("in_view", "input_ptr", [rows, cols], [cols, 1], "f16")}
+{configs._view("out_view", "output_ptr", [rows, cols], [cols, 1], "f16")}
+    scf.for %row = %start to %end step %c1 : index {{
+      %c0 = arith.constant 0 : index
+{configs._tile("in_acc", "in_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      %x = ktdp.load %in_acc : {at} -> {T}
+      %neg_inf = arith.constant 0xFC00 : f16
+      %max_init = tensor.splat %neg_inf : tensor<1xf16>
+      %row_max = linalg.reduce {{ arith.maxnumf }} ins(%x : {T}) outs(%max_init : tensor<1xf16>) dimensions = [1]
+      %m = tensor.extract %row_max[%c0] : tensor<1xf16>
+      %mb = tensor.splat %m : {T}
+      %d = arith.subf %x, %mb : {T}
+      %e = math.exp %d : {T}
+      %zero = arith.constant 0.0 : f16
+      %sum_init = tensor.splat %zero : tensor<1xf16>
+      %sum = linalg.reduce {{ arith.addf }} ins(%e : {T}) outs(%sum_init : tensor<1xf16>) dimensions = [1]
+      %s = tensor.extract %sum[%c0] : tensor<1xf16>
+      %sb = tensor.splat %s : {T}
+      %y = arith.divf %e, %sb : {T}
+{configs._tile("out_acc", "out_view", ["%row", "%c0"], [1, cols], [rows, cols], "f16", "      ")}
+      ktdp.store %y, %out_acc : {T}, {at}
+      scf.yield
+    }}
+    return
+  }}
+}}
+"""
+    rng = np.random.default_rng(5)
+    return src, "softmax_kernel", dict(output_ptr=np.zeros((rows, cols), np.float16),
+                                       input_ptr=rng.standard_normal((rows, cols)).astype(np.float16))
+
+
+def scalar_broadcast(shape=(4, 64), dt="f16"):
+    """The reference's examples/ktir/scalar_broadcast.mlir: a 1x1 tile
+    collapsed to a 0-d tensor and broadcast over every dimension of the
+    output (linalg.broadcast dimensions [0, 1])."""
+    T = configs._t(list(shape), dt)
+    src = f"""module {{
+  func.func @scalar_broadcast(%in_ptr: index, %out_ptr: index) attributes {{grid = [1]}} {{
+    %c0 = arith.constant 0 : index
+{configs._view("in_view", "in_ptr", [1, 1], [1, 1], dt)}
+{configs._tile("in_tile", "in_view", ["%c0", "%c0"], [1, 1], [1, 1], dt)}
+    %in = ktdp.load %in_tile : !ktdp.access_tile<1x1xindex> -> {configs._t([1, 1], dt)}
+    %s = tensor.collapse_shape %in [] : {configs._t([1, 1], dt)} into tensor<{dt}>
+    %init = tensor.empty() : {T}
+    %b = linalg.broadcast ins(%s : tensor<{dt}>) outs(%init : {T}) dimensions = [0, 1]
+{configs._view("out_view", "out_ptr", list(shape), [shape[1], 1], dt)}
+{configs._tile("out_tile", "out_view", ["%c0", "%c0"], list(shape), list(shape), dt)}
+    ktdp.store %b, %out_tile : {T}, !ktdp.access_tile<{shape[0]}x{shape[1]}xindex>
+    return
+  }}
+}}
+"""
+    npdt = np.float16 if dt == "f16" else np.float32
+    return src, "scalar_broadcast", dict(in_ptr=np.array([[-3.25]], npdt), out_ptr=np.zeros(shape, npdt))

@@ -277,6 +277,18 @@ def test_row_reduce_bit_exact(cols, combiner, limit, row_grid_limit):
     np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
 
 
+@pytest.mark.parametrize("cols,dt", [(40000, "f32"), (70001, "f32"), (65536, "f16")])
+@pytest.mark.parametrize("combiner", ["arith.addf", "arith.maximumf"])
+def test_row_reduce_longer_than_lds_bit_exact(cols, dt, combiner):
+    """Rows longer than a row program folds in LDS (16384): the first
+    halving levels run as elementwise programs on the two halves (an odd
+    last element carried, 70001 columns), the rest as the row program; the
+    result is the reference's pairwise-halving fold bit for bit."""
+    ref, out, _ = _run(_cases.row_reduce(rows=4, cols=cols, rblk=2, combiner=combiner, dt=dt,
+                                         decades=6 if dt == "f32" else 2))
+    np.testing.assert_array_equal(out["y_ptr"], ref["y_ptr"])
+
+
 @pytest.mark.parametrize("cols", [256, 4096])
 def test_row_reduce_f16_bit_exact(cols):
     ref, out, _ = _run(_cases.row_reduce(rows=16, cols=cols, dt="f16"))

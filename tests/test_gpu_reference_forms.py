@@ -107,3 +107,20 @@ def test_nested_yield(outer, inner):
     got, ref, _ = _both(src, fn, kw, "out")
     np.testing.assert_array_equal(got, ref)
     np.testing.assert_array_equal(got, np.full(4, float(outer), np.float32))
+
+
+@pytest.mark.parametrize("rows,cols,cores", [(2, 4096, 1), (8, 16384, 4), (3, 262144, 2)])
+def test_softmax_wide_within_tolerance(rows, cols, cores):
+    """The f16 row softmax of examples/ktir/softmax_wide.mlir, up to its own
+    262144-element rows."""
+    src, fn, kw = C.softmax_wide(rows, cols, cores)
+    got, ref, _ = _both(src, fn, kw, "output_ptr")
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_scalar_broadcast_bit_exact(dt):
+    src, fn, kw = C.scalar_broadcast(dt=dt)
+    got, ref, _ = _both(src, fn, kw, "out_ptr")
+    np.testing.assert_array_equal(got, ref)
+    assert np.all(got == kw["in_ptr"][0, 0])
