@@ -302,6 +302,105 @@ __global__ __launch_bounds__(256) void prog_map(const ktir_prog_t P, const FlatD
   }
 }
 
+// Three or four inputs of one dtype DI, four registers (the host's register
+// allocation reuses an input's register once it is dead, so a RoPE half
+// (x1 cos - x2 sin) fits), one store: the form of prog_map with NIN inputs,
+// every array indexed by constants only (named per-chunk values).
+struct MapOffs4 {
+  int64_t in[4], o, lane;
+};
+
+__device__ __forceinline__ MapOffs4 map_offsets4(const ktir_prog_t& P, const FlatDivs& D, int nin,
+                                                 const ktir_leaf_t& LO, uint32_t vid) {
+  const int nd = P.ndim;
+  uint32_t c[KTIR_MAX_DIMS] = {0, 0, 0, 0};
+  const uint32_t row = fdiv(vid, D.nvi);
+  const int64_t col = (int64_t)(vid - row * D.nvi.d) * 8;
+  uint32_t t = row;
+#pragma unroll
+  for (int d = KTIR_MAX_DIMS - 2; d >= 0; --d) {
+    if (d < nd - 1) {
+      const uint32_t q = fdiv(t, D.dim[d]);
+      c[d] = t - q * D.dim[d].d;
+      t = q;
+    }
+  }
+  MapOffs4 m;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const ktir_leaf_t& L = P.leaves[P.pf_leaf[k < nin ? k : nin - 1]];   // a fourth slot repeats the last input
+    int64_t o = lane_offset(L, t) + (L.strides[nd - 1] == 0 ? 0 : col);
+#pragma unroll
+    for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
+      if (d < nd - 1) o += (int64_t)c[d] * L.strides[d];
+    m.in[k] = o;
+  }
+  m.o = lane_offset(LO, t) + col;
+#pragma unroll
+  for (int d = 0; d < KTIR_MAX_DIMS - 1; ++d)
+    if (d < nd - 1) m.o += (int64_t)c[d] * LO.strides[d];
+  m.lane = t;
+  return m;
+}
+
+template <int DI, int NIN>
+__device__ __forceinline__ void map_run4(const ktir_prog_t& P, int n_ops, int out_reg, int64_t lane, const float (&x0)[8],
+                                         const float (&x1)[8], const float (&x2)[8], const float (&x3)[8], float (&out)[8]) {
+  Reg4 R[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) R[e] = Reg4{x0[e], x1[e], x2[e], NIN > 3 ? x3[e] : 0.f};
+  for (int pc = 0; pc < n_ops; ++pc) exec8(P, P.instr[pc], R, lane);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = R[e].get(out_reg);
+}
+
+template <int DI, int DO, int NIN>
+__global__ __launch_bounds__(256) void prog_map_n(const ktir_prog_t P, const FlatDivs D, uint32_t total, int st_leaf) {
+  const ktir_leaf_t& LO = P.leaves[st_leaf];
+  const ktir_leaf_t& L0 = P.leaves[P.pf_leaf[0]];
+  const ktir_leaf_t& L1 = P.leaves[P.pf_leaf[1]];
+  const ktir_leaf_t& L2 = P.leaves[P.pf_leaf[2]];
+  const ktir_leaf_t& L3 = P.leaves[P.pf_leaf[NIN > 3 ? 3 : 2]];
+  const int nd = P.ndim;
+  const int n_ops = P.n_instr - 1;
+  const int out_reg = P.instr[n_ops].a;
+  const bool bc0 = L0.strides[nd - 1] == 0, bc1 = L1.strides[nd - 1] == 0, bc2 = L2.strides[nd - 1] == 0,
+             bc3 = L3.strides[nd - 1] == 0;
+  const uint32_t step = gridDim.x * 512;
+  for (uint32_t v0 = blockIdx.x * 512 + threadIdx.x; v0 < total; v0 += step) {
+    const bool on1 = v0 + 256 < total;
+    const MapOffs4 m0 = map_offsets4(P, D, NIN, LO, v0);
+    const MapOffs4 m1 = map_offsets4(P, D, NIN, LO, on1 ? v0 + 256 : v0);
+    float a0[8], b0[8], c0[8], d0[8], a1[8], b1[8], c1[8], d1[8];
+    auto in = [](const ktir_leaf_t& L, int64_t o) { return o >= L.lo && o + 8 <= L.hi; };
+    bool inb = on1 && !bc0 && !bc1 && !bc2 && !bc3;
+    inb = inb && in(L0, m0.in[0]) && in(L0, m1.in[0]) && in(L1, m0.in[1]) && in(L1, m1.in[1]) &&
+          in(L2, m0.in[2]) && in(L2, m1.in[2]) && in(L3, m0.in[3]) && in(L3, m1.in[3]);
+    if (__all(inb)) {
+      const Raw8<DI> r00 = raw_load<DI>(L0.ptr, m0.in[0]), r01 = raw_load<DI>(L1.ptr, m0.in[1]),
+                     r02 = raw_load<DI>(L2.ptr, m0.in[2]), r03 = raw_load<DI>(L3.ptr, m0.in[3]);
+      const Raw8<DI> r10 = raw_load<DI>(L0.ptr, m1.in[0]), r11 = raw_load<DI>(L1.ptr, m1.in[1]),
+                     r12 = raw_load<DI>(L2.ptr, m1.in[2]), r13 = raw_load<DI>(L3.ptr, m1.in[3]);
+      raw_decode<DI>(r00, a0); raw_decode<DI>(r01, b0); raw_decode<DI>(r02, c0); raw_decode<DI>(r03, d0);
+      raw_decode<DI>(r10, a1); raw_decode<DI>(r11, b1); raw_decode<DI>(r12, c1); raw_decode<DI>(r13, d1);
+    } else {
+      load8<DI>(L0, m0.in[0], a0, bc0); load8<DI>(L1, m0.in[1], b0, bc1);
+      load8<DI>(L2, m0.in[2], c0, bc2); load8<DI>(L3, m0.in[3], d0, bc3);
+      if (on1) {
+        load8<DI>(L0, m1.in[0], a1, bc0); load8<DI>(L1, m1.in[1], b1, bc1);
+        load8<DI>(L2, m1.in[2], c1, bc2); load8<DI>(L3, m1.in[3], d1, bc3);
+      }
+    }
+    float out[8];
+    map_run4<DI, NIN>(P, n_ops, out_reg, m0.lane, a0, b0, c0, d0, out);
+    store8<DO>(LO, m0.o, out);
+    if (on1) {
+      map_run4<DI, NIN>(P, n_ops, out_reg, m1.lane, a1, b1, c1, d1, out);
+      store8<DO>(LO, m1.o, out);
+    }
+  }
+}
+
 // The single-binary-op form in a kernel of its own (no interpreter, so few
 // registers): MAP_BU chunks per thread per step, 256 chunks apart.  When the
 // whole wavefront's chunks lie inside their allocations (one uniform test)
@@ -407,9 +506,27 @@ static bool pick_b(int db, int dout, const ktir_prog_t& Q, const FlatDivs& D, ui
   return false;
 }
 
+template <int DI>
+static bool pick_n(int dout, const ktir_prog_t& Q, const FlatDivs& D, uint32_t total, int st) {
+  int64_t blocks = ((int64_t)total + 511) / 512;
+  if (blocks > 1048576) blocks = 1048576;
+  const dim3 g((unsigned)blocks), b(256);
+#define KTIR_MAPN(DO)                                                                           \
+  if (Q.n_pf == 3) hipLaunchKernelGGL((prog_map_n<DI, DO, 3>), g, b, 0, stream(), Q, D, total, st); \
+  else hipLaunchKernelGGL((prog_map_n<DI, DO, 4>), g, b, 0, stream(), Q, D, total, st);           \
+  return true;
+  switch (dout) {
+    case KTIR_F16: KTIR_MAPN(KTIR_F16)
+    case KTIR_BF16: KTIR_MAPN(KTIR_BF16)
+    case KTIR_F32: KTIR_MAPN(KTIR_F32)
+  }
+#undef KTIR_MAPN
+  return false;
+}
+
 // Launch `Q` through a map kernel if it has the supported form.
 bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner) {
-  if (Q.mode != 0 || Q.n_pf < 1 || Q.n_pf > 2 || Q.n_instr < 1 || inner % 8) return false;
+  if (Q.mode != 0 || Q.n_pf < 1 || Q.n_pf > 4 || Q.n_instr < 1 || inner % 8) return false;
   const ktir_instr_t& st = Q.instr[Q.n_instr - 1];
   if (st.op != KTIR_OP_ST || st.a > 3) return false;
   for (int i = 0; i < Q.n_instr - 1; ++i) {
@@ -437,6 +554,16 @@ bool try_launch_map(const ktir_prog_t& Q, int64_t rows, int64_t inner) {
   const int db = Q.n_pf == 2 ? Q.leaves[Q.pf_leaf[1]].dtype : da;
   const int dout = Q.leaves[st.aux].dtype;
   const uint32_t total = (uint32_t)chunks;
+  if (Q.n_pf > 2) {
+    for (int k = 1; k < Q.n_pf; ++k)
+      if (Q.leaves[Q.pf_leaf[k]].dtype != da) return false;
+    switch (da) {
+      case KTIR_F16: return pick_n<KTIR_F16>(dout, Q, D, total, st.aux);
+      case KTIR_BF16: return pick_n<KTIR_BF16>(dout, Q, D, total, st.aux);
+      case KTIR_F32: return pick_n<KTIR_F32>(dout, Q, D, total, st.aux);
+    }
+    return false;
+  }
   if (Q.n_pf == 1) {
     switch (da) {
       case KTIR_F16: return pick_b<KTIR_F16, 1>(db, dout, Q, D, total, st.aux);

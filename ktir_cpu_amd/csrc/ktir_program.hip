@@ -285,6 +285,10 @@ extern "C" int ktir_launch_program(const ktir_prog_t* P) {
     }
     dim3 b(256);
     uint32_t nv = (uint32_t)vecs;
+    if (!full && P->n_pf > 2 && try_launch_map(*P, rows, inner)) {   // three or four inputs in four registers
+      KTIR_HIP_CHECK(hipGetLastError());
+      return KTIR_OK;
+    }
     if (!full && try_launch_tile(*P, P->lanes, per_lane, inner)) {
       KTIR_HIP_CHECK(hipGetLastError());
       return KTIR_OK;
