@@ -114,10 +114,9 @@ __device__ __forceinline__ float fmax3_nan(float a, float b, float c) { return f
 
 // x = -inf in the lanes of mask, in place (v_cndmask_b32 on x's own
 // register: the caller's S values keep the registers the MFMAs wrote)
-__device__ __forceinline__ float mask_ninf(float x, uint64_t mask) {
-  asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(x) : "v"(-__builtin_inff()), "s"(mask));
-  return x;
-}
+// -inf where `kill` holds: a plain select, so the compiler inserts the wait
+// states between an MFMA result and this VALU read itself
+__device__ __forceinline__ float mask_ninf(float x, bool kill) { return kill ? -__builtin_inff() : x; }
 
 // e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32)
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(__fmul_rn(x, LOG2E)); }
@@ -589,12 +588,10 @@ __global__ __launch_bounds__(512, 1) void attn_pp(const ktir_attn_t d, int mlo, 
       const bool all_keep = !d.causal ||                                                             \
           (minv ? (dbase + 127 < mlo || dbase > mhi) : (dbase >= mlo && dbase + 127 <= mhi));        \
       if (!__all(all_keep)) {                                                                        \
-        /* wait states between the MFMA writes of S and these VALU reads */                          \
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");                                  \
         _Pragma("unroll") for (int kt = 0; kt < 4; ++kt) {                                           \
           _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                           \
             const int df = dbase + kt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);                         \
-            sc[kt][i] = mask_ninf(sc[kt][i], __builtin_amdgcn_ballot_w64((df >= mlo && df <= mhi) == (bool)minv)); \
+            sc[kt][i] = mask_ninf(sc[kt][i], (df >= mlo && df <= mhi) == (bool)minv);                \
           }                                                                                          \
         }                                                                                            \
       }                                                                                              \

@@ -298,7 +298,6 @@ def _row_rmw(ex, op, lb, st, trips):
     bs = vs.base - as_.addr // rt.ELEM_BYTES[vs.dtype]
     if np.any(bd != bd[0]) or np.any(bs != bs[0]):
         return None
-    dst_t = ex.get_value(dst_load.results[0], peek=True) if False else None
     dt_dst = vd.dtype
     dt_src = vs.dtype
     # result dtype of the combine op (NumPy promotion as in the op-by-op path)
