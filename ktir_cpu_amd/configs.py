@@ -664,7 +664,7 @@ def _gen1(ins, out_t, args, body, res, indent="      "):
 
 def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head: int = 128,
                     page: int = 16, blocks: int = 64, max_pages: int = 16, block_q: int = 2,
-                    total_tokens: int = 0) -> str:
+                    total_tokens: int = 0, dt: str = "f16", causal: bool = True) -> str:
     """Causal grouped-query attention over a paged KV cache, in the form of
     the reference's unified 2-D attention example
     (examples/triton-ktir/paged_attention.mlir, parameters in its header and
@@ -678,18 +678,20 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
     reads page block_tables[0, offset + j] of K and V through indirect access
     tiles, masks key position j*page + c above context_len + token position,
     and keeps the online-softmax state (row max M, row sum L starting at 1,
-    f32 accumulator).  Output = acc / L, truncated to f16.
+    f32 accumulator).  Output = acc / L, truncated to f16.  `dt` sets the
+    element type of query, caches and output (f16 or bf16); `causal` False
+    drops the mask generic.
     """
     g = q_heads // kv_heads
     bm = block_q * g
     D = head
     qs, cs = [max(total_tokens, tokens), q_heads, D], [blocks, page, kv_heads, D]
     qst, cst = [q_heads * D, D, 1], [page * kv_heads * D, kv_heads * D, D, 1]
-    Q3 = _t([block_q, g, D], "f16")
-    Qh, Qf = _t([bm, D], "f16"), _t([bm, D], "f32")
-    K4 = _t([1, page, 1, D], "f16")
-    Kh, Kf = _t([page, D], "f16"), _t([page, D], "f32")
-    KTh, KTf = _t([D, page], "f16"), _t([D, page], "f32")
+    Q3 = _t([block_q, g, D], dt)
+    Qh, Qf = _t([bm, D], dt), _t([bm, D], "f32")
+    K4 = _t([1, page, 1, D], dt)
+    Kh, Kf = _t([page, D], dt), _t([page, D], "f32")
+    KTh, KTf = _t([D, page], dt), _t([D, page], "f32")
     Sf, Vf = _t([bm, page], "f32"), _t([bm], "f32")
     at_q = f"!ktdp.access_tile<{block_q}x{g}x{D}xindex>"
     at_kv = f"!ktdp.access_tile<1x{page}x1x{D}xindex>"
@@ -701,7 +703,7 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
                 f"          %{view}[ind(%bt_view[%c0, %bt_col + %e0]), (%e1), (%p1 + %e2), (%e3)] {{\n"
                 f"        variables_space_set = {vss},\n"
                 f"        variables_space_order = affine_map<(d0, d1, d2, d3) -> (d0, d1, d2, d3)>\n"
-                f"      }} : memref<{'x'.join(map(str, cs))}xf16>, memref<1x{max_pages}xi32> -> {at_kv}")
+                f"      }} : memref<{'x'.join(map(str, cs))}x{dt}>, memref<1x{max_pages}xi32> -> {at_kv}")
 
     mask = _gen2([("%s", Sf)], ["d0, d1", "d0, d1"], Sf, "%sv: f32, %o: f32", [
         "%r = linalg.index 0 : index",
@@ -715,7 +717,8 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
         "linalg.yield %mv : f32"], "%sm_init")
     m_new = _gen1([("%M", Vf), ("%rm", Vf)], Vf, "%a: f32, %b: f32, %o: f32",
                   ["%mx = arith.maximumf %a, %b : f32", "linalg.yield %mx : f32"], "%mn_init")
-    p = _gen2([("%sm", Sf), ("%m_new", Vf)], ["d0, d1", "d0", "d0, d1"], Sf, "%sv: f32, %mv: f32, %o: f32",
+    sm = "%sm" if causal else "%s"
+    p = _gen2([(sm, Sf), ("%m_new", Vf)], ["d0, d1", "d0", "d0, d1"], Sf, "%sv: f32, %mv: f32, %o: f32",
               ["%dd = arith.subf %sv, %mv : f32", "%ee = math.exp %dd : f32", "linalg.yield %ee : f32"], "%p_init")
     alpha = _gen1([("%M", Vf), ("%m_new", Vf)], Vf, "%a: f32, %b: f32, %o: f32",
                   ["%dd = arith.subf %a, %b : f32", "%ee = math.exp %dd : f32", "linalg.yield %ee : f32"],
@@ -725,6 +728,7 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
     l_new = _gen1([("%L", Vf), ("%alpha", Vf), ("%ls", Vf)], Vf, "%l: f32, %al: f32, %lj: f32, %o: f32",
                   ["%la = arith.mulf %l, %al : f32", "%ln = arith.addf %la, %lj : f32", "linalg.yield %ln : f32"],
                   "%ln_init")
+    masked = f"      %sm_init = tensor.empty() : {Sf}\n      %sm = {mask}\n" if causal else ""
     fin = _gen2([("%acc_f", Qf), ("%L_f", Vf)], ["d0, d1", "d0", "d0, d1"], Qf, "%av: f32, %lv: f32, %o: f32",
                 ["%qq = arith.divf %av, %lv : f32", "linalg.yield %qq : f32"], "%fin_init", "    ")
     return f"""module {{
@@ -741,12 +745,12 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
     %p0_q = arith.muli %p0, %cBQ : index
     %q_row = arith.addi %cur_batch_start_index, %p0_q : index
     %head0 = arith.muli %p1, %cG : index
-{_view("q_view", "query_ptr", qs, qst, "f16")}
-{_view("k_view", "key_cache_ptr", cs, cst, "f16")}
-{_view("v_view", "value_cache_ptr", cs, cst, "f16")}
+{_view("q_view", "query_ptr", qs, qst, dt)}
+{_view("k_view", "key_cache_ptr", cs, cst, dt)}
+{_view("v_view", "value_cache_ptr", cs, cst, dt)}
 {_view("bt_view", "block_tables_ptr", [1, max_pages], [max_pages, 1], "i32")}
-{_view("o_view", "output_ptr", qs, qst, "f16")}
-{_tile("q_acc", "q_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, "f16")}
+{_view("o_view", "output_ptr", qs, qst, dt)}
+{_tile("q_acc", "q_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, dt)}
     %q3 = ktdp.load %q_acc : {at_q} -> {Q3}
     %qh = tensor.collapse_shape %q3 [[0, 1], [2]] : {Q3} into {Qh}
     %q = arith.extf %qh : {Qh} to {Qf}
@@ -775,10 +779,8 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
       %scale_t = tensor.splat %scale : {Sf}
       %s = arith.mulf %scale_t, %qk : {Sf}
       %k0 = arith.muli %j, %cP : index
-      %sm_init = tensor.empty() : {Sf}
-      %sm = {mask}
-      %rm_init = tensor.splat %neg_inf : {Vf}
-      %rm = linalg.reduce ins(%sm : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
+{masked}      %rm_init = tensor.splat %neg_inf : {Vf}
+      %rm = linalg.reduce ins({sm} : {Sf}) outs(%rm_init : {Vf}) dimensions = [1]
         (%a: f32, %b: f32) {{
           %mx = arith.maximumf %a, %b : f32
           linalg.yield %mx : f32
@@ -806,7 +808,7 @@ def paged_attention(tokens: int = 8, q_heads: int = 32, kv_heads: int = 8, head:
     %of = {fin}
     %oh = arith.truncf %of : {Qf} to {Qh}
     %o3 = tensor.expand_shape %oh [[0, 1], [2]] output_shape [{block_q}, {g}, {D}] : {Qh} into {Q3}
-{_tile("o_acc", "o_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, "f16")}
+{_tile("o_acc", "o_view", ["%q_row", "%head0", "%c0"], [block_q, g, D], qs, dt)}
     ktdp.store %o3, %o_acc : {Q3}, {at_q}
     return
   }}

@@ -124,3 +124,54 @@ def test_scalar_broadcast_bit_exact(dt):
     got, ref, _ = _both(src, fn, kw, "out_ptr")
     np.testing.assert_array_equal(got, ref)
     assert np.all(got == kw["in_ptr"][0, 0])
+
+
+def _bf16_f32(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_paged_attention_bf16_within_tolerance():
+    from oracle.interp import bf16_bits
+    kw = {k: (bf16_bits(v.astype(np.float32)) if k != "block_tables_ptr" else v) for k, v in paged_inputs().items()}
+    got, ref, plan = _both(configs.paged_attention(dt="bf16"), PA_FN, dict(kw, **PA_ARGS), "output_ptr")
+    np.testing.assert_allclose(_bf16_f32(got), _bf16_f32(ref), rtol=1e-2, atol=1e-3)
+    assert plan.counts().get("pattn") == 1
+
+
+def test_paged_attention_without_mask_within_tolerance():
+    kw = dict(paged_inputs(seed=3), **PA_ARGS)
+    got, ref, plan = _both(configs.paged_attention(causal=False), PA_FN, kw, "output_ptr")
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+    assert plan.counts().get("pattn") == 1
+
+
+def test_paged_attention_no_tiles_gives_zero():
+    """num_tiles = 0: the loop does not run; acc / L = 0 / 1."""
+    kw = dict(paged_inputs(), **dict(PA_ARGS, num_tiles=0))
+    got, ref, _ = _both(configs.paged_attention(), PA_FN, kw, "output_ptr")
+    np.testing.assert_array_equal(got, ref)
+    assert not np.any(got)
+
+
+def test_paged_attention_page_past_the_cache_reads_zero():
+    """A table entry beyond the cache's blocks: its K and V rows read as
+    zeros (the reference's zero-pad on over-read), on both paths."""
+    kw = paged_inputs()
+    kw["block_tables_ptr"][0, 3] = 64 + 5
+    got, ref, _ = _both(configs.paged_attention(), PA_FN, dict(kw, **PA_ARGS), "output_ptr")
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+
+
+def test_paged_attention_negative_page_raises():
+    from ktir_cpu_amd.interpreter import KTIRInterpreter
+    kw = paged_inputs()
+    kw["block_tables_ptr"][0, 2] = -1
+    args = dict(kw, **PA_ARGS)
+    o = OracleInterpreter()
+    o.load(configs.paged_attention())
+    with pytest.raises(IndexError):
+        o.execute_function(PA_FN, **{k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in args.items()})
+    g = KTIRInterpreter()
+    g.load(configs.paged_attention())
+    with pytest.raises(IndexError):
+        g.execute_function(PA_FN, **args)
