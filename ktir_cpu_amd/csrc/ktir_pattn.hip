@@ -211,7 +211,15 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
       if (live) {
         const float* q = Qs + r * DP;
         const float* k = Ks + c * DP;
-        for (int x = part; x < D; x += TP) s = __fmaf_rn(q[x], k[x], s);
+        float s2 = 0.f;
+        int x = part;
+#pragma unroll 4
+        for (; x + TP < D; x += 2 * TP) {
+          s = __fmaf_rn(q[x], k[x], s);
+          s2 = __fmaf_rn(q[x + TP], k[x + TP], s2);
+        }
+        if (x < D) s = __fmaf_rn(q[x], k[x], s);
+        s += s2;
       }
       for (int o = 1; o < TP; o <<= 1) s += __shfl_xor(s, o);
       s = __fmul_rn(d.scale, s);
@@ -304,9 +312,15 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
       if (i < M * D) {
         const int r = i / D, x = i - r * D;
         const float* p = S + r * N;
-        float pv = 0.f;
-        for (int c = 0; c < N; ++c) pv = __fmaf_rn(p[c], Vs[c * D + x], pv);
-        acc[k] = __fadd_rn(__fmul_rn(acc[k], arow[r]), pv);
+        float pv = 0.f, pw = 0.f;         // two chains: the LDS reads of one overlap the other's
+        int c = 0;
+#pragma unroll 4
+        for (; c + 1 < N; c += 2) {
+          pv = __fmaf_rn(p[c], Vs[c * D + x], pv);
+          pw = __fmaf_rn(p[c + 1], Vs[(c + 1) * D + x], pw);
+        }
+        if (c < N) pv = __fmaf_rn(p[c], Vs[c * D + x], pv);
+        acc[k] = __fadd_rn(__fmul_rn(acc[k], arow[r]), pv + pw);
       }
     }
     __syncthreads();
