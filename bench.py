@@ -242,7 +242,7 @@ def _traffic(config, kind):
     # attention launch's f16 copy of V included, since every timed replay
     # converts V as a call with a new V does
     b = [v["bytes"] for k, v in t.get("kernels", {}).items()
-         if any(p in k for p in pats) and (v.get("every_run", True) or kind == "attn")]
+         if any(p in k for p in pats) and (v.get("every_run", True) or kind in ("attn", "pattn"))]
     return round(sum(b)) if b else None
 
 
