@@ -414,8 +414,8 @@ int ktir_launch_attention(const ktir_attn_t* d);
  *   m' = maximumf(m, max_c s); p = exp(s - m'); alpha = exp(m - m')
  *   acc' = acc * alpha + p V; l' = l * alpha + sum_c p; m = m'
  * all in f32.  Final m, l -> m_out / l_out [lanes, M], acc -> acc_out
- * [lanes, M, D].  Limits: M * D <= 8192; LDS 4 * (M (D+1) + N (D+1) + N D +
- * M N + 3 M) bytes <= 160 KiB. */
+ * [lanes, M, D].  Limits: D a multiple of 4, M * D <= 8192; LDS 4 * (M (D+8)
+ * + N (D+8) + N D + M N + 3 M) bytes <= 160 KiB. */
 typedef struct ktir_pattn {
   int64_t lanes, M, N, D;
   uint64_t q_ptr, q_base;              /* q_base: const int64_t* [lanes] */

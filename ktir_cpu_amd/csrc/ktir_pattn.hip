@@ -54,8 +54,10 @@ __device__ __forceinline__ int64_t load_index(uint64_t ptr, int64_t e, int dt) {
   return ((const int32_t*)ptr)[e];
 }
 
+// Q and K rows are padded to D + 8 floats: 16-byte aligned rows for vector
+// LDS reads, consecutive rows two 16-byte bank groups apart
 static int64_t pa_lds_floats(int64_t M, int64_t N, int64_t D) {
-  return M * (D + 1) + N * (D + 1) + N * D + M * N + 3 * M;
+  return M * (D + 8) + N * (D + 8) + N * D + M * N + 3 * M;
 }
 
 constexpr int PA_PF = 4;                   // largest prefetch: 8-element vectors per thread and tensor (N * D <= 8192)
@@ -70,6 +72,22 @@ struct PagePf {
   uint4 k[PF], v[PF];
   int64_t k0, v0;
 };
+
+// sum over the 4-element groups g = p, p + TP, ... of q . k (16-byte aligned rows)
+__device__ __forceinline__ float dot4(const float* q, const float* k, int p, int TP, int D) {
+  const float4* q4 = (const float4*)q;
+  const float4* k4 = (const float4*)k;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll 4
+  for (int g = p; g < D / 4; g += TP) {
+    const float4 a = q4[g], b = k4[g];
+    s0 = __fmaf_rn(a.x, b.x, s0);
+    s1 = __fmaf_rn(a.y, b.y, s1);
+    s0 = __fmaf_rn(a.z, b.z, s0);
+    s1 = __fmaf_rn(a.w, b.w, s1);
+  }
+  return s0 + s1;
+}
 
 __device__ __forceinline__ int64_t page_of(const ktir_pattn_t& d, int64_t tp, int j, int* err, bool lead) {
   const int64_t te = tp + (int64_t)j * d.tbl_step;
@@ -98,9 +116,9 @@ __device__ __forceinline__ void unpack8(uint4 w, int dt, float* o) {
 template <int ACC, int PF>
 __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d, int vec, int* err) {
   extern __shared__ float sm[];
-  const int M = (int)d.M, N = (int)d.N, D = (int)d.D, DP = D + 1;
-  float* Qs = sm;                  // [M][D + 1]
-  float* Ks = Qs + M * DP;         // [N][D + 1]
+  const int M = (int)d.M, N = (int)d.N, D = (int)d.D, DP = D + 8;
+  float* Qs = sm;                  // [M][D + 8]
+  float* Ks = Qs + M * DP;         // [N][D + 8]
   float* Vs = Ks + N * DP;         // [N][D]
   float* S = Vs + N * D;           // [M][N]
   float* mrow = S + M * N;         // [M]
@@ -127,11 +145,12 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
   const int64_t qp0 = ((const int64_t*)d.qpos0)[lane], kp0 = ((const int64_t*)d.kpos0)[lane];
   const int nvec = N * D / 8;      // 8-element vectors of one page tile (vectorised form)
   vec = vec && !(kb & 7) && !(vb & 7);   // this lane's tiles start on 16-byte boundaries
-  // S = Q K^T: TP threads per (row, key) pair, each a strided part of the
-  // dot product, combined by lane shuffles (TP a power of two <= 64)
+  // S = Q K^T: TP threads per (row, key) pair, each the 4-element groups
+  // p, p + TP, ... of the dot product (16-byte LDS reads), combined by lane
+  // shuffles (TP a power of two <= 64)
   int TP = PA_THREADS / (M * N);
   if (TP < 1) TP = 1;
-  while (TP > 1 && (D % TP || (TP & (TP - 1)))) TP >>= 1;
+  while (TP > 1 && (D % (4 * TP) || (TP & (TP - 1)))) TP >>= 1;
   // row statistics by N lanes per row when N is a power of two <= 64 and
   // the rows fit the workgroup at once; otherwise one thread per row
   const bool rows_par = (N & (N - 1)) == 0 && N <= 64 && M * N <= PA_THREADS;
@@ -177,11 +196,12 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
 #pragma unroll
             for (int t = 0; t < 8; ++t) vv[t] = (ev + t >= d.v_lo && ev + t < d.v_hi) ? load_elem(d.v_ptr, ev + t, d.kv_dtype) : 0.f;
           }
-#pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            Ks[c * DP + x + t] = kv[t];
-            Vs[c * D + x + t] = vv[t];
-          }
+          float4* kd = (float4*)(Ks + c * DP + x);
+          float4* vd = (float4*)(Vs + c * D + x);
+          kd[0] = make_float4(kv[0], kv[1], kv[2], kv[3]);
+          kd[1] = make_float4(kv[4], kv[5], kv[6], kv[7]);
+          vd[0] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+          vd[1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
         }
       }
     } else {
@@ -211,15 +231,7 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
       if (live) {
         const float* q = Qs + r * DP;
         const float* k = Ks + c * DP;
-        float s2 = 0.f;
-        int x = part;
-#pragma unroll 4
-        for (; x + TP < D; x += 2 * TP) {
-          s = __fmaf_rn(q[x], k[x], s);
-          s2 = __fmaf_rn(q[x + TP], k[x + TP], s2);
-        }
-        if (x < D) s = __fmaf_rn(q[x], k[x], s);
-        s += s2;
+        s = dot4(q, k, part, TP, D);
       }
       for (int o = 1; o < TP; o <<= 1) s += __shfl_xor(s, o);
       s = __fmul_rn(d.scale, s);
@@ -252,7 +264,7 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
         const int r = pair / N, c = pair - r * N;
         const float* q = Qs + r * DP;
         const float* k = Ks + c * DP;
-        for (int x = part; x < D; x += TP) s = __fmaf_rn(q[x], k[x], s);
+        s = dot4(q, k, part, TP, D);
       }
       for (int o = 1; o < TP; o <<= 1) s += __shfl_xor(s, o);
       if (pair < M * N && part == 0) {
@@ -306,21 +318,30 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
     }
     }
     __syncthreads();
+    // the accumulator: group g = tid + k * 256 holds the 4 consecutive
+    // elements 4g .. 4g + 3 of the row-major M x D block
 #pragma unroll
-    for (int k = 0; k < ACC; ++k) {
-      const int i = tid + k * PA_THREADS;
+    for (int k = 0; k < ACC / 4; ++k) {
+      const int i = 4 * (tid + k * PA_THREADS);
       if (i < M * D) {
         const int r = i / D, x = i - r * D;
         const float* p = S + r * N;
-        float pv = 0.f, pw = 0.f;         // two chains: the LDS reads of one overlap the other's
-        int c = 0;
+        const float4* v4 = (const float4*)(Vs + x);
+        float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 4
-        for (; c + 1 < N; c += 2) {
-          pv = __fmaf_rn(p[c], Vs[c * D + x], pv);
-          pw = __fmaf_rn(p[c + 1], Vs[(c + 1) * D + x], pw);
+        for (int c = 0; c < N; ++c) {
+          const float pc = p[c];
+          const float4 v = v4[c * (D / 4)];
+          pv.x = __fmaf_rn(pc, v.x, pv.x);
+          pv.y = __fmaf_rn(pc, v.y, pv.y);
+          pv.z = __fmaf_rn(pc, v.z, pv.z);
+          pv.w = __fmaf_rn(pc, v.w, pv.w);
         }
-        if (c < N) pv = __fmaf_rn(p[c], Vs[c * D + x], pv);
-        acc[k] = __fadd_rn(__fmul_rn(acc[k], arow[r]), pv + pw);
+        const float al = arow[r];
+        acc[4 * k] = __fadd_rn(__fmul_rn(acc[4 * k], al), pv.x);
+        acc[4 * k + 1] = __fadd_rn(__fmul_rn(acc[4 * k + 1], al), pv.y);
+        acc[4 * k + 2] = __fadd_rn(__fmul_rn(acc[4 * k + 2], al), pv.z);
+        acc[4 * k + 3] = __fadd_rn(__fmul_rn(acc[4 * k + 3], al), pv.w);
       }
     }
     __syncthreads();
@@ -330,9 +351,10 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
     ((float*)d.l_out)[lane * M + r] = lrow[r];
   }
 #pragma unroll
-  for (int k = 0; k < ACC; ++k) {
-    const int i = tid + k * PA_THREADS;
-    if (i < M * D) ((float*)d.acc_out)[lane * M * D + i] = acc[k];
+  for (int k = 0; k < ACC / 4; ++k) {
+    const int i = 4 * (tid + k * PA_THREADS);
+    if (i < M * D)
+      *(float4*)((float*)d.acc_out + lane * M * D + i) = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
   }
 }
 
@@ -342,7 +364,7 @@ using namespace ktir;
 
 extern "C" int ktir_launch_paged_attention(const ktir_pattn_t* d) {
   if (!d) return set_error(KTIR_E_ARG, "ktir_launch_paged_attention: null descriptor");
-  if (d->M < 1 || d->N < 1 || d->D < 1 || d->M * d->D > (int64_t)PA_THREADS * PA_ACC || d->row_div < 1)
+  if (d->M < 1 || d->N < 1 || d->D < 4 || d->D % 4 || d->M * d->D > (int64_t)PA_THREADS * PA_ACC || d->row_div < 1)
     return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_paged_attention: M=%lld N=%lld D=%lld row_div=%lld",
                      (long long)d->M, (long long)d->N, (long long)d->D, (long long)d->row_div);
   const int64_t lds = pa_lds_floats(d->M, d->N, d->D) * (int64_t)sizeof(float);

@@ -998,8 +998,8 @@ def _paged_attention(ex, trips, tm1, q, probes, peeled, l0, slots, mask):
             or k[9] != v[9] or k[8] not in ("f16", "bf16", "f32") or k[7] not in ("i8", "i16", "i32", "i64"):
         return None
     N = k[9]
-    lds = 4 * (M * (D + 1) + N * (D + 1) + N * D + M * N + 3 * M)
-    if M * D > 8192 or lds > 160 * 1024:
+    lds = 4 * (M * (D + 8) + N * (D + 8) + N * D + M * N + 3 * M)
+    if M * D > 8192 or lds > 160 * 1024 or D % 4:
         return None
     d = rt.PATTN()
     d.lanes, d.M, d.N, d.D = L, M, N, D
