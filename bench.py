@@ -35,7 +35,6 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_TFLOPS = 2500.0
-FP32_TFLOPS = 157.3        # dense f32 (VALU FMA and MFMA alike)
 
 
 def _vector_add():
@@ -207,9 +206,9 @@ def _paged_attention():
     keys = sum(ctx + t + 1 for t in range(T))
     return dict(src=configs.paged_attention(T, HQ, HK, D, P, blocks, max_pages, BQ), fn="kernel_unified_attention_spyre_2d",
                 kw=kw, cores=(T // BQ) * HK, bytes=2 * HQ * T * D * 2 + 2 * blocks * P * HK * D * 2,
-                flops=4 * HQ * keys * D, bound="fp32",
-                dtype="f16 in/out; f32 Q K^T, scores, online-softmax state and P V (f32 FMA, the reference's "
-                      "extf'd operands)",
+                flops=4 * HQ * keys * D, bound="mfma",
+                dtype="f16 in/out; Q K^T and P V on f16 MFMA (exact f16 products, f32 accumulation, P as f16 "
+                      "hi + lo), f32 scores and online-softmax state",
                 workload=f"paged attention {T} tokens after a {ctx}-token context, {HQ} query / {HK} KV heads, "
                          f"D={D}, page {P}, {BQ} tokens per core (the reference's triton-ktir paged_attention form)")
 
@@ -421,8 +420,6 @@ def measure(name, steps, warmup, with_cpu):
     # algorithmic units (all bytes moved / all flops)
     if cfg["bound"] == "hbm":
         units, unit, peak, scale = cfg["bytes"], "GB/s", HBM_PEAK_GBS, 1e9
-    elif cfg["bound"] == "fp32":
-        units, unit, peak, scale = cfg["flops"], "TFLOP/s", FP32_TFLOPS, 1e12
     else:
         units, unit, peak, scale = cfg["flops"], "TFLOP/s", MFMA_F16_TFLOPS, 1e12
     value = units / (ms * 1e-3) / scale

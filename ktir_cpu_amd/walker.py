@@ -2832,22 +2832,48 @@ def _replace(e: Expr, old: Expr, new: Expr, memo=None) -> Expr:
 
 
 def _reshape_strides(strides, old, new) -> Optional[Tuple[int, ...]]:
-    """Strides of a reshape of a strided view, if expressible without a copy:
-    either only size-1 dims change, or the non-unit dims form one contiguous run."""
+    """Strides of a row-major reshape of a strided view, if expressible
+    without a copy (NumPy's rule): the non-unit dims of both shapes split
+    into consecutive groups of equal size; a group of old dims must be one
+    contiguous run (each stride the next one times its size), and is then
+    split into its group of new dims, whatever its stride (a broadcast dim,
+    stride 0, splits into stride-0 dims).  Size-1 dims get stride 0."""
     od = [(int(s), int(t)) for s, t in zip(old, strides) if int(s) != 1]
     nd = [int(n) for n in new]
-    if [s for s, _ in od] == [n for n in nd if n != 1]:
+    nn = [n for n in nd if n != 1]
+    if [s for s, _ in od] == nn:
         it = iter(t for _, t in od)
         return tuple(0 if n == 1 else next(it) for n in nd)
-    for (s0, t0), (s1, t1) in zip(od, od[1:]):
-        if t0 != t1 * s1:
-            return None
-    inner = od[-1][1] if od else 1
-    out, acc = [], inner
-    for n in reversed(nd):
-        out.append(0 if n == 1 else acc)
-        acc *= n
-    return tuple(reversed(out))
+    if any(s == 0 for s, _ in od) or 0 in nn:
+        return None
+    out: List[int] = []
+    i = j = 0
+    while i < len(od) and j < len(nn):
+        i2, j2, pi, pj = i + 1, j + 1, od[i][0], nn[j]
+        while pi != pj:
+            if pi < pj:
+                if i2 >= len(od):
+                    return None
+                pi *= od[i2][0]
+                i2 += 1
+            else:
+                if j2 >= len(nn):
+                    return None
+                pj *= nn[j2]
+                j2 += 1
+        for k in range(i, i2 - 1):
+            if od[k][1] != od[k + 1][1] * od[k + 1][0]:
+                return None
+        acc, grp = od[i2 - 1][1], []
+        for k in range(j2 - 1, j - 1, -1):
+            grp.append(acc)
+            acc *= nn[k]
+        out.extend(reversed(grp))
+        i, j = i2, j2
+    if i != len(od) or j != len(nn):
+        return None
+    it = iter(out)
+    return tuple(0 if n == 1 else next(it) for n in nd)
 
 
 def _use_counts(ops) -> Dict[str, int]:

@@ -52,6 +52,31 @@ def test_paged_attention_many_tokens_within_tolerance():
     assert plan.counts().get("pattn") == 1
 
 
+PA_SHAPES = [
+    # matrix-core form: head sizes 32 and 256, 16 rows per core (4 tokens x 4 heads)
+    ("d32", dict(head=32), dict(head=32), {}),
+    ("d256", dict(tokens=8, q_heads=8, kv_heads=2, head=256, blocks=32, max_pages=8),
+     dict(tokens=8, q_heads=8, kv_heads=2, head=256, blocks=32, max_pages=8), {}),
+    ("rows16", dict(block_q=4), {}, {}),
+    # f32-FMA form: pages of 32 keys, 32 rows per core (8 tokens x 4 heads)
+    ("page32", dict(page=32, blocks=32, max_pages=8), dict(page=32, blocks=32, max_pages=8),
+     dict(num_tiles=4, context_len=100)),
+    ("rows32", dict(tokens=16, block_q=8), dict(tokens=16), {}),
+]
+
+
+@pytest.mark.parametrize("gen,inp,args", [c[1:] for c in PA_SHAPES], ids=[c[0] for c in PA_SHAPES])
+def test_paged_attention_shapes_within_tolerance(gen, inp, args):
+    """Shapes on either side of the matrix-core form's limits (pages of 16
+    keys, at most 16 query rows per core, D in {32, 64, 128, 256}): both the
+    MFMA kernel and the f32 FMA kernel against the oracle."""
+    kw = dict(paged_inputs(seed=11, **inp), **dict(PA_ARGS, **args))
+    got, ref, plan = _both(configs.paged_attention(**gen), PA_FN, kw, "output_ptr")
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), rtol=1e-2, atol=1e-3)
+    assert plan.counts().get("pattn") == 1
+
+
 @pytest.mark.parametrize("n,d,rows", [(32, 64, 32), (256, 128, 64)])
 def test_sdpa_f16_within_tolerance(n, d, rows):
     kw = sdpa_inputs(n, d, seed=n)

@@ -115,6 +115,56 @@ def test_reshape_strides(strides, old, new, expect):
     assert _reshape_strides(strides, old, new) == expect
 
 
+@pytest.mark.parametrize("strides,old,new,expect", [
+    ((1, 0), (8, 128), (2, 4, 128), (4, 1, 0)),        # a row-broadcast leaf split by rows
+    ((0, 1), (8, 128), (2, 4, 128), (0, 0, 1)),        # a column-broadcast leaf
+    ((0, 1), (4, 8), (32,), None),                     # broadcast rows do not merge
+    ((24, 4, 1), (2, 6, 4), (2, 3, 8), (24, 8, 1)),    # split 6 and merge with the contiguous 4
+])
+def test_reshape_strides_split_groups(strides, old, new, expect):
+    assert _reshape_strides(strides, old, new) == expect
+
+
+def test_reshape_strides_against_brute_force():
+    """Every reshape the function expresses lands on the same element
+    offsets as NumPy's row-major reshape of the view's offset array, over
+    random shapes and strides (contiguous, padded, broadcast and permuted)."""
+    rng = np.random.default_rng(5)
+    factor = {4: [(4,), (2, 2), (1, 4, 1)], 6: [(6,), (2, 3), (3, 2)], 8: [(8,), (2, 4), (4, 2), (2, 2, 2)],
+              12: [(12,), (3, 4), (2, 6), (2, 2, 3)]}
+    found = 0
+    for _ in range(3000):
+        dims = [int(rng.choice(list(factor))) for _ in range(int(rng.integers(1, 4)))]
+        old = tuple(x for d in dims for x in factor[d][int(rng.integers(len(factor[d])))])
+        new = tuple(x for d in dims for x in factor[d][int(rng.integers(len(factor[d])))])
+        kind = int(rng.integers(4))
+        st, acc = [], 1
+        for n in reversed(old):
+            st.append(acc)
+            acc *= n + (1 if kind == 1 else 0)
+        st = list(reversed(st))
+        if kind == 2:
+            st[int(rng.integers(len(st)))] = 0
+        if kind == 3:
+            st = list(rng.permutation(st))
+        offs = np.zeros(old, np.int64)
+        for ax, (n, t) in enumerate(zip(old, st)):
+            sh = [1] * len(old)
+            sh[ax] = n
+            offs = offs + (np.arange(n) * t).reshape(sh)
+        got = _reshape_strides(tuple(st), old, new)
+        if got is None:
+            continue
+        found += 1
+        mine = np.zeros(new, np.int64)
+        for ax, (n, t) in enumerate(zip(new, got)):
+            sh = [1] * len(new)
+            sh[ax] = n
+            mine = mine + (np.arange(n) * t).reshape(sh)
+        np.testing.assert_array_equal(mine, offs.reshape(new))
+    assert found > 1000
+
+
 def test_lane_offsets_affine_detection():
     lo = LaneOff.from_array(np.array([4, 12, 20, 28]))
     assert lo.arr is None and (lo.base, lo.stride) == (4, 8)
