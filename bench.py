@@ -209,8 +209,8 @@ def _paged_attention():
     return dict(src=configs.paged_attention(T, HQ, HK, D, P, blocks, max_pages, BQ), fn="kernel_unified_attention_spyre_2d",
                 kw=kw, cores=(T // BQ) * HK, bytes=2 * HQ * T * D * 2 + 2 * blocks * P * HK * D * 2,
                 flops=4 * HQ * keys * D, bound="mfma",
-                dtype="f16 in/out; Q K^T and P V on f16 MFMA (exact f16 products, f32 accumulation, P as f16 "
-                      "hi + lo), f32 scores and online-softmax state",
+                dtype="f16 in/out; Q K^T and P V on f16 MFMA (exact f16 products, f32 accumulation, P rounded "
+                      "once to f16), f32 scores and online-softmax state",
                 workload=f"paged attention {T} tokens after a {ctx}-token context, {HQ} query / {HK} KV heads, "
                          f"D={D}, page {P}, {BQ} tokens per core (the reference's triton-ktir paged_attention form)")
 

@@ -417,8 +417,9 @@ int ktir_launch_attention(const ktir_attn_t* d);
  * [lanes, M, D].  Limits: D a multiple of 4, M * D <= 8192; LDS 4 * (M (D+8)
  * + N (D+8) + N D + M N + 3 M) bytes <= 160 KiB.  N = 16, M <= 16, D in
  * {32, 64, 128, 256} and one 16-bit type for q, k and v run on MFMA: exact
- * products, f32 sums in the MFMA's order, p as hi + lo in the operand type
- * (within rtol 1e-2 / atol 1e-3 of the f32 loop, not bit-exact). */
+ * products, f32 sums in the MFMA's order, p rounded once to f16 (f16
+ * operands) or as bf16 hi + lo (within rtol 1e-2 / atol 1e-3 of the f32
+ * loop, not bit-exact). */
 typedef struct ktir_pattn {
   int64_t lanes, M, N, D;
   uint64_t q_ptr, q_base;              /* q_base: const int64_t* [lanes] */

@@ -691,21 +691,28 @@ __global__ __launch_bounds__(64) void pattn_mfma(const ktir_pattn_t d, int vec, 
     sum = __fadd_rn(pr.x, pr.y);
     pr = pair32(sum);
     lsum = __fadd_rn(lsum, __fadd_rn(pr.x, pr.y));
-    // P^T as hi + lo in the operand type
+    // P^T in the operand type: f16 rounds once (P <= e^8 keeps 11
+    // significant bits, as the flash attention kernel's f16 P V), bf16
+    // carries hi + lo (about 16 bits instead of 8)
     const uint32_t h0 = pa_cvt2<BF16>(p[0], p[1]), h1 = pa_cvt2<BF16>(p[2], p[3]);
-    const pa_f2 a = pa_uncvt2<BF16>(h0), c = pa_uncvt2<BF16>(h1);
     const uint2 ph = make_uint2(h0, h1);
-    const uint2 pl = make_uint2(pa_cvt2<BF16>(__fsub_rn(p[0], a.x), __fsub_rn(p[1], a.y)),
-                                pa_cvt2<BF16>(__fsub_rn(p[2], c.x), __fsub_rn(p[3], c.y)));
+    uint2 pl = make_uint2(0u, 0u);
+    if constexpr (BF16) {
+      const pa_f2 a = pa_uncvt2<BF16>(h0), c = pa_uncvt2<BF16>(h1);
+      pl = make_uint2(pa_cvt2<BF16>(__fsub_rn(p[0], a.x), __fsub_rn(p[1], a.y)),
+                      pa_cvt2<BF16>(__fsub_rn(p[2], c.x), __fsub_rn(p[3], c.y)));
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int w = t >> 1;
-      const uint32_t x0 = pa_vword<DT>(cur, 0, w), x1 = pa_vword<DT>(cur, 1, w);
-      const uint32_t x2 = pa_vword<DT>(cur, 2, w), x3 = pa_vword<DT>(cur, 3, w);
-      const uint32_t a0 = (t & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-      const uint32_t a1 = (t & 1) ? ((x2 >> 16) | (x3 & 0xffff0000u)) : ((x2 & 0xffffu) | (x3 << 16));
+      // 16-bit element t & 1 of keys 4 g .. 4 g + 3, two per word (v_perm_b32:
+      // bytes 0-1 or 2-3 of each source)
+      const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t a0 = __builtin_amdgcn_perm(pa_vword<DT>(cur, 1, w), pa_vword<DT>(cur, 0, w), sel);
+      const uint32_t a1 = __builtin_amdgcn_perm(pa_vword<DT>(cur, 3, w), pa_vword<DT>(cur, 2, w), sel);
       const uint2 va = make_uint2(a0, a1);
-      o[t] = mfma_k16<BF16>(va, pl, mfma_k16<BF16>(va, ph, o[t]));
+      o[t] = mfma_k16<BF16>(va, ph, o[t]);
+      if constexpr (BF16) o[t] = mfma_k16<BF16>(va, pl, o[t]);
     }
   };
 
