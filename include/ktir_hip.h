@@ -437,6 +437,14 @@ typedef struct ktir_pattn {
   int32_t causal, pad;
   float scale, neg, m0, l0;
   uint64_t m_out, l_out, acc_out;
+  /* optional finalisation (out_ptr != 0), the division and cast that follow
+   * the reference's loop: out[o(r, x)] = (out_dtype)(acc[r][x] / l[r]) with
+   * o(r, x) = out_base[l] + (r / out_grp) * out_gstride + (r % out_grp) *
+   * out_row + x, elements outside [out_lo, out_hi) not written; m, l and acc
+   * are written as well */
+  uint64_t out_ptr, out_base;          /* out_base: const int64_t* [lanes] */
+  int64_t out_grp, out_gstride, out_row, out_lo, out_hi;
+  int32_t out_dtype, out_pad;
 } ktir_pattn_t;
 int ktir_launch_paged_attention(const ktir_pattn_t* d);
 

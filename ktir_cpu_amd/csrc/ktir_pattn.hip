@@ -356,6 +356,21 @@ __global__ __launch_bounds__(PA_THREADS) void pattn_kernel(const ktir_pattn_t d,
     if (i < M * D)
       *(float4*)((float*)d.acc_out + lane * M * D + i) = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
   }
+  if (d.out_ptr) {
+    // the loop's finalisation: acc / l rounded to the output's dtype
+    const int64_t obase = ((const int64_t*)d.out_base)[lane];
+#pragma unroll
+    for (int k = 0; k < ACC / 4; ++k) {
+      const int i = 4 * (tid + k * PA_THREADS);
+      if (i < M * D) {
+        const int r = i / D, x = i - r * D;
+        const int64_t ob = obase + (int64_t)(r / d.out_grp) * d.out_gstride + (int64_t)(r % d.out_grp) * d.out_row + x;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (ob + u >= d.out_lo && ob + u < d.out_hi) store_elem(d.out_ptr, ob + u, d.out_dtype, __fdiv_rn(acc[4 * k + u], lrow[r]));
+      }
+    }
+  }
 }
 
 // ---- MFMA form ---------------------------------------------------------------
@@ -794,6 +809,40 @@ __global__ __launch_bounds__(64) void pattn_mfma(const ktir_pattn_t d, int vec, 
       ((float*)d.m_out)[lane * M + n] = m;
       ((float*)d.l_out)[lane * M + n] = lsum;
     }
+    if (d.out_ptr) {
+      // the loop's finalisation: acc / l rounded to the output's dtype
+      const int64_t ob = ((const int64_t*)d.out_base)[lane] + (int64_t)(n / d.out_grp) * d.out_gstride +
+                         (int64_t)(n % d.out_grp) * d.out_row;
+      const bool w16 = d.out_dtype != KTIR_F32 && !(d.out_ptr & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t e0 = ob + NT * (4 * g + i);
+        float v[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) v[t] = __fdiv_rn(o[t][i], lsum);
+        if constexpr (NT % 8 == 0) {
+          // the row's NT consecutive elements as 16-byte stores when they
+          // lie in the window on a 16-byte boundary
+          if (w16 && !(e0 & 7) && e0 >= d.out_lo && e0 + NT <= d.out_hi) {
+#pragma unroll
+            for (int q = 0; q < NT / 8; ++q) {
+              uint32_t w[4];
+#pragma unroll
+              for (int h = 0; h < 4; ++h)
+                w[h] = d.out_dtype == KTIR_BF16
+                           ? (__float_as_uint(round_bf16(v[8 * q + 2 * h])) >> 16) |
+                                 (__float_as_uint(round_bf16(v[8 * q + 2 * h + 1])) & 0xffff0000u)
+                           : pa_cvt2<false>(v[8 * q + 2 * h], v[8 * q + 2 * h + 1]);
+              *(KTIR_G(pa_u4)*)((KTIR_G(uint16_t)*)d.out_ptr + e0 + 8 * q) = pa_u4{w[0], w[1], w[2], w[3]};
+            }
+            continue;
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          if (e0 + t >= d.out_lo && e0 + t < d.out_hi) store_elem(d.out_ptr, e0 + t, d.out_dtype, v[t]);
+      }
+    }
     float* ao = (float*)d.acc_out + (lane * M + n) * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -835,6 +884,9 @@ extern "C" int ktir_launch_paged_attention(const ktir_pattn_t* d) {
       default: return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_paged_attention: mask predicate %d", d->pred);
     }
   }
+  if (d->out_ptr && (d->out_grp < 1 || (d->out_dtype != KTIR_F16 && d->out_dtype != KTIR_BF16 && d->out_dtype != KTIR_F32)))
+    return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_paged_attention: output dtype %d / group %lld", d->out_dtype,
+                     (long long)d->out_grp);
   if (d->lanes == 0) return KTIR_OK;
   if (d->lanes > INT_MAX) return set_error(KTIR_E_UNSUPPORTED, "ktir_launch_paged_attention: too many lanes");
   // the matrix-core form: pages of 16 keys, at most 16 rows, D = 32, 64,

@@ -129,7 +129,10 @@ class PATTN(C.Structure):
                 ("order", C.c_uint64), ("qpos0", C.c_uint64), ("kpos0", C.c_uint64), ("kpos_step", C.c_int64), ("row_div", C.c_int64),
                 ("causal", C.c_int32), ("pad", C.c_int32), ("scale", C.c_float), ("neg", C.c_float),
                 ("m0", C.c_float), ("l0", C.c_float), ("m_out", C.c_uint64), ("l_out", C.c_uint64),
-                ("acc_out", C.c_uint64)]
+                ("acc_out", C.c_uint64),
+                ("out_ptr", C.c_uint64), ("out_base", C.c_uint64), ("out_grp", C.c_int64),
+                ("out_gstride", C.c_int64), ("out_row", C.c_int64), ("out_lo", C.c_int64), ("out_hi", C.c_int64),
+                ("out_dtype", C.c_int32), ("out_pad", C.c_int32)]
 
 
 class KTIRDeviceError(RuntimeError):

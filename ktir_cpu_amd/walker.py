@@ -804,6 +804,8 @@ class Executor:
                 raise NotImplementedError(f"a tile expression of rank {len(e.shape)} whose dims do not collapse "
                                           f"to {rt.MAX_DIMS}")
             e, dest = c
+        if depth == 0 and self._pattn_finalise(e, dest):
+            return
         try:
             prog, keep = compile_program(e, self.L, dest)
         except CompileError:
@@ -812,6 +814,59 @@ class Executor:
             e2 = self._split(e)
             return self._emit_store(e2, dest, depth + 1)
         self.launch("prog", prog, keep + [dest])
+
+    def _pattn_finalise(self, e: Expr, dest: LeafSpec) -> bool:
+        """The store right after a paged attention launch of
+        cast(acc / l) -- the division and cast that end the reference's
+        unified attention kernel (examples/triton-ktir/paged_attention.mlir) --
+        runs in that launch's epilogue instead of a launch of its own.  Only
+        the exact form: the launch's own acc and l buffers, row-major over the
+        stored shape, an output with unit inner stride whose rows are groups
+        of evenly spaced rows, no overlap with anything the launch reads."""
+        if self.eager or not self.plan.launches:
+            return False
+        kind, d, keep = self.plan.launches[-1]
+        if kind != "pattn" or d.out_ptr or not isinstance(keep, list) or d.lanes != self.L:
+            return False
+        if e.kind != "cast" or e.attr != "f32" or e.dtype not in ("f16", "bf16", "f32"):
+            return False
+        dv = e.args[0]
+        if dv.kind != "bin" or dv.attr != rt.op("DIVF") or dv.dtype != "f32":
+            return False
+        a, b = dv.args
+        if a.kind != "ld" or b.kind != "ld":
+            return False
+        A, B = a.attr, b.attr
+        M, D = int(d.M), int(d.D)
+        shape = tuple(int(x) for x in e.shape)
+        if not shape or shape[-1] != D or _prod(shape[:-1]) != M or len(shape) > 3:
+            return False
+        rows = shape[:-1]
+        if A.ptr != d.acc_out or A.dtype != "f32" or A.offsets is not None or A.lane.arr is not None \
+                or A.lane.base != 0 or A.lane.stride != M * D or A.strides != _cstrides(shape):
+            return False
+        if B.ptr != d.l_out or B.dtype != "f32" or B.offsets is not None or B.lane.arr is not None \
+                or B.lane.base != 0 or B.lane.stride != M or B.strides != _cstrides(rows) + (0,):
+            return False
+        if dest.dtype != e.dtype or dest.offsets is not None or dest.winner or dest.strides[-1] != 1:
+            return False
+        if len(rows) == 1:
+            grp, gstride, row = M, 0, dest.strides[0]
+        else:
+            grp, gstride, row = rows[1], dest.strides[0], dest.strides[1]
+        es = rt.ELEM_BYTES[dest.dtype]
+        lo_b, hi_b = dest.ptr + dest.lo * es, dest.ptr + dest.hi * es
+        width = {c: rt.ELEM_BYTES[n] for n, c in rt.DTYPE_CODE.items() if n in rt.ELEM_BYTES}
+        reads = [(d.q_ptr, d.q_lo, d.q_hi, width[d.q_dtype]), (d.k_ptr, d.k_lo, d.k_hi, width[d.kv_dtype]),
+                 (d.v_ptr, d.v_lo, d.v_hi, width[d.kv_dtype]), (d.tbl_ptr, d.tbl_lo, d.tbl_hi, width[d.tbl_dtype])]
+        if any(p + l * w < hi_b and lo_b < p + h * w for p, l, h, w in reads):
+            return False
+        base = self.pool.upload(np.ascontiguousarray(dest.lane.values(self.L).astype(np.int64)))
+        keep += [base, dest]
+        d.out_ptr, d.out_base = dest.ptr, base.ptr
+        d.out_grp, d.out_gstride, d.out_row, d.out_lo, d.out_hi = grp, gstride, row, dest.lo, dest.hi
+        d.out_dtype = rt.DTYPE_CODE[dest.dtype]
+        return True
 
     def _split(self, e: Expr) -> Expr:
         """Materialise the largest non-trivial subtree of `e` and return the
